@@ -1,0 +1,183 @@
+/* c4s_sampling.h -- C ABI of the MI355X (gfx950) token-sampling library for
+ * the c4tts Text2Semantic AR loop (libc4s_sampling.so).
+ *
+ * Plain C: pointers, sizes, status codes. No HIP or torch types appear in the
+ * signatures; a HIP stream is passed as `void*` (NULL = the default stream).
+ *
+ * Reference interfaces replaced (paths in the c4tts tree):
+ *   include/c4tts/t2s.h:82-89          c4::t2s::sampling::{temperature,
+ *                                      repetition_penalty, top_k, top_p, argmax}
+ *   src/t2s/sampling.cpp:14-76         their bodies
+ *   src/t2s/text2semantic.cpp:142-166  per-step processor chain + xorshift64
+ *                                      inverse-CDF draw (single stream)
+ *   src/t2s/text2semantic.cpp:303-337  the same, per row of generate_batch
+ *   src/t2s/text2semantic.cpp:109, :292-294   RNG seeding
+ *   src/t2s/text2semantic.cpp:118-121, :283-286  LM head (final_norm +
+ *                                      semantic_head), src/nn/nn.cpp:11-16, :73-83
+ *
+ * Conventions
+ *   - Every function returns C4S_OK (0) or an error code; no exceptions cross
+ *     the ABI. Degenerate sampling parameters keep the reference's no-op
+ *     meaning (temperature 1 or <= 0, penalty 1, top_k <= 0 or >= vocab,
+ *     out-of-range history ids) and are not errors.
+ *   - Device entry points are asynchronous on the given stream; the caller
+ *     owns every input/output buffer (device memory); the context owns its
+ *     workspace. A context is not thread-safe: use one per host thread.
+ *   - Input contract: logits are finite or -inf (no +inf/NaN), temperature is
+ *     1, <= 0, or keeps logits/temperature finite.
+ *   - top_p tie order: when the nucleus cut falls inside a group of equal
+ *     values, the lower token ids of that group survive. (The reference's
+ *     unstable std::sort leaves this choice to the host's sort permutation.)
+ */
+#ifndef C4S_SAMPLING_H
+#define C4S_SAMPLING_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  C4S_OK = 0,
+  C4S_EINVAL = 1, /* null pointer, bad size/dtype/mode, unsupported shape */
+  C4S_EHIP = 2,   /* a HIP call failed; see c4s_last_error */
+  C4S_ENOMEM = 3
+};
+
+enum { C4S_DTYPE_F32 = 0, C4S_DTYPE_BF16 = 1 };
+
+/* Processor selection (c4s_rows.mode).
+ * C4S_MODE_CHAIN runs the reference chain per row (text2semantic.cpp:142-166):
+ *   repetition penalty, then do_sample[b] ? temperature -> top_k -> top_p ->
+ *   draw : argmax.
+ * C4S_MODE_CUSTOM | C4S_P_* | (C4S_T_ARGMAX or C4S_T_DRAW or neither) runs only
+ *   the listed processors, in chain order, on every row (this is what backs the
+ *   single-processor legacy functions). */
+enum {
+  C4S_MODE_CHAIN = 0,
+  C4S_P_PENALTY = 1u << 0,
+  C4S_P_TEMPERATURE = 1u << 1,
+  C4S_P_TOP_K = 1u << 2,
+  C4S_P_TOP_P = 1u << 3,
+  C4S_T_ARGMAX = 1u << 4,
+  C4S_T_DRAW = 1u << 5,
+  C4S_MODE_CUSTOM = 1u << 8
+};
+
+/* Per-row statistics (c4s_rows.out_stats, 4 words per row). */
+enum {
+  C4S_STAT_PATH = 0,       /* bit0 drawn, bit1 top-k applied, bit2 top-p applied, bit3 greedy */
+  C4S_STAT_TOPP_EXACT = 1, /* nucleus cut fell inside the error bound -> exact pass ran */
+  C4S_STAT_DRAW_EXACT = 2, /* draw fell inside the error bound -> exact pass ran */
+  C4S_STAT_KEPT = 3        /* ids left with nonzero weight before the draw */
+};
+
+typedef struct c4s_ctx c4s_ctx;
+
+/* One AR step over a batch of rows (device pointers).
+ * Replaces the per-row body of text2semantic.cpp:303-337 (and :142-166 for one
+ * row); the logits stay on the device and only tokens are produced. */
+typedef struct c4s_rows {
+  const void* logits;           /* [n_rows][ld] f32 or bf16 */
+  int64_t ld;                   /* row stride in elements, >= vocab */
+  int32_t dtype;                /* C4S_DTYPE_* */
+  int32_t n_rows;
+  int32_t vocab;                /* 1 .. 1048576 */
+  const int32_t* hist_ids;      /* CSR history (generated ids), may be NULL if no penalty */
+  const int64_t* hist_offsets;  /* [n_rows+1] */
+  const float* temperature;     /* [n_rows] */
+  const int32_t* top_k;         /* [n_rows] */
+  const float* top_p;           /* [n_rows] */
+  const float* rep_penalty;     /* [n_rows] */
+  const int32_t* min_keep;      /* [n_rows] or NULL (= 1, the reference default) */
+  const uint8_t* do_sample;     /* [n_rows] or NULL (= all sample) */
+  const uint8_t* row_active;    /* [n_rows] or NULL; inactive rows: token -1, RNG untouched */
+  uint64_t* rng_state;          /* [n_rows] xorshift64 state, advanced once per drawn row */
+  int32_t* out_token;           /* [n_rows] */
+  float* out_masked;            /* [n_rows][vocab] or NULL: row state before argmax/draw */
+  uint32_t* out_stats;          /* [n_rows][4] or NULL */
+  uint32_t mode;                /* C4S_MODE_CHAIN or C4S_MODE_CUSTOM | ... */
+} c4s_rows;
+
+/* Many AR steps of a batch whose logits are already known (synthetic or
+ * replayed streams): row b's history starts from its CSR ids and grows by each
+ * token it samples that is not stop_token; a row that samples stop_token is
+ * done (later steps report -1, RNG frozen), as generate_batch does
+ * (text2semantic.cpp:333-334). Requires vocab <= 9216 (row staged in LDS). */
+typedef struct c4s_stream {
+  const float* logits;          /* step s, row b at logits + s*step_stride + b*ld */
+  int64_t ld;
+  int64_t step_stride;
+  int32_t n_steps;
+  int32_t n_rows;
+  int32_t vocab;
+  int32_t stop_token;           /* < 0: never stop */
+  const int32_t* hist_ids;
+  const int64_t* hist_offsets;
+  const float* temperature;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* rep_penalty;
+  const uint8_t* do_sample;     /* or NULL */
+  uint64_t* rng_state;
+  int32_t* out_tokens;          /* [n_steps][n_rows] */
+  uint32_t* out_stats;          /* [n_rows][4] (summed over steps) or NULL */
+} c4s_stream;
+
+/* LM head: LayerNorm(hidden) -> bf16 -> hidden @ weight^T + bias -> f32 logits
+ * (text2semantic.cpp:118-121; nn.cpp:73-83 eps/biased variance, nn.cpp:11-16
+ * weight stored (out, in)). hidden_dim must be a multiple of 32. */
+typedef struct c4s_head {
+  const uint16_t* hidden;       /* [M][D] bf16 */
+  const float* gamma;           /* [D] */
+  const float* beta;            /* [D] */
+  float eps;                    /* 1e-5 in the reference (nn.h:49-50) */
+  const uint16_t* weight;       /* [V][D] bf16 */
+  const float* bias;            /* [V] */
+  int32_t M, D, V;
+  float* logits;                /* [M][ld_out] f32 */
+  int64_t ld_out;
+} c4s_head;
+
+int c4s_create(int device, c4s_ctx** out);
+int c4s_destroy(c4s_ctx* ctx);
+const char* c4s_last_error(const c4s_ctx* ctx);
+const char* c4s_version(void);
+
+/* text2semantic.cpp:303-337 (batched) / :142-166 (single row). */
+int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream);
+/* text2semantic.cpp:296-337 over n_steps with precomputed logits. */
+int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream);
+/* text2semantic.cpp:118-121 / :283-286 (head(cur)). */
+int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);
+/* head(cur) then the chain on its logits (text2semantic.cpp:297-337 in one
+ * call); rows->logits/ld/dtype/vocab/n_rows are taken from `head`. */
+int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);
+
+/* Seeds (host only): text2semantic.cpp:109 and :292-294. */
+uint64_t c4s_seed_single(uint64_t seed);
+void c4s_seed_batch(uint64_t seed, int32_t n, uint64_t* out);
+
+/* Host-buffer single-row helpers: synchronous, copy in/out through the
+ * context's staging memory. They back the reference's five C++ entry points
+ * (include/c4tts/t2s.h:82-89, bodies sampling.cpp:14-76) and the inline draw
+ * (text2semantic.cpp:150-165). n == 0 is a no-op (argmax returns 0). */
+int c4s_host_temperature(c4s_ctx* ctx, float* logits, int32_t n, float temp);
+int c4s_host_repetition_penalty(c4s_ctx* ctx, float* logits, int32_t n, const int32_t* ids,
+                                int64_t n_ids, float penalty);
+int c4s_host_top_k(c4s_ctx* ctx, float* logits, int32_t n, int32_t k);
+int c4s_host_top_p(c4s_ctx* ctx, float* logits, int32_t n, float p, int32_t min_keep);
+int c4s_host_argmax(c4s_ctx* ctx, const float* logits, int32_t n, int32_t* out);
+int c4s_host_draw(c4s_ctx* ctx, const float* logits, int32_t n, uint64_t* rng, int32_t* out);
+
+/* Achievable-bandwidth probe: mode 0 copies `bytes` from src to dst, mode 1
+ * only reads src (dst needs 4 bytes). bytes must be a multiple of 16. */
+int c4s_hbm_probe(c4s_ctx* ctx, const void* src, void* dst, int64_t bytes, int32_t mode,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* C4S_SAMPLING_H */

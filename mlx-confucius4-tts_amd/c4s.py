@@ -1,0 +1,244 @@
+"""Python binding of libc4s_sampling.so (C ABI in include/c4s_sampling.h).
+
+ctypes only; torch supplies device memory and streams, nothing else. Loading
+fails loudly when the library has not been built or no gfx950 device is
+present: there is no CPU fallback in this package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "lib", "libc4s_sampling.so")
+HEADER = os.path.join(REPO, "include", "c4s_sampling.h")
+
+OK, EINVAL, EHIP, ENOMEM = 0, 1, 2, 3
+F32, BF16 = 0, 1
+MODE_CHAIN = 0
+P_PENALTY, P_TEMPERATURE, P_TOP_K, P_TOP_P = 1, 2, 4, 8
+T_ARGMAX, T_DRAW = 16, 32
+MODE_CUSTOM = 256
+STAT_PATH, STAT_TOPP_EXACT, STAT_DRAW_EXACT, STAT_KEPT = 0, 1, 2, 3
+
+_vp = C.c_void_p
+
+
+class Rows(C.Structure):
+    _fields_ = [("logits", _vp), ("ld", C.c_int64), ("dtype", C.c_int32), ("n_rows", C.c_int32),
+                ("vocab", C.c_int32), ("hist_ids", _vp), ("hist_offsets", _vp),
+                ("temperature", _vp), ("top_k", _vp), ("top_p", _vp), ("rep_penalty", _vp),
+                ("min_keep", _vp), ("do_sample", _vp), ("row_active", _vp), ("rng_state", _vp),
+                ("out_token", _vp), ("out_masked", _vp), ("out_stats", _vp), ("mode", C.c_uint32)]
+
+
+class Stream(C.Structure):
+    _fields_ = [("logits", _vp), ("ld", C.c_int64), ("step_stride", C.c_int64),
+                ("n_steps", C.c_int32), ("n_rows", C.c_int32), ("vocab", C.c_int32),
+                ("stop_token", C.c_int32), ("hist_ids", _vp), ("hist_offsets", _vp),
+                ("temperature", _vp), ("top_k", _vp), ("top_p", _vp), ("rep_penalty", _vp),
+                ("do_sample", _vp), ("rng_state", _vp), ("out_tokens", _vp), ("out_stats", _vp)]
+
+
+class Head(C.Structure):
+    _fields_ = [("hidden", _vp), ("gamma", _vp), ("beta", _vp), ("eps", C.c_float),
+                ("weight", _vp), ("bias", _vp), ("M", C.c_int32), ("D", C.c_int32),
+                ("V", C.c_int32), ("logits", _vp), ("ld_out", C.c_int64)]
+
+
+def header_functions() -> list[str]:
+    """Names of every function the public header declares."""
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(c4s_[a-z0-9_]+)\s*\(", txt)))
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    L.c4s_create.argtypes = [C.c_int, C.POINTER(_vp)]
+    L.c4s_destroy.argtypes = [_vp]
+    L.c4s_last_error.argtypes = [_vp]
+    L.c4s_last_error.restype = C.c_char_p
+    L.c4s_version.restype = C.c_char_p
+    L.c4s_sample_rows.argtypes = [_vp, C.POINTER(Rows), _vp]
+    L.c4s_sample_stream.argtypes = [_vp, C.POINTER(Stream), _vp]
+    L.c4s_lmhead.argtypes = [_vp, C.POINTER(Head), _vp]
+    L.c4s_lmhead_sample.argtypes = [_vp, C.POINTER(Head), C.POINTER(Rows), _vp]
+    L.c4s_seed_single.argtypes = [C.c_uint64]
+    L.c4s_seed_single.restype = C.c_uint64
+    L.c4s_seed_batch.argtypes = [C.c_uint64, C.c_int32, _vp]
+    L.c4s_host_temperature.argtypes = [_vp, _vp, C.c_int32, C.c_float]
+    L.c4s_host_repetition_penalty.argtypes = [_vp, _vp, C.c_int32, _vp, C.c_int64, C.c_float]
+    L.c4s_host_top_k.argtypes = [_vp, _vp, C.c_int32, C.c_int32]
+    L.c4s_host_top_p.argtypes = [_vp, _vp, C.c_int32, C.c_float, C.c_int32]
+    L.c4s_host_argmax.argtypes = [_vp, _vp, C.c_int32, _vp]
+    L.c4s_host_draw.argtypes = [_vp, _vp, C.c_int32, _vp, _vp]
+    L.c4s_hbm_probe.argtypes = [_vp, _vp, _vp, C.c_int64, C.c_int32, _vp]
+    _lib = L
+    return L
+
+
+def _p(t):
+    """Device (or host numpy) pointer of a tensor/array, or None."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def _stream_handle(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if hasattr(stream, "cuda_stream"):
+        return stream.cuda_stream
+    return stream
+
+
+class C4SError(RuntimeError):
+    pass
+
+
+class Context:
+    """One library context on one device (not thread-safe)."""
+
+    def __init__(self, device: int = 0):
+        self._h = _vp()
+        rc = lib().c4s_create(device, C.byref(self._h))
+        if rc != OK:
+            raise C4SError(f"c4s_create(device={device}) failed with code {rc} "
+                           "(no gfx950 device visible?)")
+        self.device = device
+
+    def close(self):
+        if self._h:
+            lib().c4s_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != OK:
+            msg = lib().c4s_last_error(self._h).decode()
+            raise C4SError(f"{what}: code {rc}: {msg}")
+
+    # ---- device entry points (torch tensors on the GPU) ------------------------
+    def sample_rows(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_token,
+                    do_sample=None, min_keep=None, row_active=None, out_masked=None,
+                    out_stats=None, mode=MODE_CHAIN, vocab=None, stream=None):
+        import torch
+        n_rows, ld = logits.shape
+        r = Rows(logits=_p(logits), ld=ld, dtype=BF16 if logits.dtype == torch.bfloat16 else F32,
+                 n_rows=n_rows, vocab=vocab or ld, hist_ids=_p(hist_ids), hist_offsets=_p(hist_off),
+                 temperature=_p(temp), top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen),
+                 min_keep=_p(min_keep), do_sample=_p(do_sample), row_active=_p(row_active),
+                 rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
+                 out_stats=_p(out_stats), mode=mode)
+        self._check(lib().c4s_sample_rows(self._h, C.byref(r), _stream_handle(stream)), "sample_rows")
+
+    def sample_stream(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_tokens,
+                      do_sample=None, stop_token=-1, out_stats=None, stream=None):
+        n_steps, n_rows, ld = logits.shape
+        s = Stream(logits=_p(logits), ld=ld, step_stride=n_rows * ld, n_steps=n_steps,
+                   n_rows=n_rows, vocab=ld, stop_token=stop_token, hist_ids=_p(hist_ids),
+                   hist_offsets=_p(hist_off), temperature=_p(temp), top_k=_p(top_k),
+                   top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
+                   rng_state=_p(rng), out_tokens=_p(out_tokens), out_stats=_p(out_stats))
+        self._check(lib().c4s_sample_stream(self._h, C.byref(s), _stream_handle(stream)),
+                    "sample_stream")
+
+    def _head(self, hidden, gamma, beta, weight, bias, logits, eps):
+        M, D = hidden.shape
+        V = weight.shape[0]
+        return Head(hidden=_p(hidden), gamma=_p(gamma), beta=_p(beta), eps=eps, weight=_p(weight),
+                    bias=_p(bias), M=M, D=D, V=V, logits=_p(logits),
+                    ld_out=(logits.shape[1] if logits is not None else V))
+
+    def lmhead(self, hidden, gamma, beta, weight, bias, logits, eps=1e-5, stream=None):
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+        self._check(lib().c4s_lmhead(self._h, C.byref(h), _stream_handle(stream)), "lmhead")
+
+    def lmhead_sample(self, hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k,
+                      top_p, pen, rng, out_token, logits=None, do_sample=None, out_masked=None,
+                      out_stats=None, eps=1e-5, stream=None):
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+        r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp),
+                 top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
+                 rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
+                 out_stats=_p(out_stats), mode=MODE_CHAIN)
+        self._check(lib().c4s_lmhead_sample(self._h, C.byref(h), C.byref(r), _stream_handle(stream)),
+                    "lmhead_sample")
+
+    def hbm_probe(self, src, dst, nbytes, mode=0, stream=None):
+        self._check(lib().c4s_hbm_probe(self._h, _p(src), _p(dst), nbytes, mode,
+                                        _stream_handle(stream)), "hbm_probe")
+
+    # ---- host-buffer single-row helpers (numpy, synchronous) ---------------------
+    def host_temperature(self, row, temp):
+        import numpy as np
+        v = np.array(row, dtype=np.float32, copy=True)
+        self._check(lib().c4s_host_temperature(self._h, v.ctypes.data, v.size, temp), "temperature")
+        return v
+
+    def host_repetition_penalty(self, row, ids, pen):
+        import numpy as np
+        v = np.array(row, dtype=np.float32, copy=True)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        self._check(lib().c4s_host_repetition_penalty(self._h, v.ctypes.data, v.size,
+                                                      ids.ctypes.data if ids.size else None,
+                                                      ids.size, pen), "repetition_penalty")
+        return v
+
+    def host_top_k(self, row, k):
+        import numpy as np
+        v = np.array(row, dtype=np.float32, copy=True)
+        self._check(lib().c4s_host_top_k(self._h, v.ctypes.data, v.size, k), "top_k")
+        return v
+
+    def host_top_p(self, row, p, min_keep=1):
+        import numpy as np
+        v = np.array(row, dtype=np.float32, copy=True)
+        self._check(lib().c4s_host_top_p(self._h, v.ctypes.data, v.size, p, min_keep), "top_p")
+        return v
+
+    def host_argmax(self, row):
+        import numpy as np
+        v = np.ascontiguousarray(row, dtype=np.float32)
+        out = C.c_int32(0)
+        self._check(lib().c4s_host_argmax(self._h, v.ctypes.data, v.size, C.addressof(out)), "argmax")
+        return out.value
+
+    def host_draw(self, row, state):
+        import numpy as np
+        v = np.ascontiguousarray(row, dtype=np.float32)
+        s = C.c_uint64(state)
+        out = C.c_int32(0)
+        self._check(lib().c4s_host_draw(self._h, v.ctypes.data, v.size, C.addressof(s),
+                                        C.addressof(out)), "draw")
+        return out.value, s.value
+
+
+def seed_single(seed: int) -> int:
+    return int(lib().c4s_seed_single(seed))
+
+
+def seed_batch(seed: int, n: int):
+    import numpy as np
+    out = np.zeros(n, dtype=np.uint64)
+    lib().c4s_seed_batch(seed, n, out.ctypes.data)
+    return out

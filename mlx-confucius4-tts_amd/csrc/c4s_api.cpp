@@ -1,0 +1,464 @@
+// C ABI of libc4s_sampling.so (declarations and contracts in include/c4s_sampling.h).
+//
+// Host side only: argument validation, per-context workspace, dispatch to the
+// gfx950 kernels. There is no CPU fallback: a missing device or a failed launch
+// is reported as an error.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/c4s_sampling.h"
+#include "c4s_internal.h"
+
+struct c4s_ctx {
+  int device = 0;
+  std::string err;
+  hipStream_t host_stream = nullptr;  // used by the synchronous host helpers
+  void* ws = nullptr;                 // large-vocab exact-pass key buffers
+  size_t ws_bytes = 0;
+  void* hnorm = nullptr;              // LM head: normalised bf16 rows
+  size_t hnorm_bytes = 0;
+  void* logits_ws = nullptr;          // LM head + sample: logits when the caller gives none
+  size_t logits_bytes = 0;
+  // host-helper staging (device)
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
+};
+
+namespace {
+
+constexpr int kStreamVocabMax = 9216;
+constexpr size_t kLdsLimit = 160 * 1024;
+
+int fail(c4s_ctx* ctx, int code, const std::string& msg) {
+  if (ctx) ctx->err = msg;
+  return code;
+}
+
+int hip_fail(c4s_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, C4S_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  hipError_t err = hipSuccess;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) err = hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+int ensure(c4s_ctx* ctx, void** buf, size_t* have, size_t need, const char* what) {
+  if (need <= *have) return C4S_OK;
+  if (*buf) {
+    hipError_t e = hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
+    if (e != hipSuccess) return hip_fail(ctx, e, what);
+  }
+  hipError_t e = hipMalloc(buf, need);
+  if (e != hipSuccess) {
+    *buf = nullptr;
+    return e == hipErrorOutOfMemory ? fail(ctx, C4S_ENOMEM, std::string(what) + ": out of memory")
+                                    : hip_fail(ctx, e, what);
+  }
+  *have = need;
+  return C4S_OK;
+}
+
+size_t pow2_at_least(size_t n) {
+  size_t p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+int validate_rows(c4s_ctx* ctx, const c4s_rows* r) {
+  if (!r) return fail(ctx, C4S_EINVAL, "rows descriptor is NULL");
+  if (r->n_rows < 0) return fail(ctx, C4S_EINVAL, "n_rows < 0");
+  if (r->n_rows == 0) return C4S_OK;
+  if (r->vocab < 1 || r->vocab > c4s::kMaxVocab) return fail(ctx, C4S_EINVAL, "vocab out of range");
+  if (r->ld < r->vocab) return fail(ctx, C4S_EINVAL, "ld < vocab");
+  if (r->dtype != C4S_DTYPE_F32 && r->dtype != C4S_DTYPE_BF16)
+    return fail(ctx, C4S_EINVAL, "unknown dtype");
+  if (!r->logits || !r->out_token) return fail(ctx, C4S_EINVAL, "logits/out_token is NULL");
+  const uint32_t m = r->mode;
+  const bool custom = (m & C4S_MODE_CUSTOM) != 0;
+  const uint32_t known = C4S_P_PENALTY | C4S_P_TEMPERATURE | C4S_P_TOP_K | C4S_P_TOP_P |
+                         C4S_T_ARGMAX | C4S_T_DRAW | C4S_MODE_CUSTOM;
+  if (m & ~known) return fail(ctx, C4S_EINVAL, "unknown mode bits");
+  if (!custom && m != C4S_MODE_CHAIN) return fail(ctx, C4S_EINVAL, "processor bits need C4S_MODE_CUSTOM");
+  if (custom && (m & C4S_T_ARGMAX) && (m & C4S_T_DRAW))
+    return fail(ctx, C4S_EINVAL, "argmax and draw are exclusive");
+  const bool pen = !custom || (m & C4S_P_PENALTY);
+  if (pen && (!r->rep_penalty || !r->hist_offsets))
+    return fail(ctx, C4S_EINVAL, "penalty needs rep_penalty and hist_offsets");
+  if (pen && !r->hist_ids) {
+    // allowed only when every history is empty; the kernel never reads ids then
+  }
+  if ((!custom || (m & C4S_P_TEMPERATURE)) && !r->temperature)
+    return fail(ctx, C4S_EINVAL, "temperature is NULL");
+  if ((!custom || (m & C4S_P_TOP_K)) && !r->top_k) return fail(ctx, C4S_EINVAL, "top_k is NULL");
+  if ((!custom || (m & C4S_P_TOP_P)) && !r->top_p) return fail(ctx, C4S_EINVAL, "top_p is NULL");
+  const bool draws = !custom || (m & C4S_T_DRAW);
+  if (draws && !r->rng_state) return fail(ctx, C4S_EINVAL, "rng_state is NULL");
+  return C4S_OK;
+}
+
+c4s::RowsArgs to_args(const c4s_rows* r) {
+  c4s::RowsArgs a{};
+  a.logits = r->logits;
+  a.ld = r->ld;
+  a.dtype = r->dtype;
+  a.n_rows = r->n_rows;
+  a.vocab = r->vocab;
+  a.hist_ids = r->hist_ids;
+  a.hist_off = r->hist_offsets;
+  a.temp = r->temperature;
+  a.top_k = r->top_k;
+  a.top_p = r->top_p;
+  a.pen = r->rep_penalty;
+  a.min_keep = r->min_keep;
+  a.do_sample = r->do_sample;
+  a.row_active = r->row_active;
+  a.rng = r->rng_state;
+  a.out_tok = r->out_token;
+  a.out_masked = r->out_masked;
+  a.stats = r->out_stats;
+  a.mode = r->mode;
+  return a;
+}
+
+int launch_rows_checked(c4s_ctx* ctx, const c4s_rows* r, hipStream_t s) {
+  c4s::RowsArgs a = to_args(r);
+  if (r->vocab > c4s::kLdsVocabMax) {
+    const size_t per_row = pow2_at_least((size_t)r->vocab) * sizeof(uint32_t);
+    int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, per_row * (size_t)r->n_rows, "sort workspace");
+    if (rc) return rc;
+    a.sort_ws = static_cast<uint32_t*>(ctx->ws);
+    a.sort_ws_stride = (int64_t)(per_row / sizeof(uint32_t));
+  }
+  hipError_t e = c4s::launch_rows(a, s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sample_rows launch");
+  return C4S_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* c4s_version(void) { return "c4s-sampling 0.1 gfx950"; }
+
+int c4s_create(int device, c4s_ctx** out) {
+  if (!out) return C4S_EINVAL;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return C4S_EHIP;
+  if (device < 0 || device >= n) return C4S_EINVAL;
+  c4s_ctx* ctx = new c4s_ctx();
+  ctx->device = device;
+  DeviceGuard g(device);
+  if (g.err != hipSuccess) { delete ctx; return C4S_EHIP; }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) { delete ctx; return C4S_EHIP; }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    // The code objects are built for gfx950 only.
+    delete ctx;
+    return C4S_EINVAL;
+  }
+  if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete ctx;
+    return C4S_EHIP;
+  }
+  *out = ctx;
+  return C4S_OK;
+}
+
+int c4s_destroy(c4s_ctx* ctx) {
+  if (!ctx) return C4S_OK;
+  DeviceGuard g(ctx->device);
+  if (ctx->host_stream) (void)hipStreamSynchronize(ctx->host_stream);
+  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage})
+    if (p) (void)hipFree(p);
+  if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
+  delete ctx;
+  return C4S_OK;
+}
+
+const char* c4s_last_error(const c4s_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  int rc = validate_rows(ctx, rows);
+  if (rc || rows->n_rows == 0) return rc;
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  return launch_rows_checked(ctx, rows, static_cast<hipStream_t>(stream));
+}
+
+int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!st) return fail(ctx, C4S_EINVAL, "stream descriptor is NULL");
+  if (st->n_rows < 0 || st->n_steps < 0) return fail(ctx, C4S_EINVAL, "negative size");
+  if (st->n_rows == 0 || st->n_steps == 0) return C4S_OK;
+  if (st->vocab < 1 || st->vocab > kStreamVocabMax)
+    return fail(ctx, C4S_EINVAL, "stream needs 1 <= vocab <= 9216");
+  if (st->ld < st->vocab) return fail(ctx, C4S_EINVAL, "ld < vocab");
+  if (!st->logits || !st->hist_offsets || !st->temperature || !st->top_k || !st->top_p ||
+      !st->rep_penalty || !st->rng_state || !st->out_tokens)
+    return fail(ctx, C4S_EINVAL, "stream: required pointer is NULL");
+  c4s::StreamArgs a{};
+  a.logits = st->logits;
+  a.ld = st->ld;
+  a.step_stride = st->step_stride;
+  a.n_steps = st->n_steps;
+  a.n_rows = st->n_rows;
+  a.vocab = st->vocab;
+  a.hist_ids = st->hist_ids;
+  a.hist_off = st->hist_offsets;
+  a.temp = st->temperature;
+  a.top_k = st->top_k;
+  a.top_p = st->top_p;
+  a.pen = st->rep_penalty;
+  a.do_sample = st->do_sample;
+  a.stop_token = st->stop_token;
+  a.rng = st->rng_state;
+  a.out_tok = st->out_tokens;
+  a.stats = st->out_stats;
+  a.max_unique = st->vocab;  // distinct ids are a subset of [0, vocab)
+  if (c4s::stream_lds_bytes(a.vocab, a.max_unique) + 4096 > kLdsLimit)
+    return fail(ctx, C4S_EINVAL, "stream: row state exceeds LDS");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  hipError_t e = c4s::launch_stream(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");
+  return C4S_OK;
+}
+
+static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out,
+                       hipStream_t s) {
+  if (!h->hidden || !h->gamma || !h->beta || !h->weight || !h->bias || !logits)
+    return fail(ctx, C4S_EINVAL, "lmhead: required pointer is NULL");
+  if (h->M < 1 || h->D < 32 || h->V < 1 || (h->D % 32) != 0)
+    return fail(ctx, C4S_EINVAL, "lmhead: needs M >= 1, V >= 1, D a positive multiple of 32");
+  if (ld_out < h->V) return fail(ctx, C4S_EINVAL, "lmhead: ld_out < V");
+  if ((reinterpret_cast<uintptr_t>(h->hidden) | reinterpret_cast<uintptr_t>(h->weight)) & 15u)
+    return fail(ctx, C4S_EINVAL, "lmhead: hidden and weight must be 16-byte aligned");
+  const size_t mpad = (size_t)((h->M + 63) / 64 * 64);
+  int rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, mpad * (size_t)h->D * 2, "lmhead workspace");
+  if (rc) return rc;
+  c4s::LmHeadArgs a{};
+  a.hidden = h->hidden;
+  a.gamma = h->gamma;
+  a.beta = h->beta;
+  a.eps = h->eps;
+  a.weight = h->weight;
+  a.bias = h->bias;
+  a.logits = logits;
+  a.ld_out = ld_out;
+  a.M = h->M;
+  a.D = h->D;
+  a.V = h->V;
+  a.hnorm = static_cast<uint16_t*>(ctx->hnorm);
+  hipError_t e = c4s::launch_layernorm_bf16(a, s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "layernorm launch");
+  e = c4s::launch_lmhead_gemm(a, s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "lmhead gemm launch");
+  return C4S_OK;
+}
+
+int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!head) return fail(ctx, C4S_EINVAL, "lmhead descriptor is NULL");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  return lmhead_impl(ctx, head, head->logits, head->ld_out, static_cast<hipStream_t>(stream));
+}
+
+int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!head || !rows) return fail(ctx, C4S_EINVAL, "descriptor is NULL");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  float* logits = head->logits;
+  int64_t ld = head->ld_out;
+  if (!logits) {
+    int rc = ensure(ctx, &ctx->logits_ws, &ctx->logits_bytes,
+                    (size_t)std::max(head->M, 1) * (size_t)std::max(head->V, 1) * 4, "logits workspace");
+    if (rc) return rc;
+    logits = static_cast<float*>(ctx->logits_ws);
+    ld = head->V;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = lmhead_impl(ctx, head, logits, ld, s);
+  if (rc) return rc;
+  c4s_rows r = *rows;
+  r.logits = logits;
+  r.ld = ld;
+  r.dtype = C4S_DTYPE_F32;
+  r.n_rows = head->M;
+  r.vocab = head->V;
+  rc = validate_rows(ctx, &r);
+  if (rc) return rc;
+  return launch_rows_checked(ctx, &r, s);
+}
+
+uint64_t c4s_seed_single(uint64_t seed) { return seed ? seed : 0x9E3779B97F4A7C15ull; }
+
+void c4s_seed_batch(uint64_t seed, int32_t n, uint64_t* out) {
+  if (!out) return;
+  const uint64_t base = c4s_seed_single(seed);
+  for (int32_t b = 0; b < n; ++b) out[b] = base + static_cast<uint64_t>(b) * 0x100000001b3ull;
+}
+
+// ---- synchronous single-row helpers -----------------------------------------------
+
+namespace {
+
+struct Stage {
+  float* logits;
+  int32_t* ids;
+  int64_t* off;
+  float* fparams;   // temp, top_p, penalty
+  int32_t* iparams; // top_k, min_keep
+  uint64_t* rng;
+  int32_t* tok;
+};
+
+int stage_for(c4s_ctx* ctx, int32_t n, int64_t n_ids, Stage* st) {
+  auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t b_logits = al((size_t)n * 4), b_ids = al((size_t)std::max<int64_t>(n_ids, 1) * 4);
+  const size_t need = b_logits + b_ids + al(16) + al(12) + al(8) + al(8) + al(4);
+  int rc = ensure(ctx, &ctx->stage, &ctx->stage_bytes, need, "staging");
+  if (rc) return rc;
+  char* p = static_cast<char*>(ctx->stage);
+  st->logits = reinterpret_cast<float*>(p); p += b_logits;
+  st->ids = reinterpret_cast<int32_t*>(p); p += b_ids;
+  st->off = reinterpret_cast<int64_t*>(p); p += al(16);
+  st->fparams = reinterpret_cast<float*>(p); p += al(12);
+  st->iparams = reinterpret_cast<int32_t*>(p); p += al(8);
+  st->rng = reinterpret_cast<uint64_t*>(p); p += al(8);
+  st->tok = reinterpret_cast<int32_t*>(p);
+  return C4S_OK;
+}
+
+int host_call(c4s_ctx* ctx, float* logits, int32_t n, const int32_t* ids, int64_t n_ids,
+              float temp, int32_t k, float p, float pen, int32_t min_keep, uint64_t* rng,
+              uint32_t mode, bool write_back, int32_t* tok_out) {
+  if (!ctx) return C4S_EINVAL;
+  if (n < 0 || n_ids < 0) return fail(ctx, C4S_EINVAL, "negative size");
+  if (n > c4s::kMaxVocab) return fail(ctx, C4S_EINVAL, "row too long");
+  if (n > 0 && !logits) return fail(ctx, C4S_EINVAL, "logits is NULL");
+  if (n_ids > 0 && !ids) return fail(ctx, C4S_EINVAL, "ids is NULL");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  Stage st;
+  int rc = stage_for(ctx, n, n_ids, &st);
+  if (rc) return rc;
+  hipStream_t s = ctx->host_stream;
+  const int64_t off[2] = {0, n_ids};
+  const float fp[3] = {temp, p, pen};
+  const int32_t ip[2] = {k, min_keep};
+  hipError_t e = hipMemcpyAsync(st.logits, logits, (size_t)n * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && n_ids > 0)
+    e = hipMemcpyAsync(st.ids, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(st.off, off, sizeof(off), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(st.fparams, fp, sizeof(fp), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(st.iparams, ip, sizeof(ip), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && rng) e = hipMemcpyAsync(st.rng, rng, 8, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "staging copy");
+  c4s_rows r{};
+  r.logits = st.logits;
+  r.ld = n;
+  r.dtype = C4S_DTYPE_F32;
+  r.n_rows = 1;
+  r.vocab = n;
+  r.hist_ids = st.ids;
+  r.hist_offsets = st.off;
+  r.temperature = st.fparams;
+  r.top_p = st.fparams + 1;
+  r.rep_penalty = st.fparams + 2;
+  r.top_k = st.iparams;
+  r.min_keep = st.iparams + 1;
+  r.rng_state = st.rng;
+  r.out_token = st.tok;
+  r.out_masked = write_back ? st.logits : nullptr;
+  r.mode = mode;
+  rc = validate_rows(ctx, &r);
+  if (rc) return rc;
+  rc = launch_rows_checked(ctx, &r, s);
+  if (rc) return rc;
+  if (write_back) e = hipMemcpyAsync(logits, st.logits, (size_t)n * 4, hipMemcpyDeviceToHost, s);
+  int32_t tok = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&tok, st.tok, 4, hipMemcpyDeviceToHost, s);
+  uint64_t r_out = 0;
+  if (e == hipSuccess && rng) e = hipMemcpyAsync(&r_out, st.rng, 8, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "single-row call");
+  if (rng) *rng = r_out;
+  if (tok_out) *tok_out = tok;
+  return C4S_OK;
+}
+
+}  // namespace
+
+int c4s_host_temperature(c4s_ctx* ctx, float* logits, int32_t n, float temp) {
+  if (ctx && n == 0) return C4S_OK;
+  return host_call(ctx, logits, n, nullptr, 0, temp, 0, 1.0f, 1.0f, 1, nullptr,
+                   C4S_MODE_CUSTOM | C4S_P_TEMPERATURE, true, nullptr);
+}
+
+int c4s_host_repetition_penalty(c4s_ctx* ctx, float* logits, int32_t n, const int32_t* ids,
+                                int64_t n_ids, float penalty) {
+  if (ctx && n == 0) return C4S_OK;
+  return host_call(ctx, logits, n, ids, n_ids, 1.0f, 0, 1.0f, penalty, 1, nullptr,
+                   C4S_MODE_CUSTOM | C4S_P_PENALTY, true, nullptr);
+}
+
+int c4s_host_top_k(c4s_ctx* ctx, float* logits, int32_t n, int32_t k) {
+  if (ctx && n == 0) return C4S_OK;
+  return host_call(ctx, logits, n, nullptr, 0, 1.0f, k, 1.0f, 1.0f, 1, nullptr,
+                   C4S_MODE_CUSTOM | C4S_P_TOP_K, true, nullptr);
+}
+
+int c4s_host_top_p(c4s_ctx* ctx, float* logits, int32_t n, float p, int32_t min_keep) {
+  if (ctx && n == 0) return C4S_OK;  // the reference dereferences an empty max_element
+  return host_call(ctx, logits, n, nullptr, 0, 1.0f, 0, p, 1.0f, min_keep, nullptr,
+                   C4S_MODE_CUSTOM | C4S_P_TOP_P, true, nullptr);
+}
+
+int c4s_host_argmax(c4s_ctx* ctx, const float* logits, int32_t n, int32_t* out) {
+  if (!out) return fail(ctx, C4S_EINVAL, "out is NULL");
+  if (ctx && n == 0) { *out = 0; return C4S_OK; }   // max_element(empty) - begin == 0
+  return host_call(ctx, const_cast<float*>(logits), n, nullptr, 0, 1.0f, 0, 1.0f, 1.0f, 1,
+                   nullptr, C4S_MODE_CUSTOM | C4S_T_ARGMAX, false, out);
+}
+
+int c4s_host_draw(c4s_ctx* ctx, const float* logits, int32_t n, uint64_t* rng, int32_t* out) {
+  if (!out || !rng) return fail(ctx, C4S_EINVAL, "out/rng is NULL");
+  if (ctx && n == 0) return fail(ctx, C4S_EINVAL, "draw over an empty row");
+  return host_call(ctx, const_cast<float*>(logits), n, nullptr, 0, 1.0f, 0, 1.0f, 1.0f, 1, rng,
+                   C4S_MODE_CUSTOM | C4S_T_DRAW, false, out);
+}
+
+int c4s_hbm_probe(c4s_ctx* ctx, const void* src, void* dst, int64_t bytes, int32_t mode,
+                  void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!src || !dst || bytes < 0 || (bytes % 16) != 0 || (mode != 0 && mode != 1))
+    return fail(ctx, C4S_EINVAL, "hbm_probe: bad arguments");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  hipError_t e = c4s::launch_hbm_probe(src, dst, bytes, mode, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(ctx, e, "hbm_probe launch");
+  return C4S_OK;
+}
+
+}  // extern "C"

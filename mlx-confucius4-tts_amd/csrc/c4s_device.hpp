@@ -1,0 +1,178 @@
+// Device primitives for the gfx950 token-sampling kernels: order-preserving
+// float keys, the xorshift64 step, and wave64 / workgroup reductions and scans.
+//
+// Everything here is written for CDNA wave64: a workgroup of NT threads is
+// NT/64 waves, wave-level steps use cross-lane shuffles, workgroup-level steps
+// combine one value per wave through LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace c4s {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+// Order-preserving map float -> uint32 (a < b as floats <=> key(a) < key(b)),
+// with -0.0 folded onto +0.0 because the reference compares with `<`, under
+// which the two are equal. NaN is outside the input contract.
+__device__ __forceinline__ uint32_t fkey(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float kfloat(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+constexpr uint32_t kKeyNegInf = 0x007fffffu;  // fkey(-inf)
+
+// Reference RNG step, src/t2s/text2semantic.cpp:158.
+__device__ __forceinline__ uint64_t xorshift64(uint64_t s) {
+  s ^= s << 13;
+  s ^= s >> 7;
+  s ^= s << 17;
+  return s;
+}
+
+// Uniform in [0,1) from the top 53 bits, as text2semantic.cpp:159 forms it.
+__device__ __forceinline__ double unit_from_state(uint64_t s) {
+  return static_cast<double>(s >> 11) / static_cast<double>(1ull << 53);
+}
+
+// ---- wave64 reductions ------------------------------------------------------
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// (value, index) pair: larger value wins, equal values -> smaller index
+// (std::max_element keeps the first maximum).
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, kWave);
+    const int oi = __shfl_xor(i, o, kWave);
+    argmax_merge(v, i, ov, oi);
+  }
+}
+
+// Inclusive prefix sums across the wave (lane order).
+__device__ __forceinline__ double wave_incl_scan_f64(double v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double t = __shfl_up(v, o, kWave);
+    if (l >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_up((int)v, o, kWave);
+    if (l >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// ---- workgroup reductions ------------------------------------------------------
+// `red` is LDS scratch with room for one entry per wave (typed views of the same
+// bytes are fine). Every thread returns the result. Two barriers: the trailing
+// one lets the caller reuse `red` immediately.
+template <int NT>
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+  v = wave_sum_f64(v);
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < NT / kWave; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+template <int NT>
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t* red) {
+  v = wave_sum_u32(v);
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (int w = 0; w < NT / kWave; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_max_f32(float v, float* red) {
+  v = wave_max_f32(v);
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / kWave; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+template <int NT>
+__device__ __forceinline__ int block_min_i32(int v, int* red) {
+  v = wave_min_i32(v);
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  int r = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / kWave; ++w) r = min(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+template <int NT>
+__device__ __forceinline__ void block_argmax(float& v, int& i, float* redv, int* redi) {
+  wave_argmax(v, i);
+  if (lane_id() == 0) { redv[wave_id()] = v; redi[wave_id()] = i; }
+  __syncthreads();
+  v = redv[0];
+  i = redi[0];
+#pragma unroll
+  for (int w = 1; w < NT / kWave; ++w) argmax_merge(v, i, redv[w], redi[w]);
+  __syncthreads();
+}
+
+}  // namespace c4s

@@ -1,0 +1,102 @@
+// Launch descriptors shared by the HIP kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace c4s {
+
+// Per-row processor selection (kernel side of the public C4S_* mode bits).
+enum : uint32_t {
+  kPenalty = 1u << 0,
+  kTemperature = 1u << 1,
+  kTopK = 1u << 2,
+  kTopP = 1u << 3,
+  kArgmax = 1u << 4,
+  kDraw = 1u << 5,
+  kCustom = 1u << 8,
+};
+
+// Rows at or below this vocabulary size are staged whole in LDS (one
+// workgroup per row); larger rows are streamed from HBM in several passes.
+constexpr int kLdsVocabMax = 12288;
+constexpr int kMaxVocab = 1 << 20;
+constexpr int kThreads = 1024;
+
+// Per-row statistics written when the caller asks for them (4 words per row).
+enum : int {
+  kStatPath = 0,        // bit0 sampled, bit1 top-k applied, bit2 top-p applied, bit3 greedy
+  kStatTopPExact = 1,   // 1 if the nucleus cut needed the exact sequential pass
+  kStatDrawExact = 2,   // 1 if the draw needed the exact sequential pass
+  kStatKept = 3,        // number of ids surviving the chain (before the draw)
+};
+
+struct RowsArgs {
+  const void* logits;
+  int64_t ld;
+  int dtype;  // 0 f32, 1 bf16
+  int n_rows;
+  int vocab;
+  const int32_t* hist_ids;
+  const int64_t* hist_off;
+  const float* temp;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* pen;
+  const int32_t* min_keep;
+  const uint8_t* do_sample;
+  const uint8_t* row_active;
+  uint64_t* rng;
+  int32_t* out_tok;
+  float* out_masked;
+  uint32_t* stats;
+  uint32_t mode;        // kCustom | processor bits, or 0 for the reference chain
+  uint32_t* sort_ws;    // large-vocab exact pass: per-row key buffer
+  int64_t sort_ws_stride;
+};
+
+struct StreamArgs {
+  const float* logits;   // [n_steps][n_rows] rows of ld floats
+  int64_t ld;
+  int64_t step_stride;   // elements between steps
+  int n_steps;
+  int n_rows;
+  int vocab;
+  const int32_t* hist_ids;
+  const int64_t* hist_off;
+  const float* temp;
+  const int32_t* top_k;
+  const float* top_p;
+  const float* pen;
+  const uint8_t* do_sample;
+  int stop_token;
+  uint64_t* rng;
+  int32_t* out_tok;      // [n_steps][n_rows]
+  uint32_t* stats;       // optional [n_rows][4], accumulated over steps
+  int max_unique;        // capacity of the per-row penalised-id list in LDS
+};
+
+struct LmHeadArgs {
+  const uint16_t* hidden;  // [M][D] bf16
+  const float* gamma;
+  const float* beta;
+  float eps;
+  const uint16_t* weight;  // [V][D] bf16
+  const float* bias;       // [V]
+  float* logits;           // [M][V] f32 (row stride ld_out)
+  int64_t ld_out;
+  int M, D, V;
+  uint16_t* hnorm;         // [M][D] bf16 scratch (normalised rows)
+};
+
+size_t rows_lds_bytes(int vocab);
+size_t rows_global_lds_bytes(int vocab);
+size_t stream_lds_bytes(int vocab, int max_unique);
+
+hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
+hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
+hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
+hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);
+hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);
+
+}  // namespace c4s

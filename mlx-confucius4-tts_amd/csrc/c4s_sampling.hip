@@ -1,0 +1,961 @@
+// gfx950 kernels for the c4tts Text2Semantic token-sampling path.
+//
+// One workgroup (1024 threads = 16 wave64) owns one row. The chain follows the
+// reference order (src/t2s/text2semantic.cpp:142-166):
+//   repetition penalty -> greedy ? argmax : temperature -> top_k -> top_p -> draw
+// with the per-processor semantics of src/t2s/sampling.cpp:14-76 and the
+// xorshift64 inverse-CDF draw of text2semantic.cpp:150-165.
+//
+// Exactness. Penalty, temperature and top-k are single IEEE fp32 operations or
+// comparisons and are reproduced bit for bit. top_p and the draw accumulate
+// double sums sequentially in the reference (ascending value order, resp. id
+// order). Here those sums are formed in parallel; every decision taken from
+// them (does the nucleus cut remove this position, does r <= acc hold at this
+// id) is accepted only when its margin exceeds a bound on the difference
+// between any sequential and any parallel evaluation (relative
+// (4n+64)*2^-53 + 2^-48, which also covers a few ulp of exp(double) between
+// libm implementations). Otherwise the row re-runs that step as an exact
+// sequential emulation in reference order. Selections use radix passes over
+// order-preserving 32-bit keys (no sort); the top_p tie order is the declared
+// one: within a tie group cut by the nucleus the lower ids survive.
+//
+// Rows with vocab <= kLdsVocabMax are staged in LDS (values + cached double
+// masses); larger rows are re-read from HBM on every pass (penalty via an LDS
+// bitmap, temperature re-applied on the fly).
+
+#include <limits.h>
+#include <math.h>
+
+#include "c4s_device.hpp"
+#include "c4s_internal.h"
+
+namespace c4s {
+namespace {
+
+constexpr int NT = kThreads;
+constexpr int NW = NT / kWave;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+struct Scratch {
+  uint32_t hcnt[256];
+  double hmass[256];
+  double redd[NW];
+  float redf[NW];
+  int redi[NW];
+  uint32_t redu[NW];
+  double wmass[NW];
+  uint32_t wcnt[NW];
+  uint32_t bu[8];
+  double bd[8];
+  int bi[8];
+  uint32_t counter;
+};
+
+// Bound on |sequential - parallel| for non-negative double sums over n terms,
+// relative to the compared quantities (see file header).
+__device__ __forceinline__ double rel_eps(int n) {
+  return (4.0 * (double)n + 64.0) * 0x1p-53 + 0x1p-48;
+}
+
+struct RowCfg {
+  int V;
+  bool pen_on;
+  float pen;
+  bool greedy;
+  bool draw;
+  bool temp_on;
+  float temp;
+  bool topk_on;
+  int k;
+  bool topp_on;
+  float p;
+  int min_keep;
+};
+
+__device__ RowCfg make_cfg(const uint32_t mode, int V, int row, const float* temp,
+                           const int32_t* top_k, const float* top_p, const float* pen,
+                           const int32_t* min_keep, const uint8_t* do_sample) {
+  RowCfg c;
+  c.V = V;
+  c.pen = pen ? pen[row] : 1.0f;
+  c.temp = temp ? temp[row] : 1.0f;
+  c.k = top_k ? top_k[row] : 0;
+  c.p = top_p ? top_p[row] : 1.0f;
+  c.min_keep = min_keep ? min_keep[row] : 1;
+  if (!(mode & kCustom)) {
+    const bool sample = do_sample ? (do_sample[row] != 0) : true;
+    c.pen_on = c.pen != 1.0f;                      // sampling.cpp:21
+    c.greedy = !sample;                            // text2semantic.cpp:144-145
+    c.draw = sample;
+    c.temp_on = sample && !(c.temp == 1.0f || c.temp <= 0.0f);  // sampling.cpp:15
+    c.topk_on = sample && c.k > 0 && c.k < V;      // sampling.cpp:32
+    c.topp_on = sample;                            // sampling.cpp:42 has no early return
+  } else {
+    c.pen_on = (mode & kPenalty) && c.pen != 1.0f;
+    c.greedy = (mode & kArgmax) != 0;
+    c.draw = !c.greedy && (mode & kDraw) != 0;
+    c.temp_on = !c.greedy && (mode & kTemperature) && !(c.temp == 1.0f || c.temp <= 0.0f);
+    c.topk_on = !c.greedy && (mode & kTopK) && c.k > 0 && c.k < V;
+    c.topp_on = !c.greedy && (mode & kTopP);
+  }
+  return c;
+}
+
+// ---- element sources ---------------------------------------------------------
+
+// Row staged in LDS. `val` holds the penalised logits, then (after
+// apply_temperature) the divided ones. `E` caches double masses by id and
+// doubles as the key buffer of the exact top_p pass.
+struct LdsRow {
+  float* val;
+  double* E;
+  int V;
+  uint32_t thr_key;
+  bool topk_on;
+  static constexpr bool kCache = true;
+
+  __device__ float zraw(int i) const { return val[i]; }
+  __device__ float z(int i) const {
+    const float v = val[i];
+    return (topk_on && fkey(v) < thr_key) ? neg_inf() : v;
+  }
+  __device__ double cached(int i) const { return E[i]; }
+  __device__ void cache(int i, double e) { E[i] = e; }
+  __device__ void apply_temperature(float t, int lo, int hi) {
+    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = val[i] / t;
+    __syncthreads();
+  }
+  __device__ uint32_t* sort_buf() const { return reinterpret_cast<uint32_t*>(E); }
+};
+
+// Row re-read from HBM on every pass.
+struct GlobalRow {
+  const float* xf;
+  const uint16_t* xb;
+  int V;
+  const uint32_t* bitmap;  // LDS, penalised ids
+  bool pen_on;
+  float pen;
+  bool temp_on;
+  float temp;
+  uint32_t thr_key;
+  bool topk_on;
+  uint32_t* sortbuf;       // global workspace for the exact top_p pass
+  static constexpr bool kCache = false;
+
+  __device__ float y(int i) const {
+    float x = xf ? xf[i] : __uint_as_float(static_cast<uint32_t>(xb[i]) << 16);
+    if (pen_on && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = (x < 0) ? x * pen : x / pen;
+    return x;
+  }
+  __device__ float zraw(int i) const {
+    const float v = y(i);
+    return temp_on ? v / temp : v;
+  }
+  __device__ float z(int i) const {
+    const float v = zraw(i);
+    return (topk_on && fkey(v) < thr_key) ? neg_inf() : v;
+  }
+  __device__ double cached(int) const { return 0.0; }
+  __device__ void cache(int, double) {}
+  __device__ void apply_temperature(float t, int, int) { temp_on = true; temp = t; }
+  __device__ uint32_t* sort_buf() const { return sortbuf; }
+};
+
+// Wave w owns ids [w*seg, min(V, (w+1)*seg)), visited in slices of 64.
+struct Seg {
+  int lo, hi;
+};
+__device__ __forceinline__ Seg my_seg(int V) {
+  const int seg = (V + NW - 1) / NW;
+  const int lo = min(V, wave_id() * seg);
+  return Seg{lo, min(V, lo + seg)};
+}
+
+// ---- count-based radix select (descending) -----------------------------------
+// Key of the m-th largest element (1-based, with multiplicity) among keyfn(i)
+// for i in [0, V); also the number of keys strictly greater (`gt`) and equal
+// (`eq`) to it.
+template <class KeyFn>
+__device__ uint32_t select_desc(KeyFn keyfn, Seg sg, Scratch& sh, uint32_t m, uint32_t& gt,
+                                uint32_t& eq) {
+  uint32_t prefix = 0, mask = 0, rem = m;
+  gt = 0;
+  eq = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = threadIdx.x; b < 256; b += NT) sh.hcnt[b] = 0;
+    __syncthreads();
+    for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
+      const uint32_t k = keyfn(i);
+      if ((k & mask) == prefix) atomicAdd(&sh.hcnt[(k >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+      const int l = lane_id();
+      uint32_t c[4], lc = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { c[j] = sh.hcnt[255 - (4 * l + j)]; lc += c[j]; }
+      const uint32_t incl = wave_incl_scan_u32(lc);
+      uint32_t run = incl - lc;
+      int hitb = -1;
+      uint32_t above = 0, ceq = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (hitb < 0 && run + c[j] >= rem) { hitb = 255 - (4 * l + j); above = run; ceq = c[j]; }
+        run += c[j];
+      }
+      const uint64_t hit = __ballot(hitb >= 0);
+      const int first = __ffsll((unsigned long long)hit) - 1;
+      if (l == first) { sh.bu[0] = (uint32_t)hitb; sh.bu[1] = above; sh.bu[2] = ceq; }
+    }
+    __syncthreads();
+    const uint32_t b = sh.bu[0];
+    rem -= sh.bu[1];
+    gt += sh.bu[1];
+    eq = sh.bu[2];
+    prefix |= b << shift;
+    mask |= 0xFFu << shift;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// ---- nucleus cut from the bottom, by mass (top_p) -----------------------------
+// Finds the first value group, in ascending order, whose cumulative mass exceeds
+// A = (1 - p) * S. Returns false when a decision falls inside the error bound.
+// On success: R = positions (ascending, all V ids) the reference removes by
+// `cum <= 1 - p`, wkey/eq = the crossing group, nkeep = how many of that group
+// stay (its lowest ids).
+template <class Src>
+__device__ bool cut_by_mass(const Src& src, Seg sg, Scratch& sh, float maxv, double A, double eps,
+                            int V, long long& R, uint32_t& wkey, uint32_t& eq, uint32_t& nkeep) {
+  uint32_t prefix = 0, mask = 0;
+  double blow = 0.0;
+  uint32_t cnt_low = 0;
+  bool ok = true;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int b = threadIdx.x; b < 256; b += NT) { sh.hcnt[b] = 0; sh.hmass[b] = 0.0; }
+    __syncthreads();
+    for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
+      const float zi = src.z(i);
+      const uint32_t k = fkey(zi);
+      if ((k & mask) == prefix) {
+        const uint32_t b = (k >> shift) & 255u;
+        atomicAdd(&sh.hcnt[b], 1u);
+        const double e = Src::kCache ? src.cached(i)
+                                     : (zi == neg_inf() ? 0.0 : exp((double)(zi - maxv)));
+        if (e != 0.0) atomicAdd(&sh.hmass[b], e);
+      }
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+      const int l = lane_id();
+      uint32_t c[4], lc = 0;
+      double m[4], lm = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        c[j] = sh.hcnt[4 * l + j];
+        m[j] = sh.hmass[4 * l + j];
+        lc += c[j];
+        lm += m[j];
+      }
+      const double mincl = wave_incl_scan_f64(lm);
+      double mexcl = __shfl_up(mincl, 1, kWave);
+      if (l == 0) mexcl = 0.0;
+      const uint32_t cincl = wave_incl_scan_u32(lc);
+      uint32_t crun = cincl - lc;
+      double run = blow + mexcl;
+      int hitb = -1;
+      double before = 0.0, end = 0.0;
+      uint32_t cbefore = 0, ceq = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const double e2 = run + m[j];
+        if (hitb < 0 && e2 > A) { hitb = 4 * l + j; before = run; end = e2; cbefore = crun; ceq = c[j]; }
+        run = e2;
+        crun += c[j];
+      }
+      const uint64_t hit = __ballot(hitb >= 0);
+      const int first = hit ? __ffsll((unsigned long long)hit) - 1 : -1;
+      if (first < 0) {
+        if (l == 63) { sh.bu[0] = 0xFFFFFFFFu; sh.bd[0] = run; }
+      } else if (l == first) {
+        sh.bu[0] = (uint32_t)hitb;
+        sh.bu[1] = cbefore;
+        sh.bu[2] = ceq;
+        sh.bd[0] = before;
+        sh.bd[1] = end;
+      }
+    }
+    __syncthreads();
+    const uint32_t b = sh.bu[0];
+    if (b == 0xFFFFFFFFu) {
+      // Nothing in range ends above A: every position has cum <= 1 - p.
+      const double tot = sh.bd[0];
+      __syncthreads();
+      if (!(A - tot > eps * A)) return false;
+      R = V;
+      wkey = 0;
+      eq = 0;
+      nkeep = 0;
+      return true;
+    }
+    const double before = sh.bd[0], end = sh.bd[1];
+    const uint32_t cb = sh.bu[1], ceq = sh.bu[2];
+    __syncthreads();
+    if (!(end - A > eps * end)) ok = false;
+    if (before > 0.0 && !(A - before > eps * A)) ok = false;
+    if (!ok) return false;
+    blow = before;
+    cnt_low += cb;
+    prefix |= b << shift;
+    mask |= 0xFFu << shift;
+    eq = ceq;
+  }
+  // Positions inside the crossing group: position j (1-based, ascending order)
+  // is removed iff blow + j*q <= A.
+  wkey = prefix;
+  const double q = (wkey == kKeyNegInf) ? 0.0 : exp((double)(kfloat(wkey) - maxv));
+  long long j = 0;
+  if (q > 0.0) {
+    double jf = floor((A - blow) / q);
+    j = (long long)fmax(0.0, fmin(jf, (double)eq - 1.0));
+    while (j > 0 && blow + (double)j * q > A) --j;
+    while (j + 1 < (long long)eq && blow + (double)(j + 1) * q <= A) ++j;
+    if (j >= 1) {
+      const double bj = blow + (double)j * q;
+      if (!(A - bj > eps * A)) return false;
+    }
+    if (j + 1 <= (long long)eq) {
+      const double bj1 = blow + (double)(j + 1) * q;
+      if (!(bj1 - A > eps * bj1)) return false;
+    }
+  }
+  R = (long long)cnt_low + j;
+  nkeep = eq - (uint32_t)j;
+  return true;
+}
+
+// ---- exact sequential emulations -----------------------------------------------
+
+// In-buffer ascending bitonic sort of P (a power of two) keys by the workgroup.
+__device__ void bitonic_sort_u32(uint32_t* buf, int P) {
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int t = threadIdx.x; t < (P >> 1); t += NT) {
+        const int i = (t / j) * 2 * j + (t % j);
+        const int pi = i + j;
+        const uint32_t a = buf[i], b = buf[pi];
+        const bool up = (i & k) == 0;
+        if ((a > b) == up) { buf[i] = b; buf[pi] = a; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Exact top_p removal count: sorts the finite keys ascending, then wave 0 runs
+// sampling.cpp:52-65 literally (sequential double sum, then sequential
+// cum += prob/sum against 1 - p). Returns R over all V positions (the -inf
+// positions come first in ascending order with probability 0).
+template <class Src>
+__device__ long long exact_top_p(const Src& src, Seg sg, Scratch& sh, float maxv, double thr,
+                                 int V, uint32_t* buf, uint32_t& n_fin_out) {
+  if (threadIdx.x == 0) sh.counter = 0;
+  __syncthreads();
+  for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
+    const float zi = src.z(i);
+    if (zi != neg_inf()) {
+      const uint32_t slot = atomicAdd(&sh.counter, 1u);
+      buf[slot] = fkey(zi);
+    }
+  }
+  __syncthreads();
+  const uint32_t n_fin = sh.counter;
+  int P = 1;
+  while (P < (int)n_fin) P <<= 1;
+  for (int i = n_fin + threadIdx.x; i < P; i += NT) buf[i] = 0xFFFFFFFFu;
+  __syncthreads();
+  bitonic_sort_u32(buf, P);
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    double total = 0.0;
+    for (int base = 0; base < (int)n_fin; base += kWave) {
+      const int j = base + l;
+      const double e = (j < (int)n_fin) ? exp((double)(kfloat(buf[j]) - maxv)) : 0.0;
+      const int cnt = min(kWave, (int)n_fin - base);
+      for (int t = 0; t < cnt; ++t) total += __shfl(e, t, kWave);
+    }
+    double cum = 0.0;
+    uint32_t removed = 0;
+    bool stop = false;
+    for (int base = 0; base < (int)n_fin && !stop; base += kWave) {
+      const int j = base + l;
+      const double q = (j < (int)n_fin) ? exp((double)(kfloat(buf[j]) - maxv)) / total : 0.0;
+      const int cnt = min(kWave, (int)n_fin - base);
+      for (int t = 0; t < cnt; ++t) {
+        cum += __shfl(q, t, kWave);
+        if (cum <= thr) removed = base + t + 1;
+        else { stop = true; break; }
+      }
+    }
+    if (l == 0) sh.bu[4] = removed;
+  }
+  __syncthreads();
+  const uint32_t rfin = sh.bu[4];
+  __syncthreads();
+  n_fin_out = n_fin;
+  return (long long)(V - (int)n_fin) + rfin;
+}
+
+// ---- keep predicate after top_p ------------------------------------------------
+enum KeepMode { kKeepAll = 0, kKeepMassPos = 1, kKeepBoundary = 2, kKeepNone = 3 };
+
+struct Keep {
+  int mode;
+  uint32_t wkey;
+  uint32_t nkeep;   // how many of the wkey group stay (lowest ids first)
+  bool ranked;      // nkeep < group size: needs tie ranks in id order
+};
+
+// Does position i survive, given its value, the mass w.r.t. the top_p maximum
+// and its rank among the wkey group in id order.
+__device__ __forceinline__ bool keep_test(const Keep& kp, uint32_t key, double e_tp, uint32_t rank) {
+  switch (kp.mode) {
+    case kKeepAll: return true;
+    case kKeepMassPos: return e_tp > 0.0;
+    case kKeepBoundary:
+      return key > kp.wkey || (key == kp.wkey && (!kp.ranked || rank < kp.nkeep));
+    default: return false;
+  }
+}
+
+// ---- the chain ------------------------------------------------------------------
+template <class Src>
+__device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, float* masked,
+                         uint32_t* stats) {
+  const int V = c.V;
+  const Seg sg = my_seg(V);
+  const int lane = lane_id();
+  uint32_t st_path = 0, st_tp_exact = 0, st_draw_exact = 0, st_kept = 0;
+
+  if (c.greedy) {
+    float bv = neg_inf();
+    int bi = INT_MAX;
+    for (int i = sg.lo + lane; i < sg.hi; i += kWave) argmax_merge(bv, bi, src.z(i), i);
+    block_argmax<NT>(bv, bi, sh.redf, sh.redi);
+    if (masked)
+      for (int i = sg.lo + lane; i < sg.hi; i += kWave) masked[i] = src.z(i);
+    if (stats && threadIdx.x == 0) { stats[0] = 8u; stats[1] = 0; stats[2] = 0; stats[3] = V; }
+    return bi;
+  }
+
+  if (c.temp_on) src.apply_temperature(c.temp, sg.lo, sg.hi);
+
+  if (c.topk_on) {
+    uint32_t gt, eq;
+    const uint32_t tk = select_desc([&](int i) { return fkey(src.zraw(i)); }, sg, sh,
+                                    (uint32_t)c.k, gt, eq);
+    src.thr_key = tk;
+    src.topk_on = true;
+    st_path |= 2u;
+  }
+
+  float maxv = neg_inf();
+  if (c.topp_on || c.draw) {
+    float lm = neg_inf();
+    for (int i = sg.lo + lane; i < sg.hi; i += kWave) lm = fmaxf(lm, src.z(i));
+    maxv = block_max_f32<NT>(lm, sh.redf);
+  }
+
+  Keep kp{kKeepAll, 0u, 0u, false};
+  bool cache_ok = false;   // E[] holds exp(z - maxv) for every id (LDS rows)
+  bool any_kept = true;
+  if (c.topp_on && maxv != neg_inf()) {
+    st_path |= 4u;
+    double sl = 0.0;
+    uint32_t zl = 0;
+    for (int i = sg.lo + lane; i < sg.hi; i += kWave) {
+      const float zi = src.z(i);
+      const double e = (zi == neg_inf()) ? 0.0 : exp((double)(zi - maxv));
+      if (Src::kCache) src.cache(i, e);
+      sl += e;
+      zl += (e == 0.0) ? 1u : 0u;
+    }
+    const double S = block_sum_f64<NT>(sl, sh.redd);
+    cache_ok = Src::kCache;
+    const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 compares cum <= (1.0 - p)
+    long long R = 0;
+    bool have_cross = false;
+    uint32_t cwkey = 0, ceq = 0, cnkeep = 0;
+    if (thr < 0.0) {
+      R = 0;
+    } else if (thr == 0.0) {
+      R = block_sum_u32<NT>(zl, sh.redu);  // only zero-probability positions have cum == 0
+    } else {
+      const double eps = rel_eps(V);
+      if (cut_by_mass(src, sg, sh, maxv, thr * S, eps, V, R, cwkey, ceq, cnkeep)) {
+        have_cross = (R < V);
+      } else {
+        uint32_t nfin;
+        R = exact_top_p(src, sg, sh, maxv, thr, V, src.sort_buf(), nfin);
+        cache_ok = false;
+        st_tp_exact = 1;
+      }
+    }
+    // min_tokens_to_keep: the last min_keep ascending positions are never removed.
+    const long long mk = c.min_keep;
+    const long long lim = (long long)V - mk < 0 ? 0 : (long long)V - mk;
+    const long long Rf = R < lim ? R : lim;
+    if (Rf <= 0) {
+      kp.mode = kKeepAll;
+    } else if (Rf >= V) {
+      kp.mode = kKeepNone;
+      any_kept = false;
+    } else if (have_cross && Rf == R) {
+      kp.mode = kKeepBoundary;
+      kp.wkey = cwkey;
+      kp.nkeep = cnkeep;
+      kp.ranked = cnkeep < ceq;
+    } else if (thr == 0.0 && Rf == R) {
+      kp.mode = kKeepMassPos;
+    } else {
+      // Keep exactly the top m = V - Rf positions in (value desc, id asc) order.
+      uint32_t gt, eq;
+      const uint32_t wk = select_desc([&](int i) { return fkey(src.z(i)); }, sg, sh,
+                                      (uint32_t)((long long)V - Rf), gt, eq);
+      kp.mode = kKeepBoundary;
+      kp.wkey = wk;
+      kp.nkeep = (uint32_t)((long long)V - Rf) - gt;
+      kp.ranked = kp.nkeep < eq;
+    }
+  }
+
+  // Tie-rank bases: how many wkey-group members precede each wave's segment.
+  uint32_t tie_base = 0;
+  if (kp.mode == kKeepBoundary && kp.ranked) {
+    uint32_t cl = 0;
+    for (int i = sg.lo + lane; i < sg.hi; i += kWave) cl += (fkey(src.z(i)) == kp.wkey) ? 1u : 0u;
+    cl = wave_sum_u32(cl);
+    if (lane == 0) sh.wcnt[wave_id()] = cl;
+    __syncthreads();
+    for (int w = 0; w < wave_id(); ++w) tie_base += sh.wcnt[w];
+    __syncthreads();
+  }
+
+  // Draw maximum (text2semantic.cpp:150-151): max over surviving values, from -1e30f.
+  const float maxv_d = fmaxf(-1e30f, any_kept ? maxv : neg_inf());
+  const bool reuse = cache_ok && (maxv_d == maxv);
+
+  // Finalize: survivors in id order, masked output, draw masses per wave.
+  double wm = 0.0;
+  uint32_t kl = 0;
+  {
+    uint32_t carry = tie_base;
+    for (int base = sg.lo; base < sg.hi; base += kWave) {
+      const int i = base + lane;
+      const bool valid = i < sg.hi;
+      const float zi = valid ? src.z(i) : neg_inf();
+      const uint32_t key = fkey(zi);
+      const bool is_w = valid && kp.mode == kKeepBoundary && key == kp.wkey;
+      const uint64_t bal = __ballot(is_w);
+      const uint32_t rank = carry + (uint32_t)__popcll(bal & lanemask_lt());
+      carry += (uint32_t)__popcll(bal);
+      double e_tp = 0.0;
+      if (kp.mode == kKeepMassPos)
+        e_tp = cache_ok ? (valid ? src.cached(i) : 0.0)
+                        : (zi == neg_inf() ? 0.0 : exp((double)(zi - maxv)));
+      const bool kept = valid && keep_test(kp, key, e_tp, rank);
+      const float out = kept ? zi : neg_inf();
+      if (masked && valid) masked[i] = out;
+      if (kept && zi != neg_inf()) ++kl;
+      if (c.draw && valid) {
+        double e = 0.0;
+        if (kept && zi != neg_inf())   // +inf/NaN are outside the input contract
+          e = reuse ? src.cached(i) : exp((double)(out - maxv_d));
+        wm += e;
+        if (Src::kCache) src.cache(i, e);
+      }
+    }
+  }
+  st_kept = block_sum_u32<NT>(kl, sh.redu);
+
+  int tok = 0;
+  if (c.draw) {
+    wm = wave_sum_f64(wm);
+    if (lane == 0) sh.wmass[wave_id()] = wm;
+    __syncthreads();
+    // Per-wave exclusive prefixes and the total, summed in a fixed order.
+    double X[NW];
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) { X[w] = tot; tot += sh.wmass[w]; }
+    rng = xorshift64(rng);
+    const double u = unit_from_state(rng);
+    const double r = u * tot;
+    int owner = NW - 1;
+#pragma unroll
+    for (int w = NW - 1; w >= 0; --w)
+      if (X[w] + sh.wmass[w] >= r) owner = w;
+    __syncthreads();
+    const double eps = rel_eps(V);
+    if (wave_id() == owner) {
+      double carry_m = X[owner];
+      int found = -1;
+      double acc = 0.0, prev = 0.0;
+      uint32_t carry = tie_base;
+      for (int base = sg.lo; base < sg.hi && found < 0; base += kWave) {
+        const int i = base + lane;
+        const bool valid = i < sg.hi;
+        double e = 0.0;
+        if (Src::kCache) {
+          e = valid ? src.cached(i) : 0.0;
+        } else {
+          const float zi = valid ? src.z(i) : neg_inf();
+          const uint32_t key = fkey(zi);
+          const bool is_w = valid && kp.mode == kKeepBoundary && key == kp.wkey;
+          const uint64_t bal = __ballot(is_w);
+          const uint32_t rank = carry + (uint32_t)__popcll(bal & lanemask_lt());
+          carry += (uint32_t)__popcll(bal);
+          const double e_tp = (kp.mode == kKeepMassPos && zi != neg_inf())
+                                  ? exp((double)(zi - maxv)) : 0.0;
+          if (valid && zi != neg_inf() && keep_test(kp, key, e_tp, rank))
+            e = exp((double)(zi - maxv_d));
+        }
+        const double inc = wave_incl_scan_f64(e) + carry_m;
+        const uint64_t hit = __ballot(valid && inc >= r);
+        if (hit) {
+          const int L = __ffsll((unsigned long long)hit) - 1;
+          found = base + L;
+          acc = __shfl(inc, L, kWave);
+          const double before = __shfl_up(inc, 1, kWave);
+          const double pb = __shfl(before, L, kWave);
+          prev = (L == 0) ? carry_m : pb;
+        }
+        carry_m = __shfl(inc, kWave - 1, kWave);
+      }
+      const bool certain = found >= 0 && (acc - r > eps * acc) && (r - prev > eps * r);
+      if (lane == 0) { sh.bi[0] = found; sh.bi[1] = certain ? 1 : 0; }
+    }
+    __syncthreads();
+    tok = sh.bi[0];
+    const bool certain = sh.bi[1] != 0;
+    __syncthreads();
+    if (!certain) {
+      // text2semantic.cpp:152-165 literally: sequential sums in id order.
+      st_draw_exact = 1;
+      if (wave_id() == 0) {
+        double total = 0.0;
+        for (int pass = 0; pass < 2; ++pass) {
+          double acc = 0.0, rr = 0.0;
+          if (pass == 1) rr = u * total;
+          int t = V - 1;
+          bool done = false;
+          uint32_t carry = 0;
+          for (int base = 0; base < V && !done; base += kWave) {
+            const int i = base + lane;
+            const bool valid = i < V;
+            double e = 0.0;
+            if (Src::kCache) {
+              e = valid ? src.cached(i) : 0.0;
+            } else {
+              const float zi = valid ? src.z(i) : neg_inf();
+              const uint32_t key = fkey(zi);
+              const bool is_w = valid && kp.mode == kKeepBoundary && key == kp.wkey;
+              const uint64_t bal = __ballot(is_w);
+              const uint32_t rank = carry + (uint32_t)__popcll(bal & lanemask_lt());
+              carry += (uint32_t)__popcll(bal);
+              const double e_tp = (kp.mode == kKeepMassPos && zi != neg_inf())
+                                      ? exp((double)(zi - maxv)) : 0.0;
+              if (valid && zi != neg_inf() && keep_test(kp, key, e_tp, rank))
+                e = exp((double)(zi - maxv_d));
+            }
+            const int cnt = min(kWave, V - base);
+            for (int q = 0; q < cnt; ++q) {
+              const double eq = __shfl(e, q, kWave);
+              if (pass == 0) {
+                total += eq;
+              } else {
+                acc += eq;
+                if (rr <= acc) { t = base + q; done = true; break; }
+              }
+            }
+          }
+          if (pass == 1 && lane == 0) sh.bi[2] = t;
+        }
+      }
+      __syncthreads();
+      tok = sh.bi[2];
+      __syncthreads();
+    }
+  }
+  if (stats && threadIdx.x == 0) {
+    stats[0] = st_path | (c.draw ? 1u : 0u);
+    stats[1] = st_tp_exact;
+    stats[2] = st_draw_exact;
+    stats[3] = st_kept;
+  }
+  return tok;
+}
+
+__device__ __forceinline__ float load_logit(const void* base, int dtype, int64_t off) {
+  if (dtype == 1) {
+    const uint16_t b = static_cast<const uint16_t*>(base)[off];
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  }
+  return static_cast<const float*>(base)[off];
+}
+
+struct LdsLayout {
+  double* E;
+  float* val;
+  uint32_t* bitmap;
+  int32_t* uniq;
+};
+
+__device__ __forceinline__ int vpad(int V) { return (V + 3) & ~3; }
+
+__device__ LdsLayout lds_layout(unsigned char* smem, int V) {
+  LdsLayout L;
+  L.E = reinterpret_cast<double*>(smem);
+  L.val = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
+  L.bitmap = reinterpret_cast<uint32_t*>(L.val + vpad(V));
+  L.uniq = reinterpret_cast<int32_t*>(L.bitmap + ((V + 31) / 32 + 3) / 4 * 4);
+  return L;
+}
+
+// ---- kernels -------------------------------------------------------------------
+
+__global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ Scratch sh;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  if (a.row_active && !a.row_active[row]) {
+    if (threadIdx.x == 0) a.out_tok[row] = -1;
+    return;
+  }
+  const RowCfg c = make_cfg(a.mode, V, row, a.temp, a.top_k, a.top_p, a.pen, a.min_keep,
+                            a.do_sample);
+  LdsLayout L = lds_layout(smem, V);
+  const int64_t roff = (int64_t)row * a.ld;
+  for (int i = threadIdx.x; i < V; i += NT) L.val[i] = load_logit(a.logits, a.dtype, roff + i);
+  if (c.pen_on) {
+    const int nw = (V + 31) / 32;
+    for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
+    __syncthreads();
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+      const int id = a.hist_ids[j];
+      if (id < 0 || id >= V) continue;   // sampling.cpp:24
+      const uint32_t bit = 1u << (id & 31);
+      const uint32_t old = atomicOr(&L.bitmap[id >> 5], bit);
+      if (!(old & bit)) {
+        const float s = L.val[id];
+        L.val[id] = (s < 0) ? s * c.pen : s / c.pen;   // sampling.cpp:26
+      }
+    }
+  }
+  __syncthreads();
+  LdsRow src{L.val, L.E, V, 0u, false};
+  uint64_t rng = a.rng ? a.rng[row] : 0ull;
+  float* masked = a.out_masked ? a.out_masked + (int64_t)row * V : nullptr;
+  uint32_t* st = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
+  const int tok = run_chain(src, sh, c, rng, masked, st);
+  if (threadIdx.x == 0) {
+    a.out_tok[row] = tok;
+    if (c.draw && a.rng) a.rng[row] = rng;
+  }
+}
+
+__global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ Scratch sh;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  if (a.row_active && !a.row_active[row]) {
+    if (threadIdx.x == 0) a.out_tok[row] = -1;
+    return;
+  }
+  const RowCfg c = make_cfg(a.mode, V, row, a.temp, a.top_k, a.top_p, a.pen, a.min_keep,
+                            a.do_sample);
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem);
+  const int nw = (V + 31) / 32;
+  for (int w = threadIdx.x; w < nw; w += NT) bitmap[w] = 0u;
+  __syncthreads();
+  if (c.pen_on) {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+      const int id = a.hist_ids[j];
+      if (id < 0 || id >= V) continue;
+      atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+  }
+  const int64_t roff = (int64_t)row * a.ld;
+  GlobalRow src;
+  src.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
+  src.xb = a.dtype == 1 ? static_cast<const uint16_t*>(a.logits) + roff : nullptr;
+  src.V = V;
+  src.bitmap = bitmap;
+  src.pen_on = c.pen_on;
+  src.pen = c.pen;
+  src.temp_on = false;
+  src.temp = 1.0f;
+  src.thr_key = 0u;
+  src.topk_on = false;
+  src.sortbuf = a.sort_ws + (int64_t)row * a.sort_ws_stride;
+  uint64_t rng = a.rng ? a.rng[row] : 0ull;
+  float* masked = a.out_masked ? a.out_masked + (int64_t)row * V : nullptr;
+  uint32_t* st = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
+  const int tok = run_chain(src, sh, c, rng, masked, st);
+  if (threadIdx.x == 0) {
+    a.out_tok[row] = tok;
+    if (c.draw && a.rng) a.rng[row] = rng;
+  }
+}
+
+// Multi-step AR stream for rows staged in LDS: one persistent workgroup per
+// row walks all steps; the row's distinct penalised ids live in LDS (bitmap +
+// list) and grow with every sampled token that is not the stop token
+// (text2semantic.cpp:333-334). A stopped row reports -1 afterwards and its RNG
+// stays frozen.
+__global__ __launch_bounds__(NT) void k_stream_lds(StreamArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ Scratch sh;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  LdsLayout L = lds_layout(smem, V);
+  const int nw = (V + 31) / 32;
+  for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
+  if (threadIdx.x == 0) sh.counter = 0;
+  __syncthreads();
+  {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+      const int id = a.hist_ids[j];
+      if (id < 0 || id >= V) continue;
+      const uint32_t bit = 1u << (id & 31);
+      const uint32_t old = atomicOr(&L.bitmap[id >> 5], bit);
+      if (!(old & bit)) {
+        const uint32_t slot = atomicAdd(&sh.counter, 1u);
+        if ((int)slot < a.max_unique) L.uniq[slot] = id;
+      }
+    }
+  }
+  __syncthreads();
+  int n_uniq = min((int)sh.counter, a.max_unique);
+  uint64_t rng = a.rng[row];
+  bool done = false;
+  uint32_t acc_stats[4] = {0, 0, 0, 0};
+  for (int s = 0; s < a.n_steps; ++s) {
+    int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
+    if (done) {
+      if (threadIdx.x == 0) *outp = -1;
+      continue;
+    }
+    const int64_t roff = (int64_t)s * a.step_stride + (int64_t)row * a.ld;
+    for (int i = threadIdx.x; i < V; i += NT) L.val[i] = a.logits[roff + i];
+    __syncthreads();
+    if (c.pen_on) {
+      for (int j = threadIdx.x; j < n_uniq; j += NT) {
+        const int id = L.uniq[j];
+        const float v = L.val[id];
+        L.val[id] = (v < 0) ? v * c.pen : v / c.pen;
+      }
+      __syncthreads();
+    }
+    LdsRow src{L.val, L.E, V, 0u, false};
+    uint32_t st[4];
+    const int tok = run_chain(src, sh, c, rng, nullptr, a.stats ? st : nullptr);
+    if (a.stats && threadIdx.x == 0) {
+      acc_stats[0] |= st[0];
+      acc_stats[1] += st[1];
+      acc_stats[2] += st[2];
+      acc_stats[3] += st[3];
+    }
+    if (threadIdx.x == 0) *outp = tok;
+    if (tok == a.stop_token) {
+      done = true;
+    } else if (tok >= 0 && tok < V) {
+      // Appending a token already in the history changes nothing: the penalty
+      // applies once per distinct id (sampling.cpp:22).
+      if (threadIdx.x == 0) {
+        const uint32_t bit = 1u << (tok & 31);
+        int appended = 0;
+        if (!(L.bitmap[tok >> 5] & bit) && n_uniq < a.max_unique) {
+          L.bitmap[tok >> 5] |= bit;
+          L.uniq[n_uniq] = tok;
+          appended = 1;
+        }
+        sh.bi[3] = appended;
+      }
+      __syncthreads();
+      n_uniq += sh.bi[3];
+      __syncthreads();
+    }
+  }
+  if (threadIdx.x == 0) {
+    a.rng[row] = rng;
+    if (a.stats) {
+      uint32_t* o = a.stats + 4 * (int64_t)row;
+      o[0] = acc_stats[0]; o[1] = acc_stats[1]; o[2] = acc_stats[2]; o[3] = acc_stats[3];
+    }
+  }
+}
+
+}  // namespace
+
+size_t rows_lds_bytes(int V) {
+  const size_t vp = (size_t)((V + 3) & ~3);
+  const size_t bw = (size_t)(((V + 31) / 32 + 3) / 4 * 4);
+  return 8 * vp + 4 * vp + 4 * bw;
+}
+
+size_t stream_lds_bytes(int V, int max_unique) {
+  return rows_lds_bytes(V) + 4 * (size_t)max_unique;
+}
+
+size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
+
+// Opt each kernel into the full gfx950 LDS for its dynamic allocation (once).
+template <class K>
+static hipError_t allow_lds(K kernel, bool& done) {
+  if (done) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           160 * 1024 - (int)sizeof(Scratch));
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
+  if (a.n_rows <= 0) return hipSuccess;
+  static bool lds_ok = false, glob_ok = false;
+  if (a.vocab <= kLdsVocabMax) {
+    const hipError_t e = allow_lds(k_rows_lds, lds_ok);
+    if (e != hipSuccess) return e;
+    const size_t lds = rows_lds_bytes(a.vocab);
+    hipLaunchKernelGGL(k_rows_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
+  } else {
+    const hipError_t e = allow_lds(k_rows_global, glob_ok);
+    if (e != hipSuccess) return e;
+    const size_t lds = rows_global_lds_bytes(a.vocab);
+    hipLaunchKernelGGL(k_rows_global, dim3(a.n_rows), dim3(NT), lds, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_stream(const StreamArgs& a, hipStream_t s) {
+  if (a.n_rows <= 0 || a.n_steps <= 0) return hipSuccess;
+  static bool ok = false;
+  const hipError_t e = allow_lds(k_stream_lds, ok);
+  if (e != hipSuccess) return e;
+  const size_t lds = stream_lds_bytes(a.vocab, a.max_unique);
+  hipLaunchKernelGGL(k_stream_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace c4s

@@ -1,0 +1,181 @@
+"""GPU parity: the HIP sampling path vs the CPU oracle, bit for bit.
+
+Tokens, RNG states and the masked rows (the row state before argmax/draw) must
+be identical. Each workload runs at a size the oracle finishes in seconds.
+"""
+import numpy as np
+import pytest
+
+import c4s
+import c4s_workloads as W
+from gpu_util import assert_same_rows, compare_with_oracle, dev, gpu_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def test_single_row_sampled_and_greedy(orc, gpu_ctx):
+    samp, greedy = W.single_row(seed=1)
+    print("single_row sampled", flush=True)
+    compare_with_oracle(orc, gpu_ctx, samp)
+    print("single_row greedy", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, greedy)
+    assert tok[0] == orc.argmax(orc.repetition_penalty(greedy.logits[0],
+                                                       greedy.hist_ids, 10.0))
+
+
+@pytest.mark.parametrize("seed", [2, 21, 22])
+def test_batch64_one_step(orc, gpu_ctx, seed):
+    b = W.batch64(seed=seed, rows=64)
+    print(f"batch64 seed={seed}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    print("exact top_p passes", int(st[:, 1].sum()), "exact draws", int(st[:, 2].sum()))
+
+
+def test_batch64_general_rows(orc, gpu_ctx):
+    """top_k = 0 rows (full-vocabulary nucleus) with assorted p and temperatures."""
+    b = W.batch64(seed=31, rows=64)
+    b.top_k[:] = 0
+    b.top_p[:] = np.resize(np.array([0.5, 0.8, 0.9, 0.95, 0.99, 1.0, 0.2, 0.999], np.float32), 64)
+    b.temp[:] = np.resize(np.array([0.6, 1.2, 1.0, 2.0, 0.3], np.float32), 64)
+    compare_with_oracle(orc, gpu_ctx, b)
+
+
+@pytest.mark.parametrize("sweep", ["greedy", "top_k1", "top_p"])
+def test_bf16_ties(orc, gpu_ctx, sweep):
+    b = W.bf16_ties(seed=3, rows=512, sweep=sweep)
+    print(f"bf16_ties {sweep}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    if sweep == "top_k1":
+        assert (st[:, 3] > 1).all()      # the tied maxima all survive top_k=1
+
+
+def test_bf16_ties_literal_sort_divergence(orc):
+    """How often the reference's value-only std::sort (this host's libstdc++)
+    keeps different ids than the declared order inside a cut tie group."""
+    b = W.bf16_ties(seed=3, rows=64, sweep="top_p")
+    x = W.bf16_bits_to_f32(b.logits)
+    differ = 0
+    for r in range(b.n_rows):
+        a = orc.top_p(x[r], 0.5)
+        lit = orc.top_p(x[r], 0.5, literal=True)
+        assert np.isfinite(a).sum() == np.isfinite(lit).sum()   # same count, maybe other ids
+        differ += int(not np.array_equal(np.isfinite(a), np.isfinite(lit)))
+    print(f"literal std::sort keeps other ids in {differ}/{b.n_rows} rows")
+
+
+def test_large_vocab(orc, gpu_ctx):
+    b = W.large_vocab(seed=4, rows=64)
+    print("large_vocab 64 rows", flush=True)
+    compare_with_oracle(orc, gpu_ctx, b, masked=True)
+
+
+def test_large_vocab_general_and_bf16(orc, gpu_ctx):
+    b = W.large_vocab(seed=41, rows=8, V=20000, hist_len=300)
+    b.top_k[:] = np.array([0, 0, 50, 0, 1, 0, 20000, 19999], np.int32)
+    b.top_p[:] = np.array([0.9, 1.0, 0.95, 0.5, 1.0, 0.99, 0.7, 0.8], np.float32)
+    b.do_sample[3] = 0
+    compare_with_oracle(orc, gpu_ctx, b)
+    b.logits = W.f32_to_bf16_bits(b.logits)
+    compare_with_oracle(orc, gpu_ctx, b)
+
+
+def _rows_from(rows, temp, top_k, top_p, pen, hist, do_sample=None, seed=1234):
+    n = len(rows)
+    V = max(len(r) for r in rows)
+    x = np.full((n, V), -np.inf, np.float32)
+    for i, r in enumerate(rows):
+        x[i, :len(r)] = r
+    ids, off = W.csr(hist)
+    return W.Batch(logits=x, hist_ids=ids, hist_off=off, temp=np.asarray(temp, np.float32),
+                   top_k=np.asarray(top_k, np.int32), top_p=np.asarray(top_p, np.float32),
+                   pen=np.asarray(pen, np.float32),
+                   do_sample=np.ones(n, np.uint8) if do_sample is None else np.asarray(do_sample, np.uint8),
+                   rng=W.seed_batch(seed, n))
+
+
+@pytest.mark.parametrize("V", [1, 2, 3, 63, 64, 65, 1000, 9216, 12288, 12289, 40000])
+def test_vocab_sizes(orc, gpu_ctx, V):
+    g = np.random.default_rng(V)
+    n = 24
+    x = (g.standard_normal((n, V)) * 2).astype(np.float32)
+    hist = [g.integers(-5, V + 5, size=int(g.integers(0, 50))).astype(np.int32) for _ in range(n)]
+    ids, off = W.csr(hist)
+    b = W.Batch(logits=x, hist_ids=ids, hist_off=off,
+                temp=g.choice(np.array([0.7, 1.0, 1.3, 0.0, -1.0], np.float32), n),
+                top_k=g.choice(np.array([0, 1, 2, 5, V - 1, V, V + 1, -3], np.int32), n),
+                top_p=g.choice(np.array([0.0, 0.3, 0.8, 1.0, 1.2], np.float32), n),
+                pen=g.choice(np.array([1.0, 1.3, 10.0, 0.5], np.float32), n),
+                do_sample=(g.random(n) > 0.2).astype(np.uint8), rng=W.seed_batch(V, n))
+    mk = g.choice(np.array([1, 1, 1, 0, 2, 7, V + 4], np.int32), n)
+    compare_with_oracle(orc, gpu_ctx, b, min_keep=mk)
+
+
+def test_edge_rows(orc, gpu_ctx):
+    ninf = -np.inf
+    rows = [
+        [ninf] * 16,                                        # all -inf
+        [ninf, 1.0, ninf, 1.0, 0.5] + [ninf] * 11,          # -inf mixed, tie at max
+        [0.0] * 16,                                         # all equal
+        [-0.0, 0.0, -0.0, 0.0] * 4,                         # signed zeros
+        [3.0, 3.0, 3.0, 1.0] * 4,                           # tie groups
+        list(np.linspace(-1e30, 1e30, 16)),                 # huge range
+        [-1e31] * 16,                                       # below the draw's -1e30 floor
+        [5.0] + [-200.0] * 15,                              # underflowing weights
+        [-800.0, 0.0, -745.0, -746.0, -744.0] + [-9000.0] * 11,
+    ]
+    n = len(rows)
+    for temp, k, p in [(1.0, 0, 1.0), (0.8, 2, 0.5), (1.0, 1, 0.0), (2.0, 0, 0.3), (0.5, 3, 1.0)]:
+        b = _rows_from(rows, [temp] * n, [k] * n, [p] * n, [1.0] * n, [[]] * n)
+        compare_with_oracle(orc, gpu_ctx, b)
+        for mk in (0, 2, 17):
+            compare_with_oracle(orc, gpu_ctx, b, min_keep=np.full(n, mk, np.int32))
+
+
+def test_row_active_and_mixed_greedy(orc, gpu_ctx):
+    b = W.batch64(seed=5, rows=64)
+    b.do_sample[::3] = 0
+    active = np.ones(64, np.uint8)
+    active[::5] = 0
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, row_active=active)
+    assert (tok[active == 0] == -1).all()
+
+
+def test_custom_single_processors(orc, gpu_ctx):
+    """The single-processor modes behind the legacy functions, on many rows."""
+    import torch
+    b = W.batch64(seed=6, rows=16)
+    x = b.logits
+    cases = [
+        (c4s.P_TEMPERATURE, lambda r: orc.temperature(x[r], b.temp[r])),
+        (c4s.P_PENALTY, lambda r: orc.repetition_penalty(
+            x[r], b.hist_ids[b.hist_off[r]:b.hist_off[r + 1]], b.pen[r])),
+        (c4s.P_TOP_K, lambda r: orc.top_k(x[r], int(b.top_k[r]))),
+        (c4s.P_TOP_P, lambda r: orc.top_p(x[r], b.top_p[r])),
+    ]
+    for bit, ref in cases:
+        _, rng, m, _ = gpu_rows(gpu_ctx, b, mode=c4s.MODE_CUSTOM | bit)
+        want = np.stack([ref(r) for r in range(16)])
+        assert_same_rows(m, want)
+        assert np.array_equal(rng, b.rng)           # no draw, RNG untouched
+    tok, _, _, _ = gpu_rows(gpu_ctx, b, mode=c4s.MODE_CUSTOM | c4s.T_ARGMAX)
+    assert list(tok) == [orc.argmax(x[r]) for r in range(16)]
+    tok, rng, _, _ = gpu_rows(gpu_ctx, b, mode=c4s.MODE_CUSTOM | c4s.T_DRAW)
+    for r in range(16):
+        assert (tok[r], rng[r]) == orc.draw(x[r], int(b.rng[r]))
+
+
+def test_host_helpers_match_oracle(orc, gpu_ctx):
+    g = np.random.default_rng(8)
+    for n in (1, 5, 64, 8194, 15000):
+        x = (g.standard_normal(n) * 3).astype(np.float32)
+        ids = g.integers(-2, n + 2, size=40).astype(np.int32)
+        assert np.array_equal(gpu_ctx.host_temperature(x, 0.7), orc.temperature(x, 0.7))
+        assert np.array_equal(gpu_ctx.host_repetition_penalty(x, ids, 1.3),
+                              orc.repetition_penalty(x, ids, 1.3))
+        assert np.array_equal(gpu_ctx.host_top_k(x, 10), orc.top_k(x, 10))
+        for p, mk in ((0.9, 1), (0.3, 4), (1.0, 1)):
+            assert np.array_equal(gpu_ctx.host_top_p(x, p, mk), orc.top_p(x, p, mk))
+        assert gpu_ctx.host_argmax(x) == orc.argmax(x)
+        y = orc.top_p(orc.top_k(x, 30), 0.8)
+        assert gpu_ctx.host_draw(y, 1234) == orc.draw(y, 1234)
+    assert gpu_ctx.host_argmax(np.zeros(0, np.float32)) == 0
