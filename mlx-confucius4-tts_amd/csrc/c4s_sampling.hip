@@ -920,28 +920,13 @@ size_t stream_lds_bytes(int V, int max_unique) {
 
 size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
 
-// Opt each kernel into the full gfx950 LDS for its dynamic allocation (once).
-template <class K>
-static hipError_t allow_lds(K kernel, bool& done) {
-  if (done) return hipSuccess;
-  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           160 * 1024 - (int)sizeof(Scratch));
-  if (e == hipSuccess) done = true;
-  return e;
-}
-
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
-  static bool lds_ok = false, glob_ok = false;
+  (void)hipGetLastError();  // report only this launch's status
   if (a.vocab <= kLdsVocabMax) {
-    const hipError_t e = allow_lds(k_rows_lds, lds_ok);
-    if (e != hipSuccess) return e;
     const size_t lds = rows_lds_bytes(a.vocab);
     hipLaunchKernelGGL(k_rows_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
   } else {
-    const hipError_t e = allow_lds(k_rows_global, glob_ok);
-    if (e != hipSuccess) return e;
     const size_t lds = rows_global_lds_bytes(a.vocab);
     hipLaunchKernelGGL(k_rows_global, dim3(a.n_rows), dim3(NT), lds, s, a);
   }
@@ -950,9 +935,7 @@ hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
 
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s) {
   if (a.n_rows <= 0 || a.n_steps <= 0) return hipSuccess;
-  static bool ok = false;
-  const hipError_t e = allow_lds(k_stream_lds, ok);
-  if (e != hipSuccess) return e;
+  (void)hipGetLastError();
   const size_t lds = stream_lds_bytes(a.vocab, a.max_unique);
   hipLaunchKernelGGL(k_stream_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
   return hipGetLastError();
