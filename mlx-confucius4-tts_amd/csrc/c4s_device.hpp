@@ -111,6 +111,73 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
   return l == 0 ? 0ull : (~0ull >> (64 - l));
 }
 
+// ---- DPP (data-parallel primitives, no LDS traffic) ------------------------------
+// gfx9 DPP controls: row_shr:n = 0x110+n (lane i reads lane i-n of its 16-lane
+// row), row_bcast:15 = 0x142 (lane 15 of row r-1 to row r), row_bcast:31 =
+// 0x143 (lane 31 to rows 2 and 3). Lanes without a source read `fill`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_f64(double v, double fill) {
+  const uint64_t b = __double_as_longlong(v), f = __double_as_longlong(fill);
+  const uint32_t lo = dpp_u32<CTRL, ROW_MASK>((uint32_t)b, (uint32_t)f);
+  const uint32_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(b >> 32), (uint32_t)(f >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Inclusive scans in lane order (Hillis-Steele inside 16-lane rows, then the
+// row totals through row_bcast:15 / row_bcast:31).
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp_u32<0x111>(v, 0u);
+  v += dpp_u32<0x112>(v, 0u);
+  v += dpp_u32<0x114>(v, 0u);
+  v += dpp_u32<0x118>(v, 0u);
+  v += dpp_u32<0x142, 0xA>(v, 0u);
+  v += dpp_u32<0x143, 0xC>(v, 0u);
+  return v;
+}
+__device__ __forceinline__ double wave_scan_f64(double v) {
+  v += dpp_f64<0x111>(v, 0.0);
+  v += dpp_f64<0x112>(v, 0.0);
+  v += dpp_f64<0x114>(v, 0.0);
+  v += dpp_f64<0x118>(v, 0.0);
+  v += dpp_f64<0x142, 0xA>(v, 0.0);
+  v += dpp_f64<0x143, 0xC>(v, 0.0);
+  return v;
+}
+// Max over the wave, valid in lane 63 after the scan pattern; broadcast.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  uint32_t u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x111>(u, u))); u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x112>(u, u))); u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x114>(u, u))); u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x118>(u, u))); u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x142, 0xA>(u, u))); u = __float_as_uint(v);
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x143, 0xC>(u, u)));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+}
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+  v = wave_scan_f64(v);
+  const uint64_t b = __double_as_longlong(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)b, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(b >> 32), 63);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return __builtin_amdgcn_readlane(v, l);
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), l));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = __double_as_longlong(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)b, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 // ---- workgroup reductions ------------------------------------------------------
 // `red` is LDS scratch with room for one entry per wave (typed views of the same
 // bytes are fine). Every thread returns the result. Two barriers: the trailing

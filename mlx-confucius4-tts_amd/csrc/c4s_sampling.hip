@@ -42,6 +42,8 @@ struct Scratch {
   double hmass[256];
   double redd[NW];
   float redf[NW];
+  float redf2[NW];
+  float redf3[NW];
   int redi[NW];
   uint32_t redu[NW];
   double wmass[NW];
@@ -431,6 +433,299 @@ __device__ __forceinline__ bool keep_test(const Keep& kp, uint32_t key, double e
   }
 }
 
+// ---- fast path for top-k rows (row staged in LDS) ------------------------------
+//
+// For 0 < k <= 64 the survivors of top_k are a few dozen ids, so the chain can
+// be decided on a small candidate set instead of the whole row:
+//  1. one pass over each thread's contiguous id chunk: row maximum and, per
+//     wave, the j-th largest thread maximum (j = ceil(k/16)); the minimum L0 of
+//     those over the 16 waves is a lower bound of the k-th largest value
+//     (16*j distinct ids are >= L0);
+//  2. a 256-bucket count histogram of the ids in [L0, max] (only those ids
+//     touch LDS) gives the bucket holding the k-th largest value;
+//  3. the ids of that bucket and above are compacted in id order (<= 64);
+//  4. the k-th largest value is selected among the boundary bucket's ids,
+//     survivors are candidates whose divided value reaches it, and a
+//     non-candidate is checked never to tie it after the division;
+//  5. for every survivor, the mass at or below it in ascending order (value
+//     asc, id desc) is summed over survivors by all 16 waves (4 partners each);
+//  6. one wave cuts the nucleus (cum <= 1 - p with the error bound), applies
+//     min_tokens_to_keep and draws in id order; a draw inside the bound is
+//     replayed sequentially in that wave.
+// Any undecidable case returns false before the RNG or outputs change.
+constexpr int kFastCap = 64;
+constexpr int kMaxChunk = kLdsVocabMax / NT;
+static_assert(kMaxChunk * NT == kLdsVocabMax, "chunking assumes kLdsVocabMax = 12 * 1024");
+constexpr int kPartners = kFastCap / NW;
+
+struct FastBuf {
+  double* cE;
+  double* part;
+  float* cz;
+  float* cy;
+  int* cid;
+  uint32_t* cb;
+  uint32_t* pcnt;
+};
+constexpr size_t kFastBytes = 8 * kFastCap + 8 * NW * kFastCap + 4 * 4 * kFastCap + 4 * NW * kFastCap;
+
+__device__ __forceinline__ FastBuf fast_buf(unsigned char* work) {
+  FastBuf f;
+  f.cE = reinterpret_cast<double*>(work);
+  f.part = f.cE + kFastCap;
+  f.cz = reinterpret_cast<float*>(f.part + NW * kFastCap);
+  f.cy = f.cz + kFastCap;
+  f.cid = reinterpret_cast<int*>(f.cy + kFastCap);
+  f.cb = reinterpret_cast<uint32_t*>(f.cid + kFastCap);
+  f.pcnt = f.cb + kFastCap;
+  return f;
+}
+
+__device__ __forceinline__ bool fast_topk_applies(const RowCfg& c, int V) {
+  return c.draw && c.topk_on && c.k <= kFastCap && V <= kLdsVocabMax &&
+         (size_t)8 * ((V + 3) & ~3) >= kFastBytes;
+}
+
+__device__ __forceinline__ uint32_t near_top_bucket(float maxY, float y, float inv) {
+  return (uint32_t)min(255, (int)((maxY - y) * inv));
+}
+
+__device__ bool fast_topk(const float* val, int V, const RowCfg& c, Scratch& sh,
+                          unsigned char* work, uint64_t& rng, int& tok_out, float* masked,
+                          uint32_t* stats) {
+  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  const float ninf = neg_inf();
+  const FastBuf fb = fast_buf(work);
+
+  // 1. my chunk, maxima, per-wave bound
+  const int lo = (int)(((long long)t * V) / NT);
+  const int hi = (int)(((long long)(t + 1) * V) / NT);
+  float yv[kMaxChunk];
+  float tmax = ninf;
+#pragma unroll
+  for (int j = 0; j < kMaxChunk; ++j) {
+    yv[j] = (lo + j < hi) ? val[lo + j] : ninf;
+    tmax = fmaxf(tmax, yv[j]);
+  }
+  for (int b = t; b < 256; b += NT) sh.hcnt[b] = 0u;
+  const float wmax = wave_max_dpp(tmax);
+  float cur = tmax, lw = wmax;
+  const int jj = (c.k + NW - 1) / NW;
+  for (int r = 1; r < jj; ++r) {
+    const uint64_t m = __ballot(cur == lw);
+    if (lane == __ffsll((unsigned long long)m) - 1) cur = ninf;
+    lw = wave_max_dpp(cur);
+  }
+  if (lane == 0) { sh.redf[w] = wmax; sh.redf2[w] = lw; }
+  if (masked)
+    for (int i = t; i < V; i += NT) masked[i] = ninf;
+  __syncthreads();
+  float maxY = ninf, L0 = __builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NW; ++i) { maxY = fmaxf(maxY, sh.redf[i]); L0 = fminf(L0, sh.redf2[i]); }
+  const float R = maxY - L0;
+  if (!(L0 > ninf) || !(R < __builtin_inff())) { __syncthreads(); return false; }
+  const float inv = (R > 0.0f) ? 256.0f / R : 0.0f;
+
+  // 2. near-top count histogram
+#pragma unroll
+  for (int j = 0; j < kMaxChunk; ++j)
+    if (yv[j] >= L0) atomicAdd(&sh.hcnt[near_top_bucket(maxY, yv[j], inv)], 1u);
+  __syncthreads();
+  if (w == 0) {
+    uint32_t c4[4], lc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { c4[j] = sh.hcnt[4 * lane + j]; lc += c4[j]; }
+    const uint32_t incl = wave_scan_u32(lc);
+    uint32_t run = incl - lc, cum_b = 0, above_b = 0;
+    int hit = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (hit < 0 && run + c4[j] >= (uint32_t)c.k) { hit = 4 * lane + j; above_b = run; cum_b = run + c4[j]; }
+      run += c4[j];
+    }
+    const uint64_t hm = __ballot(hit >= 0);
+    if (!hm) {
+      if (lane == 0) sh.bu[0] = 0xFFFFFFFFu;
+    } else if (lane == __ffsll((unsigned long long)hm) - 1) {
+      sh.bu[0] = (uint32_t)hit; sh.bu[1] = cum_b; sh.bu[2] = above_b;
+    }
+  }
+  __syncthreads();
+  const uint32_t bstar = sh.bu[0], C = sh.bu[1], above = sh.bu[2];
+  if (bstar == 0xFFFFFFFFu || C > (uint32_t)kFastCap) { __syncthreads(); return false; }
+
+  // 3. id-ordered compaction of buckets <= bstar; largest value left out
+  const float maxv = c.temp_on ? maxY / c.temp : maxY;
+  uint32_t cnt = 0, inmask = 0;
+  float ync = ninf;
+#pragma unroll
+  for (int j = 0; j < kMaxChunk; ++j) {
+    const bool ok = (yv[j] >= L0) && near_top_bucket(maxY, yv[j], inv) <= bstar;
+    inmask |= ok ? (1u << j) : 0u;
+    cnt += ok ? 1u : 0u;
+    if (!ok) ync = fmaxf(ync, yv[j]);
+  }
+  const uint32_t incl = wave_scan_u32(cnt);
+  const float wync = wave_max_dpp(ync);
+  if (lane == 63) sh.wcnt[w] = incl;
+  if (lane == 0) sh.redf3[w] = wync;
+  __syncthreads();
+  uint32_t base = incl - cnt;
+  float ync_all = ninf;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    if (i < w) base += sh.wcnt[i];
+    ync_all = fmaxf(ync_all, sh.redf3[i]);
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxChunk; ++j) {
+    if ((inmask & (1u << j)) && base < (uint32_t)kFastCap) {
+      const float y = yv[j];
+      const float z = c.temp_on ? y / c.temp : y;
+      fb.cy[base] = y;
+      fb.cz[base] = z;
+      fb.cid[base] = lo + j;
+      fb.cb[base] = near_top_bucket(maxY, y, inv);
+      fb.cE[base] = exp((double)(z - maxv));
+      ++base;
+    }
+  }
+  __syncthreads();
+
+  // 4. k-th largest value (every wave, redundantly), survivors
+  const bool valid = lane < (int)C;
+  const float cy = valid ? fb.cy[lane] : ninf;
+  const float cz = valid ? fb.cz[lane] : ninf;
+  const uint32_t cbk = valid ? fb.cb[lane] : 0xFFFFFFFFu;
+  const uint32_t need = (uint32_t)c.k - above;
+  float yk = ninf;
+  {
+    uint64_t mm = __ballot(valid && cbk == bstar);
+    while (mm) {
+      const int q = __ffsll((unsigned long long)mm) - 1;
+      mm &= mm - 1;
+      const float yq = readlane_f32(cy, q);
+      const uint32_t gt = (uint32_t)__popcll(__ballot(valid && cbk == bstar && cy > yq));
+      const uint32_t ge = (uint32_t)__popcll(__ballot(valid && cbk == bstar && cy >= yq));
+      if (gt < need && need <= ge) { yk = yq; break; }
+    }
+  }
+  const float zthr = c.temp_on ? yk / c.temp : yk;
+  if (!(yk > ninf) || (c.temp_on && !(ync_all / c.temp < zthr))) { __syncthreads(); return false; }
+  const bool surv = valid && cz >= zthr;
+
+  // 5. mass at or below each survivor (ascending order: value asc, id desc)
+  {
+    double mp = 0.0;
+    uint32_t cp = 0;
+#pragma unroll
+    for (int i = 0; i < kPartners; ++i) {
+      const int j = w * kPartners + i;
+      if (j < (int)C) {
+        const float zj = fb.cz[j];
+        if (zj >= zthr) {
+          const bool below = (zj < cz) || (zj == cz && j >= lane);
+          if (surv && below) { mp += fb.cE[j]; cp += 1u; }
+        }
+      }
+    }
+    fb.part[w * kFastCap + lane] = mp;
+    fb.pcnt[w * kFastCap + lane] = cp;
+  }
+  __syncthreads();
+
+  // 6. nucleus cut, min_keep, draw (wave 0)
+  if (w == 0) {
+    double M = 0.0;
+    uint32_t cntq = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) { M += fb.part[i * kFastCap + lane]; cntq += fb.pcnt[i * kFastCap + lane]; }
+    const double Eq = valid ? fb.cE[lane] : 0.0;
+    const int cid = valid ? fb.cid[lane] : 0;
+    const uint32_t n_surv = (uint32_t)__popcll(__ballot(surv));
+    const double S = wave_sum_dpp(surv ? Eq : 0.0);
+    const double thr = 1.0 - (double)c.p;
+    const double eps = rel_eps(V);
+    bool removed = false, unsure = false;
+    if (c.topp_on && thr >= 0.0) {
+      if (thr == 0.0) {
+        removed = surv && M == 0.0;
+      } else {
+        const double A = thr * S;
+        removed = surv && M <= A;
+        unsure = surv && !(fabs(M - A) > eps * fmax(M, A));
+      }
+    }
+    // subnormal masses may differ between libm implementations: let the general path decide
+    unsure = unsure || (surv && Eq < 0x1p-1000);
+    const bool bail = __ballot(unsure) != 0ull;
+    const long long R = (c.topp_on && thr >= 0.0)
+                            ? (long long)(V - (int)n_surv) + (long long)__popcll(__ballot(removed))
+                            : 0ll;
+    const long long lim = (long long)V - (long long)c.min_keep < 0 ? 0 : (long long)V - (long long)c.min_keep;
+    const long long m = (V - (R < lim ? R : lim));
+    const uint32_t rank = n_surv - cntq;
+    const bool kept = surv && (long long)rank < m;
+    const double Ek = kept ? Eq : 0.0;
+    const double acc = wave_scan_f64(Ek);
+    const double excl = acc - Ek;
+    const double Sd = readlane_f64(acc, 63);
+    const uint64_t st = xorshift64(rng);
+    const double u = unit_from_state(st);
+    const double r = u * Sd;
+    int tok = 0;
+    bool sure = false;
+    const uint64_t hm = __ballot(kept && acc >= r);
+    if (r > 0.0 && hm) {
+      const int f = __ffsll((unsigned long long)hm) - 1;
+      const double af = readlane_f64(acc, f), pf = readlane_f64(excl, f);
+      sure = (af - r > eps * af) && (r - pf > eps * r);
+      tok = (int)readlane_u32((uint32_t)cid, f);
+    }
+    uint32_t draw_exact = 0;
+    if (!sure) {
+      // text2semantic.cpp:152-164 in id order; ids outside the candidate list weigh 0
+      draw_exact = 1;
+      double tot = 0.0;
+      for (int q = 0; q < (int)C; ++q) tot += readlane_f64(Ek, q);
+      const double rr = u * tot;
+      double a2 = 0.0;
+      tok = V - 1;
+      if (rr <= 0.0) {
+        tok = 0;
+      } else {
+        for (int q = 0; q < (int)C; ++q) {
+          a2 += readlane_f64(Ek, q);
+          if (rr <= a2) { tok = (int)readlane_u32((uint32_t)cid, q); break; }
+        }
+      }
+    }
+    if (masked && kept) masked[cid] = cz;
+    if (lane == 0) {
+      sh.bi[0] = tok;
+      sh.bi[1] = bail ? 1 : 0;
+      sh.bu[3] = (uint32_t)__popcll(__ballot(kept));
+      sh.bu[4] = draw_exact;
+    }
+  }
+  __syncthreads();
+  const bool bail = sh.bi[1] != 0;
+  const int tok = sh.bi[0];
+  const uint32_t nk = sh.bu[3], dex = sh.bu[4];
+  __syncthreads();
+  if (bail) return false;
+  rng = xorshift64(rng);
+  tok_out = tok;
+  if (stats && t == 0) {
+    stats[0] = 1u | 2u | (c.topp_on ? 4u : 0u) | 16u;
+    stats[1] = 0u;
+    stats[2] = dex;
+    stats[3] = nk;
+  }
+  return true;
+}
+
 // ---- the chain ------------------------------------------------------------------
 template <class Src>
 __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, float* masked,
@@ -762,7 +1057,10 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
   uint64_t rng = a.rng ? a.rng[row] : 0ull;
   float* masked = a.out_masked ? a.out_masked + (int64_t)row * V : nullptr;
   uint32_t* st = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
-  const int tok = run_chain(src, sh, c, rng, masked, st);
+  int tok = 0;
+  if (!(fast_topk_applies(c, V) &&
+        fast_topk(L.val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, masked, st)))
+    tok = run_chain(src, sh, c, rng, masked, st);
   if (threadIdx.x == 0) {
     a.out_tok[row] = tok;
     if (c.draw && a.rng) a.rng[row] = rng;
@@ -869,7 +1167,11 @@ __global__ __launch_bounds__(NT) void k_stream_lds(StreamArgs a) {
     }
     LdsRow src{L.val, L.E, V, 0u, false};
     uint32_t st[4];
-    const int tok = run_chain(src, sh, c, rng, nullptr, a.stats ? st : nullptr);
+    int tok = 0;
+    if (!(fast_topk_applies(c, V) &&
+          fast_topk(L.val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, nullptr,
+                    a.stats ? st : nullptr)))
+      tok = run_chain(src, sh, c, rng, nullptr, a.stats ? st : nullptr);
     if (a.stats && threadIdx.x == 0) {
       acc_stats[0] |= st[0];
       acc_stats[1] += st[1];

@@ -1,0 +1,25 @@
+// Test-only kernels: run the wave64 DPP primitives of c4s_device.hpp on given
+// inputs so tests/test_gpu_primitives.py can check them against the host.
+// One workgroup of 64 threads; every access is within the 64-element arrays.
+#include <hip/hip_runtime.h>
+
+#include "../../mlx-confucius4-tts_amd/csrc/c4s_device.hpp"
+
+using namespace c4s;
+
+__global__ __launch_bounds__(64) void k_selftest(const uint32_t* u_in, const double* d_in,
+                                                 const float* f_in, uint32_t* u_scan,
+                                                 double* d_scan, float* f_max, double* d_sum) {
+  const int l = threadIdx.x;
+  u_scan[l] = wave_scan_u32(u_in[l]);
+  d_scan[l] = wave_scan_f64(d_in[l]);
+  f_max[l] = wave_max_dpp(f_in[l]);
+  d_sum[l] = wave_sum_dpp(d_in[l]);
+}
+
+extern "C" int c4s_selftest_wave(const uint32_t* u_in, const double* d_in, const float* f_in,
+                                 uint32_t* u_scan, double* d_scan, float* f_max, double* d_sum) {
+  hipLaunchKernelGGL(k_selftest, dim3(1), dim3(64), 0, nullptr, u_in, d_in, f_in, u_scan, d_scan,
+                     f_max, d_sum);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
