@@ -104,7 +104,7 @@ typedef struct c4s_rows {
  * replayed streams): row b's history starts from its CSR ids and grows by each
  * token it samples that is not stop_token; a row that samples stop_token is
  * done (later steps report -1, RNG frozen), as generate_batch does
- * (text2semantic.cpp:333-334). Requires vocab <= 9216 (row staged in LDS). */
+ * (text2semantic.cpp:333-334). Requires vocab <= 12288 (row staged in LDS). */
 typedef struct c4s_stream {
   const float* logits;          /* step s, row b at logits + s*step_stride + b*ld */
   int64_t ld;

@@ -32,7 +32,7 @@ struct c4s_ctx {
 
 namespace {
 
-constexpr int kStreamVocabMax = 9216;
+constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
@@ -210,7 +210,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   if (st->n_rows < 0 || st->n_steps < 0) return fail(ctx, C4S_EINVAL, "negative size");
   if (st->n_rows == 0 || st->n_steps == 0) return C4S_OK;
   if (st->vocab < 1 || st->vocab > kStreamVocabMax)
-    return fail(ctx, C4S_EINVAL, "stream needs 1 <= vocab <= 9216");
+    return fail(ctx, C4S_EINVAL, "stream needs 1 <= vocab <= 12288");
   if (st->ld < st->vocab) return fail(ctx, C4S_EINVAL, "ld < vocab");
   if (!st->logits || !st->hist_offsets || !st->temperature || !st->top_k || !st->top_p ||
       !st->rep_penalty || !st->rng_state || !st->out_tokens)
@@ -233,8 +233,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   a.rng = st->rng_state;
   a.out_tok = st->out_tokens;
   a.stats = st->out_stats;
-  a.max_unique = st->vocab;  // distinct ids are a subset of [0, vocab)
-  if (c4s::stream_lds_bytes(a.vocab, a.max_unique) + 4096 > kLdsLimit)
+  if (c4s::stream_lds_bytes(a.vocab, 0) + 4096 > kLdsLimit)
     return fail(ctx, C4S_EINVAL, "stream: row state exceeds LDS");
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");

@@ -9,6 +9,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Phase marker for cycle accounting. Expands to nothing here; an instrumented
+// build may define it before including this header.
+#ifndef C4S_PHASE
+#define C4S_PHASE(n) ((void)0)
+#endif
+
 namespace c4s {
 
 constexpr int kWave = 64;

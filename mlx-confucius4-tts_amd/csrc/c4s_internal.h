@@ -73,7 +73,6 @@ struct StreamArgs {
   uint64_t* rng;
   int32_t* out_tok;      // [n_steps][n_rows]
   uint32_t* stats;       // optional [n_rows][4], accumulated over steps
-  int max_unique;        // capacity of the per-row penalised-id list in LDS
 };
 
 struct LmHeadArgs {
@@ -91,7 +90,7 @@ struct LmHeadArgs {
 
 size_t rows_lds_bytes(int vocab);
 size_t rows_global_lds_bytes(int vocab);
-size_t stream_lds_bytes(int vocab, int max_unique);
+size_t stream_lds_bytes(int vocab, int unused);
 
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s);

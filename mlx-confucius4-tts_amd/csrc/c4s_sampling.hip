@@ -52,6 +52,7 @@ struct Scratch {
   double bd[8];
   int bi[8];
   uint32_t counter;
+  uint32_t step_stats[4];
 };
 
 // Bound on |sequential - parallel| for non-negative double sums over n terms,
@@ -435,54 +436,65 @@ __device__ __forceinline__ bool keep_test(const Keep& kp, uint32_t key, double e
 
 // ---- fast path for top-k rows (row staged in LDS) ------------------------------
 //
-// For 0 < k <= 64 the survivors of top_k are a few dozen ids, so the chain can
-// be decided on a small candidate set instead of the whole row:
-//  1. one pass over each thread's contiguous id chunk: row maximum and, per
-//     wave, the j-th largest thread maximum (j = ceil(k/16)); the minimum L0 of
-//     those over the 16 waves is a lower bound of the k-th largest value
-//     (16*j distinct ids are >= L0);
-//  2. a 256-bucket count histogram of the ids in [L0, max] (only those ids
-//     touch LDS) gives the bucket holding the k-th largest value;
-//  3. the ids of that bucket and above are compacted in id order (<= 64);
-//  4. the k-th largest value is selected among the boundary bucket's ids,
-//     survivors are candidates whose divided value reaches it, and a
-//     non-candidate is checked never to tie it after the division;
-//  5. for every survivor, the mass at or below it in ascending order (value
-//     asc, id desc) is summed over survivors by all 16 waves (4 partners each);
-//  6. one wave cuts the nucleus (cum <= 1 - p with the error bound), applies
-//     min_tokens_to_keep and draws in id order; a draw inside the bound is
-//     replayed sequentially in that wave.
-// Any undecidable case returns false before the RNG or outputs change.
-constexpr int kFastCap = 64;
-constexpr int kMaxChunk = kLdsVocabMax / NT;
-static_assert(kMaxChunk * NT == kLdsVocabMax, "chunking assumes kLdsVocabMax = 12 * 1024");
-constexpr int kPartners = kFastCap / NW;
+// For 0 < k <= 64 the chain is decided on a few dozen candidates instead of the
+// whole row. Layout: wave w owns ids [w*S, (w+1)*S), S = 64 * slots; lane l of
+// slot j holds id w*S + 64*j + l (LDS reads are bank-conflict free and a wave's
+// slot-major order is id order).
+//  P1 (all waves)  per-lane maximum; per wave the j-th largest lane maximum L_w
+//                  (j = ceil(k/10)): wave w holds j distinct ids >= L_w.
+//  P2 (wave 0)     L0 = the ceil(k/j)-th largest L_w, a lower bound of the k-th
+//                  largest value (ceil(k/j) * j >= k distinct ids are >= L0).
+//  P3 (all)        ids with value >= L0 are compacted per wave, in id order.
+//  P4 (all)        each wave copies its candidates into one id-ordered list at
+//                  its prefix and adds them to a 256-bucket histogram of
+//                  [L0, max].
+//  P5 (wave 0)     the bucket holding the k-th largest value, the k-th value
+//                  itself (ties counted with multiplicity), survivors of top_k
+//                  (divided value >= threshold; a non-candidate can not reach it
+//                  because fl(pred(L0)/t) < threshold is checked), exact
+//                  masses exp(double(z - max)).
+//  P6 (all)        for each survivor, mass and count at or below it in the
+//                  ascending order (value asc, id desc), summed over survivors.
+//  P7 (wave 0)     nucleus cut (cum <= 1 - p, with the error bound), min_keep,
+//                  inverse-CDF draw in id order; a draw inside the bound is
+//                  replayed sequentially in this wave.
+// Anything undecidable returns false before the RNG or any output changes.
+constexpr int kFastCap = 128;     // candidates handled by wave 0 (two per lane)
+constexpr int kRegionCap = 64;    // candidates one wave may contribute
+constexpr int kMaxSlots = kLdsVocabMax / (NW * kWave);
+static_assert(kMaxSlots * NW * kWave == kLdsVocabMax, "slots cover the LDS-staged rows");
+
+__device__ __forceinline__ int odd_chunk(int V) { return ((V + NT - 1) / NT) | 1; }
 
 struct FastBuf {
-  double* cE;
-  double* part;
-  float* cz;
-  float* cy;
-  int* cid;
-  uint32_t* cb;
-  uint32_t* pcnt;
+  float* ry;       // [NW][kRegionCap]
+  int* rid;        // [NW][kRegionCap]
+  float* fy;       // [kFastCap] id-ordered candidate values
+  int* fid;        // [kFastCap]
+  uint32_t* fb;    // [kFastCap] histogram bucket
+  float* sz;       // [kFastCap] divided value (survivors)
+  double* sE;      // [kFastCap] mass (0 for non-survivors)
+  double* M;       // [kFastCap] mass at or below, over survivors
+  uint32_t* Mc;    // [kFastCap] count at or below
 };
-constexpr size_t kFastBytes = 8 * kFastCap + 8 * NW * kFastCap + 4 * 4 * kFastCap + 4 * NW * kFastCap;
+constexpr size_t kFastBytes = (size_t)NW * kRegionCap * 8 + (size_t)kFastCap * (4 + 4 + 4 + 4 + 8 + 8 + 4);
 
 __device__ __forceinline__ FastBuf fast_buf(unsigned char* work) {
   FastBuf f;
-  f.cE = reinterpret_cast<double*>(work);
-  f.part = f.cE + kFastCap;
-  f.cz = reinterpret_cast<float*>(f.part + NW * kFastCap);
-  f.cy = f.cz + kFastCap;
-  f.cid = reinterpret_cast<int*>(f.cy + kFastCap);
-  f.cb = reinterpret_cast<uint32_t*>(f.cid + kFastCap);
-  f.pcnt = f.cb + kFastCap;
+  f.sE = reinterpret_cast<double*>(work);
+  f.M = f.sE + kFastCap;
+  f.ry = reinterpret_cast<float*>(f.M + kFastCap);
+  f.rid = reinterpret_cast<int*>(f.ry + NW * kRegionCap);
+  f.fy = reinterpret_cast<float*>(f.rid + NW * kRegionCap);
+  f.fid = reinterpret_cast<int*>(f.fy + kFastCap);
+  f.fb = reinterpret_cast<uint32_t*>(f.fid + kFastCap);
+  f.sz = reinterpret_cast<float*>(f.fb + kFastCap);
+  f.Mc = reinterpret_cast<uint32_t*>(f.sz + kFastCap);
   return f;
 }
 
 __device__ __forceinline__ bool fast_topk_applies(const RowCfg& c, int V) {
-  return c.draw && c.topk_on && c.k <= kFastCap && V <= kLdsVocabMax &&
+  return c.draw && c.topk_on && c.k <= 64 && V <= kLdsVocabMax &&
          (size_t)8 * ((V + 3) & ~3) >= kFastBytes;
 }
 
@@ -490,27 +502,31 @@ __device__ __forceinline__ uint32_t near_top_bucket(float maxY, float y, float i
   return (uint32_t)min(255, (int)((maxY - y) * inv));
 }
 
+template <int NS>
 __device__ bool fast_topk(const float* val, int V, const RowCfg& c, Scratch& sh,
                           unsigned char* work, uint64_t& rng, int& tok_out, float* masked,
                           uint32_t* stats) {
+  constexpr int S = NS * kWave;
   const int t = threadIdx.x, lane = lane_id(), w = wave_id();
   const float ninf = neg_inf();
   const FastBuf fb = fast_buf(work);
+  const int jj = min(8, max(1, (c.k + 9) / 10));
+  const int need_w = (c.k + jj - 1) / jj;
 
-  // 1. my chunk, maxima, per-wave bound
-  const int lo = (int)(((long long)t * V) / NT);
-  const int hi = (int)(((long long)(t + 1) * V) / NT);
-  float yv[kMaxChunk];
+  // P1: values, lane maxima, per-wave bound
+  const int base = w * S;
+  float yv[NS];
   float tmax = ninf;
 #pragma unroll
-  for (int j = 0; j < kMaxChunk; ++j) {
-    yv[j] = (lo + j < hi) ? val[lo + j] : ninf;
+  for (int j = 0; j < NS; ++j) {
+    const int i = base + kWave * j + lane;
+    yv[j] = (i < V) ? val[i] : ninf;
     tmax = fmaxf(tmax, yv[j]);
   }
-  for (int b = t; b < 256; b += NT) sh.hcnt[b] = 0u;
+  if (t < 256) sh.hcnt[t] = 0u;
+  if (t < kFastCap) { fb.M[t] = 0.0; fb.Mc[t] = 0u; }
   const float wmax = wave_max_dpp(tmax);
   float cur = tmax, lw = wmax;
-  const int jj = (c.k + NW - 1) / NW;
   for (int r = 1; r < jj; ++r) {
     const uint64_t m = __ballot(cur == lw);
     if (lane == __ffsll((unsigned long long)m) - 1) cur = ninf;
@@ -520,196 +536,237 @@ __device__ bool fast_topk(const float* val, int V, const RowCfg& c, Scratch& sh,
   if (masked)
     for (int i = t; i < V; i += NT) masked[i] = ninf;
   __syncthreads();
-  float maxY = ninf, L0 = __builtin_inff();
+  C4S_PHASE(2);
+
+  // P2: L0 (wave 0)
+  if (w == 0) {
+    const float lwl = lane < NW ? sh.redf2[lane] : ninf;
+    const float maxY = wave_max_dpp(lane < NW ? sh.redf[lane] : ninf);
+    uint32_t ge = 0;
 #pragma unroll
-  for (int i = 0; i < NW; ++i) { maxY = fmaxf(maxY, sh.redf[i]); L0 = fminf(L0, sh.redf2[i]); }
+    for (int i = 0; i < NW; ++i) ge += (readlane_f32(lwl, i) >= lwl) ? 1u : 0u;
+    const float L0 = wave_max_dpp((lane < NW && ge >= (uint32_t)need_w) ? lwl : ninf);
+    if (lane == 0) { sh.bd[0] = (double)maxY; sh.bd[1] = (double)L0; }
+  }
+  __syncthreads();
+  C4S_PHASE(3);
+  const float maxY = (float)sh.bd[0], L0 = (float)sh.bd[1];
   const float R = maxY - L0;
   if (!(L0 > ninf) || !(R < __builtin_inff())) { __syncthreads(); return false; }
   const float inv = (R > 0.0f) ? 256.0f / R : 0.0f;
 
-  // 2. near-top count histogram
+  // P3: per-wave compaction, id order within the wave
+  uint32_t wcount = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxChunk; ++j)
-    if (yv[j] >= L0) atomicAdd(&sh.hcnt[near_top_bucket(maxY, yv[j], inv)], 1u);
+  for (int j = 0; j < NS; ++j) {
+    const bool f = yv[j] >= L0;
+    const uint64_t m = __ballot(f);
+    if (m) {
+      const uint32_t pos = wcount + (uint32_t)__popcll(m & lanemask_lt());
+      if (f && pos < (uint32_t)kRegionCap) {
+        fb.ry[w * kRegionCap + pos] = yv[j];
+        fb.rid[w * kRegionCap + pos] = base + kWave * j + lane;
+      }
+      wcount += (uint32_t)__popcll(m);
+    }
+  }
+  if (lane == 0) sh.wcnt[w] = wcount;
   __syncthreads();
+  C4S_PHASE(4);
+
+  // P4: one id-ordered list + histogram
+  uint32_t C = 0, pre = 0;
+  bool over = false;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const uint32_t ci = sh.wcnt[i];
+    over = over || ci > (uint32_t)kRegionCap;
+    if (i < w) pre += ci;
+    C += ci;
+  }
+  if (over || C > (uint32_t)kFastCap) { __syncthreads(); return false; }
+  if (lane < (int)wcount) {
+    const float y = fb.ry[w * kRegionCap + lane];
+    const uint32_t bk = near_top_bucket(maxY, y, inv);
+    fb.fy[pre + lane] = y;
+    fb.fid[pre + lane] = fb.rid[w * kRegionCap + lane];
+    fb.fb[pre + lane] = bk;
+    atomicAdd(&sh.hcnt[bk], 1u);
+  }
+  __syncthreads();
+  C4S_PHASE(5);
+
+  // P5: k-th value, survivors, masses (wave 0; entries lane and lane + 64)
+  const float maxv = c.temp_on ? maxY / c.temp : maxY;
   if (w == 0) {
     uint32_t c4[4], lc = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) { c4[j] = sh.hcnt[4 * lane + j]; lc += c4[j]; }
     const uint32_t incl = wave_scan_u32(lc);
-    uint32_t run = incl - lc, cum_b = 0, above_b = 0;
+    uint32_t run = incl - lc, above_b = 0;
     int hit = -1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (hit < 0 && run + c4[j] >= (uint32_t)c.k) { hit = 4 * lane + j; above_b = run; cum_b = run + c4[j]; }
+      if (hit < 0 && run + c4[j] >= (uint32_t)c.k) { hit = 4 * lane + j; above_b = run; }
       run += c4[j];
     }
     const uint64_t hm = __ballot(hit >= 0);
-    if (!hm) {
-      if (lane == 0) sh.bu[0] = 0xFFFFFFFFu;
-    } else if (lane == __ffsll((unsigned long long)hm) - 1) {
-      sh.bu[0] = (uint32_t)hit; sh.bu[1] = cum_b; sh.bu[2] = above_b;
+    bool bail = hm == 0ull;
+    float zthr = ninf;
+    uint32_t nsurv = 0;
+    if (!bail) {
+      const int fl = __ffsll((unsigned long long)hm) - 1;
+      const uint32_t bstar = readlane_u32((uint32_t)hit, fl);
+      const uint32_t need = (uint32_t)c.k - readlane_u32(above_b, fl);
+      const bool v0 = lane < (int)C, v1 = lane + kWave < (int)C;
+      const float y0 = v0 ? fb.fy[lane] : ninf, y1 = v1 ? fb.fy[lane + kWave] : ninf;
+      const bool in0 = v0 && fb.fb[lane] == bstar, in1 = v1 && fb.fb[lane + kWave] == bstar;
+      // need-th largest value among the boundary bucket (multiplicity counted)
+      float yk = ninf;
+      uint64_t m0 = __ballot(in0), m1 = __ballot(in1);
+      while (m0 | m1) {
+        float yq;
+        if (m0) { const int q = __ffsll((unsigned long long)m0) - 1; m0 &= m0 - 1; yq = readlane_f32(y0, q); }
+        else { const int q = __ffsll((unsigned long long)m1) - 1; m1 &= m1 - 1; yq = readlane_f32(y1, q); }
+        const uint32_t gt = (uint32_t)(__popcll(__ballot(in0 && y0 > yq)) + __popcll(__ballot(in1 && y1 > yq)));
+        const uint32_t ge = (uint32_t)(__popcll(__ballot(in0 && y0 >= yq)) + __popcll(__ballot(in1 && y1 >= yq)));
+        if (gt < need && need <= ge) { yk = yq; break; }
+      }
+      zthr = c.temp_on ? yk / c.temp : yk;
+      // every id left out is <= pred(L0); after the division it must stay below the threshold
+      const float l0m = nextafterf(L0, ninf);
+      bail = !(yk > ninf) || (c.temp_on ? !(l0m / c.temp < zthr) : !(l0m < zthr));
+      const float z0 = c.temp_on ? y0 / c.temp : y0, z1 = c.temp_on ? y1 / c.temp : y1;
+      const bool s0 = v0 && z0 >= zthr, s1 = v1 && z1 >= zthr;
+      fb.sz[lane] = z0;
+      fb.sz[lane + kWave] = z1;
+      fb.sE[lane] = s0 ? exp((double)(z0 - maxv)) : -1.0;
+      fb.sE[lane + kWave] = s1 ? exp((double)(z1 - maxv)) : -1.0;
+      nsurv = (uint32_t)(__popcll(__ballot(s0)) + __popcll(__ballot(s1)));
     }
+    if (lane == 0) { sh.bi[0] = bail ? 1 : 0; sh.bu[0] = nsurv; sh.bd[2] = (double)zthr; }
   }
   __syncthreads();
-  const uint32_t bstar = sh.bu[0], C = sh.bu[1], above = sh.bu[2];
-  if (bstar == 0xFFFFFFFFu || C > (uint32_t)kFastCap) { __syncthreads(); return false; }
+  C4S_PHASE(6);
+  if (sh.bi[0]) { __syncthreads(); return false; }
+  const uint32_t nsurv = sh.bu[0];
 
-  // 3. id-ordered compaction of buckets <= bstar; largest value left out
-  const float maxv = c.temp_on ? maxY / c.temp : maxY;
-  uint32_t cnt = 0, inmask = 0;
-  float ync = ninf;
-#pragma unroll
-  for (int j = 0; j < kMaxChunk; ++j) {
-    const bool ok = (yv[j] >= L0) && near_top_bucket(maxY, yv[j], inv) <= bstar;
-    inmask |= ok ? (1u << j) : 0u;
-    cnt += ok ? 1u : 0u;
-    if (!ok) ync = fmaxf(ync, yv[j]);
-  }
-  const uint32_t incl = wave_scan_u32(cnt);
-  const float wync = wave_max_dpp(ync);
-  if (lane == 63) sh.wcnt[w] = incl;
-  if (lane == 0) sh.redf3[w] = wync;
-  __syncthreads();
-  uint32_t base = incl - cnt;
-  float ync_all = ninf;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    if (i < w) base += sh.wcnt[i];
-    ync_all = fmaxf(ync_all, sh.redf3[i]);
-  }
-#pragma unroll
-  for (int j = 0; j < kMaxChunk; ++j) {
-    if ((inmask & (1u << j)) && base < (uint32_t)kFastCap) {
-      const float y = yv[j];
-      const float z = c.temp_on ? y / c.temp : y;
-      fb.cy[base] = y;
-      fb.cz[base] = z;
-      fb.cid[base] = lo + j;
-      fb.cb[base] = near_top_bucket(maxY, y, inv);
-      fb.cE[base] = exp((double)(z - maxv));
-      ++base;
-    }
-  }
-  __syncthreads();
-
-  // 4. k-th largest value (every wave, redundantly), survivors
-  const bool valid = lane < (int)C;
-  const float cy = valid ? fb.cy[lane] : ninf;
-  const float cz = valid ? fb.cz[lane] : ninf;
-  const uint32_t cbk = valid ? fb.cb[lane] : 0xFFFFFFFFu;
-  const uint32_t need = (uint32_t)c.k - above;
-  float yk = ninf;
+  // P6: survivor pairs; wave w takes partner entries [8w, 8w + 8)
   {
-    uint64_t mm = __ballot(valid && cbk == bstar);
-    while (mm) {
-      const int q = __ffsll((unsigned long long)mm) - 1;
-      mm &= mm - 1;
-      const float yq = readlane_f32(cy, q);
-      const uint32_t gt = (uint32_t)__popcll(__ballot(valid && cbk == bstar && cy > yq));
-      const uint32_t ge = (uint32_t)__popcll(__ballot(valid && cbk == bstar && cy >= yq));
-      if (gt < need && need <= ge) { yk = yq; break; }
-    }
-  }
-  const float zthr = c.temp_on ? yk / c.temp : yk;
-  if (!(yk > ninf) || (c.temp_on && !(ync_all / c.temp < zthr))) { __syncthreads(); return false; }
-  const bool surv = valid && cz >= zthr;
-
-  // 5. mass at or below each survivor (ascending order: value asc, id desc)
-  {
-    double mp = 0.0;
-    uint32_t cp = 0;
+    constexpr int kPer = kFastCap / NW;
+    const float zq0 = fb.sz[lane], zq1 = fb.sz[lane + kWave];
+    const bool sq0 = fb.sE[lane] >= 0.0, sq1 = fb.sE[lane + kWave] >= 0.0;
+    double m0 = 0.0, m1 = 0.0;
+    uint32_t c0 = 0, c1 = 0;
 #pragma unroll
-    for (int i = 0; i < kPartners; ++i) {
-      const int j = w * kPartners + i;
-      if (j < (int)C) {
-        const float zj = fb.cz[j];
-        if (zj >= zthr) {
-          const bool below = (zj < cz) || (zj == cz && j >= lane);
-          if (surv && below) { mp += fb.cE[j]; cp += 1u; }
-        }
+    for (int i = 0; i < kPer; ++i) {
+      const int j = w * kPer + i;
+      const double Ej = fb.sE[j];
+      if (Ej >= 0.0) {
+        const float zj = fb.sz[j];
+        // j is at or below q in ascending order: z_j < z_q, or equal and id_j >= id_q
+        if (sq0 && ((zj < zq0) || (zj == zq0 && j >= lane))) { m0 += Ej; ++c0; }
+        if (sq1 && ((zj < zq1) || (zj == zq1 && j >= lane + kWave))) { m1 += Ej; ++c1; }
       }
     }
-    fb.part[w * kFastCap + lane] = mp;
-    fb.pcnt[w * kFastCap + lane] = cp;
+    if (c0) { atomicAdd(&fb.M[lane], m0); atomicAdd(&fb.Mc[lane], c0); }
+    if (c1) { atomicAdd(&fb.M[lane + kWave], m1); atomicAdd(&fb.Mc[lane + kWave], c1); }
   }
   __syncthreads();
+  C4S_PHASE(7);
 
-  // 6. nucleus cut, min_keep, draw (wave 0)
+  // P7: nucleus cut, min_keep, draw (wave 0)
   if (w == 0) {
-    double M = 0.0;
-    uint32_t cntq = 0;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) { M += fb.part[i * kFastCap + lane]; cntq += fb.pcnt[i * kFastCap + lane]; }
-    const double Eq = valid ? fb.cE[lane] : 0.0;
-    const int cid = valid ? fb.cid[lane] : 0;
-    const uint32_t n_surv = (uint32_t)__popcll(__ballot(surv));
-    const double S = wave_sum_dpp(surv ? Eq : 0.0);
+    const double e0r = fb.sE[lane], e1r = fb.sE[lane + kWave];
+    const bool s0 = e0r >= 0.0, s1 = e1r >= 0.0;
+    const double E0 = s0 ? e0r : 0.0, E1 = s1 ? e1r : 0.0;
+    const double M0 = fb.M[lane], M1 = fb.M[lane + kWave];
+    const uint32_t q0 = fb.Mc[lane], q1 = fb.Mc[lane + kWave];
+    const int id0 = (lane < (int)C) ? fb.fid[lane] : 0;
+    const int id1 = (lane + kWave < (int)C) ? fb.fid[lane + kWave] : 0;
+    const double S = wave_sum_dpp(E0 + E1);
     const double thr = 1.0 - (double)c.p;
     const double eps = rel_eps(V);
-    bool removed = false, unsure = false;
+    bool r0 = false, r1 = false, unsure = false;
     if (c.topp_on && thr >= 0.0) {
       if (thr == 0.0) {
-        removed = surv && M == 0.0;
+        r0 = s0 && M0 == 0.0;
+        r1 = s1 && M1 == 0.0;
       } else {
         const double A = thr * S;
-        removed = surv && M <= A;
-        unsure = surv && !(fabs(M - A) > eps * fmax(M, A));
+        r0 = s0 && M0 <= A;
+        r1 = s1 && M1 <= A;
+        unsure = (s0 && !(fabs(M0 - A) > eps * fmax(M0, A))) || (s1 && !(fabs(M1 - A) > eps * fmax(M1, A)));
       }
     }
     // subnormal masses may differ between libm implementations: let the general path decide
-    unsure = unsure || (surv && Eq < 0x1p-1000);
+    unsure = unsure || (s0 && E0 < 0x1p-1000) || (s1 && E1 < 0x1p-1000);
     const bool bail = __ballot(unsure) != 0ull;
     const long long R = (c.topp_on && thr >= 0.0)
-                            ? (long long)(V - (int)n_surv) + (long long)__popcll(__ballot(removed))
+                            ? (long long)(V - (int)nsurv) + (long long)(__popcll(__ballot(r0)) + __popcll(__ballot(r1)))
                             : 0ll;
     const long long lim = (long long)V - (long long)c.min_keep < 0 ? 0 : (long long)V - (long long)c.min_keep;
-    const long long m = (V - (R < lim ? R : lim));
-    const uint32_t rank = n_surv - cntq;
-    const bool kept = surv && (long long)rank < m;
-    const double Ek = kept ? Eq : 0.0;
-    const double acc = wave_scan_f64(Ek);
-    const double excl = acc - Ek;
-    const double Sd = readlane_f64(acc, 63);
+    const long long m = (long long)V - (R < lim ? R : lim);
+    const bool k0 = s0 && (long long)(nsurv - q0) < m;
+    const bool k1 = s1 && (long long)(nsurv - q1) < m;
+    const double K0 = k0 ? E0 : 0.0, K1 = k1 ? E1 : 0.0;
+    const double a0 = wave_scan_f64(K0);
+    const double h0 = readlane_f64(a0, kWave - 1);
+    const double a1 = wave_scan_f64(K1) + h0;
+    const double Sd = readlane_f64(a1, kWave - 1);
     const uint64_t st = xorshift64(rng);
     const double u = unit_from_state(st);
     const double r = u * Sd;
     int tok = 0;
     bool sure = false;
-    const uint64_t hm = __ballot(kept && acc >= r);
-    if (r > 0.0 && hm) {
-      const int f = __ffsll((unsigned long long)hm) - 1;
-      const double af = readlane_f64(acc, f), pf = readlane_f64(excl, f);
+    const uint64_t hm0 = __ballot(k0 && a0 >= r), hm1 = __ballot(k1 && a1 >= r);
+    if (r > 0.0 && (hm0 | hm1)) {
+      double af, pf;
+      if (hm0) {
+        const int f = __ffsll((unsigned long long)hm0) - 1;
+        af = readlane_f64(a0, f); pf = af - readlane_f64(K0, f); tok = (int)readlane_u32((uint32_t)id0, f);
+      } else {
+        const int f = __ffsll((unsigned long long)hm1) - 1;
+        af = readlane_f64(a1, f); pf = af - readlane_f64(K1, f); tok = (int)readlane_u32((uint32_t)id1, f);
+      }
       sure = (af - r > eps * af) && (r - pf > eps * r);
-      tok = (int)readlane_u32((uint32_t)cid, f);
     }
     uint32_t draw_exact = 0;
     if (!sure) {
-      // text2semantic.cpp:152-164 in id order; ids outside the candidate list weigh 0
+      // text2semantic.cpp:152-164 in id order; ids outside the list weigh 0
       draw_exact = 1;
       double tot = 0.0;
-      for (int q = 0; q < (int)C; ++q) tot += readlane_f64(Ek, q);
+      for (int q = 0; q < kWave; ++q) tot += readlane_f64(K0, q);
+      for (int q = 0; q < kWave; ++q) tot += readlane_f64(K1, q);
       const double rr = u * tot;
-      double a2 = 0.0;
+      double acc = 0.0;
       tok = V - 1;
       if (rr <= 0.0) {
         tok = 0;
       } else {
-        for (int q = 0; q < (int)C; ++q) {
-          a2 += readlane_f64(Ek, q);
-          if (rr <= a2) { tok = (int)readlane_u32((uint32_t)cid, q); break; }
+        bool fnd = false;
+        for (int q = 0; q < 2 * kWave && !fnd; ++q) {
+          acc += (q < kWave) ? readlane_f64(K0, q) : readlane_f64(K1, q - kWave);
+          if (rr <= acc) {
+            tok = (int)((q < kWave) ? readlane_u32((uint32_t)id0, q) : readlane_u32((uint32_t)id1, q - kWave));
+            fnd = true;
+          }
         }
       }
     }
-    if (masked && kept) masked[cid] = cz;
+    if (masked) {
+      if (k0) masked[id0] = fb.sz[lane];
+      if (k1) masked[id1] = fb.sz[lane + kWave];
+    }
     if (lane == 0) {
       sh.bi[0] = tok;
       sh.bi[1] = bail ? 1 : 0;
-      sh.bu[3] = (uint32_t)__popcll(__ballot(kept));
+      sh.bu[3] = (uint32_t)(__popcll(__ballot(k0)) + __popcll(__ballot(k1)));
       sh.bu[4] = draw_exact;
     }
   }
   __syncthreads();
+  C4S_PHASE(8);
   const bool bail = sh.bi[1] != 0;
   const int tok = sh.bi[0];
   const uint32_t nk = sh.bu[3], dex = sh.bu[4];
@@ -724,6 +781,14 @@ __device__ bool fast_topk(const float* val, int V, const RowCfg& c, Scratch& sh,
     stats[3] = nk;
   }
   return true;
+}
+
+// Dispatch on the slot count (9 slots cover 9216 ids, 12 cover 12288).
+__device__ __forceinline__ bool fast_topk_any(const float* val, int V, const RowCfg& c, Scratch& sh,
+                                              unsigned char* work, uint64_t& rng, int& tok,
+                                              float* masked, uint32_t* stats) {
+  if (V <= 9 * NW * kWave) return fast_topk<9>(val, V, c, sh, work, rng, tok, masked, stats);
+  return fast_topk<12>(val, V, c, sh, work, rng, tok, masked, stats);
 }
 
 // ---- the chain ------------------------------------------------------------------
@@ -882,21 +947,25 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
     if (lane == 0) sh.wmass[wave_id()] = wm;
     __syncthreads();
     // Per-wave exclusive prefixes and the total, summed in a fixed order.
-    double X[NW];
     double tot = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) { X[w] = tot; tot += sh.wmass[w]; }
+    for (int w = 0; w < NW; ++w) tot += sh.wmass[w];
     rng = xorshift64(rng);
     const double u = unit_from_state(rng);
     const double r = u * tot;
     int owner = NW - 1;
-#pragma unroll
-    for (int w = NW - 1; w >= 0; --w)
-      if (X[w] + sh.wmass[w] >= r) owner = w;
+    double xown = 0.0;
+    {
+      double x = 0.0;
+      for (int w = 0; w < NW; ++w) {
+        const double nx = x + sh.wmass[w];
+        if (nx >= r) { owner = w; xown = x; break; }
+        x = nx;
+      }
+    }
     __syncthreads();
     const double eps = rel_eps(V);
     if (wave_id() == owner) {
-      double carry_m = X[owner];
+      double carry_m = xown;
       int found = -1;
       double acc = 0.0, prev = 0.0;
       uint32_t carry = tie_base;
@@ -1006,18 +1075,85 @@ struct LdsLayout {
   double* E;
   float* val;
   uint32_t* bitmap;
-  int32_t* uniq;
 };
 
 __device__ __forceinline__ int vpad(int V) { return (V + 3) & ~3; }
+__host__ __device__ __forceinline__ int bitmap_words(int V) { return ((V + 31) / 32 + 1 + 3) & ~3; }
 
+// `val` is the row buffer base (vpad(V) + 4 floats); a row is stored at
+// val + shift so that its float4 body is 16-byte aligned in LDS.
 __device__ LdsLayout lds_layout(unsigned char* smem, int V) {
   LdsLayout L;
   L.E = reinterpret_cast<double*>(smem);
   L.val = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
-  L.bitmap = reinterpret_cast<uint32_t*>(L.val + vpad(V));
-  L.uniq = reinterpret_cast<int32_t*>(L.bitmap + ((V + 31) / 32 + 3) / 4 * 4);
+  L.bitmap = reinterpret_cast<uint32_t*>(L.val + vpad(V) + 4);
   return L;
+}
+
+// Coalesced fetch of one f32 row of at most kLdsVocabMax ids into registers:
+// the 0-3 ids before the first 16-byte boundary and the 0-3 ids after the
+// last one go one per thread, the rest as float4 (at most 3 per thread).
+struct RowFetch {
+  float4 body[3];
+  float edge;
+};
+
+struct RowShape {
+  int head, nq, tail;
+};
+__device__ __forceinline__ RowShape row_shape(const float* p, int V) {
+  RowShape r;
+  r.head = min(V, (int)(((16u - ((uint32_t)(uintptr_t)p & 15u)) & 15u) >> 2));
+  r.nq = (V - r.head) >> 2;
+  r.tail = V - r.head - 4 * r.nq;
+  return r;
+}
+
+__device__ __forceinline__ void fetch_row(const float* p, int V, RowFetch& f) {
+  const RowShape r = row_shape(p, V);
+  const float4* p4 = reinterpret_cast<const float4*>(p + r.head);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int q = t + NT * j;
+    f.body[j] = (q < r.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  f.edge = (t < r.head) ? p[t] : ((t < r.head + r.tail) ? p[r.head + 4 * r.nq + (t - r.head)] : 0.f);
+}
+
+// Writes the fetched row into LDS and returns where it starts (buf + 0..3).
+__device__ __forceinline__ float* store_row(const float* p, int V, const RowFetch& f, float* buf) {
+  const RowShape r = row_shape(p, V);
+  float* val = buf + ((4 - r.head) & 3);
+  const int t = threadIdx.x;
+  float4* body = reinterpret_cast<float4*>(val + r.head);
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int q = t + NT * j;
+    if (q < r.nq) body[q] = f.body[j];
+  }
+  if (t < r.head) val[t] = f.edge;
+  else if (t < r.head + r.tail) val[r.head + 4 * r.nq + (t - r.head)] = f.edge;
+  return val;
+}
+
+// Repetition penalty on the LDS row (sampling.cpp:19-28): every id whose bit is
+// set in `bitmap` is penalised once. Thread t handles its own id chunk.
+__device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitmap, int V, float pen) {
+  const int ch = odd_chunk(V);
+  const int lo = min(V, (int)threadIdx.x * ch);
+  const int hi = min(V, lo + ch);
+  if (lo >= hi) return;
+  const int w0 = lo >> 5;
+  uint64_t bits = (uint64_t)bitmap[w0] | ((uint64_t)bitmap[w0 + 1] << 32);
+  bits >>= (lo - 32 * w0);
+  bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
+  while (bits) {
+    const int i = lo + __ffsll((unsigned long long)bits) - 1;
+    bits &= bits - 1;
+    const float s = val[i];
+    val[i] = (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
+  }
 }
 
 // ---- kernels -------------------------------------------------------------------
@@ -1035,22 +1171,26 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
                             a.do_sample);
   LdsLayout L = lds_layout(smem, V);
   const int64_t roff = (int64_t)row * a.ld;
-  for (int i = threadIdx.x; i < V; i += NT) L.val[i] = load_logit(a.logits, a.dtype, roff + i);
+  if (a.dtype == 0) {
+    RowFetch f;
+    const float* p = static_cast<const float*>(a.logits) + roff;
+    fetch_row(p, V, f);
+    L.val = store_row(p, V, f, L.val);
+  } else {
+    for (int i = threadIdx.x; i < V; i += NT) L.val[i] = load_logit(a.logits, a.dtype, roff + i);
+  }
   if (c.pen_on) {
-    const int nw = (V + 31) / 32;
+    const int nw = bitmap_words(V);
     for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
     __syncthreads();
     const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
     for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
       const int id = a.hist_ids[j];
       if (id < 0 || id >= V) continue;   // sampling.cpp:24
-      const uint32_t bit = 1u << (id & 31);
-      const uint32_t old = atomicOr(&L.bitmap[id >> 5], bit);
-      if (!(old & bit)) {
-        const float s = L.val[id];
-        L.val[id] = (s < 0) ? s * c.pen : s / c.pen;   // sampling.cpp:26
-      }
+      atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
     }
+    __syncthreads();
+    penalise_chunk(L.val, L.bitmap, V, c.pen);
   }
   __syncthreads();
   LdsRow src{L.val, L.E, V, 0u, false};
@@ -1059,7 +1199,7 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
   uint32_t* st = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
   int tok = 0;
   if (!(fast_topk_applies(c, V) &&
-        fast_topk(L.val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, masked, st)))
+        fast_topk_any(L.val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, masked, st)))
     tok = run_chain(src, sh, c, rng, masked, st);
   if (threadIdx.x == 0) {
     a.out_tok[row] = tok;
@@ -1119,6 +1259,12 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
 // list) and grow with every sampled token that is not the stop token
 // (text2semantic.cpp:333-334). A stopped row reports -1 afterwards and its RNG
 // stays frozen.
+// Multi-step AR stream for rows staged in LDS: one persistent workgroup per
+// row walks all steps. The row's distinct penalised ids live in an LDS bitmap
+// that gains every sampled token that is not the stop token
+// (text2semantic.cpp:333-334). While step s runs, the logits of step s+1 are
+// already in flight into registers. A stopped row reports -1 afterwards and its
+// RNG stays frozen.
 __global__ __launch_bounds__(NT) void k_stream_lds(StreamArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ Scratch sh;
@@ -1126,78 +1272,60 @@ __global__ __launch_bounds__(NT) void k_stream_lds(StreamArgs a) {
   const int V = a.vocab;
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
   LdsLayout L = lds_layout(smem, V);
-  const int nw = (V + 31) / 32;
+  const int nw = bitmap_words(V);
   for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
-  if (threadIdx.x == 0) sh.counter = 0;
   __syncthreads();
   {
     const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
     for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
       const int id = a.hist_ids[j];
       if (id < 0 || id >= V) continue;
-      const uint32_t bit = 1u << (id & 31);
-      const uint32_t old = atomicOr(&L.bitmap[id >> 5], bit);
-      if (!(old & bit)) {
-        const uint32_t slot = atomicAdd(&sh.counter, 1u);
-        if ((int)slot < a.max_unique) L.uniq[slot] = id;
-      }
+      atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
     }
   }
-  __syncthreads();
-  int n_uniq = min((int)sh.counter, a.max_unique);
   uint64_t rng = a.rng[row];
   bool done = false;
   uint32_t acc_stats[4] = {0, 0, 0, 0};
+  const float* base = a.logits + (int64_t)row * a.ld;
+  RowFetch pf;
+  fetch_row(base, V, pf);
   for (int s = 0; s < a.n_steps; ++s) {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     if (done) {
       if (threadIdx.x == 0) *outp = -1;
       continue;
     }
-    const int64_t roff = (int64_t)s * a.step_stride + (int64_t)row * a.ld;
-    for (int i = threadIdx.x; i < V; i += NT) L.val[i] = a.logits[roff + i];
+    C4S_PHASE(0);
+    const float* cur = base + (int64_t)s * a.step_stride;
+    float* val = store_row(cur, V, pf, L.val);
+    if (s + 1 < a.n_steps) fetch_row(cur + a.step_stride, V, pf);
     __syncthreads();
     if (c.pen_on) {
-      for (int j = threadIdx.x; j < n_uniq; j += NT) {
-        const int id = L.uniq[j];
-        const float v = L.val[id];
-        L.val[id] = (v < 0) ? v * c.pen : v / c.pen;
-      }
+      penalise_chunk(val, L.bitmap, V, c.pen);
       __syncthreads();
     }
-    LdsRow src{L.val, L.E, V, 0u, false};
-    uint32_t st[4];
+    C4S_PHASE(1);
+    LdsRow src{val, L.E, V, 0u, false};
+    uint32_t* st = a.stats ? sh.step_stats : nullptr;   // written and read by thread 0 only
     int tok = 0;
     if (!(fast_topk_applies(c, V) &&
-          fast_topk(L.val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, nullptr,
-                    a.stats ? st : nullptr)))
-      tok = run_chain(src, sh, c, rng, nullptr, a.stats ? st : nullptr);
-    if (a.stats && threadIdx.x == 0) {
-      acc_stats[0] |= st[0];
-      acc_stats[1] += st[1];
-      acc_stats[2] += st[2];
-      acc_stats[3] += st[3];
-    }
-    if (threadIdx.x == 0) *outp = tok;
-    if (tok == a.stop_token) {
-      done = true;
-    } else if (tok >= 0 && tok < V) {
+          fast_topk_any(val, V, c, sh, reinterpret_cast<unsigned char*>(L.E), rng, tok, nullptr, st)))
+      tok = run_chain(src, sh, c, rng, nullptr, st);
+    C4S_PHASE(8);
+    if (threadIdx.x == 0) {
+      *outp = tok;
+      if (a.stats) {
+        acc_stats[0] |= st[0];
+        acc_stats[1] += st[1];
+        acc_stats[2] += st[2];
+        acc_stats[3] += st[3];
+      }
       // Appending a token already in the history changes nothing: the penalty
       // applies once per distinct id (sampling.cpp:22).
-      if (threadIdx.x == 0) {
-        const uint32_t bit = 1u << (tok & 31);
-        int appended = 0;
-        if (!(L.bitmap[tok >> 5] & bit) && n_uniq < a.max_unique) {
-          L.bitmap[tok >> 5] |= bit;
-          L.uniq[n_uniq] = tok;
-          appended = 1;
-        }
-        sh.bi[3] = appended;
-      }
-      __syncthreads();
-      n_uniq += sh.bi[3];
-      __syncthreads();
+      if (tok != a.stop_token && tok >= 0 && tok < V) L.bitmap[tok >> 5] |= 1u << (tok & 31);
     }
+    if (tok == a.stop_token) done = true;
+    __syncthreads();
   }
   if (threadIdx.x == 0) {
     a.rng[row] = rng;
@@ -1212,13 +1340,10 @@ __global__ __launch_bounds__(NT) void k_stream_lds(StreamArgs a) {
 
 size_t rows_lds_bytes(int V) {
   const size_t vp = (size_t)((V + 3) & ~3);
-  const size_t bw = (size_t)(((V + 31) / 32 + 3) / 4 * 4);
-  return 8 * vp + 4 * vp + 4 * bw;
+  return 8 * vp + 4 * (vp + 4) + 4 * (size_t)bitmap_words(V);
 }
 
-size_t stream_lds_bytes(int V, int max_unique) {
-  return rows_lds_bytes(V) + 4 * (size_t)max_unique;
-}
+size_t stream_lds_bytes(int V, int) { return rows_lds_bytes(V); }
 
 size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
 
@@ -1238,7 +1363,7 @@ hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s) {
   if (a.n_rows <= 0 || a.n_steps <= 0) return hipSuccess;
   (void)hipGetLastError();
-  const size_t lds = stream_lds_bytes(a.vocab, a.max_unique);
+  const size_t lds = stream_lds_bytes(a.vocab, 0);
   hipLaunchKernelGGL(k_stream_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
   return hipGetLastError();
 }
