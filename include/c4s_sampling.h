@@ -123,7 +123,12 @@ typedef struct c4s_stream {
   uint64_t* rng_state;
   int32_t* out_tokens;          /* [n_steps][n_rows] */
   uint32_t* out_stats;          /* [n_rows][4] (summed over steps) or NULL */
+  uint32_t flags;               /* C4S_STREAM_* */
 } c4s_stream;
+
+/* c4s_stream.flags: run every step of every row in one persistent kernel
+ * instead of the two-phase path (scan of all steps, then the per-row chain). */
+#define C4S_STREAM_SEQUENTIAL 1u
 
 /* LM head: LayerNorm(hidden) -> bf16 -> hidden @ weight^T + bias -> f32 logits
  * (text2semantic.cpp:118-121; nn.cpp:73-83 eps/biased variance, nn.cpp:11-16

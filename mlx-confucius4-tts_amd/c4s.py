@@ -22,6 +22,7 @@ P_PENALTY, P_TEMPERATURE, P_TOP_K, P_TOP_P = 1, 2, 4, 8
 T_ARGMAX, T_DRAW = 16, 32
 MODE_CUSTOM = 256
 STAT_PATH, STAT_TOPP_EXACT, STAT_DRAW_EXACT, STAT_KEPT = 0, 1, 2, 3
+STREAM_SEQUENTIAL = 1
 
 _vp = C.c_void_p
 
@@ -39,7 +40,8 @@ class Stream(C.Structure):
                 ("n_steps", C.c_int32), ("n_rows", C.c_int32), ("vocab", C.c_int32),
                 ("stop_token", C.c_int32), ("hist_ids", _vp), ("hist_offsets", _vp),
                 ("temperature", _vp), ("top_k", _vp), ("top_p", _vp), ("rep_penalty", _vp),
-                ("do_sample", _vp), ("rng_state", _vp), ("out_tokens", _vp), ("out_stats", _vp)]
+                ("do_sample", _vp), ("rng_state", _vp), ("out_tokens", _vp), ("out_stats", _vp),
+                ("flags", C.c_uint32)]
 
 
 class Head(C.Structure):
@@ -58,12 +60,25 @@ def header_functions() -> list[str]:
 _lib = None
 
 
+def _share_torch_runtime() -> None:
+    """torch ships its own HIP runtime library. When torch is present its runtime
+    is started before this library loads, so that the library binds to the same
+    runtime: a second HIP runtime in the process could not open the device."""
+    try:
+        import torch
+    except ImportError:
+        return
+    if torch.cuda.device_count() > 0:
+        torch.cuda.init()
+
+
 def lib() -> C.CDLL:
     global _lib
     if _lib is not None:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    _share_torch_runtime()
     L = C.CDLL(LIB_PATH)
     L.c4s_create.argtypes = [C.c_int, C.POINTER(_vp)]
     L.c4s_destroy.argtypes = [_vp]
@@ -152,13 +167,14 @@ class Context:
         self._check(lib().c4s_sample_rows(self._h, C.byref(r), _stream_handle(stream)), "sample_rows")
 
     def sample_stream(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_tokens,
-                      do_sample=None, stop_token=-1, out_stats=None, stream=None):
+                      do_sample=None, stop_token=-1, out_stats=None, stream=None, sequential=False):
         n_steps, n_rows, ld = logits.shape
         s = Stream(logits=_p(logits), ld=ld, step_stride=n_rows * ld, n_steps=n_steps,
                    n_rows=n_rows, vocab=ld, stop_token=stop_token, hist_ids=_p(hist_ids),
                    hist_offsets=_p(hist_off), temperature=_p(temp), top_k=_p(top_k),
                    top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
-                   rng_state=_p(rng), out_tokens=_p(out_tokens), out_stats=_p(out_stats))
+                   rng_state=_p(rng), out_tokens=_p(out_tokens), out_stats=_p(out_stats),
+                   flags=STREAM_SEQUENTIAL if sequential else 0)
         self._check(lib().c4s_sample_stream(self._h, C.byref(s), _stream_handle(stream)),
                     "sample_stream")
 

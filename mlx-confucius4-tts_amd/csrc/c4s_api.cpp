@@ -28,12 +28,21 @@ struct c4s_ctx {
   // host-helper staging (device)
   void* stage = nullptr;
   size_t stage_bytes = 0;
+  // two-phase stream: summaries of one chunk of steps, per-row carried state
+  void* sum_ws = nullptr;
+  size_t sum_bytes = 0;
+  void* state_ws = nullptr;
+  size_t state_bytes = 0;
 };
 
 namespace {
 
 constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
+constexpr size_t kChainStaticLds = 32 * 1024;      // chain kernel static LDS (upper bound)
+constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
+constexpr int kScanStepsPerGroup = 8;
+constexpr int kFastRounds = 3;
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
   if (ctx) ctx->err = msg;
@@ -233,12 +242,48 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   a.rng = st->rng_state;
   a.out_tok = st->out_tokens;
   a.stats = st->out_stats;
+  if (st->flags & ~(uint32_t)C4S_STREAM_SEQUENTIAL) return fail(ctx, C4S_EINVAL, "stream: unknown flags");
   if (c4s::stream_lds_bytes(a.vocab, 0) + 4096 > kLdsLimit)
     return fail(ctx, C4S_EINVAL, "stream: row state exceeds LDS");
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
-  hipError_t e = c4s::launch_stream(a, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const bool two_phase = !(st->flags & C4S_STREAM_SEQUENTIAL) &&
+                         c4s::stream_chain_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit;
+  if (!two_phase) {
+    hipError_t e = c4s::launch_stream(a, hs);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");
+    return C4S_OK;
+  }
+  // Steps go in chunks whose summaries fit the workspace budget; the chain
+  // carries its per-row state from chunk to chunk.
+  const size_t per_step = (size_t)a.n_rows * c4s::kSumStride;
+  const int chunk = (int)std::max<size_t>(1, std::min<size_t>((size_t)a.n_steps, kSumBudget / per_step));
+  int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, per_step * (size_t)chunk, "stream summaries");
+  if (rc) return rc;
+  rc = ensure(ctx, &ctx->state_ws, &ctx->state_bytes, (size_t)a.n_rows * c4s::kStateWords * 4, "stream state");
+  if (rc) return rc;
+  for (int s0 = 0; s0 < a.n_steps; s0 += chunk) {
+    c4s::StreamWs w{};
+    w.sum = static_cast<unsigned char*>(ctx->sum_ws);
+    w.state = static_cast<uint32_t*>(ctx->state_ws);
+    w.s_begin = s0;
+    w.s_end = std::min(a.n_steps, s0 + chunk);
+    w.steps_per_group = kScanStepsPerGroup;
+    hipError_t e = c4s::launch_stream_scan(a, w, hs);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream scan launch");
+    // Fast passes stop a row at a step they cannot decide; the repair kernel
+    // runs that step exactly; the finisher completes whatever is left.
+    for (int r = 0; r < kFastRounds; ++r) {
+      w.round = r;
+      e = c4s::launch_stream_fast(a, w, hs);
+      if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream fast launch");
+      e = c4s::launch_stream_repair(a, w, hs);
+      if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream repair launch");
+    }
+    e = c4s::launch_stream_chain(a, w, hs);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
+  }
   return C4S_OK;
 }
 

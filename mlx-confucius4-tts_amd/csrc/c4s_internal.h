@@ -75,6 +75,27 @@ struct StreamArgs {
   uint32_t* stats;       // optional [n_rows][4], accumulated over steps
 };
 
+// Two-phase stream (scan, then chain). The scan writes one summary per
+// (step, row); its layout is fixed here so that host code can size the
+// workspace.
+constexpr int kListSmall = 128;     // greedy and top-k rows
+constexpr int kListLarge = 512;     // full-vocabulary nucleus rows
+constexpr int kCandCap = 1024;      // candidates the scan may sort
+constexpr int kChunkIds = 64;       // ids per mass chunk
+constexpr int kMaxChunks = kLdsVocabMax / kChunkIds + 1;
+constexpr int kSumHdrBytes = 64;
+constexpr size_t kSumStride =
+    ((size_t)kSumHdrBytes + 8 * (size_t)kListLarge + 8 * (size_t)kMaxChunks + 127) & ~(size_t)127;
+constexpr int kStateWords = 8 + 400;  // done, stats[4], pad, new-id bitmap
+
+struct StreamWs {
+  unsigned char* sum;      // [steps in chunk][n_rows] summaries of kSumStride bytes
+  uint32_t* state;         // [n_rows][kStateWords] carried across kernels and chunks
+  int s_begin, s_end;      // steps of this chunk
+  int steps_per_group;     // scan: steps per workgroup
+  int round;               // chain rounds within the chunk (0: the first)
+};
+
 struct LmHeadArgs {
   const uint16_t* hidden;  // [M][D] bf16
   const float* gamma;
@@ -94,6 +115,11 @@ size_t stream_lds_bytes(int vocab, int unused);
 
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
+hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_fast(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+size_t stream_chain_lds_bytes(int vocab);
 hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);

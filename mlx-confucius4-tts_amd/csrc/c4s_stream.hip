@@ -1,0 +1,1466 @@
+// Two-phase AR token stream for rows staged in LDS (vocab <= 12288).
+//
+// The stream of text2semantic.cpp:296-337 is sequential only through the
+// generated history: step s penalises H0 + {tokens of steps < s}
+// (sampling.cpp:19-28, text2semantic.cpp:333-334), while its logits are given
+// and its RNG advances once per sampled step whatever was drawn
+// (text2semantic.cpp:158). So the bulk of the work is split off:
+//
+//  scan  (k_stream_scan, all CUs, every (step, row) independently)
+//        reads the row once from HBM, applies the initial history H0 and writes
+//        a summary: the top of the row sorted by (value desc, id asc), a key
+//        bound on everything left out, and, for rows without top-k, chunk masses
+//        exp(z - m0) of the whole row in 64-id chunks with an absolute error
+//        bound (fp32 exp2 with a per-element relative bound).
+//  chain (k_stream_chain, one workgroup per row, steps in order)
+//        applies the penalty of ids drawn during the stream to the summary
+//        (only those ids change), then decides top-k / top-p / the draw on
+//        the candidates. Every decision is accepted only with a margin larger
+//        than the error bounds; otherwise the step runs the exact chain on the
+//        full row (fetched into LDS), as the single-kernel stream does.
+//
+// Row modes (stream_mode): greedy rows and top-k rows with k <= 64 use the
+// candidate list alone; full-vocabulary rows (top-k off) also use the chunk
+// masses and stream their raw row into LDS for the few corrections; rows whose
+// penalty can raise values (penalty < 1) take the exact chain every step.
+
+#include "c4s_chain.hpp"
+
+namespace c4s {
+namespace {
+
+constexpr int NTA = 256;
+constexpr int NWA = NTA / kWave;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+enum : int { kModeExact = 0, kModeList = 1, kModeRow = 2 };
+
+__device__ __forceinline__ int stream_mode(const RowCfg& c, int V) {
+  if (!(c.pen >= 1.0f) || V > kLdsVocabMax) return kModeExact;   // pen < 1 raises values
+  if (c.greedy) return kModeList;
+  if (!c.draw) return kModeExact;
+  if (c.topk_on) return c.k <= 64 ? kModeList : kModeExact;
+  return kModeRow;
+}
+
+__device__ __forceinline__ int list_cap(const RowCfg& c) {
+  return (!c.greedy && !c.topk_on && c.p > 0.0f && c.p < 1.0f) ? kListLarge : kListSmall;
+}
+
+// Chunk masses are computed as the reference does, exp((double)fl(fl(y/T) - m0)):
+// the nucleus cut and the full-vocabulary draw are then decided with margins of
+// a few ulp (the fp32 exp2 variant below is kept for rows that opt out).
+__device__ __forceinline__ bool exact_masses(const RowCfg&) { return true; }
+
+__device__ __forceinline__ float pen_exact(float s, float pen) {
+  return (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
+}
+
+struct SumHdr {
+  int n;            // list entries
+  uint32_t tout;    // key bound on every value outside the list (0: nothing outside)
+  uint32_t flags;   // bit 0: unusable (candidate overflow or empty list)
+  float m0;         // chunk masses are exp(z - m0)
+  int nchunk;
+  int head;         // ids before the first 16-byte boundary of the row
+  double err;       // absolute error bound of the chunk masses, summed over the row
+  int pad[8];
+};
+static_assert(sizeof(SumHdr) == kSumHdrBytes, "summary header size");
+
+// List entry: key of the value, then the id and the id-order rank among the
+// scan's candidates; larger entries come first (value desc, id asc).
+__device__ __forceinline__ uint64_t make_entry(float y, int id, int rank) {
+  return ((uint64_t)fkey(y) << 32) | ((uint32_t)(16383 - id) << 10) | (uint32_t)rank;
+}
+__device__ __forceinline__ uint32_t ent_key(uint64_t e) { return (uint32_t)(e >> 32); }
+__device__ __forceinline__ int ent_id(uint64_t e) { return 16383 - (int)(((uint32_t)e >> 10) & 16383u); }
+__device__ __forceinline__ int ent_rank(uint64_t e) { return (int)((uint32_t)e & 1023u); }
+
+__device__ __forceinline__ const SumHdr* sum_hdr(const StreamWs& w, int n_rows, int s, int row) {
+  return reinterpret_cast<const SumHdr*>(w.sum + ((size_t)(s - w.s_begin) * n_rows + row) * kSumStride);
+}
+__device__ __forceinline__ const uint64_t* sum_list(const SumHdr* h) {
+  return reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(h) + kSumHdrBytes);
+}
+__device__ __forceinline__ const double* sum_chunks(const SumHdr* h) {
+  return reinterpret_cast<const double*>(reinterpret_cast<const unsigned char*>(h) + kSumHdrBytes +
+                                         8 * kListLarge);
+}
+
+// Approximate masses: exp(fl(y/T) - m0) as exp2(y*a - b) (v_exp_f32). Against
+// the reference's exp((double)fl(fl(y/T) - m0)) its relative error is below
+// (4|m0| + 4|t| + 8) * 2^-23: rounding of the quotient and of the difference
+// (<= 2^-24 (|z| + |d|) each), of a, b and the fma, and a few ulp of v_exp_f32.
+struct MassCoef {
+  float a, b, relc;
+};
+__device__ __forceinline__ MassCoef mass_coef(const RowCfg& c, float m0) {
+  MassCoef k;
+  k.a = c.temp_on ? kLog2e / c.temp : kLog2e;
+  k.b = m0 * kLog2e;
+  k.relc = 4.0f * fabsf(m0) + 8.0f;
+  return k;
+}
+__device__ __forceinline__ float mass_approx(float y, const MassCoef& k, float& err) {
+  const float t = fmaf(y, k.a, -k.b);
+  const float e = __builtin_amdgcn_exp2f(t);
+  err = e * (k.relc + 4.0f * fabsf(t)) * 0x1p-23f;
+  return e;
+}
+// The reference's mass of value y: exp((double)fl(fl(y/T) - m0)) (sampling.cpp:55).
+__device__ __forceinline__ double mass_exact(float y, const RowCfg& c, float m0) {
+  const float z = c.temp_on ? y / c.temp : y;
+  return exp((double)(z - m0));
+}
+// Penalised value for a mass only (x / pen within 2 ulp).
+__device__ __forceinline__ float pen_approx(float x, float pen, float rpen) {
+  return (x < 0) ? x * pen : x * rpen;
+}
+
+__device__ __forceinline__ int chunk_of(int id, int head, int nchunk) {
+  return id < head ? 0 : min(nchunk - 1, (id - head) >> 6);
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* bm, int id) {
+  return (bm[id >> 5] >> (id & 31)) & 1u;
+}
+
+// ---- scan (all CUs) -----------------------------------------------------------------
+
+struct ScanSh {
+  uint32_t hist[2048];
+  uint64_t cand[kCandCap];
+  uint32_t bm[kStateWords];
+  uint32_t wtot[16][NWA];
+  uint32_t red[NWA];
+  uint32_t redm[NWA];
+  double redd[NWA];
+  double chunk[kMaxChunks];
+  double edge[8];
+  uint32_t bu[4];
+};
+
+// Block exclusive scan over the NTA threads (thread order).
+__device__ __forceinline__ uint32_t scan_excl_nta(uint32_t v, uint32_t* red, uint32_t& total) {
+  const uint32_t inc = wave_scan_u32(v);
+  if (lane_id() == kWave - 1) red[wave_id()] = inc;
+  __syncthreads();
+  uint32_t pre = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < NWA; ++w) {
+    const uint32_t x = red[w];
+    pre += (w < wave_id()) ? x : 0u;
+    total += x;
+  }
+  __syncthreads();
+  return pre + inc - v;
+}
+
+// Bin (of 2048, scanned from the top) holding the m-th largest counted key.
+// Returns false when fewer than m keys were counted.
+__device__ bool hist_pick(ScanSh& sh, uint32_t m, uint32_t& bin, uint32_t& above) {
+  const int t = threadIdx.x;
+  uint32_t c[8], loc = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { c[i] = sh.hist[2047 - 8 * t - i]; loc += c[i]; }
+  uint32_t total;
+  const uint32_t ex = scan_excl_nta(loc, sh.red, total);
+  if (total < m) return false;
+  if (ex < m && ex + loc >= m) {
+    uint32_t run = ex;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (run < m && run + c[i] >= m) { sh.bu[0] = 2047 - 8 * t - i; sh.bu[1] = run; }
+      run += c[i];
+    }
+  }
+  __syncthreads();
+  bin = sh.bu[0];
+  above = sh.bu[1];
+  __syncthreads();
+  return true;
+}
+
+// Descending block bitonic sort of P (power of two) 64-bit entries in LDS.
+__device__ void bitonic_desc_u64(uint64_t* v, int P) {
+  for (int k = 2; k <= P; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (P >> 1); i += NTA) {
+        const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+        const int hi = lo + j;
+        const uint64_t x = v[lo], y = v[hi];
+        if ((x < y) == ((lo & k) == 0)) { v[lo] = y; v[hi] = x; }
+      }
+      __syncthreads();
+    }
+}
+
+// One workgroup scans steps [s0, s1) of one row. Thread t holds the float4
+// quads t + 256 j of the 16-byte aligned body and one head or tail id.
+template <int NQ>
+__global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w) {
+  __shared__ ScanSh sh;
+  const int row = blockIdx.y;
+  const int V = a.vocab;
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  const int mode = stream_mode(c, V);
+  if (mode == kModeExact) return;
+  const int s0 = w.s_begin + (int)blockIdx.x * w.steps_per_group;
+  const int s1 = min(w.s_end, s0 + w.steps_per_group);
+  if (s0 >= s1) return;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  const int cap = list_cap(c);
+  const bool large = cap == kListLarge;
+  const uint32_t msel = (uint32_t)cap - 16u;
+  const bool masses = mode == kModeRow;
+
+  const int nwords = bitmap_words(V);
+  for (int i = t; i < nwords; i += NTA) sh.bm[i] = 0u;
+  __syncthreads();
+  {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + t; j < h1; j += NTA) {
+      const int id = a.hist_ids[j];
+      if (id >= 0 && id < V) atomicOr(&sh.bm[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+    }
+  }
+  __syncthreads();
+  const float pen = c.pen, rpen = 1.0f / c.pen;
+
+  for (int s = s0; s < s1; ++s) {
+    const float* p = a.logits + (int64_t)s * a.step_stride + (int64_t)row * a.ld;
+    const RowShape rs = row_shape(p, V);
+    const float4* p4 = reinterpret_cast<const float4*>(p + rs.head);
+    float4 xv[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int q = t + NTA * j;
+      xv[j] = (q < rs.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const bool eh = t < rs.head;
+    const bool et = !eh && t < rs.head + rs.tail;
+    const int eid = eh ? t : rs.head + 4 * rs.nq + (t - rs.head);
+    const float xe = (eh || et) ? p[eid] : 0.f;
+
+    // Per-thread top-2 (top-4 for large lists) keys.
+    uint32_t t1 = 0, t2 = 0, t3 = 0, t4 = 0;
+    auto ins = [&](uint32_t k) {
+      if (large) { t4 = max(t4, min(t3, k)); t3 = max(t3, min(t2, k)); }
+      t2 = max(t2, min(t1, k));
+      t1 = max(t1, k);
+    };
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if (t + NTA * j < rs.nq) {
+        ins(fkey(xv[j].x)); ins(fkey(xv[j].y)); ins(fkey(xv[j].z)); ins(fkey(xv[j].w));
+      }
+    }
+    if (eh || et) ins(fkey(xe));
+
+    // L0: a key at or below the msel-th largest of those keys (two 11-bit passes).
+    for (int i = t; i < 2048; i += NTA) sh.hist[i] = 0u;
+    __syncthreads();
+    if (t1) atomicAdd(&sh.hist[t1 >> 21], 1u);
+    if (t2) atomicAdd(&sh.hist[t2 >> 21], 1u);
+    if (t3) atomicAdd(&sh.hist[t3 >> 21], 1u);
+    if (t4) atomicAdd(&sh.hist[t4 >> 21], 1u);
+    __syncthreads();
+    uint32_t L0 = 0;
+    {
+      uint32_t b1, ab1;
+      if (hist_pick(sh, msel, b1, ab1)) {
+        for (int i = t; i < 2048; i += NTA) sh.hist[i] = 0u;
+        __syncthreads();
+        if (t1 && (t1 >> 21) == b1) atomicAdd(&sh.hist[(t1 >> 10) & 2047u], 1u);
+        if (t2 && (t2 >> 21) == b1) atomicAdd(&sh.hist[(t2 >> 10) & 2047u], 1u);
+        if (t3 && (t3 >> 21) == b1) atomicAdd(&sh.hist[(t3 >> 10) & 2047u], 1u);
+        if (t4 && (t4 >> 21) == b1) atomicAdd(&sh.hist[(t4 >> 10) & 2047u], 1u);
+        __syncthreads();
+        uint32_t b2, ab2;
+        hist_pick(sh, msel - ab1, b2, ab2);
+        L0 = (b1 << 21) | (b2 << 10);
+      }
+    }
+
+    // Candidates (key >= L0) compacted in id order: head, body quads by slot, tail.
+    uint32_t cnt[NQ + 2];
+    uint32_t below = 0;   // largest key under L0 (raw value: bounds the penalised one)
+    {
+      const uint32_t ke = fkey(xe);
+      cnt[0] = (eh && ke >= L0) ? 1u : 0u;
+      cnt[NQ + 1] = (et && ke >= L0) ? 1u : 0u;
+      if ((eh || et) && ke < L0) below = ke;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        uint32_t cj = 0;
+        if (t + NTA * j < rs.nq) {
+          const uint32_t k0 = fkey(xv[j].x), k1 = fkey(xv[j].y), k2 = fkey(xv[j].z), k3 = fkey(xv[j].w);
+          cj = (k0 >= L0) + (k1 >= L0) + (k2 >= L0) + (k3 >= L0);
+          below = max(below, max(max(k0 < L0 ? k0 : 0u, k1 < L0 ? k1 : 0u),
+                                 max(k2 < L0 ? k2 : 0u, k3 < L0 ? k3 : 0u)));
+        }
+        cnt[j + 1] = cj;
+      }
+    }
+    uint32_t ex[NQ + 2];
+#pragma unroll
+    for (int sl = 0; sl < NQ + 2; ++sl) {
+      const uint32_t inc = wave_scan_u32(cnt[sl]);
+      ex[sl] = inc - cnt[sl];
+      if (lane == kWave - 1) sh.wtot[sl][wv] = inc;
+    }
+    {
+      const uint32_t bm = wave_max_u32(below);
+      if (lane == 0) sh.redm[wv] = bm;
+    }
+    __syncthreads();
+    uint32_t C = 0, tout = 0;
+#pragma unroll
+    for (int ww = 0; ww < NWA; ++ww) tout = max(tout, sh.redm[ww]);
+#pragma unroll
+    for (int sl = 0; sl < NQ + 2; ++sl) {
+      uint32_t pre = 0, tot = 0;
+#pragma unroll
+      for (int ww = 0; ww < NWA; ++ww) {
+        const uint32_t x = sh.wtot[sl][ww];
+        pre += (ww < wv) ? x : 0u;
+        tot += x;
+      }
+      ex[sl] += C + pre;
+      C += tot;
+    }
+    const bool overflow = C > (uint32_t)kCandCap;
+    if (!overflow) {
+      auto put = [&](uint32_t pos, float x, int id) {
+        const float y = bit_of(sh.bm, id) && c.pen_on ? pen_exact(x, pen) : x;
+        sh.cand[pos] = make_entry(y, id, (int)pos);
+      };
+      if (eh && fkey(xe) >= L0) put(ex[0], xe, eid);
+      if (et && fkey(xe) >= L0) put(ex[NQ + 1], xe, eid);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int q = t + NTA * j;
+        if (q < rs.nq && cnt[j + 1]) {
+          uint32_t pos = ex[j + 1];
+          const int id = rs.head + 4 * q;
+          if (fkey(xv[j].x) >= L0) put(pos++, xv[j].x, id);
+          if (fkey(xv[j].y) >= L0) put(pos++, xv[j].y, id + 1);
+          if (fkey(xv[j].z) >= L0) put(pos++, xv[j].z, id + 2);
+          if (fkey(xv[j].w) >= L0) put(pos++, xv[j].w, id + 3);
+        }
+      }
+    }
+    int P = 2;
+    while (P < (int)C) P <<= 1;
+    if (!overflow)
+      for (int i = (int)C + t; i < P; i += NTA) sh.cand[i] = 0ull;
+    __syncthreads();
+    if (!overflow) bitonic_desc_u64(sh.cand, P);
+
+    // Leading entries above the bound, at most cap of them.
+    uint32_t nabove = 0;
+    if (!overflow)
+      for (int i = t; i < (int)C; i += NTA) nabove += (ent_key(sh.cand[i]) > tout) ? 1u : 0u;
+    uint32_t n_all;
+    (void)scan_excl_nta(nabove, sh.red, n_all);
+    int n = min((int)n_all, cap);
+    if (!overflow && (int)n_all > cap) tout = max(tout, ent_key(sh.cand[cap]));
+    const bool bad = overflow || n == 0;
+
+    SumHdr* hdr = reinterpret_cast<SumHdr*>(w.sum + ((size_t)(s - w.s_begin) * a.n_rows + row) * kSumStride);
+    uint64_t* lst = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(hdr) + kSumHdrBytes);
+    double* chk = reinterpret_cast<double*>(reinterpret_cast<unsigned char*>(hdr) + kSumHdrBytes + 8 * kListLarge);
+    if (!bad)
+      for (int i = t; i < n; i += NTA) lst[i] = sh.cand[i];
+
+    // Chunk masses of the whole row (rows without top-k).
+    float m0 = 0.f;
+    int nchunk = 0;
+    double err = 0.0;
+    if (masses && !bad) {
+      const float ytop = kfloat(ent_key(sh.cand[0]));
+      m0 = c.temp_on ? ytop / c.temp : ytop;
+      const MassCoef mk = mass_coef(c, m0);
+      const bool exm = exact_masses(c);
+      nchunk = max(1, (rs.nq + 15) >> 4);
+      double el = 0.0;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int q = t + NTA * j;
+        double qd = 0.0;
+        if (q < rs.nq) {
+          const int id = rs.head + 4 * q;
+          const uint32_t hb = (uint32_t)(((uint64_t)sh.bm[id >> 5] | ((uint64_t)sh.bm[(id >> 5) + 1] << 32)) >>
+                                         (id & 31)) & 15u;
+          const bool pon = c.pen_on;
+          if (exm) {
+            qd = mass_exact((pon && (hb & 1u)) ? pen_exact(xv[j].x, pen) : xv[j].x, c, m0) +
+                 mass_exact((pon && (hb & 2u)) ? pen_exact(xv[j].y, pen) : xv[j].y, c, m0) +
+                 mass_exact((pon && (hb & 4u)) ? pen_exact(xv[j].z, pen) : xv[j].z, c, m0) +
+                 mass_exact((pon && (hb & 8u)) ? pen_exact(xv[j].w, pen) : xv[j].w, c, m0);
+          } else {
+            float er, qs = 0.f, qe = 0.f;
+            qs += mass_approx((pon && (hb & 1u)) ? pen_approx(xv[j].x, pen, rpen) : xv[j].x, mk, er); qe += er;
+            qs += mass_approx((pon && (hb & 2u)) ? pen_approx(xv[j].y, pen, rpen) : xv[j].y, mk, er); qe += er;
+            qs += mass_approx((pon && (hb & 4u)) ? pen_approx(xv[j].z, pen, rpen) : xv[j].z, mk, er); qe += er;
+            qs += mass_approx((pon && (hb & 8u)) ? pen_approx(xv[j].w, pen, rpen) : xv[j].w, mk, er); qe += er;
+            qe += qs * 0x1p-22f;   // fp32 sum of four
+            el += (double)qe;
+            qd = (double)qs;
+          }
+        }
+        // 16 consecutive lanes hold the 16 quads of one chunk
+        double d = qd;
+        d += dpp_f64<0x111>(d, 0.0);
+        d += dpp_f64<0x112>(d, 0.0);
+        d += dpp_f64<0x114>(d, 0.0);
+        d += dpp_f64<0x118>(d, 0.0);
+        const int ci = q >> 4;
+        if ((lane & 15) == 15 && ci < nchunk) sh.chunk[ci] = d;
+      }
+      if (t < 8) sh.edge[t] = 0.0;
+      __syncthreads();
+      if (eh || et) {
+        const bool pb = c.pen_on && bit_of(sh.bm, eid);
+        if (exm) {
+          sh.edge[t] = mass_exact(pb ? pen_exact(xe, pen) : xe, c, m0);   // t < 6
+        } else {
+          float er;
+          sh.edge[t] = (double)mass_approx(pb ? pen_approx(xe, pen, rpen) : xe, mk, er);
+          el += (double)er;
+        }
+      }
+      err = block_sum_f64<NTA>(el, sh.redd);
+      if (t == 0) {
+        double hs = 0.0, ts = 0.0;
+        for (int i = 0; i < rs.head; ++i) hs += sh.edge[i];
+        for (int i = rs.head; i < rs.head + rs.tail; ++i) ts += sh.edge[i];
+        sh.chunk[0] += hs;
+        sh.chunk[nchunk - 1] += ts;
+      }
+      __syncthreads();
+      for (int i = t; i < nchunk; i += NTA) chk[i] = sh.chunk[i];
+    }
+    if (t == 0) {
+      SumHdr h{};
+      h.n = bad ? 0 : n;
+      h.tout = tout;
+      h.flags = bad ? 1u : 0u;
+      h.m0 = m0;
+      h.nchunk = nchunk;
+      h.head = rs.head;
+      h.err = err + 0x1p-100;
+      *hdr = h;
+    }
+    __syncthreads();
+  }
+}
+
+// ---- chain (one workgroup per row) ----------------------------------------------------
+
+constexpr int kSumWords = (kSumHdrBytes + 8 * kListLarge + 8 * kMaxChunks) / 8;
+constexpr int kListWords = (kSumHdrBytes + 8 * kListSmall) / 8;   // header + small list
+
+struct ChainSh {
+  uint64_t sum[kSumWords];   // this step's summary: header words, list, chunks
+  double cdelta[kMaxChunks];
+  double slotE[kCandCap];
+  int slotId[kCandCap];
+  float lz[kListLarge];
+  int lid[kListLarge];
+  int lslot[kListLarge];
+  double wd[NW];
+  double we[NW];
+  uint64_t rng;
+  int bi[4];
+};
+
+// Per-row state carried across the chain kernels and across chunks of steps
+// (kStateWords words): done flag, statistics, next step, pending exact step,
+// then the bitmap of ids drawn during the stream.
+enum : int { kStDone = 0, kStStats = 1, kStNext = 5, kStPending = 6, kStBits = 8 };
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Inverse-CDF draw over the kept candidates (text2semantic.cpp:150-165): their
+// masses sit in cs.slotE at their id-order ranks [0, nslot) (zero elsewhere),
+// so slot order is id order. Wave 0 only. Returns the token; `exact` is set
+// when the margin test failed and the sums were replayed sequentially.
+__device__ int slot_draw(ChainSh& cs, int nslot, double u, int V, uint32_t& exact) {
+  const int lane = lane_id();
+  const double eps = rel_eps(V);
+  // pass 1: total in slot order (per lane 4 consecutive slots per block of 256)
+  double tot = 0.0;
+  for (int b = 0; b < nslot; b += 4 * kWave) {
+    double ls = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sidx = b + 4 * lane + i;
+      ls += (sidx < nslot) ? cs.slotE[sidx] : 0.0;
+    }
+    tot += wave_sum_dpp(ls);
+  }
+  const double r = u * tot;
+  int tok = -1;
+  double af = 0.0, pf = 0.0;
+  double carry = 0.0;
+  for (int b = 0; b < nslot && tok < 0; b += 4 * kWave) {
+    double e4[4], ls = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int sidx = b + 4 * lane + i;
+      e4[i] = (sidx < nslot) ? cs.slotE[sidx] : 0.0;
+      ls += e4[i];
+    }
+    const double inc = wave_scan_f64(ls);
+    double run = carry + inc - ls;
+    int hit = -1;
+    double ha = 0.0, hp = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const double nx = run + e4[i];
+      if (hit < 0 && e4[i] > 0.0 && nx >= r) { hit = b + 4 * lane + i; ha = nx; hp = run; }
+      run = nx;
+    }
+    const uint64_t hm = __ballot(hit >= 0);
+    if (hm) {
+      const int f = __ffsll((unsigned long long)hm) - 1;
+      tok = (int)readlane_u32((uint32_t)hit, f);
+      af = readlane_f64(ha, f);
+      pf = readlane_f64(hp, f);
+    }
+    carry = readlane_f64(carry + inc, kWave - 1);
+  }
+  const bool sure = r > 0.0 && tok >= 0 && (af - r > eps * af) && (r - pf > eps * r);
+  if (sure) {
+    exact = 0;
+    return cs.slotId[tok];
+  }
+  // text2semantic.cpp:152-164 sequentially in id order; ids outside the slots weigh 0
+  exact = 1;
+  int res = 0;
+  if (lane == 0) {
+    double total = 0.0;
+    for (int i = 0; i < nslot; ++i) total += cs.slotE[i];
+    const double rr = u * total;
+    res = V - 1;
+    if (rr <= 0.0) {
+      res = 0;
+    } else {
+      double acc = 0.0;
+      for (int i = 0; i < nslot; ++i) {
+        acc += cs.slotE[i];
+        if (cs.slotE[i] > 0.0 && rr <= acc) { res = cs.slotId[i]; break; }
+      }
+    }
+  }
+  return (int)readlane_u32((uint32_t)res, 0);
+}
+
+// Clears slots [0, nslot) (wave 0).
+__device__ __forceinline__ void clear_slots(ChainSh& cs, int nslot) {
+  for (int i = lane_id(); i < nslot; i += kWave) cs.slotE[i] = 0.0;
+  wave_sync();
+}
+
+__device__ __forceinline__ SumHdr hdr_from(const uint64_t* sw) {
+  SumHdr h{};
+  const uint64_t w0 = sw[0], w1 = sw[1], w2 = sw[2], w3 = sw[3];
+  h.n = (int)(uint32_t)w0;
+  h.tout = (uint32_t)(w0 >> 32);
+  h.flags = (uint32_t)w1;
+  h.m0 = __uint_as_float((uint32_t)(w1 >> 32));
+  h.nchunk = (int)(uint32_t)w2;
+  h.head = (int)(uint32_t)(w2 >> 32);
+  h.err = __longlong_as_double((long long)w3);
+  return h;
+}
+
+struct StepOut {
+  int tok;
+  uint32_t kept;
+  uint32_t dex;
+  uint32_t why;   // reason of a fallback to the exact step (bit index, see kWhy*)
+};
+
+// Fallback reasons, reported as bit 20 + reason in the per-row path statistics.
+enum : uint32_t {
+  kWhySummary = 0,    // summary unusable (candidate overflow, empty list)
+  kWhyBound = 1,      // a value outside the list may reach the decision
+  kWhyShort = 2,      // too few candidates left after the penalty
+  kWhyHit = 3,        // a penalised candidate stays above the threshold
+  kWhyTies = 4,       // equal values out of id order, or ties at a boundary
+  kWhyMargin = 5,     // top_p decision inside the error bound
+  kWhyDeep = 6,       // nucleus cut below the candidate list
+  kWhyDraw = 7,       // dense draw inside the error bound
+  kWhyTiny = 8,       // subnormal masses
+};
+
+// Candidate-list step for greedy and top-k rows (wave 0; two entries per lane).
+// Returns false (nothing changed) when a decision needs the exact step.
+__device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCfg& c, int V,
+                          const uint32_t* bmAll, const uint32_t* bmH0, uint64_t& rng, ChainSh& cs,
+                          StepOut& o) {
+  const int lane = lane_id();
+  o.why = kWhySummary;
+  if (h.flags & 1u) return false;
+  const int n = h.n;
+  const float ninf = neg_inf();
+  const bool v0 = lane < n, v1 = lane + kWave < n;
+  const int id0 = ent_id(e0), id1 = ent_id(e1);
+  const bool h0 = c.pen_on && v0 && bit_of(bmAll, id0) && !bit_of(bmH0, id0);
+  const bool h1 = c.pen_on && v1 && bit_of(bmAll, id1) && !bit_of(bmH0, id1);
+  const float yr0 = v0 ? kfloat(ent_key(e0)) : ninf, yr1 = v1 ? kfloat(ent_key(e1)) : ninf;
+  const float y0 = h0 ? pen_exact(yr0, c.pen) : yr0;
+  const float y1 = h1 ? pen_exact(yr1, c.pen) : yr1;
+
+  if (c.greedy) {   // text2semantic.cpp:144-145, argmax of the penalised row
+    float bv = ninf;
+    int bi = INT_MAX;
+    if (v0) argmax_merge(bv, bi, y0, id0);
+    if (v1) argmax_merge(bv, bi, y1, id1);
+    wave_argmax(bv, bi);
+    o.why = kWhyBound;
+    if (bi == INT_MAX || !(fkey(bv) > h.tout)) return false;
+    o.tok = bi;
+    o.kept = 1;
+    o.dex = 0;
+    return true;
+  }
+
+  // top-k on the unhit entries (sorted); hits must fall below the k-th value
+  const bool u0 = v0 && !h0, u1 = v1 && !h1;
+  const uint64_t b0 = __ballot(u0), b1 = __ballot(u1);
+  const int r0 = __popcll(b0 & lanemask_lt());
+  const int r1 = __popcll(b0) + __popcll(b1 & lanemask_lt());
+  const int nu = __popcll(b0) + __popcll(b1);
+  const int k = c.k;
+  o.why = kWhyShort;
+  if (nu < k) return false;
+  const uint64_t mk0 = __ballot(u0 && r0 == k - 1), mk1 = __ballot(u1 && r1 == k - 1);
+  const float yk = mk0 ? readlane_f32(y0, __ffsll((unsigned long long)mk0) - 1)
+                       : readlane_f32(y1, __ffsll((unsigned long long)mk1) - 1);
+  const float zk = c.temp_on ? yk / c.temp : yk;
+  float hm = ninf;
+  if (h0) hm = y0;
+  if (h1) hm = fmaxf(hm, y1);
+  hm = wave_max_dpp(hm);
+  const float zh = c.temp_on ? hm / c.temp : hm;
+  o.why = kWhyHit;
+  if (!(zh < zk) && hm != ninf) return false;
+  o.why = kWhyBound;
+  if (!(zk > ninf)) return false;
+  if (h.tout != 0u) {
+    const float yo = kfloat(h.tout);
+    const float zo = c.temp_on ? yo / c.temp : yo;
+    if (!(zo < zk)) return false;   // everything outside the list stays below the threshold
+  }
+  const float z0 = c.temp_on ? y0 / c.temp : y0;
+  const float z1 = c.temp_on ? y1 / c.temp : y1;
+  const bool s0 = u0 && z0 >= zk, s1 = u1 && z1 >= zk;
+  const int nsurv = __popcll(__ballot(s0)) + __popcll(__ballot(s1));
+  o.why = kWhyTies;
+  if (nsurv > kWave) return false;
+  if (s0) { cs.lz[r0] = z0; cs.lid[r0] = id0; cs.lslot[r0] = ent_rank(e0); }
+  if (s1) { cs.lz[r1] = z1; cs.lid[r1] = id1; cs.lslot[r1] = ent_rank(e1); }
+  wave_sync();
+  const bool sv = lane < nsurv;
+  const float zs = sv ? cs.lz[lane] : ninf;
+  const int ids = sv ? cs.lid[lane] : 0;
+  const int sl = sv ? cs.lslot[lane] : 0;
+  {
+    // equal quotients of different values must still be in id order
+    const float zn = __shfl_down(zs, 1, kWave);
+    const int idn = __shfl_down(ids, 1, kWave);
+    if (__ballot(sv && lane + 1 < nsurv && zs == zn && ids > idn)) return false;
+  }
+  // masses, top_p (sampling.cpp:52-65), min_keep (:67-68)
+  const float zmax = readlane_f32(zs, 0);
+  const double e = sv ? exp((double)(zs - zmax)) : 0.0;
+  const double S = wave_sum_dpp(e);
+  const double above = wave_scan_f64(e) - e;
+  const double M = S - above;
+  const double thr = 1.0 - (double)c.p;
+  const double eps = rel_eps(V);
+  bool rem = false, unsure = false;
+  if (c.topp_on && thr >= 0.0) {
+    if (thr == 0.0) {
+      rem = sv && M == 0.0;
+    } else {
+      const double A = thr * S;
+      rem = sv && M <= A;
+      unsure = sv && !(fabs(M - A) > eps * fmax(M, A));
+    }
+  }
+  o.why = __ballot(sv && e < 0x1p-1000) ? kWhyTiny : kWhyMargin;
+  unsure = (unsure && lane >= c.min_keep) || (sv && e < 0x1p-1000);
+  if (__ballot(unsure)) return false;
+  const long long R = (long long)(V - nsurv) + (long long)__popcll(__ballot(rem));
+  const long long lim = (long long)V - (long long)c.min_keep < 0 ? 0 : (long long)V - (long long)c.min_keep;
+  const long long m = (long long)V - (R < lim ? R : lim);
+  const bool kept = sv && (long long)lane < m;
+  const int nslot = (int)wave_max_u32(kept ? (uint32_t)(sl + 1) : 0u);
+  clear_slots(cs, nslot);
+  if (kept) { cs.slotE[sl] = e; cs.slotId[sl] = ids; }
+  wave_sync();
+  const uint64_t st = xorshift64(rng);
+  o.tok = slot_draw(cs, nslot, unit_from_state(st), V, o.dex);
+  o.kept = (uint32_t)__popcll(__ballot(kept));
+  rng = st;
+  return true;
+}
+
+// Full-vocabulary step (wave 0). The summary is in cs.sum; also needs the
+// per-chunk corrections for ids drawn during the stream (cs.cdelta, their sum
+// dsum and error derr) and the raw row in LDS (`val`).
+__device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
+                         const uint32_t* bmAll, const uint32_t* bmH0, double dsum, double derr,
+                         uint64_t& rng, ChainSh& cs, StepOut& o) {
+  const int lane = lane_id();
+  o.why = kWhySummary;
+  if (h.flags & 1u) return false;
+  const int n = h.n;
+  const float ninf = neg_inf();
+  const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
+  // unhit entries compacted in rank order; largest penalised hit value
+  int nu = 0;
+  float hm = ninf;
+  for (int b = 0; b < n; b += kWave) {
+    const int pos = b + lane;
+    const bool v = pos < n;
+    const uint64_t e = v ? lst[pos] : 0ull;
+    const int id = ent_id(e);
+    const bool hit = c.pen_on && v && bit_of(bmAll, id) && !bit_of(bmH0, id);
+    const float yr = v ? kfloat(ent_key(e)) : ninf;
+    const float y = hit ? pen_exact(yr, c.pen) : yr;
+    const bool u = v && !hit;
+    const uint64_t bl = __ballot(u);
+    if (u) {
+      const int rk = nu + __popcll(bl & lanemask_lt());
+      cs.lz[rk] = c.temp_on ? y / c.temp : y;
+      cs.lid[rk] = id;
+      cs.lslot[rk] = ent_rank(e);
+    }
+    if (hit) hm = fmaxf(hm, y);
+    nu += __popcll(bl);
+  }
+  o.why = kWhyShort;
+  if (nu == 0) return false;
+  hm = wave_max_dpp(hm);
+  wave_sync();
+  const float ztop = cs.lz[0];
+  o.why = kWhyBound;
+  if (!(ztop > ninf)) return false;
+  const float zo = (h.tout != 0u) ? (c.temp_on ? kfloat(h.tout) / c.temp : kfloat(h.tout)) : ninf;
+  const float zhm = c.temp_on ? hm / c.temp : hm;
+  // the maximum must be an unhit list entry above every hit and the bound
+  if (!(zo < ztop)) return false;
+  o.why = kWhyHit;
+  if (!(zhm < ztop)) return false;
+  const float mt = ztop;
+  const double eps = rel_eps(V);
+  // S = (sum of chunks - corrections) * exp(m0 - mt)
+  const int nchunk = h.nchunk;
+  double cv[4];
+  double cs_l = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 4 * lane + i;
+    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cs.sum[kSumHdrBytes / 8 + kListLarge + ci]) -
+                                cs.cdelta[ci]
+                          : 0.0;
+    cs_l += cv[i];
+  }
+  const double rho = exp((double)h.m0 - (double)mt);
+  const double Sraw = wave_sum_dpp(cs_l);
+  const double S = Sraw * rho;
+  // rounding of the corrections; and when the maximum moved, fl(z - mt) against
+  // fl(z - m0) + (m0 - mt): relative 2^-23 (|d| + m0 - mt) per mass, with
+  // sum(e |d|) <= 40 S + V 2^-50 (e |d| < 2^-50 once |d| > 40)
+  const double dm = (double)h.m0 - (double)mt;
+  const double err = (h.err + derr + fabs(dsum) * 0x1p-50) * rho +
+                     (dm > 0.0 ? 0x1p-23 * ((40.0 + dm) * S + (double)V * 0x1p-50) : 0.0) + eps * S;
+  const double thr = 1.0 - (double)c.p;
+  const uint64_t st = xorshift64(rng);
+  const double u = unit_from_state(st);
+
+  if (thr > 0.0) {
+    // nucleus cut on the unhit entries in rank order: removed iff above >= p * S
+    const double pS = (double)c.p * S;
+    const double marg = (double)c.p * err + eps * S;
+    double carry = 0.0;
+    int q = -1;
+    float zq1 = ninf;   // value of the last kept entry
+    for (int b = 0; b < nu && q < 0; b += kWave) {
+      const int rkk = b + lane;
+      const bool v = rkk < nu;
+      const float z = v ? cs.lz[rkk] : ninf;
+      const double em = v ? exp((double)(z - mt)) : 0.0;
+      const double inc = wave_scan_f64(em);
+      const double ab = carry + inc - em;
+      const double D = ab - pS;
+      o.why = kWhyMargin;
+      if (__ballot(v && rkk >= c.min_keep && !(fabs(D) > marg + eps * ab))) return false;
+      const uint64_t rm = __ballot(v && D >= 0.0);
+      if (rm) {
+        const int f = __ffsll((unsigned long long)rm) - 1;
+        q = max(b + f, c.min_keep);
+      }
+      carry = readlane_f64(carry + inc, kWave - 1);
+    }
+    o.why = kWhyDeep;
+    if (q < 0) return false;        // the cut lies below the list
+    if (q > nu) return false;
+    zq1 = cs.lz[q - 1];
+    o.why = kWhyBound;
+    if (!(zo < zq1)) return false;
+    o.why = kWhyHit;
+    if (!(zhm < zq1)) return false;
+    // id order inside equal values among the kept entries and the first removed one
+    for (int b = 0; b < q; b += kWave) {
+      const int rkk = b + lane;
+      const bool v = rkk + 1 < nu && rkk < q;
+      const bool bad = v && cs.lz[rkk] == cs.lz[rkk + 1] && cs.lid[rkk] > cs.lid[rkk + 1];
+      o.why = kWhyTies;
+      if (__ballot(bad)) return false;
+    }
+    // kept = ranks [0, q): draw in id order over their slots
+    int nslot = 0;
+    for (int b = 0; b < q; b += kWave) {
+      const int rkk = b + lane;
+      nslot = max(nslot, rkk < q ? cs.lslot[rkk] + 1 : 0);
+    }
+    nslot = (int)wave_max_u32((uint32_t)nslot);
+    clear_slots(cs, nslot);
+    double smin = 1.0;
+    for (int b = 0; b < q; b += kWave) {
+      const int rkk = b + lane;
+      if (rkk < q) {
+        const double em = exp((double)(cs.lz[rkk] - mt));
+        cs.slotE[cs.lslot[rkk]] = em;
+        cs.slotId[cs.lslot[rkk]] = cs.lid[rkk];
+        smin = fmin(smin, em);
+      }
+    }
+    o.why = kWhyTiny;
+    if (__ballot(smin < 0x1p-1000)) return false;
+    wave_sync();
+    o.tok = slot_draw(cs, nslot, u, V, o.dex);
+    o.kept = (uint32_t)q;
+    rng = st;
+    return true;
+  }
+
+  // Dense draw (top_p keeps every id of nonzero mass; zero masses never win):
+  // r = u * S, chunk prefixes locate r, the chunk is recomputed exactly.
+  const double r = u * S;
+  const double inc = wave_scan_f64(cs_l);
+  double run = (inc - cs_l) * rho;
+  int cstar = -1;
+  double pstar = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 4 * lane + i;
+    const double nx = run + cv[i] * rho;
+    if (cstar < 0 && ci < nchunk && nx >= r) { cstar = ci; pstar = run; }
+    run = nx;
+  }
+  const uint64_t hmk = __ballot(cstar >= 0);
+  o.why = kWhyDraw;
+  if (!hmk || !(r > 0.0)) return false;
+  const int fl = __ffsll((unsigned long long)hmk) - 1;
+  cstar = (int)readlane_u32((uint32_t)cstar, fl);
+  pstar = readlane_f64(pstar, fl);
+  const int lo = cstar == 0 ? 0 : h.head + kChunkIds * cstar;
+  const int hi = (cstar == nchunk - 1) ? V : h.head + kChunkIds * (cstar + 1);
+  double ea = 0.0, eb = 0.0;
+  const int ia = lo + lane, ib = lo + kWave + lane;
+  auto mass_at = [&](int id) -> double {
+    const float x = val[id];
+    const float y = bit_of(bmAll, id) ? pen_exact(x, c.pen) : x;
+    const float z = c.temp_on ? y / c.temp : y;
+    return (z == ninf) ? 0.0 : exp((double)(z - mt));
+  };
+  if (ia < hi) ea = mass_at(ia);
+  if (ib < hi) eb = mass_at(ib);
+  const double sa = wave_scan_f64(ea) + pstar;
+  const double ta = readlane_f64(sa, kWave - 1);
+  const double sb = wave_scan_f64(eb) + ta;
+  const double mg = 2.0 * err;
+  const uint64_t fa = __ballot(ia < hi && ea > 0.0 && sa >= r);
+  const uint64_t fb = __ballot(ib < hi && eb > 0.0 && sb >= r);
+  double af, pf;
+  int tok;
+  if (fa) {
+    const int f = __ffsll((unsigned long long)fa) - 1;
+    af = readlane_f64(sa, f);
+    pf = af - readlane_f64(ea, f);
+    tok = lo + f;
+  } else if (fb) {
+    const int f = __ffsll((unsigned long long)fb) - 1;
+    af = readlane_f64(sb, f);
+    pf = af - readlane_f64(eb, f);
+    tok = lo + kWave + f;
+  } else {
+    return false;
+  }
+  if (!((af - r > mg + eps * af) && (r - pf > mg + eps * r))) return false;
+  o.tok = tok;
+  o.kept = (uint32_t)V;
+  o.dex = 0;
+  rng = st;
+  return true;
+}
+
+// Exact step on the row in LDS (raw values at `val`): penalty of H0 and the
+// stream's ids, then the chain of the single-kernel path.
+__device__ __forceinline__ int exact_step(float* val, double* E, const uint32_t* bmAll, const RowCfg& c,
+                                       int V, Scratch& sh, uint64_t& rng, uint32_t* stp) {
+  if (c.pen_on) {
+    penalise_chunk(val, bmAll, V, c.pen);
+    __syncthreads();
+  }
+  int tok = 0;
+  if (!(fast_topk_applies(c, V) &&
+        fast_topk_any(val, V, c, sh, reinterpret_cast<unsigned char*>(E), rng, tok, nullptr, stp))) {
+    LdsRow src{val, E, V, 0u, false};
+    tok = run_chain(src, sh, c, rng, nullptr, stp);
+  }
+  return tok;
+}
+
+
+// ---- fast chain: candidate steps only, 256 threads per row ------------------------------
+//
+// No exact code here (its register demand would spill the hot loop): a step it
+// cannot decide marks the row pending and ends the row's pass; the repair
+// kernel then runs that one step exactly and the next pass resumes. The
+// summary and (full-vocabulary rows) the raw row of step s + 2 are in flight in
+// registers while step s runs.
+constexpr int NTC = 256;
+constexpr int NWC = NTC / kWave;
+constexpr int kQuadsC = kLdsVocabMax / 4 / NTC;
+static_assert(kQuadsC * 4 * NTC == kLdsVocabMax, "fast chain row fetch covers the LDS rows");
+
+struct RowRegsC {
+  float4 q[kQuadsC];
+  float e;
+};
+struct SumRegsC {
+  uint64_t w[3];
+};
+
+__device__ __forceinline__ void fetch_row_c(const float* p, int V, RowRegsC& f) {
+  const RowShape r = row_shape(p, V);
+  const float4* p4 = reinterpret_cast<const float4*>(p + r.head);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kQuadsC; ++j) {
+    const int q = t + NTC * j;
+    f.q[j] = (q < r.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  f.e = (t < r.head) ? p[t] : ((t < r.head + r.tail) ? p[r.head + 4 * r.nq + (t - r.head)] : 0.f);
+}
+
+__device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRegsC& f, float* buf) {
+  const RowShape r = row_shape(p, V);
+  float* val = buf + ((4 - r.head) & 3);
+  const int t = threadIdx.x;
+  float4* body = reinterpret_cast<float4*>(val + r.head);
+#pragma unroll
+  for (int j = 0; j < kQuadsC; ++j) {
+    const int q = t + NTC * j;
+    if (q < r.nq) body[q] = f.q[j];
+  }
+  if (t < r.head) val[t] = f.e;
+  else if (t < r.head + r.tail) val[r.head + 4 * r.nq + (t - r.head)] = f.e;
+  return val;
+}
+
+__global__ __launch_bounds__(NTC) void k_stream_fast(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ ChainSh cs;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  if (w.round == 0 && w.s_begin == 0) {
+    for (int i = t; i < kStateWords; i += NTC) stw[i] = 0u;
+    __syncthreads();
+  }
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  const int mode = stream_mode(c, V);
+  if (mode == kModeExact) return;   // the finisher runs these rows
+  const int s_first = (int)stw[kStNext];
+  if (stw[kStPending] != 0u || s_first >= w.s_end) return;
+  bool done = stw[kStDone] != 0u;
+  if (done) {   // a stopped row reports -1 (text2semantic.cpp:304)
+    for (int s = s_first + t; s < w.s_end; s += NTC) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
+    if (t == 0) stw[kStNext] = (uint32_t)w.s_end;
+    return;
+  }
+  const int nwords = bitmap_words(V);
+  float* vbuf = reinterpret_cast<float*>(smem);
+  uint32_t* bmAll = reinterpret_cast<uint32_t*>(vbuf + vpad(V) + 4);
+  uint32_t* bmH0 = bmAll + nwords;
+  for (int i = t; i < nwords; i += NTC) bmH0[i] = 0u;
+  for (int i = t; i < kMaxChunks; i += NTC) cs.cdelta[i] = 0.0;
+  __syncthreads();
+  {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + t; j < h1; j += NTC) {
+      const int id = a.hist_ids[j];
+      if (id >= 0 && id < V) atomicOr(&bmH0[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < nwords; i += NTC) bmAll[i] = bmH0[i] | stw[kStBits + i];
+  uint64_t rng = a.rng[row];
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};
+  if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
+  __syncthreads();
+
+  const float* base = a.logits + (int64_t)row * a.ld;
+  const float rpen = 1.0f / c.pen;
+  const int nsw = (mode == kModeList) ? kListWords : kSumWords;
+  const int ch = ((V + NTC - 1) / NTC) | 1;   // corrections: ids [t ch, t ch + ch)
+
+  auto load_step = [&](int s, RowRegsC& R, SumRegsC& Sg) __attribute__((always_inline)) {
+    const uint64_t* sw = reinterpret_cast<const uint64_t*>(sum_hdr(w, a.n_rows, s, row));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) Sg.w[i] = (t + NTC * i < nsw) ? sw[t + NTC * i] : 0ull;
+    if (mode == kModeRow) fetch_row_c(base + (int64_t)s * a.step_stride, V, R);
+  };
+
+  // One step; false when it has to be run exactly (nothing changed then).
+  auto step = [&](int s, RowRegsC& R, SumRegsC& Sg) __attribute__((always_inline)) -> bool {
+    int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
+    if (done) {
+      if (t == 0) *outp = -1;
+      return true;
+    }
+    const float* cur = base + (int64_t)s * a.step_stride;
+    C4S_PHASE(0);
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (t + NTC * i < nsw) cs.sum[t + NTC * i] = Sg.w[i];
+    float* val = vbuf;
+    if (mode == kModeRow) val = store_row_c(cur, V, R, vbuf);
+    C4S_PHASE(1);
+    if (s + 2 < w.s_end) load_step(s + 2, R, Sg);
+    C4S_PHASE(2);
+    __syncthreads();
+    C4S_PHASE(3);
+    StepOut o{0, 0u, 0u, 0u};
+    if (mode == kModeList) {
+      if (wv == 0) {
+        const SumHdr h = hdr_from(cs.sum);
+        const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
+        const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
+        const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
+        const bool ok = list_step(h, e0, e1, c, V, bmAll, bmH0, rng, cs, o);
+        if (lane == 0) {
+          cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
+          cs.bi[3] = (int)o.dex; cs.rng = rng;
+        }
+      }
+    } else {
+      const SumHdr h = hdr_from(cs.sum);
+      double dl = 0.0, el = 0.0;
+      // corrections for ids drawn during the stream (never in H0)
+      if (!(h.flags & 1u) && c.pen_on) {
+        const MassCoef mk = mass_coef(c, h.m0);
+        const bool exm = exact_masses(c);
+        const int lo = min(V, t * ch), hi = min(V, lo + ch);
+        if (lo < hi) {
+          const int w0 = lo >> 5;
+          uint64_t bits = ((uint64_t)(bmAll[w0] & ~bmH0[w0])) | ((uint64_t)(bmAll[w0 + 1] & ~bmH0[w0 + 1]) << 32);
+          bits >>= (lo - 32 * w0);
+          bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
+          while (bits) {
+            const int id = lo + __ffsll((unsigned long long)bits) - 1;
+            bits &= bits - 1;
+            const float x = val[id];
+            double d;
+            if (exm) {
+              d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
+            } else {
+              float er0, er1;
+              const float m_raw = mass_approx(x, mk, er0);
+              const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
+              d = (double)m_raw - (double)m_pen;
+              el += (double)er1;
+            }
+            atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
+            dl += d;
+          }
+        }
+      }
+      dl = wave_sum_f64(dl);
+      el = wave_sum_f64(el);
+      if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
+      __syncthreads();
+      C4S_PHASE(4);
+      if (wv == 0) {
+        double ds = 0.0, de = 0.0;
+        for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
+        const bool ok = row_step(h, c, V, val, bmAll, bmH0, ds, de, rng, cs, o);
+        for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
+        if (lane == 0) {
+          cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
+          cs.bi[3] = (int)o.dex; cs.rng = rng;
+        }
+      }
+    }
+    C4S_PHASE(5);
+    __syncthreads();
+    C4S_PHASE(6);
+    const bool ok = cs.bi[0] != 0;
+    rng = cs.rng;
+    if (!ok) {
+      if (t == 0) acc[0] |= 1u << (20 + (uint32_t)cs.bi[2]);
+      return false;
+    }
+    const int tok = cs.bi[1];
+    if (t == 0) {
+      *outp = tok;
+      acc[0] |= (mode == kModeList ? 32u : 64u) | 1u;
+      acc[2] += (uint32_t)cs.bi[3];
+      acc[3] += (uint32_t)cs.bi[2];
+      // text2semantic.cpp:333-334: the stop token is not appended
+      if (tok != a.stop_token && tok >= 0 && tok < V) bmAll[tok >> 5] |= 1u << (tok & 31);
+    }
+    if (tok == a.stop_token) done = true;
+    __syncthreads();
+    C4S_PHASE(7);
+    return true;
+  };
+
+  RowRegsC RA, RB;
+  SumRegsC SA, SB;
+  load_step(s_first, RA, SA);
+  if (s_first + 1 < w.s_end) load_step(s_first + 1, RB, SB);
+  int s = s_first;
+  bool pending = false;
+  while (s < w.s_end) {
+    if (!step(s, RA, SA)) { pending = true; break; }
+    if (++s >= w.s_end) break;
+    if (!step(s, RB, SB)) { pending = true; break; }
+    ++s;
+  }
+  if (t == 0) {
+    a.rng[row] = rng;
+    stw[kStDone] = done ? 1u : 0u;
+    stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
+    stw[kStNext] = (uint32_t)s;
+    stw[kStPending] = pending ? 1u : 0u;
+  }
+  for (int i = t; i < nwords; i += NTC) stw[kStBits + i] = bmAll[i] & ~bmH0[i];
+}
+
+// ---- repair: the pending step of each row, exactly ------------------------------------
+__global__ __launch_bounds__(NT) void k_stream_repair(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ Scratch sh;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x;
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  if (stw[kStPending] == 0u) return;
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  const int s = (int)stw[kStNext];
+  LdsLayout L = lds_layout(smem, V);
+  const int nwords = bitmap_words(V);
+  for (int i = t; i < nwords; i += NT) L.bitmap[i] = stw[kStBits + i];
+  __syncthreads();
+  {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + t; j < h1; j += NT) {
+      const int id = a.hist_ids[j];
+      if (id >= 0 && id < V) atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+    }
+  }
+  const float* cur = a.logits + (int64_t)row * a.ld + (int64_t)s * a.step_stride;
+  RowFetch f;
+  fetch_row(cur, V, f);
+  float* val = store_row(cur, V, f, L.val);
+  __syncthreads();
+  uint64_t rng = a.rng[row];
+  uint32_t* stp = a.stats ? sh.step_stats : nullptr;
+  const int tok = exact_step(val, L.E, L.bitmap, c, V, sh, rng, stp);
+  if (t == 0) {
+    a.out_tok[(int64_t)s * a.n_rows + row] = tok;
+    if (stp) { stw[1] |= stp[0]; stw[3] += stp[2]; stw[4] += stp[3]; }
+    stw[2] += 1u;
+    // the stop token is not appended (text2semantic.cpp:333-334)
+    if (tok != a.stop_token && tok >= 0 && tok < V) stw[kStBits + (tok >> 5)] |= 1u << (tok & 31);
+    stw[kStDone] = (tok == a.stop_token) ? 1u : 0u;
+    stw[kStNext] = (uint32_t)(s + 1);
+    stw[kStPending] = 0u;
+    a.rng[row] = rng;
+  }
+}
+
+// ---- finisher: every remaining step, exact steps inline -------------------------------
+__global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ Scratch sh;
+  __shared__ ChainSh cs;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  const int mode = stream_mode(c, V);
+  LdsLayout L = lds_layout(smem, V);
+  const int nwords = bitmap_words(V);
+  uint32_t* bmH0 = L.bitmap + nwords;
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  // The fast rounds initialised the state; rows they finished have nothing left.
+  const int s_first = (int)stw[kStNext];
+  if (s_first >= w.s_end) {
+    if (t == 0 && a.stats && w.s_end == a.n_steps)
+      for (int i = 0; i < 4; ++i) a.stats[4 * (int64_t)row + i] = stw[kStStats + i];
+    return;
+  }
+  for (int i = t; i < nwords; i += NT) bmH0[i] = 0u;
+  for (int i = t; i < kMaxChunks; i += NT) cs.cdelta[i] = 0.0;
+  __syncthreads();
+  {
+    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int64_t j = h0 + t; j < h1; j += NT) {
+      const int id = a.hist_ids[j];
+      if (id >= 0 && id < V) atomicOr(&bmH0[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < nwords; i += NT) L.bitmap[i] = bmH0[i] | stw[kStBits + i];
+  uint64_t rng = a.rng[row];
+  bool done = stw[kStDone] != 0u;
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};
+  if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
+  __syncthreads();
+  const float* base = a.logits + (int64_t)row * a.ld;
+  const float rpen = 1.0f / c.pen;
+  // Summary of the next step in flight as vector loads (barriers do not wait
+  // for them): list rows, wave 0, three words per lane of the header and the
+  // small list; full-vocabulary rows, one word per thread of the whole summary.
+  uint64_t pw0 = 0, pw1 = 0, pw2 = 0;
+  auto load_sum = [&](int s) {
+    const uint64_t* sw = reinterpret_cast<const uint64_t*>(sum_hdr(w, a.n_rows, s, row));
+    if (mode == kModeList) {
+      if (wv == 0) {
+        pw0 = sw[lane];
+        pw1 = sw[lane + kWave];
+        if (lane + 2 * kWave < kListWords) pw2 = sw[lane + 2 * kWave];
+      }
+    } else if (t < kSumWords) {
+      pw0 = sw[t];
+    }
+  };
+  auto stage_sum = [&]() {
+    if (mode == kModeList) {
+      if (wv == 0) {
+        cs.sum[lane] = pw0;
+        cs.sum[lane + kWave] = pw1;
+        if (lane + 2 * kWave < kListWords) cs.sum[lane + 2 * kWave] = pw2;
+        wave_sync();
+      }
+    } else if (t < kSumWords) {
+      cs.sum[t] = pw0;
+    }
+  };
+  const bool summaries = mode != kModeExact;
+  if (summaries) load_sum(s_first);
+
+  // fetch of the raw row of step s (full-vocabulary and exact rows)
+  RowFetch pf;
+  const bool stream_rows = mode != kModeList;
+  if (stream_rows && !done) fetch_row(base + (int64_t)s_first * a.step_stride, V, pf);
+
+  for (int s = s_first; s < w.s_end; ++s) {
+    int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
+    if (done) {
+      if (t == 0) *outp = -1;
+      continue;
+    }
+    const float* cur = base + (int64_t)s * a.step_stride;
+    float* val = L.val;
+    if (stream_rows) {
+      val = store_row(cur, V, pf, L.val);
+      if (mode == kModeRow && s + 1 < w.s_end) fetch_row(cur + a.step_stride, V, pf);
+    }
+    if (summaries) stage_sum();
+    uint32_t pbits = 0;
+    StepOut o{0, 0u, 0u, 0u};
+    if (mode == kModeList) {
+      if (wv == 0) {
+        const SumHdr h = hdr_from(cs.sum);
+        const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
+        const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
+        const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
+        const bool ok = list_step(h, e0, e1, c, V, L.bitmap, bmH0, rng, cs, o);
+        if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
+      }
+      pbits = 32u;
+      __syncthreads();
+    } else if (mode == kModeRow) {
+      __syncthreads();   // row and summary in LDS
+      const SumHdr h = hdr_from(cs.sum);
+      const uint32_t hflags = h.flags;
+      const float hm0 = h.m0;
+      const int hhead = h.head, hnch = h.nchunk;
+      // corrections for ids drawn during the stream (never in H0)
+      double dl = 0.0, el = 0.0;
+      if (!(hflags & 1u) && c.pen_on) {
+        const MassCoef mk = mass_coef(c, hm0);
+        const bool exm = exact_masses(c);
+        const int ch = odd_chunk(V);
+        const int lo = min(V, t * ch), hi = min(V, lo + ch);
+        if (lo < hi) {
+          const int w0 = lo >> 5;
+          uint64_t bits = ((uint64_t)(L.bitmap[w0] & ~bmH0[w0])) |
+                          ((uint64_t)(L.bitmap[w0 + 1] & ~bmH0[w0 + 1]) << 32);
+          bits >>= (lo - 32 * w0);
+          bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
+          while (bits) {
+            const int id = lo + __ffsll((unsigned long long)bits) - 1;
+            bits &= bits - 1;
+            const float x = val[id];
+            double d;
+            if (exm) {
+              d = mass_exact(x, c, hm0) - mass_exact(pen_exact(x, c.pen), c, hm0);
+            } else {
+              float er0, er1;
+              const float m_raw = mass_approx(x, mk, er0);
+              const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
+              d = (double)m_raw - (double)m_pen;
+              el += (double)er1;
+            }
+            atomicAdd(&cs.cdelta[chunk_of(id, hhead, hnch)], d);
+            dl += d;
+          }
+        }
+      }
+      dl = wave_sum_f64(dl);
+      el = wave_sum_f64(el);
+      if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
+      __syncthreads();
+      if (wv == 0) {
+        double ds = 0.0, de = 0.0;
+        for (int i = 0; i < NW; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
+        const bool ok = row_step(h, c, V, val, L.bitmap, bmH0, ds, de, rng, cs, o);
+        for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
+        if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
+      }
+      pbits = 64u;
+      __syncthreads();
+    } else {
+      if (t == 0) { cs.bi[0] = 0; cs.rng = rng; }
+      __syncthreads();
+    }
+    const bool ok = cs.bi[0] != 0;
+    rng = cs.rng;
+    if (summaries && s + 1 < w.s_end) load_sum(s + 1);
+    int tok = 0;
+    uint32_t stq[4] = {0u, 0u, 0u, 0u};
+    if (ok) {
+      tok = cs.bi[1];
+      stq[0] = pbits | 1u;
+      stq[2] = (uint32_t)cs.bi[3];
+      stq[3] = (uint32_t)cs.bi[2];
+    } else {
+      if (t == 0 && mode != kModeExact) acc[0] |= 1u << (20 + (uint32_t)cs.bi[2]);
+      if (mode == kModeList) {   // the row was not staged: fetch it now
+        RowFetch f1;
+        fetch_row(cur, V, f1);
+        val = store_row(cur, V, f1, L.val);
+      }
+      __syncthreads();
+      uint32_t* stp = a.stats ? sh.step_stats : nullptr;
+      tok = exact_step(val, L.E, L.bitmap, c, V, sh, rng, stp);
+      if (t == 0) {
+        if (stp) { stq[0] = stp[0]; stq[2] = stp[2]; stq[3] = stp[3]; }
+        stq[1] = (mode == kModeExact) ? 0u : 1u;
+      }
+      // the prefetched row is not kept across the exact step (register pressure)
+      if (stream_rows && s + 1 < w.s_end) fetch_row(cur + a.step_stride, V, pf);
+    }
+    if (t == 0) {
+      *outp = tok;
+      acc[0] |= stq[0];
+      acc[1] += stq[1];
+      acc[2] += stq[2];
+      acc[3] += stq[3];
+      // text2semantic.cpp:333-334: the stop token is not appended
+      if (tok != a.stop_token && tok >= 0 && tok < V) L.bitmap[tok >> 5] |= 1u << (tok & 31);
+    }
+    if (tok == a.stop_token) done = true;
+    __syncthreads();
+  }
+  if (t == 0) {
+    a.rng[row] = rng;
+    stw[kStDone] = done ? 1u : 0u;
+    stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
+    stw[kStNext] = (uint32_t)w.s_end;
+    stw[kStPending] = 0u;
+    if (a.stats && w.s_end == a.n_steps) {
+      uint32_t* o = a.stats + 4 * (int64_t)row;
+      o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
+    }
+  }
+  for (int i = t; i < nwords; i += NT) stw[kStBits + i] = L.bitmap[i] & ~bmH0[i];
+}
+
+}  // namespace
+
+size_t stream_chain_lds_bytes(int V) {
+  return rows_lds_bytes(V) + 4 * (size_t)bitmap_words(V);
+}
+
+hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  const int steps = w.s_end - w.s_begin;
+  const dim3 grid((unsigned)((steps + w.steps_per_group - 1) / w.steps_per_group), (unsigned)a.n_rows);
+  const int nq_max = a.vocab >> 2;
+  if (nq_max <= 2 * NTA)
+    hipLaunchKernelGGL(k_stream_scan<2>, grid, dim3(NTA), 0, s, a, w);
+  else if (nq_max <= 8 * NTA)
+    hipLaunchKernelGGL(k_stream_scan<8>, grid, dim3(NTA), 0, s, a, w);
+  else
+    hipLaunchKernelGGL(k_stream_scan<12>, grid, dim3(NTA), 0, s, a, w);
+  return hipGetLastError();
+}
+
+size_t stream_fast_lds_bytes(int V) {
+  return 4 * ((size_t)vpad(V) + 4) + 8 * (size_t)bitmap_words(V);
+}
+
+hipError_t launch_stream_fast(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_fast, dim3(a.n_rows), dim3(NTC), stream_fast_lds_bytes(a.vocab), s, a, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_repair, dim3(a.n_rows), dim3(NT), rows_lds_bytes(a.vocab), s, a, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_chain, dim3(a.n_rows), dim3(NT), stream_chain_lds_bytes(a.vocab), s, a, w);
+  return hipGetLastError();
+}
+
+}  // namespace c4s

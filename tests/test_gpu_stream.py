@@ -9,7 +9,7 @@ from gpu_util import dev
 pytestmark = pytest.mark.gpu
 
 
-def run_stream(ctx, p, x, stop_token=-1):
+def run_stream(ctx, p, x, stop_token=-1, sequential=False):
     import torch
     steps, rows, V = x.shape
     out = torch.full((steps, rows), -9, dtype=torch.int32, device="cuda")
@@ -18,7 +18,7 @@ def run_stream(ctx, p, x, stop_token=-1):
     ctx.sample_stream(dev(x, torch), dev(p["hist_ids"], torch), dev(p["hist_off"], torch),
                       dev(p["temp"], torch), dev(p["top_k"], torch), dev(p["top_p"], torch),
                       dev(p["pen"], torch), rng, out, do_sample=dev(p["do_sample"], torch),
-                      stop_token=stop_token, out_stats=st)
+                      stop_token=stop_token, out_stats=st, sequential=sequential)
     torch.cuda.synchronize()
     return out.cpu().numpy(), rng.cpu().numpy().view(np.uint64), st.cpu().numpy()
 
@@ -38,9 +38,59 @@ def test_stream_10k_rows_bit_exact(orc):
     bad = np.argwhere(toks != otoks)
     assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
     assert np.array_equal(rng, orng)
-    print("rows", toks.size, "exact top_p passes", int(st[:, 1].sum()),
-          "exact draws", int(st[:, 2].sum()))
+    print("rows", toks.size, "exact steps", int(st[:, 1].sum()), "exact draws", int(st[:, 2].sum()))
+    assert int(st[:, 1].sum()) < toks.size // 50      # the candidate summaries decide almost every step
     ctx.close()
+
+
+def _mixed_params(seed, rows, V):
+    """Every row mode of the two-phase stream: greedy, top-k (list), top-k > 64
+    and penalty < 1 (exact every step), full vocabulary with p < 1, p = 1, p > 1
+    and p <= 0 (chunk masses)."""
+    p = W.batch64_params(seed=seed, rows=rows, V=V)
+    g = np.random.default_rng(seed)
+    kinds = np.resize(np.arange(10), rows)
+    g.shuffle(kinds)
+    for r, kd in enumerate(kinds):
+        if kd == 0:
+            p["do_sample"][r] = 0
+        elif kd == 1:
+            p["top_k"][r] = g.choice([1, 5, 30, 64])
+        elif kd == 2:
+            p["top_k"][r] = 100
+        elif kd == 3:
+            p["pen"][r] = 0.7
+        elif kd in (4, 5):
+            p["top_k"][r] = 0
+            p["top_p"][r] = g.choice([0.3, 0.8, 0.95, 0.999])
+        elif kd == 6:
+            p["top_k"][r], p["top_p"][r] = 0, 1.0
+        elif kd == 7:
+            p["top_k"][r], p["top_p"][r] = 0, 1.5
+        elif kd == 8:
+            p["top_k"][r], p["top_p"][r] = 0, 0.0
+        else:
+            p["top_k"][r], p["temp"][r] = V, 1.0
+        if g.random() < 0.5:
+            p["pen"][r] = 1.0 if p["pen"][r] != 0.7 else 0.7
+    return p
+
+
+@pytest.mark.parametrize("V,rows,steps", [(8194, 40, 60), (1000, 30, 80), (37, 20, 50), (3000, 25, 70)])
+def test_stream_two_phase_all_modes(orc, gpu_ctx, V, rows, steps):
+    p = _mixed_params(V + rows, rows, V)
+    x = W.batch64_logits(V + 7, steps, rows, V)
+    print(f"two-phase V={V} rows={rows} steps={steps}", flush=True)
+    toks, rng, st = run_stream(gpu_ctx, p, x, stop_token=V - 1)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
+                                    p["top_p"], p["pen"], p["do_sample"], p["rng"], stop_token=V - 1,
+                                    n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
+    assert np.array_equal(rng, orng)
+    stoks, srng, _ = run_stream(gpu_ctx, p, x, stop_token=V - 1, sequential=True)
+    assert np.array_equal(stoks, toks) and np.array_equal(srng, rng)
+    print("exact steps per row", st[:, 1].tolist())
 
 
 def test_stream_stop_token_and_greedy(orc, gpu_ctx):
