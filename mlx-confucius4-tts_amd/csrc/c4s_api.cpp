@@ -33,6 +33,9 @@ struct c4s_ctx {
   size_t sum_bytes = 0;
   void* state_ws = nullptr;
   size_t state_bytes = 0;
+  // second stream: the two fast chain kernels run side by side
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -183,8 +186,11 @@ int c4s_create(int device, c4s_ctx** out) {
     delete ctx;
     return C4S_EINVAL;
   }
-  if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess) {
-    delete ctx;
+  if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess) {
+    c4s_destroy(ctx);
     return C4S_EHIP;
   }
   *out = ctx;
@@ -195,9 +201,13 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (!ctx) return C4S_OK;
   DeviceGuard g(ctx->device);
   if (ctx->host_stream) (void)hipStreamSynchronize(ctx->host_stream);
-  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage})
+  if (ctx->side) (void)hipStreamSynchronize(ctx->side);
+  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws})
     if (p) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
+  if (ctx->side) (void)hipStreamDestroy(ctx->side);
+  if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
+  if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
   delete ctx;
   return C4S_OK;
 }
@@ -276,8 +286,22 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     // runs that step exactly; the finisher completes whatever is left.
     for (int r = 0; r < kFastRounds; ++r) {
       w.round = r;
-      e = c4s::launch_stream_fast(a, w, hs);
-      if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream fast launch");
+      if (r == 0) {   // list rows here, full-vocabulary rows on the side stream, side by side
+        if ((e = hipEventRecord(ctx->ev_fork, hs)) != hipSuccess ||
+            (e = hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0)) != hipSuccess)
+          return hip_fail(ctx, e, "sample_stream fork");
+        e = c4s::launch_stream_rowk(a, w, ctx->side);
+        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream row-chain launch");
+        e = c4s::launch_stream_list(a, w, hs);
+        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream list-chain launch");
+        if ((e = hipEventRecord(ctx->ev_join, ctx->side)) != hipSuccess ||
+            (e = hipStreamWaitEvent(hs, ctx->ev_join, 0)) != hipSuccess)
+          return hip_fail(ctx, e, "sample_stream join");
+      } else {
+        e = c4s::launch_stream_list(a, w, hs);
+        if (e == hipSuccess) e = c4s::launch_stream_rowk(a, w, hs);
+        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
+      }
       e = c4s::launch_stream_repair(a, w, hs);
       if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream repair launch");
     }

@@ -164,6 +164,38 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, __uint_as_float(dpp_u32<0x143, 0xC>(u, u)));
   return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
 }
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = max(v, dpp_u32<0x111>(v, v));
+  v = max(v, dpp_u32<0x112>(v, v));
+  v = max(v, dpp_u32<0x114>(v, v));
+  v = max(v, dpp_u32<0x118>(v, v));
+  v = max(v, dpp_u32<0x142, 0xA>(v, v));
+  v = max(v, dpp_u32<0x143, 0xC>(v, v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+// Max of 64-bit keys over the wave (the same pattern on (hi, lo) pairs).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  const uint32_t olo = dpp_u32<CTRL, ROW_MASK>(lo, lo), ohi = dpp_u32<CTRL, ROW_MASK>(hi, hi);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > v ? o : v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  v = dpp_max_u64_step<0x111>(v);
+  v = dpp_max_u64_step<0x112>(v);
+  v = dpp_max_u64_step<0x114>(v);
+  v = dpp_max_u64_step<0x118>(v);
+  v = dpp_max_u64_step<0x142, 0xA>(v);
+  v = dpp_max_u64_step<0x143, 0xC>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Lane i receives lane i + 1 (wave_shl:1); lane 63 receives `fill`.
+__device__ __forceinline__ uint32_t wave_next_u32(uint32_t v, uint32_t fill) {
+  return dpp_u32<0x130>(v, fill);
+}
 __device__ __forceinline__ double wave_sum_dpp(double v) {
   v = wave_scan_f64(v);
   const uint64_t b = __double_as_longlong(v);

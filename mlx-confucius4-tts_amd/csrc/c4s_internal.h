@@ -116,7 +116,8 @@ size_t stream_lds_bytes(int vocab, int unused);
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
-hipError_t launch_stream_fast(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);

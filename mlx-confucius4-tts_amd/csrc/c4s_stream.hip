@@ -77,15 +77,16 @@ __device__ __forceinline__ uint32_t ent_key(uint64_t e) { return (uint32_t)(e >>
 __device__ __forceinline__ int ent_id(uint64_t e) { return 16383 - (int)(((uint32_t)e >> 10) & 16383u); }
 __device__ __forceinline__ int ent_rank(uint64_t e) { return (int)((uint32_t)e & 1023u); }
 
-__device__ __forceinline__ const SumHdr* sum_hdr(const StreamWs& w, int n_rows, int s, int row) {
-  return reinterpret_cast<const SumHdr*>(w.sum + ((size_t)(s - w.s_begin) * n_rows + row) * kSumStride);
-}
-__device__ __forceinline__ const uint64_t* sum_list(const SumHdr* h) {
-  return reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(h) + kSumHdrBytes);
-}
-__device__ __forceinline__ const double* sum_chunks(const SumHdr* h) {
-  return reinterpret_cast<const double*>(reinterpret_cast<const unsigned char*>(h) + kSumHdrBytes +
-                                         8 * kListLarge);
+// Summary words: list entries [0, kListLarge), header [kHdrW, kHdrW + 8),
+// chunk masses from kChunkW. List entry i sits in lane i % 64 of a wave's
+// i / 64-th load, so list rows read their entries straight into registers.
+constexpr int kHdrW = kListLarge;
+constexpr int kChunkW = kListLarge + kSumHdrBytes / 8;
+constexpr int kSumWords = kChunkW + kMaxChunks;
+static_assert((size_t)kSumWords * 8 <= kSumStride, "summary fits its stride");
+
+__device__ __forceinline__ const uint64_t* sum_words(const StreamWs& w, int n_rows, int s, int row) {
+  return reinterpret_cast<const uint64_t*>(w.sum + ((size_t)(s - w.s_begin) * n_rows + row) * kSumStride);
 }
 
 // Approximate masses: exp(fl(y/T) - m0) as exp2(y*a - b) (v_exp_f32). Against
@@ -205,6 +206,10 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
   const int row = blockIdx.y;
   const int V = a.vocab;
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (w.s_begin == 0 && blockIdx.x == 0) {   // the chain kernels' per-row state starts clear
+    uint32_t* stw = w.state + (size_t)row * kStateWords;
+    for (int i = threadIdx.x; i < kStateWords; i += NTA) stw[i] = 0u;
+  }
   const int mode = stream_mode(c, V);
   if (mode == kModeExact) return;
   const int s0 = w.s_begin + (int)blockIdx.x * w.steps_per_group;
@@ -369,9 +374,10 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
     if (!overflow && (int)n_all > cap) tout = max(tout, ent_key(sh.cand[cap]));
     const bool bad = overflow || n == 0;
 
-    SumHdr* hdr = reinterpret_cast<SumHdr*>(w.sum + ((size_t)(s - w.s_begin) * a.n_rows + row) * kSumStride);
-    uint64_t* lst = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(hdr) + kSumHdrBytes);
-    double* chk = reinterpret_cast<double*>(reinterpret_cast<unsigned char*>(hdr) + kSumHdrBytes + 8 * kListLarge);
+    uint64_t* sw = reinterpret_cast<uint64_t*>(w.sum + ((size_t)(s - w.s_begin) * a.n_rows + row) * kSumStride);
+    uint64_t* lst = sw;
+    SumHdr* hdr = reinterpret_cast<SumHdr*>(sw + kHdrW);
+    double* chk = reinterpret_cast<double*>(sw + kChunkW);
     if (!bad)
       for (int i = t; i < n; i += NTA) lst[i] = sh.cand[i];
 
@@ -460,8 +466,6 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
 
 // ---- chain (one workgroup per row) ----------------------------------------------------
 
-constexpr int kSumWords = (kSumHdrBytes + 8 * kListLarge + 8 * kMaxChunks) / 8;
-constexpr int kListWords = (kSumHdrBytes + 8 * kListSmall) / 8;   // header + small list
 
 struct ChainSh {
   uint64_t sum[kSumWords];   // this step's summary: header words, list, chunks
@@ -569,9 +573,8 @@ __device__ __forceinline__ void clear_slots(ChainSh& cs, int nslot) {
   wave_sync();
 }
 
-__device__ __forceinline__ SumHdr hdr_from(const uint64_t* sw) {
+__device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w2, uint64_t w3) {
   SumHdr h{};
-  const uint64_t w0 = sw[0], w1 = sw[1], w2 = sw[2], w3 = sw[3];
   h.n = (int)(uint32_t)w0;
   h.tout = (uint32_t)(w0 >> 32);
   h.flags = (uint32_t)w1;
@@ -580,6 +583,17 @@ __device__ __forceinline__ SumHdr hdr_from(const uint64_t* sw) {
   h.head = (int)(uint32_t)(w2 >> 32);
   h.err = __longlong_as_double((long long)w3);
   return h;
+}
+__device__ __forceinline__ SumHdr hdr_from(const uint64_t* sw) {   // sw: summary words (LDS)
+  return hdr_words(sw[kHdrW], sw[kHdrW + 1], sw[kHdrW + 2], sw[kHdrW + 3]);
+}
+// Header held in lanes 0..3 of a wave's register `hw` (word kHdrW + lane).
+__device__ __forceinline__ SumHdr hdr_lanes(uint64_t hw) {
+  auto rl = [&](int l) -> uint64_t {
+    return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)hw, l) |
+           ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(hw >> 32), l) << 32);
+  };
+  return hdr_words(rl(0), rl(1), rl(2), rl(3));
 }
 
 struct StepOut {
@@ -605,8 +619,7 @@ enum : uint32_t {
 // Candidate-list step for greedy and top-k rows (wave 0; two entries per lane).
 // Returns false (nothing changed) when a decision needs the exact step.
 __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCfg& c, int V,
-                          const uint32_t* bmAll, const uint32_t* bmH0, uint64_t& rng, ChainSh& cs,
-                          StepOut& o) {
+                          const uint32_t* bmN, uint64_t& rng, ChainSh& cs, StepOut& o) {
   const int lane = lane_id();
   o.why = kWhySummary;
   if (h.flags & 1u) return false;
@@ -614,21 +627,19 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   const float ninf = neg_inf();
   const bool v0 = lane < n, v1 = lane + kWave < n;
   const int id0 = ent_id(e0), id1 = ent_id(e1);
-  const bool h0 = c.pen_on && v0 && bit_of(bmAll, id0) && !bit_of(bmH0, id0);
-  const bool h1 = c.pen_on && v1 && bit_of(bmAll, id1) && !bit_of(bmH0, id1);
+  const bool h0 = c.pen_on && v0 && bit_of(bmN, id0);
+  const bool h1 = c.pen_on && v1 && bit_of(bmN, id1);
   const float yr0 = v0 ? kfloat(ent_key(e0)) : ninf, yr1 = v1 ? kfloat(ent_key(e1)) : ninf;
   const float y0 = h0 ? pen_exact(yr0, c.pen) : yr0;
   const float y1 = h1 ? pen_exact(yr1, c.pen) : yr1;
 
-  if (c.greedy) {   // text2semantic.cpp:144-145, argmax of the penalised row
-    float bv = ninf;
-    int bi = INT_MAX;
-    if (v0) argmax_merge(bv, bi, y0, id0);
-    if (v1) argmax_merge(bv, bi, y1, id1);
-    wave_argmax(bv, bi);
+  if (c.greedy) {   // text2semantic.cpp:144-145, argmax of the penalised row, first max wins
+    const uint64_t k0 = v0 ? ((uint64_t)fkey(y0) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id0) : 0ull;
+    const uint64_t k1 = v1 ? ((uint64_t)fkey(y1) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id1) : 0ull;
+    const uint64_t kb = wave_max_u64_dpp(k0 > k1 ? k0 : k1);
     o.why = kWhyBound;
-    if (bi == INT_MAX || !(fkey(bv) > h.tout)) return false;
-    o.tok = bi;
+    if (kb == 0ull || !((uint32_t)(kb >> 32) > h.tout)) return false;
+    o.tok = (int)(0xFFFFFFFFu - (uint32_t)kb);
     o.kept = 1;
     o.dex = 0;
     return true;
@@ -676,8 +687,8 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   const int sl = sv ? cs.lslot[lane] : 0;
   {
     // equal quotients of different values must still be in id order
-    const float zn = __shfl_down(zs, 1, kWave);
-    const int idn = __shfl_down(ids, 1, kWave);
+    const float zn = __uint_as_float(wave_next_u32(__float_as_uint(zs), 0u));
+    const int idn = (int)wave_next_u32((uint32_t)ids, 0u);
     if (__ballot(sv && lane + 1 < nsurv && zs == zn && ids > idn)) return false;
   }
   // masses, top_p (sampling.cpp:52-65), min_keep (:67-68)
@@ -705,7 +716,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   const long long lim = (long long)V - (long long)c.min_keep < 0 ? 0 : (long long)V - (long long)c.min_keep;
   const long long m = (long long)V - (R < lim ? R : lim);
   const bool kept = sv && (long long)lane < m;
-  const int nslot = (int)wave_max_u32(kept ? (uint32_t)(sl + 1) : 0u);
+  const int nslot = (int)wave_max_u32_dpp(kept ? (uint32_t)(sl + 1) : 0u);
   clear_slots(cs, nslot);
   if (kept) { cs.slotE[sl] = e; cs.slotId[sl] = ids; }
   wave_sync();
@@ -720,14 +731,14 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
 // per-chunk corrections for ids drawn during the stream (cs.cdelta, their sum
 // dsum and error derr) and the raw row in LDS (`val`).
 __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
-                         const uint32_t* bmAll, const uint32_t* bmH0, double dsum, double derr,
+                         const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
                          uint64_t& rng, ChainSh& cs, StepOut& o) {
   const int lane = lane_id();
   o.why = kWhySummary;
   if (h.flags & 1u) return false;
   const int n = h.n;
   const float ninf = neg_inf();
-  const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
+  const uint64_t* lst = cs.sum;
   // unhit entries compacted in rank order; largest penalised hit value
   int nu = 0;
   float hm = ninf;
@@ -736,7 +747,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
     const bool v = pos < n;
     const uint64_t e = v ? lst[pos] : 0ull;
     const int id = ent_id(e);
-    const bool hit = c.pen_on && v && bit_of(bmAll, id) && !bit_of(bmH0, id);
+    const bool hit = c.pen_on && v && bit_of(bmN, id);
     const float yr = v ? kfloat(ent_key(e)) : ninf;
     const float y = hit ? pen_exact(yr, c.pen) : yr;
     const bool u = v && !hit;
@@ -772,9 +783,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ci = 4 * lane + i;
-    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cs.sum[kSumHdrBytes / 8 + kListLarge + ci]) -
-                                cs.cdelta[ci]
-                          : 0.0;
+    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cs.sum[kChunkW + ci]) - cs.cdelta[ci] : 0.0;
     cs_l += cv[i];
   }
   const double rho = exp((double)h.m0 - (double)mt);
@@ -836,7 +845,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
       const int rkk = b + lane;
       nslot = max(nslot, rkk < q ? cs.lslot[rkk] + 1 : 0);
     }
-    nslot = (int)wave_max_u32((uint32_t)nslot);
+    nslot = (int)wave_max_u32_dpp((uint32_t)nslot);
     clear_slots(cs, nslot);
     double smin = 1.0;
     for (int b = 0; b < q; b += kWave) {
@@ -883,7 +892,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
   const int ia = lo + lane, ib = lo + kWave + lane;
   auto mass_at = [&](int id) -> double {
     const float x = val[id];
-    const float y = bit_of(bmAll, id) ? pen_exact(x, c.pen) : x;
+    const float y = (c.pen_on && (bit_of(bmH0, id) || bit_of(bmN, id))) ? pen_exact(x, c.pen) : x;
     const float z = c.temp_on ? y / c.temp : y;
     return (z == ninf) ? 0.0 : exp((double)(z - mt));
   };
@@ -936,17 +945,145 @@ __device__ __forceinline__ int exact_step(float* val, double* E, const uint32_t*
 }
 
 
-// ---- fast chain: candidate steps only, 256 threads per row ------------------------------
+// ---- fast chain kernels: candidate steps only -------------------------------------------
 //
-// No exact code here (its register demand would spill the hot loop): a step it
-// cannot decide marks the row pending and ends the row's pass; the repair
-// kernel then runs that one step exactly and the next pass resumes. The
-// summary and (full-vocabulary rows) the raw row of step s + 2 are in flight in
-// registers while step s runs.
+// No exact code here (its register demand would spill the hot loops): a step
+// they cannot decide marks the row pending and ends the row's pass; the repair
+// kernel then runs that one step exactly and the next pass resumes. Greedy and
+// top-k rows need only their candidate list: one wavefront per row, no
+// barriers, summaries four steps ahead in registers. Full-vocabulary rows also
+// stream their raw row for the corrections: four wavefronts per row.
+
+// State load shared by both: returns false when the row has nothing to do in
+// this pass (pending, finished, or stopped; a stopped row reports -1 for the
+// rest of the chunk, text2semantic.cpp:304).
+__device__ __forceinline__ bool fast_begin(const StreamArgs& a, const StreamWs& w, int row, int nthr,
+                                           int& s_first) {
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  s_first = (int)stw[kStNext];
+  if (stw[kStPending] != 0u || s_first >= w.s_end) return false;
+  if (stw[kStDone] != 0u) {
+    for (int s = s_first + (int)threadIdx.x; s < w.s_end; s += nthr) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
+    if (threadIdx.x == 0) stw[kStNext] = (uint32_t)w.s_end;
+    return false;
+  }
+  return true;
+}
+
+// H0 bitmap from the history and the bitmap of ids drawn during the stream
+// (kept in the state without H0 ids).
+__device__ __forceinline__ void fast_bitmaps(const StreamArgs& a, const uint32_t* stw, int row, int V,
+                                             int nthr, uint32_t* bmH0, uint32_t* bmN, bool block) {
+  const int nwords = bitmap_words(V);
+  for (int i = threadIdx.x; i < nwords; i += nthr) bmH0[i] = 0u;
+  if (block) __syncthreads(); else wave_sync();
+  const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+  for (int64_t j = h0 + threadIdx.x; j < h1; j += nthr) {
+    const int id = a.hist_ids[j];
+    if (id >= 0 && id < V) atomicOr(&bmH0[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+  }
+  if (block) __syncthreads(); else wave_sync();
+  for (int i = threadIdx.x; i < nwords; i += nthr) bmN[i] = stw[kStBits + i] & ~bmH0[i];
+  if (block) __syncthreads(); else wave_sync();
+}
+
+__device__ __forceinline__ void fast_end(const StreamArgs& a, const StreamWs& w, int row, int V, int nthr,
+                                         int s, bool pending, bool done, uint64_t rng, const uint32_t* acc,
+                                         const uint32_t* bmN) {
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  if (threadIdx.x == 0) {
+    a.rng[row] = rng;
+    stw[kStDone] = done ? 1u : 0u;
+    stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
+    stw[kStNext] = (uint32_t)s;
+    stw[kStPending] = pending ? 1u : 0u;
+  }
+  const int nwords = bitmap_words(V);
+  for (int i = threadIdx.x; i < nwords; i += nthr) stw[kStBits + i] = bmN[i];
+}
+
+struct ListRegs {
+  uint64_t e0, e1, hw;   // entries lane and lane + 64, header word lane (lanes < 8)
+};
+
+__global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w) {
+  __shared__ ChainSh cs;
+  __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int lane = lane_id();
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (stream_mode(c, V) != kModeList) return;
+  int s_first;
+  if (!fast_begin(a, w, row, kWave, s_first)) return;
+  const uint32_t* stw = w.state + (size_t)row * kStateWords;
+  fast_bitmaps(a, stw, row, V, kWave, bmH0, bmN, false);
+  uint64_t rng = a.rng[row];
+  uint32_t acc[4] = {stw[1], stw[2], stw[3], stw[4]};
+  bool done = false;
+
+  auto load = [&](int s, ListRegs& r) __attribute__((always_inline)) {
+    const uint64_t* sw = sum_words(w, a.n_rows, s, row);
+    r.e0 = sw[lane];
+    r.e1 = sw[lane + kWave];
+    r.hw = (lane < 8) ? sw[kHdrW + lane] : 0ull;
+  };
+  // One step; false when it has to be run exactly (nothing changed then).
+  auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) -> bool {
+    int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
+    if (done) {
+      if (lane == 0) *outp = -1;
+      return true;
+    }
+    const SumHdr h = hdr_lanes(r.hw);
+    const uint64_t e0 = (lane < h.n) ? r.e0 : 0ull;
+    const uint64_t e1 = (lane + kWave < h.n) ? r.e1 : 0ull;
+    if (s + 4 < w.s_end) load(s + 4, r);
+    StepOut o{0, 0u, 0u, 0u};
+    const bool ok = list_step(h, e0, e1, c, V, bmN, rng, cs, o);
+    if (!ok) {
+      if (lane == 0) acc[0] |= 1u << (20 + o.why);
+      return false;
+    }
+    const int tok = o.tok;
+    if (lane == 0) {
+      *outp = tok;
+      acc[0] |= 32u | 1u;
+      acc[2] += o.dex;
+      acc[3] += o.kept;
+      // text2semantic.cpp:333-334: the stop token is not appended
+      if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
+        bmN[tok >> 5] |= 1u << (tok & 31);
+    }
+    wave_sync();
+    if (tok == a.stop_token) done = true;
+    return true;
+  };
+
+  ListRegs P0{}, P1{}, P2{}, P3{};
+  load(s_first, P0);
+  if (s_first + 1 < w.s_end) load(s_first + 1, P1);
+  if (s_first + 2 < w.s_end) load(s_first + 2, P2);
+  if (s_first + 3 < w.s_end) load(s_first + 3, P3);
+  int s = s_first;
+  bool pending = false;
+  while (s < w.s_end) {
+    if (!step(s, P0)) { pending = true; break; }
+    if (++s >= w.s_end) break;
+    if (!step(s, P1)) { pending = true; break; }
+    if (++s >= w.s_end) break;
+    if (!step(s, P2)) { pending = true; break; }
+    if (++s >= w.s_end) break;
+    if (!step(s, P3)) { pending = true; break; }
+    ++s;
+  }
+  fast_end(a, w, row, V, kWave, s, pending, done, rng, acc, bmN);
+}
+
 constexpr int NTC = 256;
 constexpr int NWC = NTC / kWave;
 constexpr int kQuadsC = kLdsVocabMax / 4 / NTC;
-static_assert(kQuadsC * 4 * NTC == kLdsVocabMax, "fast chain row fetch covers the LDS rows");
+static_assert(kQuadsC * 4 * NTC == kLdsVocabMax, "row fetch covers the LDS rows");
 
 struct RowRegsC {
   float4 q[kQuadsC];
@@ -983,63 +1120,36 @@ __device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRe
   return val;
 }
 
-__global__ __launch_bounds__(NTC) void k_stream_fast(StreamArgs a, StreamWs w) {
+__global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ ChainSh cs;
+  __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
   const int row = blockIdx.x;
   const int V = a.vocab;
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
-  uint32_t* stw = w.state + (size_t)row * kStateWords;
-  if (w.round == 0 && w.s_begin == 0) {
-    for (int i = t; i < kStateWords; i += NTC) stw[i] = 0u;
-    __syncthreads();
-  }
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
-  const int mode = stream_mode(c, V);
-  if (mode == kModeExact) return;   // the finisher runs these rows
-  const int s_first = (int)stw[kStNext];
-  if (stw[kStPending] != 0u || s_first >= w.s_end) return;
-  bool done = stw[kStDone] != 0u;
-  if (done) {   // a stopped row reports -1 (text2semantic.cpp:304)
-    for (int s = s_first + t; s < w.s_end; s += NTC) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
-    if (t == 0) stw[kStNext] = (uint32_t)w.s_end;
-    return;
-  }
-  const int nwords = bitmap_words(V);
-  float* vbuf = reinterpret_cast<float*>(smem);
-  uint32_t* bmAll = reinterpret_cast<uint32_t*>(vbuf + vpad(V) + 4);
-  uint32_t* bmH0 = bmAll + nwords;
-  for (int i = t; i < nwords; i += NTC) bmH0[i] = 0u;
+  if (stream_mode(c, V) != kModeRow) return;
+  int s_first;
+  if (!fast_begin(a, w, row, NTC, s_first)) return;
+  const uint32_t* stw = w.state + (size_t)row * kStateWords;
   for (int i = t; i < kMaxChunks; i += NTC) cs.cdelta[i] = 0.0;
-  __syncthreads();
-  {
-    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-    for (int64_t j = h0 + t; j < h1; j += NTC) {
-      const int id = a.hist_ids[j];
-      if (id >= 0 && id < V) atomicOr(&bmH0[id >> 5], 1u << (id & 31));   // sampling.cpp:24
-    }
-  }
-  __syncthreads();
-  for (int i = t; i < nwords; i += NTC) bmAll[i] = bmH0[i] | stw[kStBits + i];
+  fast_bitmaps(a, stw, row, V, NTC, bmH0, bmN, true);
+  float* vbuf = reinterpret_cast<float*>(smem);
   uint64_t rng = a.rng[row];
   uint32_t acc[4] = {0u, 0u, 0u, 0u};
   if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
-  __syncthreads();
-
+  bool done = false;
   const float* base = a.logits + (int64_t)row * a.ld;
   const float rpen = 1.0f / c.pen;
-  const int nsw = (mode == kModeList) ? kListWords : kSumWords;
   const int ch = ((V + NTC - 1) / NTC) | 1;   // corrections: ids [t ch, t ch + ch)
 
-  auto load_step = [&](int s, RowRegsC& R, SumRegsC& Sg) __attribute__((always_inline)) {
-    const uint64_t* sw = reinterpret_cast<const uint64_t*>(sum_hdr(w, a.n_rows, s, row));
+  auto load_sum = [&](int s, SumRegsC& Sg) __attribute__((always_inline)) {
+    const uint64_t* sw = sum_words(w, a.n_rows, s, row);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) Sg.w[i] = (t + NTC * i < nsw) ? sw[t + NTC * i] : 0ull;
-    if (mode == kModeRow) fetch_row_c(base + (int64_t)s * a.step_stride, V, R);
+    for (int i = 0; i < 3; ++i) Sg.w[i] = (t + NTC * i < kSumWords) ? sw[t + NTC * i] : 0ull;
   };
-
   // One step; false when it has to be run exactly (nothing changed then).
-  auto step = [&](int s, RowRegsC& R, SumRegsC& Sg) __attribute__((always_inline)) -> bool {
+  auto step = [&](int s, SumRegsC& Sg, RowRegsC& R) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     if (done) {
       if (t == 0) *outp = -1;
@@ -1049,119 +1159,96 @@ __global__ __launch_bounds__(NTC) void k_stream_fast(StreamArgs a, StreamWs w) {
     C4S_PHASE(0);
 #pragma unroll
     for (int i = 0; i < 3; ++i)
-      if (t + NTC * i < nsw) cs.sum[t + NTC * i] = Sg.w[i];
-    float* val = vbuf;
-    if (mode == kModeRow) val = store_row_c(cur, V, R, vbuf);
+      if (t + NTC * i < kSumWords) cs.sum[t + NTC * i] = Sg.w[i];
+    float* val = store_row_c(cur, V, R, vbuf);
     C4S_PHASE(1);
-    if (s + 2 < w.s_end) load_step(s + 2, R, Sg);
+    if (s + 2 < w.s_end) load_sum(s + 2, Sg);
+    if (s + 1 < w.s_end) fetch_row_c(cur + a.step_stride, V, R);
     C4S_PHASE(2);
     __syncthreads();
     C4S_PHASE(3);
-    StepOut o{0, 0u, 0u, 0u};
-    if (mode == kModeList) {
-      if (wv == 0) {
-        const SumHdr h = hdr_from(cs.sum);
-        const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
-        const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
-        const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
-        const bool ok = list_step(h, e0, e1, c, V, bmAll, bmH0, rng, cs, o);
-        if (lane == 0) {
-          cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
-          cs.bi[3] = (int)o.dex; cs.rng = rng;
-        }
-      }
-    } else {
-      const SumHdr h = hdr_from(cs.sum);
-      double dl = 0.0, el = 0.0;
-      // corrections for ids drawn during the stream (never in H0)
-      if (!(h.flags & 1u) && c.pen_on) {
-        const MassCoef mk = mass_coef(c, h.m0);
-        const bool exm = exact_masses(c);
-        const int lo = min(V, t * ch), hi = min(V, lo + ch);
-        if (lo < hi) {
-          const int w0 = lo >> 5;
-          uint64_t bits = ((uint64_t)(bmAll[w0] & ~bmH0[w0])) | ((uint64_t)(bmAll[w0 + 1] & ~bmH0[w0 + 1]) << 32);
-          bits >>= (lo - 32 * w0);
-          bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
-          while (bits) {
-            const int id = lo + __ffsll((unsigned long long)bits) - 1;
-            bits &= bits - 1;
-            const float x = val[id];
-            double d;
-            if (exm) {
-              d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
-            } else {
-              float er0, er1;
-              const float m_raw = mass_approx(x, mk, er0);
-              const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
-              d = (double)m_raw - (double)m_pen;
-              el += (double)er1;
-            }
-            atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
-            dl += d;
+    const SumHdr h = hdr_from(cs.sum);
+    double dl = 0.0, el = 0.0;
+    // corrections for ids drawn during the stream (never in H0)
+    if (!(h.flags & 1u) && c.pen_on) {
+      const MassCoef mk = mass_coef(c, h.m0);
+      const bool exm = exact_masses(c);
+      const int lo = min(V, t * ch), hi = min(V, lo + ch);
+      if (lo < hi) {
+        const int w0 = lo >> 5;
+        uint64_t bits = (uint64_t)bmN[w0] | ((uint64_t)bmN[w0 + 1] << 32);
+        bits >>= (lo - 32 * w0);
+        bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
+        while (bits) {
+          const int id = lo + __ffsll((unsigned long long)bits) - 1;
+          bits &= bits - 1;
+          const float x = val[id];
+          double d;
+          if (exm) {
+            d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
+          } else {
+            float er0, er1;
+            const float m_raw = mass_approx(x, mk, er0);
+            const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
+            d = (double)m_raw - (double)m_pen;
+            el += (double)er1;
           }
+          atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
+          dl += d;
         }
       }
-      dl = wave_sum_f64(dl);
-      el = wave_sum_f64(el);
-      if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
-      __syncthreads();
-      C4S_PHASE(4);
-      if (wv == 0) {
-        double ds = 0.0, de = 0.0;
-        for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-        const bool ok = row_step(h, c, V, val, bmAll, bmH0, ds, de, rng, cs, o);
-        for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
-        if (lane == 0) {
-          cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
-          cs.bi[3] = (int)o.dex; cs.rng = rng;
+    }
+    dl = wave_sum_dpp(dl);
+    el = wave_sum_dpp(el);
+    if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
+    __syncthreads();
+    C4S_PHASE(4);
+    if (wv == 0) {
+      double ds = 0.0, de = 0.0;
+      for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
+      StepOut o{0, 0u, 0u, 0u};
+      const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
+      for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
+      if (lane == 0) {
+        cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
+        cs.bi[3] = (int)o.dex; cs.rng = rng;
+        if (ok) {
+          const int tok = o.tok;
+          *outp = tok;
+          acc[0] |= 64u | 1u;
+          acc[2] += o.dex;
+          acc[3] += o.kept;
+          // text2semantic.cpp:333-334: the stop token is not appended
+          if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
+            bmN[tok >> 5] |= 1u << (tok & 31);
+        } else {
+          acc[0] |= 1u << (20 + o.why);
         }
       }
     }
     C4S_PHASE(5);
     __syncthreads();
     C4S_PHASE(6);
-    const bool ok = cs.bi[0] != 0;
     rng = cs.rng;
-    if (!ok) {
-      if (t == 0) acc[0] |= 1u << (20 + (uint32_t)cs.bi[2]);
-      return false;
-    }
-    const int tok = cs.bi[1];
-    if (t == 0) {
-      *outp = tok;
-      acc[0] |= (mode == kModeList ? 32u : 64u) | 1u;
-      acc[2] += (uint32_t)cs.bi[3];
-      acc[3] += (uint32_t)cs.bi[2];
-      // text2semantic.cpp:333-334: the stop token is not appended
-      if (tok != a.stop_token && tok >= 0 && tok < V) bmAll[tok >> 5] |= 1u << (tok & 31);
-    }
-    if (tok == a.stop_token) done = true;
-    __syncthreads();
-    C4S_PHASE(7);
+    if (cs.bi[0] == 0) return false;
+    if (cs.bi[1] == a.stop_token) done = true;
     return true;
   };
 
-  RowRegsC RA, RB;
+  RowRegsC R;
   SumRegsC SA, SB;
-  load_step(s_first, RA, SA);
-  if (s_first + 1 < w.s_end) load_step(s_first + 1, RB, SB);
+  load_sum(s_first, SA);
+  if (s_first + 1 < w.s_end) load_sum(s_first + 1, SB);
+  fetch_row_c(base + (int64_t)s_first * a.step_stride, V, R);
   int s = s_first;
   bool pending = false;
   while (s < w.s_end) {
-    if (!step(s, RA, SA)) { pending = true; break; }
+    if (!step(s, SA, R)) { pending = true; break; }
     if (++s >= w.s_end) break;
-    if (!step(s, RB, SB)) { pending = true; break; }
+    if (!step(s, SB, R)) { pending = true; break; }
     ++s;
   }
-  if (t == 0) {
-    a.rng[row] = rng;
-    stw[kStDone] = done ? 1u : 0u;
-    stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
-    stw[kStNext] = (uint32_t)s;
-    stw[kStPending] = pending ? 1u : 0u;
-  }
-  for (int i = t; i < nwords; i += NTC) stw[kStBits + i] = bmAll[i] & ~bmH0[i];
+  fast_end(a, w, row, V, NTC, s, pending, done, rng, acc, bmN);
 }
 
 // ---- repair: the pending step of each row, exactly ------------------------------------
@@ -1177,15 +1264,18 @@ __global__ __launch_bounds__(NT) void k_stream_repair(StreamArgs a, StreamWs w) 
   const int s = (int)stw[kStNext];
   LdsLayout L = lds_layout(smem, V);
   const int nwords = bitmap_words(V);
-  for (int i = t; i < nwords; i += NT) L.bitmap[i] = stw[kStBits + i];
+  uint32_t* bmH0r = L.bitmap + nwords;
+  for (int i = t; i < nwords; i += NT) bmH0r[i] = 0u;
   __syncthreads();
   {
     const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
     for (int64_t j = h0 + t; j < h1; j += NT) {
       const int id = a.hist_ids[j];
-      if (id >= 0 && id < V) atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));   // sampling.cpp:24
+      if (id >= 0 && id < V) atomicOr(&bmH0r[id >> 5], 1u << (id & 31));   // sampling.cpp:24
     }
   }
+  __syncthreads();
+  for (int i = t; i < nwords; i += NT) L.bitmap[i] = bmH0r[i] | stw[kStBits + i];
   const float* cur = a.logits + (int64_t)row * a.ld + (int64_t)s * a.step_stride;
   RowFetch f;
   fetch_row(cur, V, f);
@@ -1198,8 +1288,9 @@ __global__ __launch_bounds__(NT) void k_stream_repair(StreamArgs a, StreamWs w) 
     a.out_tok[(int64_t)s * a.n_rows + row] = tok;
     if (stp) { stw[1] |= stp[0]; stw[3] += stp[2]; stw[4] += stp[3]; }
     stw[2] += 1u;
-    // the stop token is not appended (text2semantic.cpp:333-334)
-    if (tok != a.stop_token && tok >= 0 && tok < V) stw[kStBits + (tok >> 5)] |= 1u << (tok & 31);
+    // the stop token is not appended (text2semantic.cpp:333-334); H0 ids are not kept in the state
+    if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0r, tok))
+      stw[kStBits + (tok >> 5)] |= 1u << (tok & 31);
     stw[kStDone] = (tok == a.stop_token) ? 1u : 0u;
     stw[kStNext] = (uint32_t)(s + 1);
     stw[kStPending] = 0u;
@@ -1220,6 +1311,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   LdsLayout L = lds_layout(smem, V);
   const int nwords = bitmap_words(V);
   uint32_t* bmH0 = L.bitmap + nwords;
+  uint32_t* bmN = bmH0 + nwords;   // ids drawn during the stream, not in H0
   uint32_t* stw = w.state + (size_t)row * kStateWords;
   // The fast rounds initialised the state; rows they finished have nothing left.
   const int s_first = (int)stw[kStNext];
@@ -1239,7 +1331,10 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
     }
   }
   __syncthreads();
-  for (int i = t; i < nwords; i += NT) L.bitmap[i] = bmH0[i] | stw[kStBits + i];
+  for (int i = t; i < nwords; i += NT) {
+    bmN[i] = stw[kStBits + i] & ~bmH0[i];
+    L.bitmap[i] = bmH0[i] | bmN[i];
+  }
   uint64_t rng = a.rng[row];
   bool done = stw[kStDone] != 0u;
   uint32_t acc[4] = {0u, 0u, 0u, 0u};
@@ -1252,12 +1347,12 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   // small list; full-vocabulary rows, one word per thread of the whole summary.
   uint64_t pw0 = 0, pw1 = 0, pw2 = 0;
   auto load_sum = [&](int s) {
-    const uint64_t* sw = reinterpret_cast<const uint64_t*>(sum_hdr(w, a.n_rows, s, row));
+    const uint64_t* sw = sum_words(w, a.n_rows, s, row);
     if (mode == kModeList) {
       if (wv == 0) {
         pw0 = sw[lane];
         pw1 = sw[lane + kWave];
-        if (lane + 2 * kWave < kListWords) pw2 = sw[lane + 2 * kWave];
+        pw2 = (lane < 8) ? sw[kHdrW + lane] : 0ull;
       }
     } else if (t < kSumWords) {
       pw0 = sw[t];
@@ -1268,7 +1363,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       if (wv == 0) {
         cs.sum[lane] = pw0;
         cs.sum[lane + kWave] = pw1;
-        if (lane + 2 * kWave < kListWords) cs.sum[lane + 2 * kWave] = pw2;
+        if (lane < 8) cs.sum[kHdrW + lane] = pw2;
         wave_sync();
       }
     } else if (t < kSumWords) {
@@ -1301,10 +1396,10 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
     if (mode == kModeList) {
       if (wv == 0) {
         const SumHdr h = hdr_from(cs.sum);
-        const uint64_t* lst = cs.sum + kSumHdrBytes / 8;
+        const uint64_t* lst = cs.sum;
         const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
         const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
-        const bool ok = list_step(h, e0, e1, c, V, L.bitmap, bmH0, rng, cs, o);
+        const bool ok = list_step(h, e0, e1, c, V, bmN, rng, cs, o);
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
       pbits = 32u;
@@ -1354,7 +1449,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       if (wv == 0) {
         double ds = 0.0, de = 0.0;
         for (int i = 0; i < NW; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-        const bool ok = row_step(h, c, V, val, L.bitmap, bmH0, ds, de, rng, cs, o);
+        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
         for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
@@ -1398,7 +1493,10 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       acc[2] += stq[2];
       acc[3] += stq[3];
       // text2semantic.cpp:333-334: the stop token is not appended
-      if (tok != a.stop_token && tok >= 0 && tok < V) L.bitmap[tok >> 5] |= 1u << (tok & 31);
+      if (tok != a.stop_token && tok >= 0 && tok < V) {
+        L.bitmap[tok >> 5] |= 1u << (tok & 31);
+        if (!bit_of(bmH0, tok)) bmN[tok >> 5] |= 1u << (tok & 31);
+      }
     }
     if (tok == a.stop_token) done = true;
     __syncthreads();
@@ -1414,13 +1512,13 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
     }
   }
-  for (int i = t; i < nwords; i += NT) stw[kStBits + i] = L.bitmap[i] & ~bmH0[i];
+  for (int i = t; i < nwords; i += NT) stw[kStBits + i] = bmN[i];
 }
 
 }  // namespace
 
 size_t stream_chain_lds_bytes(int V) {
-  return rows_lds_bytes(V) + 4 * (size_t)bitmap_words(V);
+  return rows_lds_bytes(V) + 8 * (size_t)bitmap_words(V);
 }
 
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
@@ -1438,21 +1536,24 @@ hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_
   return hipGetLastError();
 }
 
-size_t stream_fast_lds_bytes(int V) {
-  return 4 * ((size_t)vpad(V) + 4) + 8 * (size_t)bitmap_words(V);
-}
-
-hipError_t launch_stream_fast(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_fast, dim3(a.n_rows), dim3(NTC), stream_fast_lds_bytes(a.vocab), s, a, w);
+  hipLaunchKernelGGL(k_stream_list, dim3(a.n_rows), dim3(kWave), 0, s, a, w);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_rowk, dim3(a.n_rows), dim3(NTC), 4 * ((size_t)vpad(a.vocab) + 4), s, a, w);
   return hipGetLastError();
 }
 
 hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_repair, dim3(a.n_rows), dim3(NT), rows_lds_bytes(a.vocab), s, a, w);
+  hipLaunchKernelGGL(k_stream_repair, dim3(a.n_rows), dim3(NT), stream_chain_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 

@@ -23,3 +23,18 @@ extern "C" int c4s_selftest_wave(const uint32_t* u_in, const double* d_in, const
                      f_max, d_sum);
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
+
+__global__ __launch_bounds__(64) void k_selftest2(const uint32_t* u_in, const uint64_t* q_in,
+                                                  uint32_t* u_next, uint32_t* u_max,
+                                                  uint64_t* q_max) {
+  const int l = threadIdx.x;
+  u_next[l] = wave_next_u32(u_in[l], 0xdeadbeefu);
+  u_max[l] = wave_max_u32_dpp(u_in[l]);
+  q_max[l] = wave_max_u64_dpp(q_in[l]);
+}
+
+extern "C" int c4s_selftest_wave2(const uint32_t* u_in, const uint64_t* q_in, uint32_t* u_next,
+                                  uint32_t* u_max, uint64_t* q_max) {
+  hipLaunchKernelGGL(k_selftest2, dim3(1), dim3(64), 0, nullptr, u_in, q_in, u_next, u_max, q_max);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}

@@ -38,3 +38,29 @@ def test_wave_primitives():
         assert np.allclose(od.cpu().numpy(), np.cumsum(d), rtol=1e-12, atol=1e-12 * np.abs(d).sum())
         assert (of.cpu().numpy() == f.max()).all()
         assert np.allclose(os_.cpu().numpy(), d.sum(), rtol=1e-12, atol=1e-12 * np.abs(d).sum())
+
+
+def test_wave_shift_and_integer_max():
+    """wave_shl:1 (lane i reads lane i + 1) and DPP maxima of 32/64-bit keys."""
+    import torch
+    L = C.CDLL(LIB)
+    rng = np.random.default_rng(1)
+    for trial in range(20):
+        u = rng.integers(0, 2**32, 64, dtype=np.uint64).astype(np.uint32)
+        q = rng.integers(0, 2**63, 64, dtype=np.uint64)
+        if trial % 3 == 1:
+            q[:] = q[0]                                # equal keys
+            q[rng.integers(0, 64)] ^= 1                # differ in the low word only
+        tu = torch.from_numpy(u.view(np.int32)).cuda()
+        tq = torch.from_numpy(q.view(np.int64)).cuda()
+        on = torch.zeros(64, dtype=torch.int32, device="cuda")
+        om = torch.zeros(64, dtype=torch.int32, device="cuda")
+        oq = torch.zeros(64, dtype=torch.int64, device="cuda")
+        assert L.c4s_selftest_wave2(C.c_void_p(tu.data_ptr()), C.c_void_p(tq.data_ptr()),
+                                    C.c_void_p(on.data_ptr()), C.c_void_p(om.data_ptr()),
+                                    C.c_void_p(oq.data_ptr())) == 0
+        torch.cuda.synchronize()
+        nxt = on.cpu().numpy().view(np.uint32)
+        assert np.array_equal(nxt[:63], u[1:]) and nxt[63] == 0xdeadbeef
+        assert (om.cpu().numpy().view(np.uint32) == u.max()).all()
+        assert (oq.cpu().numpy().view(np.uint64) == q.max()).all()
