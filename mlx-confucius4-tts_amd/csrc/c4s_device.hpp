@@ -173,6 +173,15 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
   v = max(v, dpp_u32<0x143, 0xC>(v, v));
   return __builtin_amdgcn_readlane(v, 63);
 }
+__device__ __forceinline__ uint32_t wave_min_u32_dpp(uint32_t v) {
+  v = min(v, dpp_u32<0x111>(v, v));
+  v = min(v, dpp_u32<0x112>(v, v));
+  v = min(v, dpp_u32<0x114>(v, v));
+  v = min(v, dpp_u32<0x118>(v, v));
+  v = min(v, dpp_u32<0x142, 0xA>(v, v));
+  v = min(v, dpp_u32<0x143, 0xC>(v, v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
 // Max of 64-bit keys over the wave (the same pattern on (hi, lo) pairs).
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {

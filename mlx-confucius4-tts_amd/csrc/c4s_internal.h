@@ -84,8 +84,11 @@ constexpr int kCandCap = 1024;      // candidates the scan may sort
 constexpr int kChunkIds = 64;       // ids per mass chunk
 constexpr int kMaxChunks = kLdsVocabMax / kChunkIds + 1;
 constexpr int kSumHdrBytes = 64;
-constexpr size_t kSumStride =
-    ((size_t)kSumHdrBytes + 8 * (size_t)kListLarge + 8 * (size_t)kMaxChunks + 127) & ~(size_t)127;
+// 1024 words: every thread of a 256-thread workgroup loads four words of a
+// summary unconditionally (no select on in-flight loads), all inside the stride.
+constexpr size_t kSumStride = 8192;
+static_assert((size_t)kSumHdrBytes + 12 * (size_t)kListLarge + 8 * (size_t)kMaxChunks <= kSumStride,
+              "summary layout fits the stride");
 constexpr int kStateWords = 8 + 400;  // done, stats[4], pad, new-id bitmap
 
 struct StreamWs {

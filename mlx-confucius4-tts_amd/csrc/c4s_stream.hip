@@ -64,12 +64,14 @@ struct SumHdr {
   int nchunk;
   int head;         // ids before the first 16-byte boundary of the row
   double err;       // absolute error bound of the chunk masses, summed over the row
-  int pad[8];
+  double s0;        // sum of the chunk masses
+  int pad[6];
 };
 static_assert(sizeof(SumHdr) == kSumHdrBytes, "summary header size");
 
-// List entry: key of the value, then the id and the id-order rank among the
-// scan's candidates; larger entries come first (value desc, id asc).
+// List entry: key of z = fl(y / T) (y itself on the greedy path), then the id
+// and the id-order rank among the scan's candidates; larger entries come first
+// (z desc, id asc), which is the declared top_p order of equal values.
 __device__ __forceinline__ uint64_t make_entry(float y, int id, int rank) {
   return ((uint64_t)fkey(y) << 32) | ((uint32_t)(16383 - id) << 10) | (uint32_t)rank;
 }
@@ -77,11 +79,13 @@ __device__ __forceinline__ uint32_t ent_key(uint64_t e) { return (uint32_t)(e >>
 __device__ __forceinline__ int ent_id(uint64_t e) { return 16383 - (int)(((uint32_t)e >> 10) & 16383u); }
 __device__ __forceinline__ int ent_rank(uint64_t e) { return (int)((uint32_t)e & 1023u); }
 
-// Summary words: list entries [0, kListLarge), header [kHdrW, kHdrW + 8),
-// chunk masses from kChunkW. List entry i sits in lane i % 64 of a wave's
-// i / 64-th load, so list rows read their entries straight into registers.
-constexpr int kHdrW = kListLarge;
-constexpr int kChunkW = kListLarge + kSumHdrBytes / 8;
+// Summary words: list entries [0, kListLarge), their values before the
+// temperature (float per entry) from kYW, header [kHdrW, kHdrW + 8), chunk
+// masses from kChunkW. List entry i sits in lane i % 64 of a wave's i / 64-th
+// load, so list rows read their entries straight into registers.
+constexpr int kYW = kListLarge;
+constexpr int kHdrW = kYW + kListLarge / 2;
+constexpr int kChunkW = kHdrW + kSumHdrBytes / 8;
 constexpr int kSumWords = kChunkW + kMaxChunks;
 static_assert((size_t)kSumWords * 8 <= kSumStride, "summary fits its stride");
 
@@ -132,6 +136,7 @@ __device__ __forceinline__ bool bit_of(const uint32_t* bm, int id) {
 struct ScanSh {
   uint32_t hist[2048];
   uint64_t cand[kCandCap];
+  float candy[kCandCap];   // value before the temperature, by candidate position
   uint32_t bm[kStateWords];
   uint32_t wtot[16][NWA];
   uint32_t red[NWA];
@@ -324,6 +329,8 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
     uint32_t C = 0, tout = 0;
 #pragma unroll
     for (int ww = 0; ww < NWA; ++ww) tout = max(tout, sh.redm[ww]);
+    // raw values bound the penalised ones; the quotient is monotone in them
+    if (tout != 0u && c.temp_on) tout = fkey(kfloat(tout) / c.temp);
 #pragma unroll
     for (int sl = 0; sl < NQ + 2; ++sl) {
       uint32_t pre = 0, tot = 0;
@@ -340,7 +347,8 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
     if (!overflow) {
       auto put = [&](uint32_t pos, float x, int id) {
         const float y = bit_of(sh.bm, id) && c.pen_on ? pen_exact(x, pen) : x;
-        sh.cand[pos] = make_entry(y, id, (int)pos);
+        sh.cand[pos] = make_entry(c.temp_on ? y / c.temp : y, id, (int)pos);   // sampling.cpp:16
+        sh.candy[pos] = y;
       };
       if (eh && fkey(xe) >= L0) put(ex[0], xe, eid);
       if (et && fkey(xe) >= L0) put(ex[NQ + 1], xe, eid);
@@ -378,16 +386,21 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
     uint64_t* lst = sw;
     SumHdr* hdr = reinterpret_cast<SumHdr*>(sw + kHdrW);
     double* chk = reinterpret_cast<double*>(sw + kChunkW);
-    if (!bad)
-      for (int i = t; i < n; i += NTA) lst[i] = sh.cand[i];
+    if (!bad) {
+      float* ly = reinterpret_cast<float*>(sw + kYW);
+      for (int i = t; i < n; i += NTA) {
+        const uint64_t e = sh.cand[i];
+        lst[i] = e;
+        ly[i] = sh.candy[ent_rank(e)];
+      }
+    }
 
     // Chunk masses of the whole row (rows without top-k).
     float m0 = 0.f;
     int nchunk = 0;
-    double err = 0.0;
+    double err = 0.0, s0 = 0.0;
     if (masses && !bad) {
-      const float ytop = kfloat(ent_key(sh.cand[0]));
-      m0 = c.temp_on ? ytop / c.temp : ytop;
+      m0 = kfloat(ent_key(sh.cand[0]));
       const MassCoef mk = mass_coef(c, m0);
       const bool exm = exact_masses(c);
       nchunk = max(1, (rs.nq + 15) >> 4);
@@ -447,7 +460,9 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
         sh.chunk[nchunk - 1] += ts;
       }
       __syncthreads();
-      for (int i = t; i < nchunk; i += NTA) chk[i] = sh.chunk[i];
+      double cl = 0.0;
+      for (int i = t; i < nchunk; i += NTA) { chk[i] = sh.chunk[i]; cl += sh.chunk[i]; }
+      s0 = block_sum_f64<NTA>(cl, sh.redd);
     }
     if (t == 0) {
       SumHdr h{};
@@ -458,6 +473,7 @@ __global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w
       h.nchunk = nchunk;
       h.head = rs.head;
       h.err = err + 0x1p-100;
+      h.s0 = s0;
       *hdr = h;
     }
     __syncthreads();
@@ -573,8 +589,10 @@ __device__ __forceinline__ void clear_slots(ChainSh& cs, int nslot) {
   wave_sync();
 }
 
-__device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w2, uint64_t w3) {
+__device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w2, uint64_t w3,
+                                            uint64_t w4) {
   SumHdr h{};
+  h.s0 = __longlong_as_double((long long)w4);
   h.n = (int)(uint32_t)w0;
   h.tout = (uint32_t)(w0 >> 32);
   h.flags = (uint32_t)w1;
@@ -585,7 +603,7 @@ __device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w
   return h;
 }
 __device__ __forceinline__ SumHdr hdr_from(const uint64_t* sw) {   // sw: summary words (LDS)
-  return hdr_words(sw[kHdrW], sw[kHdrW + 1], sw[kHdrW + 2], sw[kHdrW + 3]);
+  return hdr_words(sw[kHdrW], sw[kHdrW + 1], sw[kHdrW + 2], sw[kHdrW + 3], sw[kHdrW + 4]);
 }
 // Header held in lanes 0..3 of a wave's register `hw` (word kHdrW + lane).
 __device__ __forceinline__ SumHdr hdr_lanes(uint64_t hw) {
@@ -593,7 +611,7 @@ __device__ __forceinline__ SumHdr hdr_lanes(uint64_t hw) {
     return (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)hw, l) |
            ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(hw >> 32), l) << 32);
   };
-  return hdr_words(rl(0), rl(1), rl(2), rl(3));
+  return hdr_words(rl(0), rl(1), rl(2), rl(3), rl(4));
 }
 
 struct StepOut {
@@ -616,10 +634,61 @@ enum : uint32_t {
   kWhyTiny = 8,       // subnormal masses
 };
 
-// Candidate-list step for greedy and top-k rows (wave 0; two entries per lane).
+// Inverse-CDF draw (text2semantic.cpp:150-165) over at most one kept entry per
+// lane (id, mass e). Each lane sums the kept masses at or below its id; the
+// reference sums in id order, so the decision keeps the margin rel_eps, else
+// the sums are replayed sequentially in id order.
+__device__ int lane_draw(bool kept, int id, double e, double u, int V, uint32_t& exact) {
+  const double eps = rel_eps(V);
+  const double ek = kept ? e : 0.0;
+  double acc = 0.0;
+  for (uint64_t m = __ballot(kept); m; m &= m - 1) {
+    const int j = __ffsll((unsigned long long)m) - 1;
+    const int idj = (int)readlane_u32((uint32_t)id, j);
+    const double ej = readlane_f64(ek, j);
+    acc += (idj <= id) ? ej : 0.0;
+  }
+  const double r = u * wave_sum_dpp(ek);
+  const uint32_t tid = wave_min_u32_dpp((kept && acc >= r) ? (uint32_t)id : 0xFFFFFFFFu);
+  if (r > 0.0 && tid != 0xFFFFFFFFu) {
+    const int f = __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == tid)) - 1;
+    const double af = readlane_f64(acc, f), pf = af - readlane_f64(ek, f);
+    if ((af - r > eps * af) && (r - pf > eps * r)) {
+      exact = 0;
+      return (int)tid;
+    }
+  }
+  // text2semantic.cpp:152-164 sequentially in id order; other ids weigh 0
+  exact = 1;
+  double total = 0.0;
+  uint32_t last = 0xFFFFFFFFu;
+  for (;;) {   // pass 1: total
+    const uint32_t nx = wave_min_u32_dpp((kept && (last == 0xFFFFFFFFu || (uint32_t)id > last)) ? (uint32_t)id : 0xFFFFFFFFu);
+    if (nx == 0xFFFFFFFFu) break;
+    total += readlane_f64(ek, __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == nx)) - 1);
+    last = nx;
+  }
+  const double rr = u * total;
+  if (rr <= 0.0) return 0;
+  double run = 0.0;
+  last = 0xFFFFFFFFu;
+  for (;;) {   // pass 2: first id with rr <= acc
+    const uint32_t nx = wave_min_u32_dpp((kept && (last == 0xFFFFFFFFu || (uint32_t)id > last)) ? (uint32_t)id : 0xFFFFFFFFu);
+    if (nx == 0xFFFFFFFFu) break;
+    const double en = readlane_f64(ek, __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == nx)) - 1);
+    run += en;
+    if (en > 0.0 && rr <= run) return (int)nx;
+    last = nx;
+  }
+  return V - 1;
+}
+
+// Candidate-list step for greedy and top-k rows (one wave; two entries per
+// lane: keys e0, e1 and their values before the temperature yb0, yb1).
 // Returns false (nothing changed) when a decision needs the exact step.
-__device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCfg& c, int V,
-                          const uint32_t* bmN, uint64_t& rng, ChainSh& cs, StepOut& o) {
+__device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, float yb1,
+                          const RowCfg& c, int V, const uint32_t* bmN, uint64_t& rng, ChainSh& cs,
+                          StepOut& o) {
   const int lane = lane_id();
   o.why = kWhySummary;
   if (h.flags & 1u) return false;
@@ -629,13 +698,14 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   const int id0 = ent_id(e0), id1 = ent_id(e1);
   const bool h0 = c.pen_on && v0 && bit_of(bmN, id0);
   const bool h1 = c.pen_on && v1 && bit_of(bmN, id1);
-  const float yr0 = v0 ? kfloat(ent_key(e0)) : ninf, yr1 = v1 ? kfloat(ent_key(e1)) : ninf;
-  const float y0 = h0 ? pen_exact(yr0, c.pen) : yr0;
-  const float y1 = h1 ? pen_exact(yr1, c.pen) : yr1;
+  // z of an unhit entry is its key; a hit is penalised (sampling.cpp:26) and divided again
+  float z0 = v0 ? kfloat(ent_key(e0)) : ninf, z1 = v1 ? kfloat(ent_key(e1)) : ninf;
+  if (h0) { const float y = pen_exact(yb0, c.pen); z0 = c.temp_on ? y / c.temp : y; }
+  if (h1) { const float y = pen_exact(yb1, c.pen); z1 = c.temp_on ? y / c.temp : y; }
 
   if (c.greedy) {   // text2semantic.cpp:144-145, argmax of the penalised row, first max wins
-    const uint64_t k0 = v0 ? ((uint64_t)fkey(y0) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id0) : 0ull;
-    const uint64_t k1 = v1 ? ((uint64_t)fkey(y1) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id1) : 0ull;
+    const uint64_t k0 = v0 ? ((uint64_t)fkey(z0) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id0) : 0ull;
+    const uint64_t k1 = v1 ? ((uint64_t)fkey(z1) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id1) : 0ull;
     const uint64_t kb = wave_max_u64_dpp(k0 > k1 ? k0 : k1);
     o.why = kWhyBound;
     if (kb == 0ull || !((uint32_t)(kb >> 32) > h.tout)) return false;
@@ -645,7 +715,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
     return true;
   }
 
-  // top-k on the unhit entries (sorted); hits must fall below the k-th value
+  // top-k on the unhit entries (sorted by z desc, id asc); hits must fall below the k-th
   const bool u0 = v0 && !h0, u1 = v1 && !h1;
   const uint64_t b0 = __ballot(u0), b1 = __ballot(u1);
   const int r0 = __popcll(b0 & lanemask_lt());
@@ -655,42 +725,28 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   o.why = kWhyShort;
   if (nu < k) return false;
   const uint64_t mk0 = __ballot(u0 && r0 == k - 1), mk1 = __ballot(u1 && r1 == k - 1);
-  const float yk = mk0 ? readlane_f32(y0, __ffsll((unsigned long long)mk0) - 1)
-                       : readlane_f32(y1, __ffsll((unsigned long long)mk1) - 1);
-  const float zk = c.temp_on ? yk / c.temp : yk;
-  float hm = ninf;
-  if (h0) hm = y0;
-  if (h1) hm = fmaxf(hm, y1);
-  hm = wave_max_dpp(hm);
-  const float zh = c.temp_on ? hm / c.temp : hm;
+  const float zk = mk0 ? readlane_f32(z0, __ffsll((unsigned long long)mk0) - 1)
+                       : readlane_f32(z1, __ffsll((unsigned long long)mk1) - 1);
+  float zh = ninf;
+  if (h0) zh = z0;
+  if (h1) zh = fmaxf(zh, z1);
+  zh = wave_max_dpp(zh);
   o.why = kWhyHit;
-  if (!(zh < zk) && hm != ninf) return false;
+  if (!(zh < zk) && zh != ninf) return false;
   o.why = kWhyBound;
   if (!(zk > ninf)) return false;
-  if (h.tout != 0u) {
-    const float yo = kfloat(h.tout);
-    const float zo = c.temp_on ? yo / c.temp : yo;
-    if (!(zo < zk)) return false;   // everything outside the list stays below the threshold
-  }
-  const float z0 = c.temp_on ? y0 / c.temp : y0;
-  const float z1 = c.temp_on ? y1 / c.temp : y1;
+  if (h.tout != 0u && !(kfloat(h.tout) < zk)) return false;   // everything outside stays below
   const bool s0 = u0 && z0 >= zk, s1 = u1 && z1 >= zk;
   const int nsurv = __popcll(__ballot(s0)) + __popcll(__ballot(s1));
   o.why = kWhyTies;
   if (nsurv > kWave) return false;
+  // survivors are the unhit ranks [0, nsurv): one per lane in rank order
   if (s0) { cs.lz[r0] = z0; cs.lid[r0] = id0; cs.lslot[r0] = ent_rank(e0); }
   if (s1) { cs.lz[r1] = z1; cs.lid[r1] = id1; cs.lslot[r1] = ent_rank(e1); }
   wave_sync();
   const bool sv = lane < nsurv;
   const float zs = sv ? cs.lz[lane] : ninf;
   const int ids = sv ? cs.lid[lane] : 0;
-  const int sl = sv ? cs.lslot[lane] : 0;
-  {
-    // equal quotients of different values must still be in id order
-    const float zn = __uint_as_float(wave_next_u32(__float_as_uint(zs), 0u));
-    const int idn = (int)wave_next_u32((uint32_t)ids, 0u);
-    if (__ballot(sv && lane + 1 < nsurv && zs == zn && ids > idn)) return false;
-  }
   // masses, top_p (sampling.cpp:52-65), min_keep (:67-68)
   const float zmax = readlane_f32(zs, 0);
   const double e = sv ? exp((double)(zs - zmax)) : 0.0;
@@ -716,20 +772,17 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, const RowCf
   const long long lim = (long long)V - (long long)c.min_keep < 0 ? 0 : (long long)V - (long long)c.min_keep;
   const long long m = (long long)V - (R < lim ? R : lim);
   const bool kept = sv && (long long)lane < m;
-  const int nslot = (int)wave_max_u32_dpp(kept ? (uint32_t)(sl + 1) : 0u);
-  clear_slots(cs, nslot);
-  if (kept) { cs.slotE[sl] = e; cs.slotId[sl] = ids; }
-  wave_sync();
   const uint64_t st = xorshift64(rng);
-  o.tok = slot_draw(cs, nslot, unit_from_state(st), V, o.dex);
+  o.tok = lane_draw(kept, ids, e, unit_from_state(st), V, o.dex);
   o.kept = (uint32_t)__popcll(__ballot(kept));
   rng = st;
   return true;
 }
 
 // Full-vocabulary step (wave 0). The summary is in cs.sum; also needs the
-// per-chunk corrections for ids drawn during the stream (cs.cdelta, their sum
-// dsum and error derr) and the raw row in LDS (`val`).
+// correction of the masses for ids drawn during the stream (dsum, its error
+// derr; per chunk in cs.cdelta) and the raw row in LDS (`val`). The list is
+// compacted lazily, 64 entries at a time, only as deep as the decision needs.
 __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
                          const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
                          uint64_t& rng, ChainSh& cs, StepOut& o) {
@@ -739,44 +792,124 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
   const int n = h.n;
   const float ninf = neg_inf();
   const uint64_t* lst = cs.sum;
-  // unhit entries compacted in rank order; largest penalised hit value
-  int nu = 0;
+  const float* ly = reinterpret_cast<const float*>(cs.sum + kYW);
+  int nb = 0, nu = 0;
   float hm = ninf;
-  for (int b = 0; b < n; b += kWave) {
-    const int pos = b + lane;
+  // list block [nb, nb + 64): unhit entries to their ranks, penalised hits into hm
+  auto compact = [&]() __attribute__((always_inline)) {
+    const int pos = nb + lane;
     const bool v = pos < n;
     const uint64_t e = v ? lst[pos] : 0ull;
     const int id = ent_id(e);
     const bool hit = c.pen_on && v && bit_of(bmN, id);
-    const float yr = v ? kfloat(ent_key(e)) : ninf;
-    const float y = hit ? pen_exact(yr, c.pen) : yr;
-    const bool u = v && !hit;
-    const uint64_t bl = __ballot(u);
-    if (u) {
+    const bool un = v && !hit;
+    const uint64_t bl = __ballot(un);
+    if (un) {
       const int rk = nu + __popcll(bl & lanemask_lt());
-      cs.lz[rk] = c.temp_on ? y / c.temp : y;
+      cs.lz[rk] = kfloat(ent_key(e));
       cs.lid[rk] = id;
       cs.lslot[rk] = ent_rank(e);
     }
-    if (hit) hm = fmaxf(hm, y);
+    if (hit) {   // sampling.cpp:26 on the value before the temperature, then :16
+      const float y = pen_exact(ly[pos], c.pen);
+      hm = fmaxf(hm, c.temp_on ? y / c.temp : y);
+    }
     nu += __popcll(bl);
-  }
+    nb = min(n, nb + kWave);
+  };
+  // every list entry past the compacted ones is at or below this value
+  auto zend = [&]() -> float { return nb >= n ? ninf : kfloat(ent_key(lst[nb - 1])); };
+  compact();
+  while (nu == 0 && nb < n) compact();
+  C4S_PHASE(8);
   o.why = kWhyShort;
   if (nu == 0) return false;
-  hm = wave_max_dpp(hm);
   wave_sync();
-  const float ztop = cs.lz[0];
+  const float mt = cs.lz[0];
+  const float zo = (h.tout != 0u) ? kfloat(h.tout) : ninf;
   o.why = kWhyBound;
-  if (!(ztop > ninf)) return false;
-  const float zo = (h.tout != 0u) ? (c.temp_on ? kfloat(h.tout) / c.temp : kfloat(h.tout)) : ninf;
-  const float zhm = c.temp_on ? hm / c.temp : hm;
-  // the maximum must be an unhit list entry above every hit and the bound
-  if (!(zo < ztop)) return false;
+  if (!(mt > ninf) || !(zo < mt)) return false;
+  while (nb < n && !(zend() < mt)) compact();
   o.why = kWhyHit;
-  if (!(zhm < ztop)) return false;
-  const float mt = ztop;
+  if (!(wave_max_dpp(hm) < mt)) return false;   // the maximum is an unhit entry
+
   const double eps = rel_eps(V);
-  // S = (sum of chunks - corrections) * exp(m0 - mt)
+  // S = (chunk masses - corrections) * exp(m0 - mt). When the maximum moved,
+  // fl(z - mt) against fl(z - m0) + (m0 - mt): relative 2^-23 (|d| + m0 - mt)
+  // per mass, with sum(e |d|) <= 40 S + V 2^-50 (e |d| < 2^-50 once |d| > 40).
+  const double dm = (double)h.m0 - (double)mt;
+  const double rho = (dm == 0.0) ? 1.0 : exp(dm);
+  const double S = (h.s0 - dsum) * rho;
+  const double err = (h.err + derr + fabs(dsum) * 0x1p-50) * rho +
+                     (dm > 0.0 ? 0x1p-23 * ((40.0 + dm) * S + (double)V * 0x1p-50) : 0.0) + eps * S;
+  const double thr = 1.0 - (double)c.p;
+  const uint64_t st = xorshift64(rng);
+  const double u = unit_from_state(st);
+  C4S_PHASE(9);
+
+  if (thr > 0.0) {
+    // nucleus cut on the unhit entries in rank order: removed iff above >= p * S
+    const double pS = (double)c.p * S;
+    const double marg = (double)c.p * err + eps * S;
+    double carry = 0.0, e_first = 0.0;
+    int q = -1, rdone = 0;
+    while (q < 0) {
+      while (nu - rdone < kWave && nb < n) compact();
+      if (rdone >= nu) break;
+      wave_sync();
+      const int rk = rdone + lane;
+      const bool v = rk < nu;
+      const float z = v ? cs.lz[rk] : ninf;
+      const double em = v ? exp((double)(z - mt)) : 0.0;
+      if (rdone == 0) e_first = em;
+      const double inc = wave_scan_f64(em);
+      const double ab = carry + inc - em;
+      const double D = ab - pS;
+      o.why = kWhyMargin;
+      if (__ballot(v && rk >= c.min_keep && !(fabs(D) > marg + eps * ab))) return false;
+      o.why = kWhyTiny;   // subnormal kept masses may differ between libm implementations
+      if (__ballot(v && D < 0.0 && em < 0x1p-1000)) return false;
+      const uint64_t rm = __ballot(v && D >= 0.0);
+      if (rm) q = max(rdone + __ffsll((unsigned long long)rm) - 1, c.min_keep);
+      carry = readlane_f64(carry + inc, kWave - 1);
+      rdone += kWave;
+    }
+    C4S_PHASE(10);
+    o.why = kWhyDeep;
+    if (q < 0 || q > nu) return false;   // the cut lies below the list
+    const float zq1 = cs.lz[q - 1];
+    while (nb < n && !(zend() < zq1)) compact();
+    o.why = kWhyBound;
+    if (!(zo < zq1)) return false;
+    o.why = kWhyHit;
+    if (!(wave_max_dpp(hm) < zq1)) return false;
+    if (q <= kWave) {   // kept ranks [0, q) are the first chunk: lane = rank
+      const bool kept = lane < q;
+      o.tok = lane_draw(kept, kept ? cs.lid[lane] : 0, e_first, u, V, o.dex);
+    } else {
+      int nslot = 0;
+      for (int b = 0; b < q; b += kWave) {
+        const int rkk = b + lane;
+        nslot = max(nslot, rkk < q ? cs.lslot[rkk] + 1 : 0);
+      }
+      nslot = (int)wave_max_u32_dpp((uint32_t)nslot);
+      clear_slots(cs, nslot);
+      for (int b = 0; b < q; b += kWave) {
+        const int rkk = b + lane;
+        if (rkk < q) {
+          cs.slotE[cs.lslot[rkk]] = exp((double)(cs.lz[rkk] - mt));
+          cs.slotId[cs.lslot[rkk]] = cs.lid[rkk];
+        }
+      }
+      wave_sync();
+      o.tok = slot_draw(cs, nslot, u, V, o.dex);
+    }
+    C4S_PHASE(12);
+    o.kept = (uint32_t)q;
+    rng = st;
+    return true;
+  }
+
   const int nchunk = h.nchunk;
   double cv[4];
   double cs_l = 0.0;
@@ -786,86 +919,6 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
     cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cs.sum[kChunkW + ci]) - cs.cdelta[ci] : 0.0;
     cs_l += cv[i];
   }
-  const double rho = exp((double)h.m0 - (double)mt);
-  const double Sraw = wave_sum_dpp(cs_l);
-  const double S = Sraw * rho;
-  // rounding of the corrections; and when the maximum moved, fl(z - mt) against
-  // fl(z - m0) + (m0 - mt): relative 2^-23 (|d| + m0 - mt) per mass, with
-  // sum(e |d|) <= 40 S + V 2^-50 (e |d| < 2^-50 once |d| > 40)
-  const double dm = (double)h.m0 - (double)mt;
-  const double err = (h.err + derr + fabs(dsum) * 0x1p-50) * rho +
-                     (dm > 0.0 ? 0x1p-23 * ((40.0 + dm) * S + (double)V * 0x1p-50) : 0.0) + eps * S;
-  const double thr = 1.0 - (double)c.p;
-  const uint64_t st = xorshift64(rng);
-  const double u = unit_from_state(st);
-
-  if (thr > 0.0) {
-    // nucleus cut on the unhit entries in rank order: removed iff above >= p * S
-    const double pS = (double)c.p * S;
-    const double marg = (double)c.p * err + eps * S;
-    double carry = 0.0;
-    int q = -1;
-    float zq1 = ninf;   // value of the last kept entry
-    for (int b = 0; b < nu && q < 0; b += kWave) {
-      const int rkk = b + lane;
-      const bool v = rkk < nu;
-      const float z = v ? cs.lz[rkk] : ninf;
-      const double em = v ? exp((double)(z - mt)) : 0.0;
-      const double inc = wave_scan_f64(em);
-      const double ab = carry + inc - em;
-      const double D = ab - pS;
-      o.why = kWhyMargin;
-      if (__ballot(v && rkk >= c.min_keep && !(fabs(D) > marg + eps * ab))) return false;
-      const uint64_t rm = __ballot(v && D >= 0.0);
-      if (rm) {
-        const int f = __ffsll((unsigned long long)rm) - 1;
-        q = max(b + f, c.min_keep);
-      }
-      carry = readlane_f64(carry + inc, kWave - 1);
-    }
-    o.why = kWhyDeep;
-    if (q < 0) return false;        // the cut lies below the list
-    if (q > nu) return false;
-    zq1 = cs.lz[q - 1];
-    o.why = kWhyBound;
-    if (!(zo < zq1)) return false;
-    o.why = kWhyHit;
-    if (!(zhm < zq1)) return false;
-    // id order inside equal values among the kept entries and the first removed one
-    for (int b = 0; b < q; b += kWave) {
-      const int rkk = b + lane;
-      const bool v = rkk + 1 < nu && rkk < q;
-      const bool bad = v && cs.lz[rkk] == cs.lz[rkk + 1] && cs.lid[rkk] > cs.lid[rkk + 1];
-      o.why = kWhyTies;
-      if (__ballot(bad)) return false;
-    }
-    // kept = ranks [0, q): draw in id order over their slots
-    int nslot = 0;
-    for (int b = 0; b < q; b += kWave) {
-      const int rkk = b + lane;
-      nslot = max(nslot, rkk < q ? cs.lslot[rkk] + 1 : 0);
-    }
-    nslot = (int)wave_max_u32_dpp((uint32_t)nslot);
-    clear_slots(cs, nslot);
-    double smin = 1.0;
-    for (int b = 0; b < q; b += kWave) {
-      const int rkk = b + lane;
-      if (rkk < q) {
-        const double em = exp((double)(cs.lz[rkk] - mt));
-        cs.slotE[cs.lslot[rkk]] = em;
-        cs.slotId[cs.lslot[rkk]] = cs.lid[rkk];
-        smin = fmin(smin, em);
-      }
-    }
-    o.why = kWhyTiny;
-    if (__ballot(smin < 0x1p-1000)) return false;
-    wave_sync();
-    o.tok = slot_draw(cs, nslot, u, V, o.dex);
-    o.kept = (uint32_t)q;
-    rng = st;
-    return true;
-  }
-
   // Dense draw (top_p keeps every id of nonzero mass; zero masses never win):
   // r = u * S, chunk prefixes locate r, the chunk is recomputed exactly.
   const double r = u * S;
@@ -1004,6 +1057,7 @@ __device__ __forceinline__ void fast_end(const StreamArgs& a, const StreamWs& w,
 
 struct ListRegs {
   uint64_t e0, e1, hw;   // entries lane and lane + 64, header word lane (lanes < 8)
+  float y0, y1;          // their values before the temperature
 };
 
 __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w) {
@@ -1026,7 +1080,10 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     const uint64_t* sw = sum_words(w, a.n_rows, s, row);
     r.e0 = sw[lane];
     r.e1 = sw[lane + kWave];
-    r.hw = (lane < 8) ? sw[kHdrW + lane] : 0ull;
+    r.hw = sw[kHdrW + (lane & 7)];   // lanes 0..3 are read
+    const float* sy = reinterpret_cast<const float*>(sw + kYW);
+    r.y0 = sy[lane];
+    r.y1 = sy[lane + kWave];
   };
   // One step; false when it has to be run exactly (nothing changed then).
   auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) -> bool {
@@ -1038,9 +1095,10 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     const SumHdr h = hdr_lanes(r.hw);
     const uint64_t e0 = (lane < h.n) ? r.e0 : 0ull;
     const uint64_t e1 = (lane + kWave < h.n) ? r.e1 : 0ull;
+    const float yb0 = r.y0, yb1 = r.y1;
     if (s + 4 < w.s_end) load(s + 4, r);
     StepOut o{0, 0u, 0u, 0u};
-    const bool ok = list_step(h, e0, e1, c, V, bmN, rng, cs, o);
+    const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, bmN, rng, cs, o);
     if (!ok) {
       if (lane == 0) acc[0] |= 1u << (20 + o.why);
       return false;
@@ -1085,33 +1143,38 @@ constexpr int NWC = NTC / kWave;
 constexpr int kQuadsC = kLdsVocabMax / 4 / NTC;
 static_assert(kQuadsC * 4 * NTC == kLdsVocabMax, "row fetch covers the LDS rows");
 
+// A row of up to NQC * 4 * 256 body ids plus edge ids, in registers.
+template <int NQC>
 struct RowRegsC {
-  float4 q[kQuadsC];
+  float4 q[NQC];
   float e;
 };
 struct SumRegsC {
-  uint64_t w[3];
+  uint64_t w[4];
 };
+static_assert(4 * NTC >= kSumWords && 4 * NTC * 8 <= (int)kSumStride, "four words a thread cover a summary");
 
-__device__ __forceinline__ void fetch_row_c(const float* p, int V, RowRegsC& f) {
+template <int NQC>
+__device__ __forceinline__ void fetch_row_c(const float* p, int V, RowRegsC<NQC>& f) {
   const RowShape r = row_shape(p, V);
   const float4* p4 = reinterpret_cast<const float4*>(p + r.head);
   const int t = threadIdx.x;
 #pragma unroll
-  for (int j = 0; j < kQuadsC; ++j) {
+  for (int j = 0; j < NQC; ++j) {
     const int q = t + NTC * j;
     f.q[j] = (q < r.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   f.e = (t < r.head) ? p[t] : ((t < r.head + r.tail) ? p[r.head + 4 * r.nq + (t - r.head)] : 0.f);
 }
 
-__device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRegsC& f, float* buf) {
+template <int NQC>
+__device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRegsC<NQC>& f, float* buf) {
   const RowShape r = row_shape(p, V);
   float* val = buf + ((4 - r.head) & 3);
   const int t = threadIdx.x;
   float4* body = reinterpret_cast<float4*>(val + r.head);
 #pragma unroll
-  for (int j = 0; j < kQuadsC; ++j) {
+  for (int j = 0; j < NQC; ++j) {
     const int q = t + NTC * j;
     if (q < r.nq) body[q] = f.q[j];
   }
@@ -1120,6 +1183,7 @@ __device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRe
   return val;
 }
 
+template <int NQC>
 __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ ChainSh cs;
@@ -1146,10 +1210,10 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   auto load_sum = [&](int s, SumRegsC& Sg) __attribute__((always_inline)) {
     const uint64_t* sw = sum_words(w, a.n_rows, s, row);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) Sg.w[i] = (t + NTC * i < kSumWords) ? sw[t + NTC * i] : 0ull;
+    for (int i = 0; i < 4; ++i) Sg.w[i] = sw[t + NTC * i];   // inside the 1024-word stride
   };
   // One step; false when it has to be run exactly (nothing changed then).
-  auto step = [&](int s, SumRegsC& Sg, RowRegsC& R) __attribute__((always_inline)) -> bool {
+  auto step = [&](int s, SumRegsC& Sg, RowRegsC<NQC>& R) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     if (done) {
       if (t == 0) *outp = -1;
@@ -1158,7 +1222,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
     const float* cur = base + (int64_t)s * a.step_stride;
     C4S_PHASE(0);
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
+    for (int i = 0; i < 4; ++i)
       if (t + NTC * i < kSumWords) cs.sum[t + NTC * i] = Sg.w[i];
     float* val = store_row_c(cur, V, R, vbuf);
     C4S_PHASE(1);
@@ -1168,74 +1232,79 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
     __syncthreads();
     C4S_PHASE(3);
     const SumHdr h = hdr_from(cs.sum);
-    double dl = 0.0, el = 0.0;
-    // corrections for ids drawn during the stream (never in H0)
-    if (!(h.flags & 1u) && c.pen_on) {
-      const MassCoef mk = mass_coef(c, h.m0);
-      const bool exm = exact_masses(c);
-      const int lo = min(V, t * ch), hi = min(V, lo + ch);
-      if (lo < hi) {
-        const int w0 = lo >> 5;
-        uint64_t bits = (uint64_t)bmN[w0] | ((uint64_t)bmN[w0 + 1] << 32);
-        bits >>= (lo - 32 * w0);
-        bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
-        while (bits) {
-          const int id = lo + __ffsll((unsigned long long)bits) - 1;
-          bits &= bits - 1;
-          const float x = val[id];
-          double d;
-          if (exm) {
-            d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
-          } else {
-            float er0, er1;
-            const float m_raw = mass_approx(x, mk, er0);
-            const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
-            d = (double)m_raw - (double)m_pen;
-            el += (double)er1;
+    // Corrections for ids drawn during the stream (never in H0): fp32 masses
+    // first; a decision that falls inside their error bound is retried once
+    // with the reference's double masses.
+    for (int attempt = 0; attempt < 2; ++attempt) {
+      const bool exact = attempt == 1;
+      double dl = 0.0, el = 0.0;
+      if (!(h.flags & 1u) && c.pen_on) {
+        const MassCoef mk = mass_coef(c, h.m0);
+        const int lo = min(V, t * ch), hi = min(V, lo + ch);
+        if (lo < hi) {
+          const int w0 = lo >> 5;
+          uint64_t bits = (uint64_t)bmN[w0] | ((uint64_t)bmN[w0 + 1] << 32);
+          bits >>= (lo - 32 * w0);
+          bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
+          while (bits) {
+            const int id = lo + __ffsll((unsigned long long)bits) - 1;
+            bits &= bits - 1;
+            const float x = val[id];
+            double d;
+            if (exact) {
+              d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
+            } else {
+              float er0, er1;
+              const float m_raw = mass_approx(x, mk, er0);
+              const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
+              d = (double)m_raw - (double)m_pen;
+              el += (double)er0 + (double)er1;
+            }
+            atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
+            dl += d;
           }
-          atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
-          dl += d;
         }
       }
-    }
-    dl = wave_sum_dpp(dl);
-    el = wave_sum_dpp(el);
-    if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
-    __syncthreads();
-    C4S_PHASE(4);
-    if (wv == 0) {
-      double ds = 0.0, de = 0.0;
-      for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-      StepOut o{0, 0u, 0u, 0u};
-      const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
-      for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
-      if (lane == 0) {
-        cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
-        cs.bi[3] = (int)o.dex; cs.rng = rng;
-        if (ok) {
-          const int tok = o.tok;
-          *outp = tok;
-          acc[0] |= 64u | 1u;
-          acc[2] += o.dex;
-          acc[3] += o.kept;
-          // text2semantic.cpp:333-334: the stop token is not appended
-          if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
-            bmN[tok >> 5] |= 1u << (tok & 31);
-        } else {
-          acc[0] |= 1u << (20 + o.why);
+      dl = wave_sum_dpp(dl);
+      el = wave_sum_dpp(el);
+      if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
+      __syncthreads();
+      C4S_PHASE(4);
+      if (wv == 0) {
+        double ds = 0.0, de = 0.0;
+        for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
+        StepOut o{0, 0u, 0u, 0u};
+        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
+        for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
+        const bool retry = !ok && !exact && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
+        if (lane == 0) {
+          cs.bi[0] = ok ? 1 : (retry ? 2 : 0); cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
+          cs.bi[3] = (int)o.dex; cs.rng = rng;
+          if (ok) {
+            const int tok = o.tok;
+            *outp = tok;
+            acc[0] |= 64u | 1u;
+            acc[2] += o.dex;
+            acc[3] += o.kept;
+            // text2semantic.cpp:333-334: the stop token is not appended
+            if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
+              bmN[tok >> 5] |= 1u << (tok & 31);
+          } else if (!retry) {
+            acc[0] |= 1u << (20 + o.why);
+          }
         }
       }
+      __syncthreads();
+      if (cs.bi[0] != 2) break;
     }
     C4S_PHASE(5);
-    __syncthreads();
-    C4S_PHASE(6);
     rng = cs.rng;
     if (cs.bi[0] == 0) return false;
     if (cs.bi[1] == a.stop_token) done = true;
     return true;
   };
 
-  RowRegsC R;
+  RowRegsC<NQC> R;
   SumRegsC SA, SB;
   load_sum(s_first, SA);
   if (s_first + 1 < w.s_end) load_sum(s_first + 1, SB);
@@ -1345,7 +1414,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   // Summary of the next step in flight as vector loads (barriers do not wait
   // for them): list rows, wave 0, three words per lane of the header and the
   // small list; full-vocabulary rows, one word per thread of the whole summary.
-  uint64_t pw0 = 0, pw1 = 0, pw2 = 0;
+  uint64_t pw0 = 0, pw1 = 0, pw2 = 0, pw3 = 0;
   auto load_sum = [&](int s) {
     const uint64_t* sw = sum_words(w, a.n_rows, s, row);
     if (mode == kModeList) {
@@ -1353,6 +1422,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
         pw0 = sw[lane];
         pw1 = sw[lane + kWave];
         pw2 = (lane < 8) ? sw[kHdrW + lane] : 0ull;
+        pw3 = sw[kYW + lane];   // values of entries 2 lane, 2 lane + 1
       }
     } else if (t < kSumWords) {
       pw0 = sw[t];
@@ -1364,6 +1434,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
         cs.sum[lane] = pw0;
         cs.sum[lane + kWave] = pw1;
         if (lane < 8) cs.sum[kHdrW + lane] = pw2;
+        cs.sum[kYW + lane] = pw3;
         wave_sync();
       }
     } else if (t < kSumWords) {
@@ -1399,7 +1470,8 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
         const uint64_t* lst = cs.sum;
         const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
         const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
-        const bool ok = list_step(h, e0, e1, c, V, bmN, rng, cs, o);
+        const float* ly = reinterpret_cast<const float*>(cs.sum + kYW);
+        const bool ok = list_step(h, e0, e1, ly[lane], ly[lane + kWave], c, V, bmN, rng, cs, o);
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
       pbits = 32u;
@@ -1414,7 +1486,6 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       double dl = 0.0, el = 0.0;
       if (!(hflags & 1u) && c.pen_on) {
         const MassCoef mk = mass_coef(c, hm0);
-        const bool exm = exact_masses(c);
         const int ch = odd_chunk(V);
         const int lo = min(V, t * ch), hi = min(V, lo + ch);
         if (lo < hi) {
@@ -1428,14 +1499,12 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
             bits &= bits - 1;
             const float x = val[id];
             double d;
-            if (exm) {
-              d = mass_exact(x, c, hm0) - mass_exact(pen_exact(x, c.pen), c, hm0);
-            } else {
+            {   // fp32 masses: their error bounds join the decision margins
               float er0, er1;
               const float m_raw = mass_approx(x, mk, er0);
               const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
               d = (double)m_raw - (double)m_pen;
-              el += (double)er1;
+              el += (double)er0 + (double)er1;
             }
             atomicAdd(&cs.cdelta[chunk_of(id, hhead, hnch)], d);
             dl += d;
@@ -1546,7 +1615,11 @@ hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_
 hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_rowk, dim3(a.n_rows), dim3(NTC), 4 * ((size_t)vpad(a.vocab) + 4), s, a, w);
+  const size_t lds = 4 * ((size_t)vpad(a.vocab) + 4);
+  if ((a.vocab >> 2) <= 8 * NTC)   // body quads of any alignment fit 8 per thread
+    hipLaunchKernelGGL(k_stream_rowk<8>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
+  else
+    hipLaunchKernelGGL(k_stream_rowk<kQuadsC>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
   return hipGetLastError();
 }
 
