@@ -42,7 +42,7 @@ namespace {
 
 constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
-constexpr size_t kChainStaticLds = 32 * 1024;      // chain kernel static LDS (upper bound)
+constexpr size_t kChainStaticLds = 36 * 1024;      // chain kernels' static LDS (upper bound)
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
 constexpr int kFastRounds = 3;
@@ -259,7 +259,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   const bool two_phase = !(st->flags & C4S_STREAM_SEQUENTIAL) &&
-                         c4s::stream_chain_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit;
+                         c4s::stream_chain_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit &&
+                         c4s::stream_rowk_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit;
   if (!two_phase) {
     hipError_t e = c4s::launch_stream(a, hs);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");

@@ -41,23 +41,28 @@ constexpr int NW = NT / kWave;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 
-struct Scratch {
+// Workgroup scratch of the chain for NWX wavefronts (the chain functions take
+// their workgroup size from it).
+template <int NWX>
+struct ScratchT {
+  static constexpr int kWaves = NWX;
   uint32_t hcnt[256];
   double hmass[256];
-  double redd[NW];
-  float redf[NW];
-  float redf2[NW];
-  float redf3[NW];
-  int redi[NW];
-  uint32_t redu[NW];
-  double wmass[NW];
-  uint32_t wcnt[NW];
+  double redd[NWX];
+  float redf[NWX];
+  float redf2[NWX];
+  float redf3[NWX];
+  int redi[NWX];
+  uint32_t redu[NWX];
+  double wmass[NWX];
+  uint32_t wcnt[NWX];
   uint32_t bu[8];
   double bd[8];
   int bi[8];
   uint32_t counter;
   uint32_t step_stats[4];
 };
+using Scratch = ScratchT<NW>;
 
 // Bound on |sequential - parallel| for non-negative double sums over n terms,
 // relative to the compared quantities (see file header).
@@ -174,8 +179,9 @@ struct GlobalRow {
 struct Seg {
   int lo, hi;
 };
+template <int NWX = NW>
 __device__ __forceinline__ Seg my_seg(int V) {
-  const int seg = (V + NW - 1) / NW;
+  const int seg = (V + NWX - 1) / NWX;
   const int lo = min(V, wave_id() * seg);
   return Seg{lo, min(V, lo + seg)};
 }
@@ -184,14 +190,15 @@ __device__ __forceinline__ Seg my_seg(int V) {
 // Key of the m-th largest element (1-based, with multiplicity) among keyfn(i)
 // for i in [0, V); also the number of keys strictly greater (`gt`) and equal
 // (`eq`) to it.
-template <class KeyFn>
-__device__ uint32_t select_desc(KeyFn keyfn, Seg sg, Scratch& sh, uint32_t m, uint32_t& gt,
+template <int NWX, class KeyFn>
+__device__ uint32_t select_desc(KeyFn keyfn, Seg sg, ScratchT<NWX>& sh, uint32_t m, uint32_t& gt,
                                 uint32_t& eq) {
+  constexpr int NTX = NWX * kWave;
   uint32_t prefix = 0, mask = 0, rem = m;
   gt = 0;
   eq = 0;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += NT) sh.hcnt[b] = 0;
+    for (int b = threadIdx.x; b < 256; b += NTX) sh.hcnt[b] = 0;
     __syncthreads();
     for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
       const uint32_t k = keyfn(i);
@@ -234,15 +241,16 @@ __device__ uint32_t select_desc(KeyFn keyfn, Seg sg, Scratch& sh, uint32_t m, ui
 // On success: R = positions (ascending, all V ids) the reference removes by
 // `cum <= 1 - p`, wkey/eq = the crossing group, nkeep = how many of that group
 // stay (its lowest ids).
-template <class Src>
-__device__ bool cut_by_mass(const Src& src, Seg sg, Scratch& sh, float maxv, double A, double eps,
+template <int NWX, class Src>
+__device__ bool cut_by_mass(const Src& src, Seg sg, ScratchT<NWX>& sh, float maxv, double A, double eps,
                             int V, long long& R, uint32_t& wkey, uint32_t& eq, uint32_t& nkeep) {
+  constexpr int NTX = NWX * kWave;
   uint32_t prefix = 0, mask = 0;
   double blow = 0.0;
   uint32_t cnt_low = 0;
   bool ok = true;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += NT) { sh.hcnt[b] = 0; sh.hmass[b] = 0.0; }
+    for (int b = threadIdx.x; b < 256; b += NTX) { sh.hcnt[b] = 0; sh.hmass[b] = 0.0; }
     __syncthreads();
     for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
       const float zi = src.z(i);
@@ -346,11 +354,13 @@ __device__ bool cut_by_mass(const Src& src, Seg sg, Scratch& sh, float maxv, dou
 
 // ---- exact sequential emulations -----------------------------------------------
 
-// In-buffer ascending bitonic sort of P (a power of two) keys by the workgroup.
+// In-buffer ascending bitonic sort of P (a power of two) keys by the NTX
+// threads of the workgroup.
+template <int NTX>
 __device__ void bitonic_sort_u32(uint32_t* buf, int P) {
   for (int k = 2; k <= P; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int t = threadIdx.x; t < (P >> 1); t += NT) {
+      for (int t = threadIdx.x; t < (P >> 1); t += NTX) {
         const int i = (t / j) * 2 * j + (t % j);
         const int pi = i + j;
         const uint32_t a = buf[i], b = buf[pi];
@@ -366,9 +376,10 @@ __device__ void bitonic_sort_u32(uint32_t* buf, int P) {
 // sampling.cpp:52-65 literally (sequential double sum, then sequential
 // cum += prob/sum against 1 - p). Returns R over all V positions (the -inf
 // positions come first in ascending order with probability 0).
-template <class Src>
-__device__ long long exact_top_p(const Src& src, Seg sg, Scratch& sh, float maxv, double thr,
+template <int NWX, class Src>
+__device__ long long exact_top_p(const Src& src, Seg sg, ScratchT<NWX>& sh, float maxv, double thr,
                                  int V, uint32_t* buf, uint32_t& n_fin_out) {
+  constexpr int NTX = NWX * kWave;
   if (threadIdx.x == 0) sh.counter = 0;
   __syncthreads();
   for (int i = sg.lo + lane_id(); i < sg.hi; i += kWave) {
@@ -382,9 +393,9 @@ __device__ long long exact_top_p(const Src& src, Seg sg, Scratch& sh, float maxv
   const uint32_t n_fin = sh.counter;
   int P = 1;
   while (P < (int)n_fin) P <<= 1;
-  for (int i = n_fin + threadIdx.x; i < P; i += NT) buf[i] = 0xFFFFFFFFu;
+  for (int i = n_fin + threadIdx.x; i < P; i += NTX) buf[i] = 0xFFFFFFFFu;
   __syncthreads();
-  bitonic_sort_u32(buf, P);
+  bitonic_sort_u32<NTX>(buf, P);
   if (wave_id() == 0) {
     const int l = lane_id();
     double total = 0.0;
@@ -468,7 +479,8 @@ constexpr int kRegionCap = 64;    // candidates one wave may contribute
 constexpr int kMaxSlots = kLdsVocabMax / (NW * kWave);
 static_assert(kMaxSlots * NW * kWave == kLdsVocabMax, "slots cover the LDS-staged rows");
 
-__device__ __forceinline__ int odd_chunk(int V) { return ((V + NT - 1) / NT) | 1; }
+template <int NTX = NT>
+__device__ __forceinline__ int odd_chunk(int V) { return ((V + NTX - 1) / NTX) | 1; }
 
 struct FastBuf {
   float* ry;       // [NW][kRegionCap]
@@ -796,11 +808,12 @@ __device__ __forceinline__ bool fast_topk_any(const float* val, int V, const Row
 }
 
 // ---- the chain ------------------------------------------------------------------
-template <class Src>
-__device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, float* masked,
-                         uint32_t* stats) {
+template <int NWX, class Src>
+__device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowCfg& c, uint64_t& rng,
+                                         float* masked, uint32_t* stats) {
+  constexpr int NTX = NWX * kWave;
   const int V = c.V;
-  const Seg sg = my_seg(V);
+  const Seg sg = my_seg<NWX>(V);
   const int lane = lane_id();
   uint32_t st_path = 0, st_tp_exact = 0, st_draw_exact = 0, st_kept = 0;
 
@@ -808,7 +821,7 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
     float bv = neg_inf();
     int bi = INT_MAX;
     for (int i = sg.lo + lane; i < sg.hi; i += kWave) argmax_merge(bv, bi, src.z(i), i);
-    block_argmax<NT>(bv, bi, sh.redf, sh.redi);
+    block_argmax<NTX>(bv, bi, sh.redf, sh.redi);
     if (masked)
       for (int i = sg.lo + lane; i < sg.hi; i += kWave) masked[i] = src.z(i);
     if (stats && threadIdx.x == 0) { stats[0] = 8u; stats[1] = 0; stats[2] = 0; stats[3] = V; }
@@ -830,7 +843,7 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
   if (c.topp_on || c.draw) {
     float lm = neg_inf();
     for (int i = sg.lo + lane; i < sg.hi; i += kWave) lm = fmaxf(lm, src.z(i));
-    maxv = block_max_f32<NT>(lm, sh.redf);
+    maxv = block_max_f32<NTX>(lm, sh.redf);
   }
 
   Keep kp{kKeepAll, 0u, 0u, false};
@@ -847,7 +860,7 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
       sl += e;
       zl += (e == 0.0) ? 1u : 0u;
     }
-    const double S = block_sum_f64<NT>(sl, sh.redd);
+    const double S = block_sum_f64<NTX>(sl, sh.redd);
     cache_ok = Src::kCache;
     const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 compares cum <= (1.0 - p)
     long long R = 0;
@@ -856,7 +869,7 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
     if (thr < 0.0) {
       R = 0;
     } else if (thr == 0.0) {
-      R = block_sum_u32<NT>(zl, sh.redu);  // only zero-probability positions have cum == 0
+      R = block_sum_u32<NTX>(zl, sh.redu);  // only zero-probability positions have cum == 0
     } else {
       const double eps = rel_eps(V);
       if (cut_by_mass(src, sg, sh, maxv, thr * S, eps, V, R, cwkey, ceq, cnkeep)) {
@@ -943,7 +956,7 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
       }
     }
   }
-  st_kept = block_sum_u32<NT>(kl, sh.redu);
+  st_kept = block_sum_u32<NTX>(kl, sh.redu);
 
   int tok = 0;
   if (c.draw) {
@@ -952,15 +965,15 @@ __device__ int run_chain(Src& src, Scratch& sh, const RowCfg& c, uint64_t& rng, 
     __syncthreads();
     // Per-wave exclusive prefixes and the total, summed in a fixed order.
     double tot = 0.0;
-    for (int w = 0; w < NW; ++w) tot += sh.wmass[w];
+    for (int w = 0; w < NWX; ++w) tot += sh.wmass[w];
     rng = xorshift64(rng);
     const double u = unit_from_state(rng);
     const double r = u * tot;
-    int owner = NW - 1;
+    int owner = NWX - 1;
     double xown = 0.0;
     {
       double x = 0.0;
-      for (int w = 0; w < NW; ++w) {
+      for (int w = 0; w < NWX; ++w) {
         const double nx = x + sh.wmass[w];
         if (nx >= r) { owner = w; xown = x; break; }
         x = nx;
@@ -1142,9 +1155,10 @@ __device__ __forceinline__ float* store_row(const float* p, int V, const RowFetc
 }
 
 // Repetition penalty on the LDS row (sampling.cpp:19-28): every id whose bit is
-// set in `bitmap` is penalised once. Thread t handles its own id chunk.
+// set in `bitmap` is penalised once. Thread t of NTX handles its own id chunk.
+template <int NTX = NT>
 __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitmap, int V, float pen) {
-  const int ch = odd_chunk(V);
+  const int ch = odd_chunk<NTX>(V);
   const int lo = min(V, (int)threadIdx.x * ch);
   const int hi = min(V, lo + ch);
   if (lo >= hi) return;

@@ -124,6 +124,7 @@ hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_
 hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
+size_t stream_rowk_lds_bytes(int vocab);
 hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);

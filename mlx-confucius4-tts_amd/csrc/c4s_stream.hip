@@ -206,7 +206,7 @@ __device__ void bitonic_desc_u64(uint64_t* v, int P) {
 // One workgroup scans steps [s0, s1) of one row. Thread t holds the float4
 // quads t + 256 j of the 16-byte aligned body and one head or tail id.
 template <int NQ>
-__global__ __launch_bounds__(NTA, 4) void k_stream_scan(StreamArgs a, StreamWs w) {
+__global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w) {
   __shared__ ScanSh sh;
   const int row = blockIdx.y;
   const int V = a.vocab;
@@ -1187,6 +1187,7 @@ template <int NQC>
 __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ ChainSh cs;
+  __shared__ ScratchT<NWC> xs;   // exact steps
   __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
   const int row = blockIdx.x;
   const int V = a.vocab;
@@ -1198,7 +1199,8 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   const uint32_t* stw = w.state + (size_t)row * kStateWords;
   for (int i = t; i < kMaxChunks; i += NTC) cs.cdelta[i] = 0.0;
   fast_bitmaps(a, stw, row, V, NTC, bmH0, bmN, true);
-  float* vbuf = reinterpret_cast<float*>(smem);
+  double* E = reinterpret_cast<double*>(smem);   // exact steps: masses by id, sort keys
+  float* vbuf = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
   uint64_t rng = a.rng[row];
   uint32_t acc[4] = {0u, 0u, 0u, 0u};
   if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
@@ -1212,7 +1214,8 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) Sg.w[i] = sw[t + NTC * i];   // inside the 1024-word stride
   };
-  // One step; false when it has to be run exactly (nothing changed then).
+  // One step; false when the summary cannot settle it (nothing changed then,
+  // and the raw row of step s stays staged in LDS).
   auto step = [&](int s, SumRegsC& Sg, RowRegsC<NQC>& R) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     if (done) {
@@ -1304,20 +1307,52 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
     return true;
   };
 
+  // The fast loop stops at a step the summary cannot settle; that step runs
+  // the exact chain here, outside the loop, so that no prefetch is live across
+  // it (its register demand would otherwise spill the loop), and the loop is
+  // primed again from the next step.
   RowRegsC<NQC> R;
   SumRegsC SA, SB;
-  load_sum(s_first, SA);
-  if (s_first + 1 < w.s_end) load_sum(s_first + 1, SB);
-  fetch_row_c(base + (int64_t)s_first * a.step_stride, V, R);
   int s = s_first;
-  bool pending = false;
   while (s < w.s_end) {
-    if (!step(s, SA, R)) { pending = true; break; }
-    if (++s >= w.s_end) break;
-    if (!step(s, SB, R)) { pending = true; break; }
+    load_sum(s, SA);
+    if (s + 1 < w.s_end) load_sum(s + 1, SB);
+    fetch_row_c(base + (int64_t)s * a.step_stride, V, R);
+    bool bail = false;
+    while (s < w.s_end) {
+      if (!step(s, SA, R)) { bail = true; break; }
+      if (++s >= w.s_end) break;
+      if (!step(s, SB, R)) { bail = true; break; }
+      ++s;
+    }
+    if (!bail) break;
+    // text2semantic.cpp:142-166 on the whole staged row: penalty over H0 and
+    // the stream's ids (disjoint sets, so each id once), then the chain.
+    const float* cur = base + (int64_t)s * a.step_stride;
+    float* val = vbuf + ((4 - row_shape(cur, V).head) & 3);
+    __syncthreads();
+    if (c.pen_on) {
+      penalise_chunk<NTC>(val, bmH0, V, c.pen);
+      penalise_chunk<NTC>(val, bmN, V, c.pen);
+    }
+    __syncthreads();
+    LdsRow src{val, E, V, 0u, false};
+    const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
+    if (t == 0) {
+      const uint32_t* stp = xs.step_stats;
+      a.out_tok[(int64_t)s * a.n_rows + row] = tok;
+      acc[0] |= stp[0];
+      acc[1] += 1u;
+      acc[2] += stp[2];
+      acc[3] += stp[3];
+      if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
+        bmN[tok >> 5] |= 1u << (tok & 31);
+    }
+    __syncthreads();
+    if (tok == a.stop_token) done = true;
     ++s;
   }
-  fast_end(a, w, row, V, NTC, s, pending, done, rng, acc, bmN);
+  fast_end(a, w, row, V, NTC, s, false, done, rng, acc, bmN);
 }
 
 // ---- repair: the pending step of each row, exactly ------------------------------------
@@ -1612,10 +1647,12 @@ hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_
   return hipGetLastError();
 }
 
+size_t stream_rowk_lds_bytes(int V) { return 8 * (size_t)vpad(V) + 4 * ((size_t)vpad(V) + 4); }
+
 hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  const size_t lds = 4 * ((size_t)vpad(a.vocab) + 4);
+  const size_t lds = stream_rowk_lds_bytes(a.vocab);
   if ((a.vocab >> 2) <= 8 * NTC)   // body quads of any alignment fit 8 per thread
     hipLaunchKernelGGL(k_stream_rowk<8>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
   else
