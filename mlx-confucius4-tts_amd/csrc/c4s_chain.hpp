@@ -85,7 +85,7 @@ struct RowCfg {
   int min_keep;
 };
 
-__device__ RowCfg make_cfg(const uint32_t mode, int V, int row, const float* temp,
+__device__ __forceinline__ RowCfg make_cfg(const uint32_t mode, int V, int row, const float* temp,
                            const int32_t* top_k, const float* top_p, const float* pen,
                            const int32_t* min_keep, const uint8_t* do_sample) {
   RowCfg c;
@@ -1099,7 +1099,7 @@ __host__ __device__ __forceinline__ int bitmap_words(int V) { return ((V + 31) /
 
 // `val` is the row buffer base (vpad(V) + 4 floats); a row is stored at
 // val + shift so that its float4 body is 16-byte aligned in LDS.
-__device__ LdsLayout lds_layout(unsigned char* smem, int V) {
+__device__ __forceinline__ LdsLayout lds_layout(unsigned char* smem, int V) {
   LdsLayout L;
   L.E = reinterpret_cast<double*>(smem);
   L.val = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
@@ -1174,6 +1174,65 @@ __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitma
   }
 }
 
+
+// ---- draw over one candidate per lane ------------------------------------------
+
+// Inverse-CDF draw (text2semantic.cpp:150-165) over at most one kept entry per
+// lane: id, mass e, and slot = its rank in id order among the scan's
+// candidates (distinct, below kCandCap). The entries move to lanes in id order
+// (rank by ballots over the slot bits, then a lane permute) and one prefix
+// scan forms the id-order sums. The reference sums sequentially, so the first
+// lane reaching r = u * total decides only with the margin rel_eps; otherwise
+// the id-order sums are replayed sequentially (ids outside the kept set weigh 0).
+__device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, double u, int V, uint32_t& exact) {
+  const int lane = lane_id();
+  const double eps = rel_eps(V);
+  const uint64_t km = __ballot(kept);
+  const int nk = __popcll(km);
+  // position among the kept entries in id order
+  uint64_t same = km;
+  int pos = 0;
+#pragma unroll
+  for (int b = 9; b >= 0; --b) {
+    const bool bit = kept && ((slot >> b) & 1);
+    const uint64_t one = __ballot(bit);
+    pos += bit ? __popcll(same & ~one) : 0;
+    same &= bit ? one : ~one;
+  }
+  static_assert(kCandCap <= 1024, "slots have ten bits");
+  const int a4 = (kept ? pos : kWave - 1) << 2;   // lanes past nk are ignored
+  const uint64_t eb = (uint64_t)__double_as_longlong(e);
+  const uint32_t plo = (uint32_t)__builtin_amdgcn_ds_permute(a4, (int)(uint32_t)eb);
+  const uint32_t phi = (uint32_t)__builtin_amdgcn_ds_permute(a4, (int)(uint32_t)(eb >> 32));
+  const int pid = __builtin_amdgcn_ds_permute(a4, id);
+  const bool in = lane < nk;
+  const double es = in ? __longlong_as_double((long long)(((uint64_t)phi << 32) | plo)) : 0.0;
+  const int ids = in ? pid : 0;
+  const double acc = wave_scan_f64(es);
+  const double r = u * readlane_f64(acc, kWave - 1);
+  const uint64_t hit = __ballot(in && es > 0.0 && acc >= r);
+  if (r > 0.0 && hit) {
+    const int f = __ffsll((unsigned long long)hit) - 1;
+    const double af = readlane_f64(acc, f), pf = af - readlane_f64(es, f);
+    if ((af - r > eps * af) && (r - pf > eps * r)) {
+      exact = 0;
+      return (int)readlane_u32((uint32_t)ids, f);
+    }
+  }
+  // text2semantic.cpp:152-164 sequentially in id order
+  exact = 1;
+  double total = 0.0;
+  for (int j = 0; j < nk; ++j) total += readlane_f64(es, j);
+  const double rr = u * total;
+  if (rr <= 0.0) return 0;
+  double run = 0.0;
+  for (int j = 0; j < nk; ++j) {
+    const double ej = readlane_f64(es, j);
+    run += ej;
+    if (ej > 0.0 && rr <= run) return (int)readlane_u32((uint32_t)ids, j);
+  }
+  return V - 1;
+}
 
 }  // namespace
 }  // namespace c4s

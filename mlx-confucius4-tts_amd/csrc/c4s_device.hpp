@@ -14,6 +14,12 @@
 #ifndef C4S_PHASE
 #define C4S_PHASE(n) ((void)0)
 #endif
+#ifndef C4S_SCAN_PHASE
+#define C4S_SCAN_PHASE(n) ((void)0)
+#endif
+#ifndef C4S_LIST_PHASE
+#define C4S_LIST_PHASE(n) ((void)0)
+#endif
 
 namespace c4s {
 

@@ -240,6 +240,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
   const float pen = c.pen, rpen = 1.0f / c.pen;
 
   for (int s = s0; s < s1; ++s) {
+    C4S_SCAN_PHASE(0);
     const float* p = a.logits + (int64_t)s * a.step_stride + (int64_t)row * a.ld;
     const RowShape rs = row_shape(p, V);
     const float4* p4 = reinterpret_cast<const float4*>(p + rs.head);
@@ -268,6 +269,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       }
     }
     if (eh || et) ins(fkey(xe));
+    C4S_SCAN_PHASE(1);
 
     // L0: a key at or below the msel-th largest of those keys (two 11-bit passes).
     for (int i = t; i < 2048; i += NTA) sh.hist[i] = 0u;
@@ -293,6 +295,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
         L0 = (b1 << 21) | (b2 << 10);
       }
     }
+    C4S_SCAN_PHASE(2);
 
     // Candidates (key >= L0) compacted in id order: head, body quads by slot, tail.
     uint32_t cnt[NQ + 2];
@@ -344,6 +347,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       C += tot;
     }
     const bool overflow = C > (uint32_t)kCandCap;
+    C4S_SCAN_PHASE(3);
     if (!overflow) {
       auto put = [&](uint32_t pos, float x, int id) {
         const float y = bit_of(sh.bm, id) && c.pen_on ? pen_exact(x, pen) : x;
@@ -370,7 +374,9 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
     if (!overflow)
       for (int i = (int)C + t; i < P; i += NTA) sh.cand[i] = 0ull;
     __syncthreads();
+    C4S_SCAN_PHASE(4);
     if (!overflow) bitonic_desc_u64(sh.cand, P);
+    C4S_SCAN_PHASE(5);
 
     // Leading entries above the bound, at most cap of them.
     uint32_t nabove = 0;
@@ -395,6 +401,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       }
     }
 
+    C4S_SCAN_PHASE(6);
     // Chunk masses of the whole row (rows without top-k).
     float m0 = 0.f;
     int nchunk = 0;
@@ -464,6 +471,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       for (int i = t; i < nchunk; i += NTA) { chk[i] = sh.chunk[i]; cl += sh.chunk[i]; }
       s0 = block_sum_f64<NTA>(cl, sh.redd);
     }
+    C4S_SCAN_PHASE(7);
     if (t == 0) {
       SumHdr h{};
       h.n = bad ? 0 : n;
@@ -477,6 +485,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       *hdr = h;
     }
     __syncthreads();
+    C4S_SCAN_PHASE(8);
   }
 }
 
@@ -634,55 +643,6 @@ enum : uint32_t {
   kWhyTiny = 8,       // subnormal masses
 };
 
-// Inverse-CDF draw (text2semantic.cpp:150-165) over at most one kept entry per
-// lane (id, mass e). Each lane sums the kept masses at or below its id; the
-// reference sums in id order, so the decision keeps the margin rel_eps, else
-// the sums are replayed sequentially in id order.
-__device__ int lane_draw(bool kept, int id, double e, double u, int V, uint32_t& exact) {
-  const double eps = rel_eps(V);
-  const double ek = kept ? e : 0.0;
-  double acc = 0.0;
-  for (uint64_t m = __ballot(kept); m; m &= m - 1) {
-    const int j = __ffsll((unsigned long long)m) - 1;
-    const int idj = (int)readlane_u32((uint32_t)id, j);
-    const double ej = readlane_f64(ek, j);
-    acc += (idj <= id) ? ej : 0.0;
-  }
-  const double r = u * wave_sum_dpp(ek);
-  const uint32_t tid = wave_min_u32_dpp((kept && acc >= r) ? (uint32_t)id : 0xFFFFFFFFu);
-  if (r > 0.0 && tid != 0xFFFFFFFFu) {
-    const int f = __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == tid)) - 1;
-    const double af = readlane_f64(acc, f), pf = af - readlane_f64(ek, f);
-    if ((af - r > eps * af) && (r - pf > eps * r)) {
-      exact = 0;
-      return (int)tid;
-    }
-  }
-  // text2semantic.cpp:152-164 sequentially in id order; other ids weigh 0
-  exact = 1;
-  double total = 0.0;
-  uint32_t last = 0xFFFFFFFFu;
-  for (;;) {   // pass 1: total
-    const uint32_t nx = wave_min_u32_dpp((kept && (last == 0xFFFFFFFFu || (uint32_t)id > last)) ? (uint32_t)id : 0xFFFFFFFFu);
-    if (nx == 0xFFFFFFFFu) break;
-    total += readlane_f64(ek, __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == nx)) - 1);
-    last = nx;
-  }
-  const double rr = u * total;
-  if (rr <= 0.0) return 0;
-  double run = 0.0;
-  last = 0xFFFFFFFFu;
-  for (;;) {   // pass 2: first id with rr <= acc
-    const uint32_t nx = wave_min_u32_dpp((kept && (last == 0xFFFFFFFFu || (uint32_t)id > last)) ? (uint32_t)id : 0xFFFFFFFFu);
-    if (nx == 0xFFFFFFFFu) break;
-    const double en = readlane_f64(ek, __ffsll((unsigned long long)__ballot(kept && (uint32_t)id == nx)) - 1);
-    run += en;
-    if (en > 0.0 && rr <= run) return (int)nx;
-    last = nx;
-  }
-  return V - 1;
-}
-
 // Candidate-list step for greedy and top-k rows (one wave; two entries per
 // lane: keys e0, e1 and their values before the temperature yb0, yb1).
 // Returns false (nothing changed) when a decision needs the exact step.
@@ -702,6 +662,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   float z0 = v0 ? kfloat(ent_key(e0)) : ninf, z1 = v1 ? kfloat(ent_key(e1)) : ninf;
   if (h0) { const float y = pen_exact(yb0, c.pen); z0 = c.temp_on ? y / c.temp : y; }
   if (h1) { const float y = pen_exact(yb1, c.pen); z1 = c.temp_on ? y / c.temp : y; }
+  C4S_LIST_PHASE(2);
 
   if (c.greedy) {   // text2semantic.cpp:144-145, argmax of the penalised row, first max wins
     const uint64_t k0 = v0 ? ((uint64_t)fkey(z0) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)id0) : 0ull;
@@ -737,6 +698,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   if (!(zk > ninf)) return false;
   if (h.tout != 0u && !(kfloat(h.tout) < zk)) return false;   // everything outside stays below
   const bool s0 = u0 && z0 >= zk, s1 = u1 && z1 >= zk;
+  C4S_LIST_PHASE(3);
   const int nsurv = __popcll(__ballot(s0)) + __popcll(__ballot(s1));
   o.why = kWhyTies;
   if (nsurv > kWave) return false;
@@ -747,6 +709,8 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   const bool sv = lane < nsurv;
   const float zs = sv ? cs.lz[lane] : ninf;
   const int ids = sv ? cs.lid[lane] : 0;
+  const int slot = sv ? cs.lslot[lane] : 0;
+  C4S_LIST_PHASE(4);
   // masses, top_p (sampling.cpp:52-65), min_keep (:67-68)
   const float zmax = readlane_f32(zs, 0);
   const double e = sv ? exp((double)(zs - zmax)) : 0.0;
@@ -773,7 +737,9 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   const long long m = (long long)V - (R < lim ? R : lim);
   const bool kept = sv && (long long)lane < m;
   const uint64_t st = xorshift64(rng);
-  o.tok = lane_draw(kept, ids, e, unit_from_state(st), V, o.dex);
+  C4S_LIST_PHASE(5);
+  o.tok = lane_draw(kept, ids, slot, e, unit_from_state(st), V, o.dex);
+  C4S_LIST_PHASE(6);
   o.kept = (uint32_t)__popcll(__ballot(kept));
   rng = st;
   return true;
@@ -885,7 +851,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
     if (!(wave_max_dpp(hm) < zq1)) return false;
     if (q <= kWave) {   // kept ranks [0, q) are the first chunk: lane = rank
       const bool kept = lane < q;
-      o.tok = lane_draw(kept, kept ? cs.lid[lane] : 0, e_first, u, V, o.dex);
+      o.tok = lane_draw(kept, kept ? cs.lid[lane] : 0, kept ? cs.lslot[lane] : 0, e_first, u, V, o.dex);
     } else {
       int nslot = 0;
       for (int b = 0; b < q; b += kWave) {
@@ -1092,11 +1058,13 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
       if (lane == 0) *outp = -1;
       return true;
     }
+    C4S_LIST_PHASE(0);
     const SumHdr h = hdr_lanes(r.hw);
     const uint64_t e0 = (lane < h.n) ? r.e0 : 0ull;
     const uint64_t e1 = (lane + kWave < h.n) ? r.e1 : 0ull;
     const float yb0 = r.y0, yb1 = r.y1;
     if (s + 4 < w.s_end) load(s + 4, r);
+    C4S_LIST_PHASE(1);
     StepOut o{0, 0u, 0u, 0u};
     const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, bmN, rng, cs, o);
     if (!ok) {
@@ -1114,6 +1082,7 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
         bmN[tok >> 5] |= 1u << (tok & 31);
     }
     wave_sync();
+    C4S_LIST_PHASE(7);
     if (tok == a.stop_token) done = true;
     return true;
   };

@@ -64,3 +64,81 @@ def test_wave_shift_and_integer_max():
         assert np.array_equal(nxt[:63], u[1:]) and nxt[63] == 0xdeadbeef
         assert (om.cpu().numpy().view(np.uint32) == u.max()).all()
         assert (oq.cpu().numpy().view(np.uint64) == q.max()).all()
+
+
+def _draw_reference(ids, e, u, V):
+    """text2semantic.cpp:152-164 over ids in ascending order (other ids weigh 0)."""
+    order = np.argsort(ids, kind="stable")
+    total = 0.0
+    for j in order:
+        total += float(e[j])
+    r = u * total
+    if r <= 0.0:
+        return 0
+    acc = 0.0
+    for j in order:
+        acc += float(e[j])
+        if r <= acc:
+            return int(ids[j])
+    return V - 1
+
+
+def test_lane_draw_id_order_and_replay():
+    """lane_draw: kept entries scattered over lanes in value order; the token is
+    the reference's id-order inverse CDF, including uniforms placed on a
+    cumulative boundary (sequential replay), zero masses and r = 0."""
+    import torch
+    L = C.CDLL(LIB)
+    rng = np.random.default_rng(11)
+    V, n = 8194, 400
+    kept = np.zeros((n, 64), np.uint8)
+    ids = np.zeros((n, 64), np.int32)
+    slots = np.zeros((n, 64), np.int32)
+    es = np.zeros((n, 64), np.float64)
+    us = np.zeros(n, np.float64)
+    expect = []
+    for c in range(n):
+        nk = int(rng.integers(1, 65))
+        ncand = int(rng.integers(nk, 1025))
+        cand = np.sort(rng.choice(V, ncand, replace=False))
+        pick = np.sort(rng.choice(ncand, nk, replace=False))
+        kind = c % 4
+        if kind == 0:
+            e = rng.random(nk) * 10.0 ** float(rng.integers(-6, 2))
+        elif kind == 1:
+            e = rng.integers(0, 4, nk).astype(np.float64)
+            e[rng.integers(0, nk)] = 1.0
+        elif kind == 2:
+            e = rng.random(nk) * 1e-9
+            e[rng.integers(0, nk)] = 5.0
+        else:
+            e = np.exp(-rng.random(nk) * 30.0)
+        cum = np.cumsum(e)
+        if kind == 1:       # r on a cumulative boundary
+            u = float(cum[int(rng.integers(0, nk))]) / float(cum[-1])
+        elif c % 40 == 3:
+            u = 0.0
+        else:
+            u = float(rng.random())
+        lanes = rng.permutation(64)[:nk]
+        kept[c, lanes] = 1
+        ids[c, lanes] = cand[pick]
+        slots[c, lanes] = pick
+        es[c, lanes] = e
+        junk = np.setdiff1d(np.arange(64), lanes)
+        ids[c, junk] = rng.integers(0, V, junk.size)
+        slots[c, junk] = rng.integers(0, 1024, junk.size)
+        es[c, junk] = rng.random(junk.size)
+        us[c] = u
+        expect.append(_draw_reference(cand[pick], e, u, V))
+    t = {k: torch.from_numpy(v.reshape(-1)).cuda() for k, v in
+         dict(kept=kept, ids=ids, slots=slots, es=es).items()}
+    tu = torch.from_numpy(us).cuda()
+    out = torch.zeros(2 * n, dtype=torch.int32, device="cuda")
+    assert L.c4s_selftest_draw(C.c_void_p(t["kept"].data_ptr()), C.c_void_p(t["ids"].data_ptr()),
+                               C.c_void_p(t["slots"].data_ptr()), C.c_void_p(t["es"].data_ptr()),
+                               C.c_void_p(tu.data_ptr()), V, n, C.c_void_p(out.data_ptr())) == 0
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().reshape(n, 2)
+    assert o[:, 0].tolist() == expect
+    assert o[1::4, 1].sum() > 20      # boundary cases went through the sequential replay
