@@ -36,6 +36,10 @@ struct c4s_ctx {
   // second stream: the two fast chain kernels run side by side
   hipStream_t side = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  // third stream: the scan of the next chunk of steps beside the chain of this one
+  hipStream_t scan_s = nullptr;
+  hipEvent_t ev_start = nullptr;
+  hipEvent_t ev_scan[2] = {nullptr, nullptr}, ev_chain[2] = {nullptr, nullptr};
 };
 
 namespace {
@@ -43,8 +47,13 @@ namespace {
 constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
 constexpr size_t kChainStaticLds = 36 * 1024;      // chain kernels' static LDS (upper bound)
+constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's static LDS (upper bound)
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
+// Steps per chunk. A scan of the next chunk beside the chain of this one is
+// supported, but today's scan occupies every CU and slows the chain more than
+// it saves, so a chunk is as long as the summary budget allows.
+constexpr int kOverlapChunk = 1 << 30;
 constexpr int kFastRounds = 3;
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
@@ -188,8 +197,14 @@ int c4s_create(int device, c4s_ctx** out) {
   }
   if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->scan_s, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_scan[0], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_scan[1], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_chain[0], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_chain[1], hipEventDisableTiming) != hipSuccess) {
     c4s_destroy(ctx);
     return C4S_EHIP;
   }
@@ -202,12 +217,15 @@ int c4s_destroy(c4s_ctx* ctx) {
   DeviceGuard g(ctx->device);
   if (ctx->host_stream) (void)hipStreamSynchronize(ctx->host_stream);
   if (ctx->side) (void)hipStreamSynchronize(ctx->side);
+  if (ctx->scan_s) (void)hipStreamSynchronize(ctx->scan_s);
   for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws})
     if (p) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
-  if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
-  if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
+  if (ctx->scan_s) (void)hipStreamDestroy(ctx->scan_s);
+  for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1],
+                        ctx->ev_chain[0], ctx->ev_chain[1]})
+    if (ev) (void)hipEventDestroy(ev);
   delete ctx;
   return C4S_OK;
 }
@@ -266,23 +284,52 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");
     return C4S_OK;
   }
-  // Steps go in chunks whose summaries fit the workspace budget; the chain
-  // carries its per-row state from chunk to chunk.
+  // Steps go in chunks; the chain carries its per-row state from chunk to
+  // chunk. The scan of chunk c+1 runs on its own stream beside the chain of
+  // chunk c; summaries are double-buffered and a scan waits for the chain
+  // that last read its buffer.
   const size_t per_step = (size_t)a.n_rows * c4s::kSumStride;
-  const int chunk = (int)std::max<size_t>(1, std::min<size_t>((size_t)a.n_steps, kSumBudget / per_step));
-  int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, per_step * (size_t)chunk, "stream summaries");
+  size_t chunk_sz = std::min<size_t>({(size_t)a.n_steps, (size_t)kOverlapChunk, kSumBudget / per_step});
+  if (chunk_sz < (size_t)a.n_steps) chunk_sz = std::min(chunk_sz, kSumBudget / 2 / per_step);   // two buffers
+  const int chunk = (int)std::max<size_t>(1, chunk_sz);
+  const size_t chunk_bytes = per_step * (size_t)chunk;
+  const int n_bufs = chunk < a.n_steps ? 2 : 1;
+  int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, (size_t)n_bufs * chunk_bytes, "stream summaries");
   if (rc) return rc;
   rc = ensure(ctx, &ctx->state_ws, &ctx->state_bytes, (size_t)a.n_rows * c4s::kStateWords * 4, "stream state");
   if (rc) return rc;
-  for (int s0 = 0; s0 < a.n_steps; s0 += chunk) {
+  // Full-vocabulary rows: the pipelined chain (three rows and summaries in LDS)
+  // where it fits; its exact steps sort in a per-row global key buffer.
+  const bool pipelined = c4s::stream_rowp_lds_bytes(a.vocab) + kRowPStaticLds <= kLdsLimit;
+  const size_t sort_row = pow2_at_least((size_t)a.vocab) * sizeof(uint32_t);
+  if (pipelined) {
+    rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, sort_row * (size_t)a.n_rows, "sort workspace");
+    if (rc) return rc;
+  }
+  auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
+    return pipelined ? c4s::launch_stream_rowp(a, w, on) : c4s::launch_stream_rowk(a, w, on);
+  };
+  hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
+  if (e0 == hipSuccess) e0 = hipStreamWaitEvent(ctx->scan_s, ctx->ev_start, 0);
+  if (e0 != hipSuccess) return hip_fail(ctx, e0, "sample_stream scan stream");
+  for (int s0 = 0, ci = 0; s0 < a.n_steps; s0 += chunk, ++ci) {
+    const int buf = ci & 1;
     c4s::StreamWs w{};
-    w.sum = static_cast<unsigned char*>(ctx->sum_ws);
+    w.sum = static_cast<unsigned char*>(ctx->sum_ws) + (size_t)buf * chunk_bytes;
     w.state = static_cast<uint32_t*>(ctx->state_ws);
     w.s_begin = s0;
     w.s_end = std::min(a.n_steps, s0 + chunk);
     w.steps_per_group = kScanStepsPerGroup;
-    hipError_t e = c4s::launch_stream_scan(a, w, hs);
+    w.sortbuf = pipelined ? static_cast<uint32_t*>(ctx->ws) : nullptr;
+    w.sort_stride = (int64_t)(sort_row / sizeof(uint32_t));
+    hipError_t e = hipSuccess;
+    if (ci >= 2 && (e = hipStreamWaitEvent(ctx->scan_s, ctx->ev_chain[buf], 0)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream buffer reuse");
+    e = c4s::launch_stream_scan(a, w, ctx->scan_s);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream scan launch");
+    if ((e = hipEventRecord(ctx->ev_scan[buf], ctx->scan_s)) != hipSuccess ||
+        (e = hipStreamWaitEvent(hs, ctx->ev_scan[buf], 0)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream scan order");
     // Fast passes stop a row at a step they cannot decide; the repair kernel
     // runs that step exactly; the finisher completes whatever is left.
     for (int r = 0; r < kFastRounds; ++r) {
@@ -291,7 +338,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
         if ((e = hipEventRecord(ctx->ev_fork, hs)) != hipSuccess ||
             (e = hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0)) != hipSuccess)
           return hip_fail(ctx, e, "sample_stream fork");
-        e = c4s::launch_stream_rowk(a, w, ctx->side);
+        e = launch_row_chain(w, ctx->side);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream row-chain launch");
         e = c4s::launch_stream_list(a, w, hs);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream list-chain launch");
@@ -300,7 +347,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
           return hip_fail(ctx, e, "sample_stream join");
       } else {
         e = c4s::launch_stream_list(a, w, hs);
-        if (e == hipSuccess) e = c4s::launch_stream_rowk(a, w, hs);
+        if (e == hipSuccess) e = launch_row_chain(w, hs);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
       }
       e = c4s::launch_stream_repair(a, w, hs);
@@ -308,6 +355,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     }
     e = c4s::launch_stream_chain(a, w, hs);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
+    if ((e = hipEventRecord(ctx->ev_chain[buf], hs)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream chain order");
   }
   return C4S_OK;
 }

@@ -141,6 +141,31 @@ struct LdsRow {
   __device__ uint32_t* sort_buf() const { return reinterpret_cast<uint32_t*>(E); }
 };
 
+// Row staged in LDS without a mass cache (kernels whose LDS holds several rows):
+// masses are recomputed per pass and the exact top_p pass sorts in a global
+// key buffer.
+struct LdsRowNC {
+  float* val;
+  int V;
+  uint32_t thr_key;
+  bool topk_on;
+  uint32_t* sortbuf;
+  static constexpr bool kCache = false;
+
+  __device__ float zraw(int i) const { return val[i]; }
+  __device__ float z(int i) const {
+    const float v = val[i];
+    return (topk_on && fkey(v) < thr_key) ? neg_inf() : v;
+  }
+  __device__ double cached(int) const { return 0.0; }
+  __device__ void cache(int, double) {}
+  __device__ void apply_temperature(float t, int lo, int hi) {
+    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = val[i] / t;
+    __syncthreads();
+  }
+  __device__ uint32_t* sort_buf() const { return sortbuf; }
+};
+
 // Row re-read from HBM on every pass.
 struct GlobalRow {
   const float* xf;

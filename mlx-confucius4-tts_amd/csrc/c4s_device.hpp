@@ -20,6 +20,9 @@
 #ifndef C4S_LIST_PHASE
 #define C4S_LIST_PHASE(n) ((void)0)
 #endif
+#ifndef C4S_HELPER_PHASE
+#define C4S_HELPER_PHASE(n) ((void)0)
+#endif
 
 namespace c4s {
 

@@ -97,6 +97,8 @@ struct StreamWs {
   int s_begin, s_end;      // steps of this chunk
   int steps_per_group;     // scan: steps per workgroup
   int round;               // chain rounds within the chunk (0: the first)
+  uint32_t* sortbuf;       // exact steps of the pipelined row chain: per-row key buffer
+  int64_t sort_stride;     // words per row
 };
 
 struct LmHeadArgs {
@@ -121,10 +123,12 @@ hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
 size_t stream_rowk_lds_bytes(int vocab);
+size_t stream_rowp_lds_bytes(int vocab);  // 0 when the pipelined row chain does not fit
 hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);

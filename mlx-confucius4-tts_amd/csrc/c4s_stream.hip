@@ -521,7 +521,8 @@ __device__ __forceinline__ void wave_sync() {
 // masses sit in cs.slotE at their id-order ranks [0, nslot) (zero elsewhere),
 // so slot order is id order. Wave 0 only. Returns the token; `exact` is set
 // when the margin test failed and the sums were replayed sequentially.
-__device__ int slot_draw(ChainSh& cs, int nslot, double u, int V, uint32_t& exact) {
+template <class CS>
+__device__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact) {
   const int lane = lane_id();
   const double eps = rel_eps(V);
   // pass 1: total in slot order (per lane 4 consecutive slots per block of 256)
@@ -593,7 +594,8 @@ __device__ int slot_draw(ChainSh& cs, int nslot, double u, int V, uint32_t& exac
 }
 
 // Clears slots [0, nslot) (wave 0).
-__device__ __forceinline__ void clear_slots(ChainSh& cs, int nslot) {
+template <class CS>
+__device__ __forceinline__ void clear_slots(CS& cs, int nslot) {
   for (int i = lane_id(); i < nslot; i += kWave) cs.slotE[i] = 0.0;
   wave_sync();
 }
@@ -745,20 +747,23 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   return true;
 }
 
-// Full-vocabulary step (wave 0). The summary is in cs.sum; also needs the
-// correction of the masses for ids drawn during the stream (dsum, its error
-// derr; per chunk in cs.cdelta) and the raw row in LDS (`val`). The list is
-// compacted lazily, 64 entries at a time, only as deep as the decision needs.
+// Full-vocabulary step (wave 0). The summary words are in LDS at `sum`; also
+// needs the correction of the masses for ids drawn during the stream (dsum,
+// its error derr; per chunk in `cdelta`) and the raw row in LDS (`val`). The
+// list is compacted lazily, 64 entries at a time, only as deep as the decision
+// needs; cs provides the compaction and slot arrays.
+template <class CS>
 __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
                          const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
-                         uint64_t& rng, ChainSh& cs, StepOut& o) {
+                         const uint64_t* sum, const double* cdelta, uint64_t& rng, CS& cs,
+                         StepOut& o) {
   const int lane = lane_id();
   o.why = kWhySummary;
   if (h.flags & 1u) return false;
   const int n = h.n;
   const float ninf = neg_inf();
-  const uint64_t* lst = cs.sum;
-  const float* ly = reinterpret_cast<const float*>(cs.sum + kYW);
+  const uint64_t* lst = sum;
+  const float* ly = reinterpret_cast<const float*>(sum + kYW);
   int nb = 0, nu = 0;
   float hm = ninf;
   // list block [nb, nb + 64): unhit entries to their ranks, penalised hits into hm
@@ -882,7 +887,7 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ci = 4 * lane + i;
-    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cs.sum[kChunkW + ci]) - cs.cdelta[ci] : 0.0;
+    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)sum[kChunkW + ci]) - cdelta[ci] : 0.0;
     cs_l += cv[i];
   }
   // Dense draw (top_p keeps every id of nonzero mass; zero masses never win):
@@ -1054,10 +1059,6 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
   // One step; false when it has to be run exactly (nothing changed then).
   auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
-    if (done) {
-      if (lane == 0) *outp = -1;
-      return true;
-    }
     C4S_LIST_PHASE(0);
     const SumHdr h = hdr_lanes(r.hw);
     const uint64_t e0 = (lane < h.n) ? r.e0 : 0ull;
@@ -1092,17 +1093,23 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
   if (s_first + 1 < w.s_end) load(s_first + 1, P1);
   if (s_first + 2 < w.s_end) load(s_first + 2, P2);
   if (s_first + 3 < w.s_end) load(s_first + 3, P3);
+  // A stopped row leaves the loop (no step path skips its prefetch) and
+  // reports -1 afterwards.
   int s = s_first;
   bool pending = false;
   while (s < w.s_end) {
     if (!step(s, P0)) { pending = true; break; }
-    if (++s >= w.s_end) break;
+    if (++s >= w.s_end || done) break;
     if (!step(s, P1)) { pending = true; break; }
-    if (++s >= w.s_end) break;
+    if (++s >= w.s_end || done) break;
     if (!step(s, P2)) { pending = true; break; }
-    if (++s >= w.s_end) break;
+    if (++s >= w.s_end || done) break;
     if (!step(s, P3)) { pending = true; break; }
-    ++s;
+    if (++s >= w.s_end || done) break;
+  }
+  if (done) {
+    for (int s2 = s + lane; s2 < w.s_end; s2 += kWave) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
+    s = w.s_end;
   }
   fast_end(a, w, row, V, kWave, s, pending, done, rng, acc, bmN);
 }
@@ -1187,10 +1194,6 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   // and the raw row of step s stays staged in LDS).
   auto step = [&](int s, SumRegsC& Sg, RowRegsC<NQC>& R) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
-    if (done) {
-      if (t == 0) *outp = -1;
-      return true;
-    }
     const float* cur = base + (int64_t)s * a.step_stride;
     C4S_PHASE(0);
 #pragma unroll
@@ -1198,8 +1201,8 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
       if (t + NTC * i < kSumWords) cs.sum[t + NTC * i] = Sg.w[i];
     float* val = store_row_c(cur, V, R, vbuf);
     C4S_PHASE(1);
-    if (s + 2 < w.s_end) load_sum(s + 2, Sg);
     if (s + 1 < w.s_end) fetch_row_c(cur + a.step_stride, V, R);
+    if (s + 2 < w.s_end) load_sum(s + 2, Sg);
     C4S_PHASE(2);
     __syncthreads();
     C4S_PHASE(3);
@@ -1246,7 +1249,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
         double ds = 0.0, de = 0.0;
         for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
         StepOut o{0, 0u, 0u, 0u};
-        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
+        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, cs.sum, cs.cdelta, rng, cs, o);
         for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
         const bool retry = !ok && !exact && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
         if (lane == 0) {
@@ -1282,17 +1285,19 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   // primed again from the next step.
   RowRegsC<NQC> R;
   SumRegsC SA, SB;
+  // A stopped row leaves the loop (no step path skips its prefetch, so the
+  // loop never waits on loads still in flight) and reports -1 afterwards.
   int s = s_first;
-  while (s < w.s_end) {
+  while (s < w.s_end && !done) {
     load_sum(s, SA);
     if (s + 1 < w.s_end) load_sum(s + 1, SB);
     fetch_row_c(base + (int64_t)s * a.step_stride, V, R);
     bool bail = false;
     while (s < w.s_end) {
       if (!step(s, SA, R)) { bail = true; break; }
-      if (++s >= w.s_end) break;
+      if (++s >= w.s_end || done) break;
       if (!step(s, SB, R)) { bail = true; break; }
-      ++s;
+      if (++s >= w.s_end || done) break;
     }
     if (!bail) break;
     // text2semantic.cpp:142-166 on the whole staged row: penalty over H0 and
@@ -1321,7 +1326,440 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
     if (tok == a.stop_token) done = true;
     ++s;
   }
+  for (int s2 = s + t; s2 < w.s_end; s2 += NTC) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
+  s = w.s_end;
   fast_end(a, w, row, V, NTC, s, false, done, rng, acc, bmN);
+}
+
+// ---- pipelined full-vocabulary chain ------------------------------------------------
+//
+// Wave 0 decides step s while waves 1-3 prepare step s+1: each helper wave
+// owns a third of the ids, loads that third of the raw row and of the summary
+// straight into LDS (global_load_lds, three slots in rotation, two steps
+// ahead) and computes the mass corrections of step s+1 for the ids drawn
+// during the stream up to step s-1 (fp32 masses with their error bounds).
+// Wave 0 then adds the exact correction of the one token it drew at step s-1
+// and decides; a decision inside the error bound is retried once with exact
+// corrections computed by all four wavefronts. The drawn-id bitmap is kept twice (by
+// step parity) so that wave 0 can record step s's token while the helpers read
+// the set of step s. Barriers only wait for LDS traffic; the helpers wait for
+// their own loads before reading them. A step the summary cannot settle runs
+// the exact chain with all four wavefronts on the staged row.
+
+constexpr int kSumQuads = (kSumWords + 1) / 2;          // 16-byte units of a summary
+constexpr int kSumWordsP = 2 * kSumQuads;               // summary slot in LDS (words)
+constexpr int kSumQPerWave = (kSumQuads + 2) / 3;       // per helper wave
+constexpr int kDrawnList = 512;                         // drawn ids listed per helper wave
+static_assert((size_t)kSumWordsP * 8 <= kSumStride, "whole quads stay inside a summary");
+static_assert(kHdrW % 2 == 0, "header words start a quad");
+
+struct RowPSh {
+  double cdelta[2][kMaxChunks];   // corrections per chunk, by step parity
+  double cdx[kMaxChunks];         // exact corrections of a retried step
+  double wd[2][4];                // helper waves' correction sums, by step parity
+  double we[2][4];                // and their error bounds
+  double xd[NWC];                 // exact corrections of a retried step, per wave
+  double slotE[kCandCap];
+  int slotId[kCandCap];
+  float lz[kListLarge];
+  int lid[kListLarge];
+  int lslot[kListLarge];
+  alignas(16) uint64_t hdr[2][3][8];   // per parity and helper wave: header copy
+  int dlist[3][kDrawnList];       // per helper wave: drawn ids of its range (while they fit)
+  int nt[2];                      // token of step s when it joined bmN, else -1, at [s & 1]
+  uint64_t rng;
+  int tok[2];                     // token of step s at [s & 1]
+  int flag[2];                    // 1: wave 0 decided step s, at [s & 1]
+};
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* glb_ptr_t;
+
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are
+// complete, global loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// Waits for every global load (and LDS load) this wave has in flight.
+__device__ __forceinline__ void wait_loads() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+}
+
+// Ids of helper wave h (0..2): [lo, hi), fixed for the row (multiples of 64
+// apart from the ends), and the body quads holding any of them (a quad that
+// straddles a boundary is loaded by both neighbours).
+struct Third {
+  int q0, q1;    // body quads
+  int lo, hi;    // ids
+};
+__device__ __forceinline__ int third_bound(int V, int h) {
+  return h <= 0 ? 0 : (h >= 3 ? V : ((h * V / 3) & ~63));
+}
+__device__ __forceinline__ Third third_of(const RowShape& r, int V, int h) {
+  Third th;
+  th.lo = third_bound(V, h);
+  th.hi = third_bound(V, h + 1);
+  th.q0 = 0;
+  th.q1 = 0;
+  if (th.hi > th.lo && r.nq > 0) {
+    th.q0 = max(0, (th.lo - r.head) >> 2);
+    const int last = th.hi - 1 - r.head;   // id offset of the last id from the body start
+    th.q1 = last < 0 ? 0 : min(r.nq, (last >> 2) + 1);
+    th.q0 = min(th.q0, th.q1);
+  }
+  return th;
+}
+
+// Loads of step s issued by helper wave h into its LDS slot: its third of the
+// row, its share of the summary quads, and its own copy of the header.
+__device__ __forceinline__ void dma_step(const float* p, int V, const uint64_t* sg, float* rowslot,
+                                         uint64_t* sumslot, uint64_t* hdrcopy, int h) {
+  const int lane = lane_id();
+  const RowShape r = row_shape(p, V);
+  float* val = rowslot + ((4 - r.head) & 3);   // val + head is 16-byte aligned
+  const Third th = third_of(r, V, h);
+  for (int q0 = th.q0; q0 < th.q1; q0 += kWave) {
+    const int q = q0 + lane;
+    if (q < th.q1)
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(p + r.head + 4 * q), (lds_ptr_t)(val + r.head + 4 * q0),
+                                       16, 0, 0);
+  }
+  if (lane < r.head && lane >= th.lo && lane < th.hi)
+    __builtin_amdgcn_global_load_lds((glb_ptr_t)(p + lane), (lds_ptr_t)(val), 4, 0, 0);
+  const int e0 = r.head + 4 * r.nq;
+  if (lane < r.tail && e0 + lane >= th.lo && e0 + lane < th.hi)
+    __builtin_amdgcn_global_load_lds((glb_ptr_t)(p + e0 + lane), (lds_ptr_t)(val + e0), 4, 0, 0);
+  const int s0 = h * kSumQPerWave, s1 = min(kSumQuads, s0 + kSumQPerWave);
+  for (int q0 = s0; q0 < s1; q0 += kWave) {
+    const int q = q0 + lane;
+    if (q < s1)
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(sg + 2 * q), (lds_ptr_t)(sumslot + 2 * q0), 16, 0, 0);
+  }
+  if (lane < 4)
+    __builtin_amdgcn_global_load_lds((glb_ptr_t)(sg + kHdrW + 2 * lane), (lds_ptr_t)(hdrcopy), 16, 0, 0);
+}
+
+// Corrections of one step over ids [lo, hi) drawn during the stream (bmN,
+// never in H0): the mass of the raw value minus that of the penalised value,
+// added to its chunk. fp32 masses with their error bound (el), or exact ones.
+__device__ __forceinline__ double corrections_range(const float* val, int lo, int hi, const uint32_t* bmN,
+                                                    const SumHdr& hh, const RowCfg& c, double* cdelta,
+                                                    bool exact, double& el) {
+  double dl = 0.0;
+  el = 0.0;
+  if (hh.flags & 1u) return 0.0;
+  const MassCoef mk = mass_coef(c, hh.m0);
+  const float rpen = 1.0f / c.pen;
+  for (int wb = lo >> 5; wb < ((hi + 31) >> 5); ++wb) {
+    uint32_t bits = bmN[wb];
+    const int b0 = 32 * wb;
+    if (b0 < lo) bits &= ~0u << (lo - b0);
+    if (b0 + 32 > hi) bits &= (hi - b0 >= 32) ? ~0u : ((1u << (hi - b0)) - 1u);
+    while (bits) {
+      const int id = b0 + __ffs(bits) - 1;
+      bits &= bits - 1;
+      const float x = val[id];
+      double d;
+      if (exact) {
+        d = mass_exact(x, c, hh.m0) - mass_exact(pen_exact(x, c.pen), c, hh.m0);
+      } else {
+        float er0, er1;
+        const float m_raw = mass_approx(x, mk, er0);
+        const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
+        d = (double)m_raw - (double)m_pen;
+        el += (double)er0 + (double)er1;
+      }
+      atomicAdd(&cdelta[chunk_of(id, hh.head, hh.nchunk)], d);
+      dl += d;
+    }
+  }
+  return dl;
+}
+
+// Lists the ids of [lo, hi) set in bmN into list (at most kDrawnList of them,
+// in id order); returns how many there are (wave-uniform).
+__device__ __forceinline__ int list_drawn(const uint32_t* bmN, int lo, int hi, int* list) {
+  const int lane = lane_id();
+  const int wa = lo >> 5, wz = (hi + 31) >> 5;
+  auto word = [&](int wb) __attribute__((always_inline)) -> uint32_t {
+    uint32_t bits = bmN[wb];
+    const int b0 = 32 * wb;
+    if (b0 < lo) bits &= ~0u << (lo - b0);
+    if (b0 + 32 > hi) bits &= (hi - b0 >= 32) ? ~0u : ((1u << (hi - b0)) - 1u);
+    return bits;
+  };
+  int n = 0;
+  for (int w0 = wa; w0 < wz; w0 += kWave) {
+    const int wb = w0 + lane;
+    uint32_t bits = wb < wz ? word(wb) : 0u;
+    const uint32_t cnt = (uint32_t)__popc(bits);
+    const uint32_t incl = wave_scan_u32(cnt);
+    int p = n + (int)(incl - cnt);
+    while (bits) {
+      if (p < kDrawnList) list[p] = 32 * wb + __ffs(bits) - 1;
+      bits &= bits - 1;
+      ++p;
+    }
+    n += (int)readlane_u32(incl, kWave - 1);
+  }
+  wave_sync();
+  return n;
+}
+
+// fp32 corrections of one step by helper wave h over the listed drawn ids of
+// its range (n of them, all listed); returns the wave's total and (in el) its
+// error bound, in all lanes. Two ids per lane at a time.
+__device__ __forceinline__ double listed_corrections(const float* val, const int* list, int n, const SumHdr& hh,
+                                                     const RowCfg& c, double* cdelta, double& el) {
+  const int lane = lane_id();
+  el = 0.0;
+  if (hh.flags & 1u) return 0.0;
+  const MassCoef mk = mass_coef(c, hh.m0);
+  const float rpen = 1.0f / c.pen;
+  double dl = 0.0, ell = 0.0;
+  for (int j = lane; j < n; j += 2 * kWave) {
+    const bool v1 = j + kWave < n;
+    const int i0 = list[j], i1 = v1 ? list[j + kWave] : i0;
+    const float x0 = val[i0], x1 = val[i1];
+    float e00, e01, e10, e11;
+    const float a0 = mass_approx(x0, mk, e00), b0 = mass_approx(pen_approx(x0, c.pen, rpen), mk, e01);
+    const float a1 = mass_approx(x1, mk, e10), b1 = mass_approx(pen_approx(x1, c.pen, rpen), mk, e11);
+    const double d0 = (double)a0 - (double)b0;
+    atomicAdd(&cdelta[chunk_of(i0, hh.head, hh.nchunk)], d0);
+    dl += d0;
+    ell += (double)e00 + (double)e01;
+    if (v1) {
+      const double d1 = (double)a1 - (double)b1;
+      atomicAdd(&cdelta[chunk_of(i1, hh.head, hh.nchunk)], d1);
+      dl += d1;
+      ell += (double)e10 + (double)e11;
+    }
+  }
+  el = wave_sum_dpp(ell);
+  return wave_sum_dpp(dl);
+}
+
+// fp32 corrections of one step by helper wave h over its range: from its list
+// while the drawn ids fit, else per lane from the bitmap.
+__device__ __forceinline__ double helper_corrections(const float* val, int V, int h, const uint32_t* bmN,
+                                                     const SumHdr& hh, const RowCfg& c, double* cdelta,
+                                                     const int* list, int n, double& el) {
+  if (n <= kDrawnList) return listed_corrections(val, list, n, hh, c, cdelta, el);
+  const int lane = lane_id();
+  const int lo_h = third_bound(V, h), hi_h = third_bound(V, h + 1);
+  const int ch = (hi_h - lo_h + kWave - 1) / kWave;
+  const int lo = min(hi_h, lo_h + lane * ch), hi = min(hi_h, lo + ch);
+  const double dl = corrections_range(val, lo, hi, bmN, hh, c, cdelta, false, el);
+  el = wave_sum_dpp(el);
+  return wave_sum_dpp(dl);
+}
+
+__global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ RowPSh ps;
+  __shared__ ScratchT<NWC> xs;   // exact steps
+  __shared__ uint32_t bmH0[kStateWords], bmNb[2][kStateWords];
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id(), hw = wv - 1;
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (stream_mode(c, V) != kModeRow) return;
+  int s_first;
+  if (!fast_begin(a, w, row, NTC, s_first)) return;
+  const uint32_t* stw = w.state + (size_t)row * kStateWords;
+  const int s_end = w.s_end;
+  uint64_t* sumslots = reinterpret_cast<uint64_t*>(smem);
+  float* rowslots = reinterpret_cast<float*>(smem + 3 * (size_t)kSumWordsP * 8);
+  const int RS = vpad(V) + 4;
+  auto sumslot = [&](int s) { return sumslots + (size_t)(s % 3) * kSumWordsP; };
+  auto rowslot = [&](int s) { return rowslots + (size_t)(s % 3) * RS; };
+  const float* base = a.logits + (int64_t)row * a.ld;
+  auto rowp = [&](int s) { return base + (int64_t)s * a.step_stride; };
+  auto rowval = [&](int s) { return rowslot(s) + ((4 - row_shape(rowp(s), V).head) & 3); };
+  uint32_t* sortbuf = w.sortbuf + (int64_t)row * w.sort_stride;
+
+  // prologue: bitmaps, the first two steps in flight, corrections of the first
+  fast_bitmaps(a, stw, row, V, NTC, bmH0, bmNb[s_first & 1], true);
+  const int nwords = bitmap_words(V);
+  for (int i = t; i < nwords; i += NTC) bmNb[(s_first + 1) & 1][i] = bmNb[s_first & 1][i];
+  for (int i = t; i < 2 * kMaxChunks; i += NTC) (&ps.cdelta[0][0])[i] = 0.0;
+  if (wv > 0) {
+    dma_step(rowp(s_first), V, sum_words(w, a.n_rows, s_first, row), rowslot(s_first), sumslot(s_first),
+             ps.hdr[s_first & 1][hw], hw);
+    if (s_first + 1 < s_end)
+      dma_step(rowp(s_first + 1), V, sum_words(w, a.n_rows, s_first + 1, row), rowslot(s_first + 1),
+               sumslot(s_first + 1), ps.hdr[(s_first + 1) & 1][hw], hw);
+  }
+  __syncthreads();   // cdelta cleared, bitmaps in place (also drains the loads)
+  int ndrawn = 0;    // helper wave: drawn ids of its range (listed while they fit)
+  if (wv > 0) {
+    const uint64_t* hc = ps.hdr[s_first & 1][hw];
+    const SumHdr hh = hdr_words(hc[0], hc[1], hc[2], hc[3], hc[4]);
+    ndrawn = list_drawn(bmNb[s_first & 1], third_bound(V, hw), third_bound(V, hw + 1), ps.dlist[hw]);
+    double d = 0.0, e = 0.0;
+    if (c.pen_on)
+      d = helper_corrections(rowval(s_first), V, hw, bmNb[s_first & 1], hh, c, ps.cdelta[s_first & 1],
+                             ps.dlist[hw], ndrawn, e);
+    if (lane == 0) { ps.wd[s_first & 1][hw] = d; ps.we[s_first & 1][hw] = e; }
+  }
+  if (t == 0) ps.rng = a.rng[row];
+  uint64_t rng = a.rng[row];
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};
+  if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
+  int tprev = -1;        // wave 0: token of the previous step when it joined bmN
+  bool done = false;
+  __syncthreads();
+
+  int s = s_first;
+  for (; s < s_end; ++s) {
+    const int par = s & 1;
+    const uint32_t* bmN = bmNb[par];
+    // Attempt 0: wave 0 decides with the fp32 corrections while the helpers
+    // prepare step s+1. Attempt 1 (a decision inside their error bound): all
+    // four wavefronts compute the exact corrections of step s, wave 0 decides
+    // again. One call site of row_step keeps it inlined.
+    for (int attempt = 0;; ++attempt) {
+      if (attempt == 1) {
+        const int ch = (V + NTC - 1) / NTC;
+        const int lo = min(V, t * ch), hi = min(V, lo + ch);
+        for (int i = t; i < kMaxChunks; i += NTC) ps.cdx[i] = 0.0;
+        __syncthreads();
+        double el;
+        double d = corrections_range(rowval(s), lo, hi, bmN, hdr_from(sumslot(s)), c, ps.cdx, true, el);
+        d = wave_sum_dpp(d);
+        if (lane == 0) ps.xd[wv] = d;
+        __syncthreads();
+      }
+      if (wv == 0) {
+        C4S_PHASE(0);
+        const uint64_t* sw = sumslot(s);
+        const float* val = rowval(s);
+        const SumHdr h = hdr_from(sw);
+        double ds, de;
+        double* cd;
+        if (attempt == 0) {
+          cd = ps.cdelta[par];
+          ds = ps.wd[par][0] + ps.wd[par][1] + ps.wd[par][2];
+          de = ps.we[par][0] + ps.we[par][1] + ps.we[par][2];
+          if (tprev >= 0 && !(h.flags & 1u)) {   // step s-1's token, not in the helpers' sums
+            const float x = val[tprev];
+            const double d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
+            if (lane == 0) cd[chunk_of(tprev, h.head, h.nchunk)] += d;
+            wave_sync();
+            ds += d;
+          }
+        } else {   // the exact sums cover bmN(s), step s-1's token included
+          cd = ps.cdx;
+          ds = ps.xd[0] + ps.xd[1] + ps.xd[2] + ps.xd[3];
+          de = 0.0;
+        }
+        C4S_PHASE(1);
+        StepOut o{0, 0u, 0u, 0u};
+        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, ps, o);
+        const bool retry = attempt == 0 && !ok && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
+        C4S_PHASE(2);
+        if (attempt == 0)
+          for (int i = lane; i < kMaxChunks; i += kWave) ps.cdelta[par][i] = 0.0;
+        if (lane == 0) {
+          ps.flag[par] = ok ? 1 : (retry ? 2 : 0);
+          ps.rng = rng;
+          if (ok) {
+            const int tok = o.tok;
+            ps.tok[par] = tok;
+            acc[0] |= 64u | 1u;
+            acc[2] += o.dex;
+            acc[3] += o.kept;
+            uint32_t* nb = bmNb[par ^ 1];   // becomes the set of step s+1
+            if (tprev >= 0) nb[tprev >> 5] |= 1u << (tprev & 31);
+            tprev = -1;
+            // text2semantic.cpp:333-334: the stop token is not appended
+            if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok) && !bit_of(bmN, tok)) {
+              nb[tok >> 5] |= 1u << (tok & 31);
+              tprev = tok;
+            }
+            ps.nt[par] = tprev;
+          } else if (!retry) {
+            acc[0] |= 1u << (20 + o.why);
+          }
+        }
+        tprev = (int)readlane_u32((uint32_t)tprev, 0);
+      } else if (attempt == 0) {
+        C4S_HELPER_PHASE(0);
+        wait_loads();   // step s+1 is in LDS (this wave's range)
+        C4S_HELPER_PHASE(1);
+        if (s > s_first) {   // the previous step's token joined bmN: list it if it is ours
+          const int nt = ps.nt[par ^ 1];
+          if (nt >= third_bound(V, hw) && nt < third_bound(V, hw + 1)) {
+            if (lane == 0 && ndrawn < kDrawnList) ps.dlist[hw][ndrawn] = nt;
+            ++ndrawn;
+            wave_sync();
+          }
+        }
+        if (s + 1 < s_end) {
+          const int sn = s + 1;
+          const uint64_t* hc = ps.hdr[sn & 1][hw];
+          const SumHdr hh = hdr_words(hc[0], hc[1], hc[2], hc[3], hc[4]);
+          double d = 0.0, e = 0.0;
+          if (c.pen_on)
+            d = helper_corrections(rowval(sn), V, hw, bmN, hh, c, ps.cdelta[sn & 1], ps.dlist[hw], ndrawn, e);
+          if (lane == 0) { ps.wd[sn & 1][hw] = d; ps.we[sn & 1][hw] = e; }
+        }
+        C4S_HELPER_PHASE(2);
+        if (s + 2 < s_end)
+          dma_step(rowp(s + 2), V, sum_words(w, a.n_rows, s + 2, row), rowslot(s + 2), sumslot(s + 2),
+                   ps.hdr[s & 1][hw], hw);
+        C4S_HELPER_PHASE(3);
+        if (hw == 0 && lane == 0 && s > s_first) a.out_tok[(int64_t)(s - 1) * a.n_rows + row] = ps.tok[par ^ 1];
+      }
+      lds_barrier();
+      C4S_PHASE(3);
+      C4S_HELPER_PHASE(4);
+      if (ps.flag[par] != 2) break;
+    }
+    if (!ps.flag[par]) {
+      // text2semantic.cpp:142-166 on the whole staged row: penalty over H0 and
+      // the stream's ids (disjoint sets, so each id once), then the chain.
+      rng = ps.rng;
+      float* val = rowval(s);
+      if (c.pen_on) {
+        penalise_chunk<NTC>(val, bmH0, V, c.pen);
+        penalise_chunk<NTC>(val, bmN, V, c.pen);
+      }
+      __syncthreads();
+      LdsRowNC src{val, V, 0u, false, sortbuf};
+      const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
+      if (t == 0) {
+        const uint32_t* stp = xs.step_stats;
+        ps.rng = rng;
+        ps.tok[par] = tok;
+        acc[0] |= stp[0];
+        acc[1] += 1u;
+        acc[2] += stp[2];
+        acc[3] += stp[3];
+        uint32_t* nb = bmNb[par ^ 1];
+        if (tprev >= 0) nb[tprev >> 5] |= 1u << (tprev & 31);
+        tprev = -1;
+        if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok) && !bit_of(bmN, tok)) {
+          nb[tok >> 5] |= 1u << (tok & 31);
+          tprev = tok;
+        }
+        ps.nt[par] = tprev;
+      }
+      tprev = (int)readlane_u32((uint32_t)tprev, 0);
+      __syncthreads();
+    }
+    if (ps.tok[par] == a.stop_token) {
+      done = true;
+      ++s;
+      break;
+    }
+  }
+  // s: first step not decided here. The last decided token, and -1 after a stop.
+  wait_loads();
+  __syncthreads();
+  if (t == 0 && s > s_first) a.out_tok[(int64_t)(s - 1) * a.n_rows + row] = ps.tok[(s - 1) & 1];
+  for (int s2 = s + t; s2 < s_end; s2 += NTC) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
+  fast_end(a, w, row, V, NTC, s_end, false, done, ps.rng, acc, bmNb[s & 1]);
 }
 
 // ---- repair: the pending step of each row, exactly ------------------------------------
@@ -1522,7 +1960,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       if (wv == 0) {
         double ds = 0.0, de = 0.0;
         for (int i = 0; i < NW; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, rng, cs, o);
+        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, cs.sum, cs.cdelta, rng, cs, o);
         for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
@@ -1626,6 +2064,17 @@ hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_
     hipLaunchKernelGGL(k_stream_rowk<8>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
   else
     hipLaunchKernelGGL(k_stream_rowk<kQuadsC>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
+  return hipGetLastError();
+}
+
+size_t stream_rowp_lds_bytes(int V) {
+  return 3 * (size_t)kSumWordsP * 8 + 3 * 4 * ((size_t)vpad(V) + 4);
+}
+
+hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_rowp, dim3(a.n_rows), dim3(NTC), stream_rowp_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 
