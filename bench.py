@@ -223,8 +223,8 @@ def main():
                                "one stream call per bench step",
                    "rows": R, "vocab": V, "ar_steps": T,
                    "launch": ("k_stream_lds" if args.sequential else
-                              "k_stream_scan + k_stream_list | k_stream_rowk + k_stream_repair + "
-                              "k_stream_chain")},
+                              "k_stream_scan, then k_stream_list | k_stream_rowp side by side, "
+                              "then k_stream_repair / k_stream_chain for what is left")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic,
