@@ -46,7 +46,7 @@ namespace {
 
 constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
-constexpr size_t kChainStaticLds = 36 * 1024;      // chain kernels' static LDS (upper bound)
+constexpr size_t kChainStaticLds = 38 * 1024;      // chain kernels' static LDS (upper bound)
 constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's static LDS (upper bound)
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;

@@ -1207,11 +1207,14 @@ __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitma
 // candidates (distinct, below kCandCap). The entries move to lanes in id order
 // (rank by ballots over the slot bits, then a lane permute) and one prefix
 // scan forms the id-order sums. The reference sums sequentially, so the first
-// lane reaching r = u * total decides only with the margin rel_eps; otherwise
-// the id-order sums are replayed sequentially (ids outside the kept set weigh 0).
-__device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, double u, int V, uint32_t& exact) {
+// lane reaching r = u * total decides only with the margin rel_eps (plus
+// eps_add, the relative error of masses that are approximations); otherwise
+// the id-order sums are replayed sequentially (ids outside the kept set weigh
+// 0), or, when replay is false (approximate masses), -1 is returned.
+__device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, double u, int V, uint32_t& exact,
+                                         double eps_add = 0.0, bool replay = true) {
   const int lane = lane_id();
-  const double eps = rel_eps(V);
+  const double eps = rel_eps(V) + eps_add;
   const uint64_t km = __ballot(kept);
   const int nk = __popcll(km);
   // position among the kept entries in id order
@@ -1244,6 +1247,7 @@ __device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, 
       return (int)readlane_u32((uint32_t)ids, f);
     }
   }
+  if (!replay) return -1;
   // text2semantic.cpp:152-164 sequentially in id order
   exact = 1;
   double total = 0.0;

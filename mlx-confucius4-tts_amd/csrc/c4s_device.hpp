@@ -23,6 +23,9 @@
 #ifndef C4S_HELPER_PHASE
 #define C4S_HELPER_PHASE(n) ((void)0)
 #endif
+#ifndef C4S_ROW_TIME
+#define C4S_ROW_TIME(n) ((void)0)
+#endif
 
 namespace c4s {
 

@@ -79,9 +79,10 @@ __device__ __forceinline__ uint32_t ent_key(uint64_t e) { return (uint32_t)(e >>
 __device__ __forceinline__ int ent_id(uint64_t e) { return 16383 - (int)(((uint32_t)e >> 10) & 16383u); }
 __device__ __forceinline__ int ent_rank(uint64_t e) { return (int)((uint32_t)e & 1023u); }
 
-// Summary words: list entries [0, kListLarge), their values before the
-// temperature (float per entry) from kYW, header [kHdrW, kHdrW + 8), chunk
-// masses from kChunkW. List entry i sits in lane i % 64 of a wave's i / 64-th
+// Summary words: list entries [0, kListLarge); from kYW one float per entry:
+// its value before the temperature (greedy and top-k rows) or its mass
+// exp((double)fl(z - m0)) rounded to fp32 (full-vocabulary rows); header
+// [kHdrW, kHdrW + 8); chunk masses from kChunkW. List entry i sits in lane i % 64 of a wave's i / 64-th
 // load, so list rows read their entries straight into registers.
 constexpr int kYW = kListLarge;
 constexpr int kHdrW = kYW + kListLarge / 2;
@@ -393,11 +394,15 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
     SumHdr* hdr = reinterpret_cast<SumHdr*>(sw + kHdrW);
     double* chk = reinterpret_cast<double*>(sw + kChunkW);
     if (!bad) {
+      // greedy / top-k rows: the value before the temperature (their hits are
+      // penalised again from it); full-vocabulary rows: the entry's mass
+      // exp((double)fl(z - z_max)) as the reference computes it, in fp32.
       float* ly = reinterpret_cast<float*>(sw + kYW);
+      const float zmax = kfloat(ent_key(sh.cand[0]));
       for (int i = t; i < n; i += NTA) {
         const uint64_t e = sh.cand[i];
         lst[i] = e;
-        ly[i] = sh.candy[ent_rank(e)];
+        ly[i] = masses ? (float)exp((double)(kfloat(ent_key(e)) - zmax)) : sh.candy[ent_rank(e)];
       }
     }
 
@@ -498,6 +503,7 @@ struct ChainSh {
   double slotE[kCandCap];
   int slotId[kCandCap];
   float lz[kListLarge];
+  float lm[kListLarge];
   int lid[kListLarge];
   int lslot[kListLarge];
   double wd[NW];
@@ -517,67 +523,65 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Slot s (an id-order rank) lives at position slot_pos(s): lane l's sixteen
+// slots [16 l, 16 l + 16) are the l-th word of sixteen 64-word rows, so a wave
+// reads them without bank conflicts.
+__device__ __forceinline__ int slot_pos(int s) { return ((s & 15) << 6) | (s >> 4); }
+
 // Inverse-CDF draw over the kept candidates (text2semantic.cpp:150-165): their
 // masses sit in cs.slotE at their id-order ranks [0, nslot) (zero elsewhere),
 // so slot order is id order. Wave 0 only. Returns the token; `exact` is set
-// when the margin test failed and the sums were replayed sequentially.
+// when the margin test failed and the sums were replayed sequentially. With
+// approximate masses (relative error eps_add) and replay false, an unsure
+// decision returns -1 instead.
 template <class CS>
-__device__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact) {
+__device__ __forceinline__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact,
+                                         double eps_add = 0.0, bool replay = true) {
+  // One pass: lane l sums slots [16 l, 16 l + 16); one prefix scan over the
+  // lanes gives every slot's id-order sum and the total.
+  constexpr int kPer = kCandCap / kWave;
+  static_assert(kPer * kWave == kCandCap, "slots split evenly over the lanes");
   const int lane = lane_id();
-  const double eps = rel_eps(V);
-  // pass 1: total in slot order (per lane 4 consecutive slots per block of 256)
-  double tot = 0.0;
-  for (int b = 0; b < nslot; b += 4 * kWave) {
-    double ls = 0.0;
+  const double eps = rel_eps(V) + eps_add;
+  const int b0 = kPer * lane;
+  double e[kPer], ls = 0.0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int sidx = b + 4 * lane + i;
-      ls += (sidx < nslot) ? cs.slotE[sidx] : 0.0;
-    }
-    tot += wave_sum_dpp(ls);
+  for (int i = 0; i < kPer; ++i) {
+    e[i] = (b0 + i < nslot) ? cs.slotE[(i << 6) | lane] : 0.0;
+    ls += e[i];
   }
-  const double r = u * tot;
+  const double inc = wave_scan_f64(ls);
+  const double r = u * readlane_f64(inc, kWave - 1);
+  double run = inc - ls;
+  int hit = -1;
+  double ha = 0.0, hp = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const double nx = run + e[i];
+    if (hit < 0 && e[i] > 0.0 && nx >= r) { hit = b0 + i; ha = nx; hp = run; }
+    run = nx;
+  }
   int tok = -1;
   double af = 0.0, pf = 0.0;
-  double carry = 0.0;
-  for (int b = 0; b < nslot && tok < 0; b += 4 * kWave) {
-    double e4[4], ls = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int sidx = b + 4 * lane + i;
-      e4[i] = (sidx < nslot) ? cs.slotE[sidx] : 0.0;
-      ls += e4[i];
-    }
-    const double inc = wave_scan_f64(ls);
-    double run = carry + inc - ls;
-    int hit = -1;
-    double ha = 0.0, hp = 0.0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double nx = run + e4[i];
-      if (hit < 0 && e4[i] > 0.0 && nx >= r) { hit = b + 4 * lane + i; ha = nx; hp = run; }
-      run = nx;
-    }
-    const uint64_t hm = __ballot(hit >= 0);
-    if (hm) {
-      const int f = __ffsll((unsigned long long)hm) - 1;
-      tok = (int)readlane_u32((uint32_t)hit, f);
-      af = readlane_f64(ha, f);
-      pf = readlane_f64(hp, f);
-    }
-    carry = readlane_f64(carry + inc, kWave - 1);
+  const uint64_t hm = __ballot(hit >= 0);
+  if (hm) {
+    const int f = __ffsll((unsigned long long)hm) - 1;
+    tok = (int)readlane_u32((uint32_t)hit, f);
+    af = readlane_f64(ha, f);
+    pf = readlane_f64(hp, f);
   }
   const bool sure = r > 0.0 && tok >= 0 && (af - r > eps * af) && (r - pf > eps * r);
   if (sure) {
     exact = 0;
-    return cs.slotId[tok];
+    return cs.slotId[slot_pos(tok)];
   }
+  if (!replay) return -1;
   // text2semantic.cpp:152-164 sequentially in id order; ids outside the slots weigh 0
   exact = 1;
   int res = 0;
   if (lane == 0) {
     double total = 0.0;
-    for (int i = 0; i < nslot; ++i) total += cs.slotE[i];
+    for (int i = 0; i < nslot; ++i) total += cs.slotE[slot_pos(i)];
     const double rr = u * total;
     res = V - 1;
     if (rr <= 0.0) {
@@ -585,8 +589,9 @@ __device__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact) {
     } else {
       double acc = 0.0;
       for (int i = 0; i < nslot; ++i) {
-        acc += cs.slotE[i];
-        if (cs.slotE[i] > 0.0 && rr <= acc) { res = cs.slotId[i]; break; }
+        const double ei = cs.slotE[slot_pos(i)];
+        acc += ei;
+        if (ei > 0.0 && rr <= acc) { res = cs.slotId[slot_pos(i)]; break; }
       }
     }
   }
@@ -596,7 +601,10 @@ __device__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact) {
 // Clears slots [0, nslot) (wave 0).
 template <class CS>
 __device__ __forceinline__ void clear_slots(CS& cs, int nslot) {
-  for (int i = lane_id(); i < nslot; i += kWave) cs.slotE[i] = 0.0;
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < kCandCap / kWave; ++i)
+    if (((lane << 4) | i) < nslot) cs.slotE[(i << 6) | lane] = 0.0;
   wave_sync();
 }
 
@@ -753,7 +761,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
 // list is compacted lazily, 64 entries at a time, only as deep as the decision
 // needs; cs provides the compaction and slot arrays.
 template <class CS>
-__device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
+__device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
                          const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
                          const uint64_t* sum, const double* cdelta, uint64_t& rng, CS& cs,
                          StepOut& o) {
@@ -767,26 +775,42 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
   int nb = 0, nu = 0;
   float hm = ninf;
   // list block [nb, nb + 64): unhit entries to their ranks, penalised hits into hm
+  // (256 entries a call, four consecutive ones per lane)
   auto compact = [&]() __attribute__((always_inline)) {
-    const int pos = nb + lane;
-    const bool v = pos < n;
-    const uint64_t e = v ? lst[pos] : 0ull;
-    const int id = ent_id(e);
-    const bool hit = c.pen_on && v && bit_of(bmN, id);
-    const bool un = v && !hit;
-    const uint64_t bl = __ballot(un);
-    if (un) {
-      const int rk = nu + __popcll(bl & lanemask_lt());
-      cs.lz[rk] = kfloat(ent_key(e));
-      cs.lid[rk] = id;
-      cs.lslot[rk] = ent_rank(e);
+    const int p0 = nb + 4 * lane;
+    uint64_t e[4];
+    bool hit[4], un[4];
+    uint32_t cu = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = (p0 + i < n) ? lst[p0 + i] : 0ull;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool v = p0 + i < n;
+      // every lane reads its bitmap word (no branch around the load)
+      const bool drawn = bit_of(bmN, v ? ent_id(e[i]) : 0);
+      hit[i] = c.pen_on & v & drawn;
+      un[i] = v & !hit[i];
+      cu += un[i] ? 1u : 0u;
     }
-    if (hit) {   // sampling.cpp:26 on the value before the temperature, then :16
-      const float y = pen_exact(ly[pos], c.pen);
-      hm = fmaxf(hm, c.temp_on ? y / c.temp : y);
+    const uint32_t inc = wave_scan_u32(cu);
+    int rk = nu + (int)(inc - cu);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = ent_id(e[i]);
+      if (un[i]) {
+        cs.lz[rk] = kfloat(ent_key(e[i]));
+        cs.lm[rk] = ly[p0 + i];
+        cs.lid[rk] = id;
+        cs.lslot[rk] = ent_rank(e[i]);
+        ++rk;
+      }
+      if (hit[i]) {   // sampling.cpp:26, then :16; a drawn id is never in H0, so its value is the raw one
+        const float y = pen_exact(val[id], c.pen);
+        hm = fmaxf(hm, c.temp_on ? y / c.temp : y);
+      }
     }
-    nu += __popcll(bl);
-    nb = min(n, nb + kWave);
+    nu += (int)readlane_u32(inc, kWave - 1);
+    nb = min(n, nb + 4 * kWave);
   };
   // every list entry past the compacted ones is at or below this value
   auto zend = [&]() -> float { return nb >= n ? ninf : kfloat(ent_key(lst[nb - 1])); };
@@ -822,58 +846,130 @@ __device__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* v
     // nucleus cut on the unhit entries in rank order: removed iff above >= p * S
     const double pS = (double)c.p * S;
     const double marg = (double)c.p * err + eps * S;
-    double carry = 0.0, e_first = 0.0;
+    // While the maximum did not move, the entries' masses come from the summary
+    // (the reference's mass rounded to fp32: relative error below 2^-23 when
+    // at least 2^-100); otherwise, and for tinier ones, exp is evaluated.
+    const bool approx = dm == 0.0;
+    const double dmass = approx ? 0x1p-23 : 0.0;
+    auto mass_of = [&](int rk, bool exact_only) __attribute__((always_inline)) -> double {
+      const float m = cs.lm[rk];
+      return (approx && !exact_only && m >= 0x1p-100f) ? (double)m : exp((double)(cs.lz[rk] - mt));
+    };
+    // Masses of up to R ranks per lane: the stored ones are read first; exp runs
+    // only if some lane needs it (the maximum moved, a tiny mass, or exact_only).
+    auto masses_of = [&](const int* rks, const bool* vs, double* out, int R, bool exact_only)
+        __attribute__((always_inline)) {
+      bool need = false;
+      for (int j = 0; j < R; ++j) {
+        const float m = vs[j] ? cs.lm[rks[j]] : 0.0f;
+        out[j] = (double)m;
+        need |= vs[j] & !(approx & !exact_only & (m >= 0x1p-100f));
+      }
+      if (__ballot(need))
+        for (int j = 0; j < R; ++j)
+          if (vs[j] && !(approx && !exact_only && out[j] >= 0x1p-100)) out[j] = exp((double)(cs.lz[rks[j]] - mt));
+    };
+    // 256 ranks per iteration, four per lane, one prefix scan.
+    double carry = 0.0;
     int q = -1, rdone = 0;
     while (q < 0) {
-      while (nu - rdone < kWave && nb < n) compact();
+      C4S_PHASE(4);
+      while (nu - rdone < 4 * kWave && nb < n) compact();
       if (rdone >= nu) break;
       wave_sync();
-      const int rk = rdone + lane;
-      const bool v = rk < nu;
-      const float z = v ? cs.lz[rk] : ninf;
-      const double em = v ? exp((double)(z - mt)) : 0.0;
-      if (rdone == 0) e_first = em;
-      const double inc = wave_scan_f64(em);
-      const double ab = carry + inc - em;
-      const double D = ab - pS;
+      C4S_PHASE(5);
+      double e4[4], ls = 0.0;
+      int rk4[4];
+      bool v4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rk4[i] = rdone + 4 * lane + i;
+        v4[i] = rk4[i] < nu;
+      }
+      masses_of(rk4, v4, e4, 4, false);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ls += e4[i];
+      const double inc = wave_scan_f64(ls);
+      double ab = carry + inc - ls;
+      bool unsure = false, tiny = false;
+      int qloc = -1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rk = rdone + 4 * lane + i;
+        const bool v = rk < nu;
+        const double D = ab - pS;
+        unsure |= v && rk >= c.min_keep && !(fabs(D) > marg + (eps + dmass) * ab);
+        tiny |= v && D < 0.0 && e4[i] < 0x1p-1000;
+        if (v && D >= 0.0 && qloc < 0) qloc = rk;
+        ab += e4[i];
+      }
       o.why = kWhyMargin;
-      if (__ballot(v && rk >= c.min_keep && !(fabs(D) > marg + eps * ab))) return false;
+      if (__ballot(unsure)) return false;
       o.why = kWhyTiny;   // subnormal kept masses may differ between libm implementations
-      if (__ballot(v && D < 0.0 && em < 0x1p-1000)) return false;
-      const uint64_t rm = __ballot(v && D >= 0.0);
-      if (rm) q = max(rdone + __ffsll((unsigned long long)rm) - 1, c.min_keep);
+      if (__ballot(tiny)) return false;
+      const uint64_t rm = __ballot(qloc >= 0);
+      if (rm) q = max((int)readlane_u32((uint32_t)qloc, __ffsll((unsigned long long)rm) - 1), c.min_keep);
       carry = readlane_f64(carry + inc, kWave - 1);
-      rdone += kWave;
+      rdone += 4 * kWave;
+      C4S_PHASE(6);
     }
     C4S_PHASE(10);
     o.why = kWhyDeep;
     if (q < 0 || q > nu) return false;   // the cut lies below the list
     const float zq1 = cs.lz[q - 1];
     while (nb < n && !(zend() < zq1)) compact();
+    C4S_PHASE(15);
     o.why = kWhyBound;
     if (!(zo < zq1)) return false;
     o.why = kWhyHit;
     if (!(wave_max_dpp(hm) < zq1)) return false;
-    if (q <= kWave) {   // kept ranks [0, q) are the first chunk: lane = rank
+    // The draw on the kept ranks [0, q): first with the masses above (a decision
+    // inside their error is not replayed), then, if needed, with exact masses.
+    if (q <= kWave) {   // kept ranks are the first chunk: lane = rank
       const bool kept = lane < q;
-      o.tok = lane_draw(kept, kept ? cs.lid[lane] : 0, kept ? cs.lslot[lane] : 0, e_first, u, V, o.dex);
+      const int kid = kept ? cs.lid[lane] : 0, ks = kept ? cs.lslot[lane] : 0;
+      int tok = -1;
+      if (approx) tok = lane_draw(kept, kid, ks, kept ? mass_of(lane, false) : 0.0, u, V, o.dex, 0x1p-22, false);
+      if (tok < 0) tok = lane_draw(kept, kid, ks, kept ? mass_of(lane, true) : 0.0, u, V, o.dex);
+      o.tok = tok;
     } else {
-      int nslot = 0;
-      for (int b = 0; b < q; b += kWave) {
-        const int rkk = b + lane;
-        nslot = max(nslot, rkk < q ? cs.lslot[rkk] + 1 : 0);
-      }
-      nslot = (int)wave_max_u32_dpp((uint32_t)nslot);
-      clear_slots(cs, nslot);
-      for (int b = 0; b < q; b += kWave) {
-        const int rkk = b + lane;
-        if (rkk < q) {
-          cs.slotE[cs.lslot[rkk]] = exp((double)(cs.lz[rkk] - mt));
-          cs.slotId[cs.lslot[rkk]] = cs.lid[rkk];
+      // Every candidate slot is cleared (ranks below kCandCap), then the kept
+      // ranks lane + 64 j (q <= kListLarge) write theirs: all reads first, then
+      // the writes, so that the reads do not wait on the writes.
+      constexpr int kR = kListLarge / kWave;
+      clear_slots(cs, kCandCap);
+      C4S_PHASE(11);
+      auto scatter = [&](bool exact_only) __attribute__((always_inline)) {
+        int sp[kR], sid[kR], rkj[kR];
+        bool vj[kR];
+        double sm[kR];
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+          rkj[j] = lane + kWave * j;
+          vj[j] = rkj[j] < q;
+          const int rr = vj[j] ? rkj[j] : 0;
+          sp[j] = vj[j] ? slot_pos(cs.lslot[rr]) : -1;
+          sid[j] = cs.lid[rr];
         }
+        masses_of(rkj, vj, sm, kR, exact_only);
+#pragma unroll
+        for (int j = 0; j < kR; ++j)
+          if (sp[j] >= 0) {
+            cs.slotE[sp[j]] = sm[j];
+            cs.slotId[sp[j]] = sid[j];
+          }
+        wave_sync();
+      };
+      scatter(false);
+      C4S_PHASE(13);
+      int tok = -1;
+      if (approx) tok = slot_draw(cs, kCandCap, u, V, o.dex, 0x1p-22, false);
+      C4S_PHASE(14);
+      if (tok < 0) {
+        if (approx) scatter(true);
+        tok = slot_draw(cs, kCandCap, u, V, o.dex);
       }
-      wave_sync();
-      o.tok = slot_draw(cs, nslot, u, V, o.dex);
+      o.tok = tok;
     }
     C4S_PHASE(12);
     o.kept = (uint32_t)q;
@@ -1362,6 +1458,7 @@ struct RowPSh {
   double slotE[kCandCap];
   int slotId[kCandCap];
   float lz[kListLarge];
+  float lm[kListLarge];
   int lid[kListLarge];
   int lslot[kListLarge];
   alignas(16) uint64_t hdr[2][3][8];   // per parity and helper wave: header copy
@@ -1566,6 +1663,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   if (stream_mode(c, V) != kModeRow) return;
   int s_first;
   if (!fast_begin(a, w, row, NTC, s_first)) return;
+  C4S_ROW_TIME(0);
   const uint32_t* stw = w.state + (size_t)row * kStateWords;
   const int s_end = w.s_end;
   uint64_t* sumslots = reinterpret_cast<uint64_t*>(smem);
@@ -1760,6 +1858,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   if (t == 0 && s > s_first) a.out_tok[(int64_t)(s - 1) * a.n_rows + row] = ps.tok[(s - 1) & 1];
   for (int s2 = s + t; s2 < s_end; s2 += NTC) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
   fast_end(a, w, row, V, NTC, s_end, false, done, ps.rng, acc, bmNb[s & 1]);
+  C4S_ROW_TIME(1);
 }
 
 // ---- repair: the pending step of each row, exactly ------------------------------------
