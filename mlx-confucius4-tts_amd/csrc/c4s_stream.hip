@@ -204,6 +204,7 @@ __device__ void bitonic_desc_u64(uint64_t* v, int P) {
     }
 }
 
+
 // One workgroup scans steps [s0, s1) of one row. Thread t holds the float4
 // quads t + 256 j of the 16-byte aligned body and one head or tail id.
 template <int NQ>
@@ -350,10 +351,10 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
     const bool overflow = C > (uint32_t)kCandCap;
     C4S_SCAN_PHASE(3);
     if (!overflow) {
+      // raw value and id of each candidate at its id-order position
       auto put = [&](uint32_t pos, float x, int id) {
-        const float y = bit_of(sh.bm, id) && c.pen_on ? pen_exact(x, pen) : x;
-        sh.cand[pos] = make_entry(c.temp_on ? y / c.temp : y, id, (int)pos);   // sampling.cpp:16
-        sh.candy[pos] = y;
+        sh.candy[pos] = x;
+        sh.cand[pos] = (uint64_t)(uint32_t)id;
       };
       if (eh && fkey(xe) >= L0) put(ex[0], xe, eid);
       if (et && fkey(xe) >= L0) put(ex[NQ + 1], xe, eid);
@@ -370,23 +371,63 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
         }
       }
     }
+    __syncthreads();
+    // Each candidate, one thread each: the penalty of H0 (sampling.cpp:26), the
+    // temperature (:16), its entry.
+    if (!overflow)
+      for (int i = t; i < (int)C; i += NTA) {
+        const int id = (int)(uint32_t)sh.cand[i];
+        const float x = sh.candy[i];
+        const float y = (c.pen_on && bit_of(sh.bm, id)) ? pen_exact(x, pen) : x;
+        sh.cand[i] = make_entry(c.temp_on ? y / c.temp : y, id, i);
+        sh.candy[i] = y;
+      }
+    // Sorted entries (descending). Up to 256 of them by rank counting into the
+    // free histogram: entries are distinct (ids are), so an entry's rank is the
+    // number of larger ones; the list is padded with zero entries (every entry
+    // is positive) to a multiple of eight. More by a bitonic sort in place.
+    const bool small = C <= (uint32_t)NTA;
+    uint64_t* srt = small ? reinterpret_cast<uint64_t*>(sh.hist) : sh.cand;
+    static_assert(sizeof(sh.hist) >= NTA * sizeof(uint64_t), "the histogram holds a small sorted list");
+    const int C8 = ((int)C + 7) & ~7;
     int P = 2;
     while (P < (int)C) P <<= 1;
-    if (!overflow)
-      for (int i = (int)C + t; i < P; i += NTA) sh.cand[i] = 0ull;
+    if (!overflow) {
+      if (small) {
+        if (t < C8 - (int)C) sh.cand[C + t] = 0ull;
+      } else {
+        for (int i = (int)C + t; i < P; i += NTA) sh.cand[i] = 0ull;
+      }
+    }
     __syncthreads();
     C4S_SCAN_PHASE(4);
-    if (!overflow) bitonic_desc_u64(sh.cand, P);
+    if (!overflow) {
+      if (small) {
+        const uint64_t mine = (t < (int)C) ? sh.cand[t] : ~0ull;
+        uint32_t r = 0;
+        for (int j = 0; j < C8; j += 8) {
+          uint64_t o[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = sh.cand[j + i];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) r += (o[i] > mine) ? 1u : 0u;
+        }
+        if (t < (int)C) srt[r] = mine;
+        __syncthreads();
+      } else {
+        bitonic_desc_u64(sh.cand, P);
+      }
+    }
     C4S_SCAN_PHASE(5);
 
     // Leading entries above the bound, at most cap of them.
     uint32_t nabove = 0;
     if (!overflow)
-      for (int i = t; i < (int)C; i += NTA) nabove += (ent_key(sh.cand[i]) > tout) ? 1u : 0u;
+      for (int i = t; i < (int)C; i += NTA) nabove += (ent_key(srt[i]) > tout) ? 1u : 0u;
     uint32_t n_all;
     (void)scan_excl_nta(nabove, sh.red, n_all);
     int n = min((int)n_all, cap);
-    if (!overflow && (int)n_all > cap) tout = max(tout, ent_key(sh.cand[cap]));
+    if (!overflow && (int)n_all > cap) tout = max(tout, ent_key(srt[cap]));
     const bool bad = overflow || n == 0;
 
     uint64_t* sw = reinterpret_cast<uint64_t*>(w.sum + ((size_t)(s - w.s_begin) * a.n_rows + row) * kSumStride);
@@ -398,9 +439,9 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       // penalised again from it); full-vocabulary rows: the entry's mass
       // exp((double)fl(z - z_max)) as the reference computes it, in fp32.
       float* ly = reinterpret_cast<float*>(sw + kYW);
-      const float zmax = kfloat(ent_key(sh.cand[0]));
+      const float zmax = kfloat(ent_key(srt[0]));
       for (int i = t; i < n; i += NTA) {
-        const uint64_t e = sh.cand[i];
+        const uint64_t e = srt[i];
         lst[i] = e;
         ly[i] = masses ? (float)exp((double)(kfloat(ent_key(e)) - zmax)) : sh.candy[ent_rank(e)];
       }
@@ -412,7 +453,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
     int nchunk = 0;
     double err = 0.0, s0 = 0.0;
     if (masses && !bad) {
-      m0 = kfloat(ent_key(sh.cand[0]));
+      m0 = kfloat(ent_key(srt[0]));
       const MassCoef mk = mass_coef(c, m0);
       const bool exm = exact_masses(c);
       nchunk = max(1, (rs.nq + 15) >> 4);
