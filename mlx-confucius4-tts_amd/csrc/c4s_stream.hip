@@ -910,12 +910,13 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
         for (int j = 0; j < R; ++j)
           if (vs[j] && !(approx && !exact_only && out[j] >= 0x1p-100)) out[j] = exp((double)(cs.lz[rks[j]] - mt));
     };
-    // 256 ranks per iteration, four per lane, one prefix scan.
+    // Up to 256 ranks per iteration, four per lane, one prefix scan; the list
+    // is compacted further only once the compacted ranks are used up.
     double carry = 0.0;
     int q = -1, rdone = 0;
     while (q < 0) {
       C4S_PHASE(4);
-      while (nu - rdone < 4 * kWave && nb < n) compact();
+      while (rdone >= nu && nb < n) compact();
       if (rdone >= nu) break;
       wave_sync();
       C4S_PHASE(5);
@@ -951,7 +952,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
       const uint64_t rm = __ballot(qloc >= 0);
       if (rm) q = max((int)readlane_u32((uint32_t)qloc, __ffsll((unsigned long long)rm) - 1), c.min_keep);
       carry = readlane_f64(carry + inc, kWave - 1);
-      rdone += 4 * kWave;
+      rdone = min(nu, rdone + 4 * kWave);
       C4S_PHASE(6);
     }
     C4S_PHASE(10);
@@ -1782,10 +1783,15 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
           de = ps.we[par][0] + ps.we[par][1] + ps.we[par][2];
           if (tprev >= 0 && !(h.flags & 1u)) {   // step s-1's token, not in the helpers' sums
             const float x = val[tprev];
-            const double d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
+            const MassCoef mk = mass_coef(c, h.m0);
+            float e0, e1;
+            const float m1 = mass_approx(x, mk, e0);
+            const float m2 = mass_approx(pen_approx(x, c.pen, 1.0f / c.pen), mk, e1);
+            const double d = (double)m1 - (double)m2;
             if (lane == 0) cd[chunk_of(tprev, h.head, h.nchunk)] += d;
             wave_sync();
             ds += d;
+            de += (double)e0 + (double)e1;
           }
         } else {   // the exact sums cover bmN(s), step s-1's token included
           cd = ps.cdx;
