@@ -541,8 +541,8 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
 struct ChainSh {
   uint64_t sum[kSumWords];   // this step's summary: header words, list, chunks
   double cdelta[kMaxChunks];
-  double slotE[kCandCap];
-  int slotId[kCandCap];
+  uint32_t inv[kCandCap];   // id-order slot -> (generation << 10) | unhit rank
+  uint32_t gen;             // generation of the last row step
   float lz[kListLarge];
   float lm[kListLarge];
   int lid[kListLarge];
@@ -568,86 +568,6 @@ __device__ __forceinline__ void wave_sync() {
 // slots [16 l, 16 l + 16) are the l-th word of sixteen 64-word rows, so a wave
 // reads them without bank conflicts.
 __device__ __forceinline__ int slot_pos(int s) { return ((s & 15) << 6) | (s >> 4); }
-
-// Inverse-CDF draw over the kept candidates (text2semantic.cpp:150-165): their
-// masses sit in cs.slotE at their id-order ranks [0, nslot) (zero elsewhere),
-// so slot order is id order. Wave 0 only. Returns the token; `exact` is set
-// when the margin test failed and the sums were replayed sequentially. With
-// approximate masses (relative error eps_add) and replay false, an unsure
-// decision returns -1 instead.
-template <class CS>
-__device__ __forceinline__ int slot_draw(CS& cs, int nslot, double u, int V, uint32_t& exact,
-                                         double eps_add = 0.0, bool replay = true) {
-  // One pass: lane l sums slots [16 l, 16 l + 16); one prefix scan over the
-  // lanes gives every slot's id-order sum and the total.
-  constexpr int kPer = kCandCap / kWave;
-  static_assert(kPer * kWave == kCandCap, "slots split evenly over the lanes");
-  const int lane = lane_id();
-  const double eps = rel_eps(V) + eps_add;
-  const int b0 = kPer * lane;
-  double e[kPer], ls = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    e[i] = (b0 + i < nslot) ? cs.slotE[(i << 6) | lane] : 0.0;
-    ls += e[i];
-  }
-  const double inc = wave_scan_f64(ls);
-  const double r = u * readlane_f64(inc, kWave - 1);
-  double run = inc - ls;
-  int hit = -1;
-  double ha = 0.0, hp = 0.0;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const double nx = run + e[i];
-    if (hit < 0 && e[i] > 0.0 && nx >= r) { hit = b0 + i; ha = nx; hp = run; }
-    run = nx;
-  }
-  int tok = -1;
-  double af = 0.0, pf = 0.0;
-  const uint64_t hm = __ballot(hit >= 0);
-  if (hm) {
-    const int f = __ffsll((unsigned long long)hm) - 1;
-    tok = (int)readlane_u32((uint32_t)hit, f);
-    af = readlane_f64(ha, f);
-    pf = readlane_f64(hp, f);
-  }
-  const bool sure = r > 0.0 && tok >= 0 && (af - r > eps * af) && (r - pf > eps * r);
-  if (sure) {
-    exact = 0;
-    return cs.slotId[slot_pos(tok)];
-  }
-  if (!replay) return -1;
-  // text2semantic.cpp:152-164 sequentially in id order; ids outside the slots weigh 0
-  exact = 1;
-  int res = 0;
-  if (lane == 0) {
-    double total = 0.0;
-    for (int i = 0; i < nslot; ++i) total += cs.slotE[slot_pos(i)];
-    const double rr = u * total;
-    res = V - 1;
-    if (rr <= 0.0) {
-      res = 0;
-    } else {
-      double acc = 0.0;
-      for (int i = 0; i < nslot; ++i) {
-        const double ei = cs.slotE[slot_pos(i)];
-        acc += ei;
-        if (ei > 0.0 && rr <= acc) { res = cs.slotId[slot_pos(i)]; break; }
-      }
-    }
-  }
-  return (int)readlane_u32((uint32_t)res, 0);
-}
-
-// Clears slots [0, nslot) (wave 0).
-template <class CS>
-__device__ __forceinline__ void clear_slots(CS& cs, int nslot) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int i = 0; i < kCandCap / kWave; ++i)
-    if (((lane << 4) | i) < nslot) cs.slotE[(i << 6) | lane] = 0.0;
-  wave_sync();
-}
 
 __device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w2, uint64_t w3,
                                             uint64_t w4) {
@@ -813,6 +733,15 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
   const float ninf = neg_inf();
   const uint64_t* lst = sum;
   const float* ly = reinterpret_cast<const float*>(sum + kYW);
+  // This call's generation tags the id-order slots it fills (a kernel starts
+  // with generation 0; the slots are cleared at the first call and on wrap).
+  uint32_t gen = cs.gen + 1u;
+  if (gen == 1u || gen >= (1u << 22)) {
+#pragma unroll
+    for (int i = 0; i < kCandCap / kWave; ++i) cs.inv[(i << 6) | lane] = 0u;
+    gen = 1u;
+  }
+  if (lane == 0) cs.gen = gen;
   int nb = 0, nu = 0;
   float hm = ninf;
   // list block [nb, nb + 64): unhit entries to their ranks, penalised hits into hm
@@ -843,6 +772,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
         cs.lm[rk] = ly[p0 + i];
         cs.lid[rk] = id;
         cs.lslot[rk] = ent_rank(e[i]);
+        cs.inv[slot_pos(ent_rank(e[i]))] = (gen << 10) | (uint32_t)rk;
         ++rk;
       }
       if (hit[i]) {   // sampling.cpp:26, then :16; a drawn id is never in H0, so its value is the raw one
@@ -975,41 +905,98 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
       if (tok < 0) tok = lane_draw(kept, kid, ks, kept ? mass_of(lane, true) : 0.0, u, V, o.dex);
       o.tok = tok;
     } else {
-      // Every candidate slot is cleared (ranks below kCandCap), then the kept
-      // ranks lane + 64 j (q <= kListLarge) write theirs: all reads first, then
-      // the writes, so that the reads do not wait on the writes.
-      constexpr int kR = kListLarge / kWave;
-      clear_slots(cs, kCandCap);
-      C4S_PHASE(11);
-      auto scatter = [&](bool exact_only) __attribute__((always_inline)) {
-        int sp[kR], sid[kR], rkj[kR];
-        bool vj[kR];
-        double sm[kR];
+      // Kept ranks [0, q) in id order: lane l reads the id-order slots
+      // [16 l, 16 l + 16); a slot tagged with this call's generation names its
+      // unhit rank, every other slot (no candidate, a hit, a rank past the cut)
+      // weighs 0. First with the masses above, then with exact masses.
+      constexpr int kPer = kCandCap / kWave;
+      int rks[kPer];
+      uint32_t vb = 0u;   // bit i: slot 16 lane + i is kept
 #pragma unroll
-        for (int j = 0; j < kR; ++j) {
-          rkj[j] = lane + kWave * j;
-          vj[j] = rkj[j] < q;
-          const int rr = vj[j] ? rkj[j] : 0;
-          sp[j] = vj[j] ? slot_pos(cs.lslot[rr]) : -1;
-          sid[j] = cs.lid[rr];
-        }
-        masses_of(rkj, vj, sm, kR, exact_only);
+      for (int i = 0; i < kPer; ++i) {
+        const uint32_t x = cs.inv[(i << 6) | lane];
+        rks[i] = (int)(x & 1023u);
+        vb |= (((x >> 10) == gen && rks[i] < q) ? 1u : 0u) << i;
+      }
+      float mf[kPer];
 #pragma unroll
-        for (int j = 0; j < kR; ++j)
-          if (sp[j] >= 0) {
-            cs.slotE[sp[j]] = sm[j];
-            cs.slotId[sp[j]] = sid[j];
-          }
-        wave_sync();
-      };
-      scatter(false);
+      for (int i = 0; i < kPer; ++i) mf[i] = cs.lm[rks[i]];   // tagged ranks are below kListLarge
       C4S_PHASE(13);
+      auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
+        // in-lane inclusive prefix p[i], then one scan over the lanes
+        double e[kPer], p[kPer];
+        bool need = false;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const bool v = (vb >> i) & 1u;
+          const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
+          e[i] = (v && st) ? (double)mf[i] : 0.0;
+          need |= v && !st;
+        }
+        if (__ballot(need)) {   // exp for every slot (no per-slot branches), kept where needed
+#pragma unroll
+          for (int i = 0; i < kPer; ++i) {
+            const double x = exp((double)(cs.lz[rks[i]] - mt));
+            const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
+            e[i] = (((vb >> i) & 1u) && !st) ? x : e[i];
+          }
+        }
+        p[0] = e[0];
+#pragma unroll
+        for (int i = 1; i < kPer; ++i) p[i] = p[i - 1] + e[i];
+        const double inc = wave_scan_f64(p[kPer - 1]);
+        const double r = u * readlane_f64(inc, kWave - 1);
+        const double base = inc - p[kPer - 1];
+        double ha = 0.0, hp = 0.0;
+        int hrk = -1;
+#pragma unroll
+        for (int i = kPer - 1; i >= 0; --i) {   // the first slot reaching r wins
+          const double nx = base + p[i];
+          if (e[i] > 0.0 && nx >= r) { hrk = rks[i]; ha = nx; hp = i ? base + p[i - 1] : base; }
+        }
+        const uint64_t hb = __ballot(hrk >= 0);
+        if (!hb) return -1;
+        const int f = __ffsll((unsigned long long)hb) - 1;
+        const double af = readlane_f64(ha, f), pf = readlane_f64(hp, f);
+        const double eps = rel_eps(V) + eps_add;
+        if (!(r > 0.0 && (af - r > eps * af) && (r - pf > eps * r))) return -1;
+        return cs.lid[readlane_u32((uint32_t)hrk, f)];
+      };
       int tok = -1;
-      if (approx) tok = slot_draw(cs, kCandCap, u, V, o.dex, 0x1p-22, false);
+      o.dex = 0;
+      if (approx) tok = draw(false, 0x1p-22);
       C4S_PHASE(14);
+      if (tok < 0) tok = draw(true, 0.0);
       if (tok < 0) {
-        if (approx) scatter(true);
-        tok = slot_draw(cs, kCandCap, u, V, o.dex);
+        // text2semantic.cpp:152-164 sequentially in id order with exact masses
+        o.dex = 1;
+        int res = 0;
+        if (lane == 0) {
+          auto kept_mass = [&](int sl, int& rk) -> double {
+            const uint32_t x = cs.inv[slot_pos(sl)];
+            rk = (int)(x & 1023u);
+            return ((x >> 10) == gen && rk < q) ? exp((double)(cs.lz[rk] - mt)) : 0.0;
+          };
+          double total = 0.0;
+          for (int sl = 0; sl < kCandCap; ++sl) {
+            int rk;
+            total += kept_mass(sl, rk);
+          }
+          const double rr = u * total;
+          res = V - 1;
+          if (rr <= 0.0) {
+            res = 0;
+          } else {
+            double acc = 0.0;
+            for (int sl = 0; sl < kCandCap; ++sl) {
+              int rk;
+              const double ei = kept_mass(sl, rk);
+              acc += ei;
+              if (ei > 0.0 && rr <= acc) { res = cs.lid[rk]; break; }
+            }
+          }
+        }
+        tok = (int)readlane_u32((uint32_t)res, 0);
       }
       o.tok = tok;
     }
@@ -1312,6 +1299,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
   if (!fast_begin(a, w, row, NTC, s_first)) return;
   const uint32_t* stw = w.state + (size_t)row * kStateWords;
   for (int i = t; i < kMaxChunks; i += NTC) cs.cdelta[i] = 0.0;
+  if (t == 0) cs.gen = 0u;
   fast_bitmaps(a, stw, row, V, NTC, bmH0, bmN, true);
   double* E = reinterpret_cast<double*>(smem);   // exact steps: masses by id, sort keys
   float* vbuf = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
@@ -1497,8 +1485,8 @@ struct RowPSh {
   double wd[2][4];                // helper waves' correction sums, by step parity
   double we[2][4];                // and their error bounds
   double xd[NWC];                 // exact corrections of a retried step, per wave
-  double slotE[kCandCap];
-  int slotId[kCandCap];
+  uint32_t inv[kCandCap];         // id-order slot -> (generation << 10) | unhit rank
+  uint32_t gen;                   // generation of the last row step
   float lz[kListLarge];
   float lm[kListLarge];
   int lid[kListLarge];
@@ -1723,6 +1711,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   const int nwords = bitmap_words(V);
   for (int i = t; i < nwords; i += NTC) bmNb[(s_first + 1) & 1][i] = bmNb[s_first & 1][i];
   for (int i = t; i < 2 * kMaxChunks; i += NTC) (&ps.cdelta[0][0])[i] = 0.0;
+  if (t == 0) ps.gen = 0u;
   if (wv > 0) {
     dma_step(rowp(s_first), V, sum_words(w, a.n_rows, s_first, row), rowslot(s_first), sumslot(s_first),
              ps.hdr[s_first & 1][hw], hw);
@@ -1979,6 +1968,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   }
   for (int i = t; i < nwords; i += NT) bmH0[i] = 0u;
   for (int i = t; i < kMaxChunks; i += NT) cs.cdelta[i] = 0.0;
+  if (t == 0) cs.gen = 0u;
   __syncthreads();
   {
     const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
