@@ -40,6 +40,12 @@ struct c4s_ctx {
   hipStream_t scan_s = nullptr;
   hipEvent_t ev_start = nullptr;
   hipEvent_t ev_scan[2] = {nullptr, nullptr}, ev_chain[2] = {nullptr, nullptr};
+  // Overlapped stream: the scan and the chains on disjoint sets of CUs (half
+  // of every 32 CUs for the chains), created at first use.
+  int n_cus = 0;
+  bool cu_split_tried = false;
+  hipStream_t scan_m = nullptr, chain_m = nullptr, side_m = nullptr;
+  hipEvent_t ev_done = nullptr;
 };
 
 namespace {
@@ -50,10 +56,16 @@ constexpr size_t kChainStaticLds = 38 * 1024;      // chain kernels' static LDS 
 constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's static LDS (upper bound)
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
-// Steps per chunk. A scan of the next chunk beside the chain of this one is
-// supported, but today's scan occupies every CU and slows the chain more than
-// it saves, so a chunk is as long as the summary budget allows.
-constexpr int kOverlapChunk = 1 << 30;
+// Chunks of the overlapped stream: the first is short (its scan is not
+// hidden), each next one 1.5 times longer (its scan, on half the CUs, must end
+// before the chain of the previous one), up to kOverlapChunk steps.
+constexpr int kOverlapFirst = 64;
+constexpr int kOverlapChunk = 256;
+constexpr int kOverlapStepsPerGroup = 2;   // more, shorter scan workgroups balance a short chunk
+// Of every 32 CUs, the chains' share in the overlapped stream: room for one
+// list workgroup and one full-vocabulary workgroup per row side by side (the
+// latter holds a whole CU's LDS).
+constexpr int kChainCusPer32 = 16;
 constexpr int kFastRounds = 3;
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
@@ -190,6 +202,7 @@ int c4s_create(int device, c4s_ctx** out) {
   if (g.err != hipSuccess) { delete ctx; return C4S_EHIP; }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) != hipSuccess) { delete ctx; return C4S_EHIP; }
+  ctx->n_cus = prop.multiProcessorCount;
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
     // The code objects are built for gfx950 only.
     delete ctx;
@@ -218,13 +231,17 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (ctx->host_stream) (void)hipStreamSynchronize(ctx->host_stream);
   if (ctx->side) (void)hipStreamSynchronize(ctx->side);
   if (ctx->scan_s) (void)hipStreamSynchronize(ctx->scan_s);
+  for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
+    if (st) (void)hipStreamSynchronize(st);
   for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws})
     if (p) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->scan_s) (void)hipStreamDestroy(ctx->scan_s);
+  for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
+    if (st) (void)hipStreamDestroy(st);
   for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1],
-                        ctx->ev_chain[0], ctx->ev_chain[1]})
+                        ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_done})
     if (ev) (void)hipEventDestroy(ev);
   delete ctx;
   return C4S_OK;
@@ -239,6 +256,31 @@ int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream) {
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   return launch_rows_checked(ctx, rows, static_cast<hipStream_t>(stream));
+}
+
+// Streams of the overlapped stream, created once: the two chain streams on
+// CUs 32 j + i, i < kChainCusPer32 (the runtime spreads them evenly over the
+// XCDs), the scan on the others. False when the device or the runtime cannot
+// split.
+static bool cu_split(c4s_ctx* ctx) {
+  if (ctx->chain_m) return true;
+  if (ctx->cu_split_tried) return false;
+  ctx->cu_split_tried = true;
+  const int n = ctx->n_cus;
+  if (n < 64 || n % 32 != 0) return false;
+  std::vector<uint32_t> chain_mask((size_t)n / 32, (1u << kChainCusPer32) - 1u), scan_mask((size_t)n / 32);
+  for (size_t i = 0; i < scan_mask.size(); ++i) scan_mask[i] = ~chain_mask[i];
+  const uint32_t nw = (uint32_t)chain_mask.size();
+  if (hipExtStreamCreateWithCUMask(&ctx->scan_m, nw, scan_mask.data()) != hipSuccess ||
+      hipExtStreamCreateWithCUMask(&ctx->chain_m, nw, chain_mask.data()) != hipSuccess ||
+      hipExtStreamCreateWithCUMask(&ctx->side_m, nw, chain_mask.data()) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_done, hipEventDisableTiming) != hipSuccess) {
+    for (hipStream_t* st : {&ctx->scan_m, &ctx->chain_m, &ctx->side_m})
+      if (*st) { (void)hipStreamDestroy(*st); *st = nullptr; }
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
 }
 
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
@@ -285,13 +327,20 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     return C4S_OK;
   }
   // Steps go in chunks; the chain carries its per-row state from chunk to
-  // chunk. The scan of chunk c+1 runs on its own stream beside the chain of
-  // chunk c; summaries are double-buffered and a scan waits for the chain
-  // that last read its buffer.
+  // chunk. Overlapped (rows at most half the chains' CUs, steps for two
+  // chunks or more): the scan of chunk c+1 runs on its own CUs beside the chain of chunk
+  // c, summaries are double-buffered and a scan waits for the chain that last
+  // read its buffer; the first chunk's scan, which nothing hides, runs on every
+  // CU. Otherwise the whole stream is one chunk where the budget allows, each
+  // phase on every CU.
   const size_t per_step = (size_t)a.n_rows * c4s::kSumStride;
-  size_t chunk_sz = std::min<size_t>({(size_t)a.n_steps, (size_t)kOverlapChunk, kSumBudget / per_step});
-  if (chunk_sz < (size_t)a.n_steps) chunk_sz = std::min(chunk_sz, kSumBudget / 2 / per_step);   // two buffers
-  const int chunk = (int)std::max<size_t>(1, chunk_sz);
+  const int chain_cus = ctx->n_cus / 32 * kChainCusPer32;
+  const bool overlap = 2 * a.n_rows <= chain_cus && a.n_steps >= 4 * kOverlapFirst &&
+                       (size_t)kOverlapChunk * 2 * per_step <= kSumBudget && cu_split(ctx);
+  size_t chunk_sz = std::min<size_t>((size_t)a.n_steps, kSumBudget / per_step);
+  if (overlap) chunk_sz = std::min<size_t>((size_t)a.n_steps, kOverlapChunk);
+  else if (chunk_sz < (size_t)a.n_steps) chunk_sz = std::min(chunk_sz, kSumBudget / 2 / per_step);   // two buffers
+  const int chunk = (int)std::max<size_t>(1, chunk_sz);   // the longest chunk
   const size_t chunk_bytes = per_step * (size_t)chunk;
   const int n_bufs = chunk < a.n_steps ? 2 : 1;
   int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, (size_t)n_bufs * chunk_bytes, "stream summaries");
@@ -309,54 +358,66 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
     return pipelined ? c4s::launch_stream_rowp(a, w, on) : c4s::launch_stream_rowk(a, w, on);
   };
+  const hipStream_t chain_on = overlap ? ctx->chain_m : hs;
+  const hipStream_t side_on = overlap ? ctx->side_m : ctx->side;
   hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
   if (e0 == hipSuccess) e0 = hipStreamWaitEvent(ctx->scan_s, ctx->ev_start, 0);
+  if (e0 == hipSuccess && overlap) e0 = hipStreamWaitEvent(chain_on, ctx->ev_start, 0);
   if (e0 != hipSuccess) return hip_fail(ctx, e0, "sample_stream scan stream");
-  for (int s0 = 0, ci = 0; s0 < a.n_steps; s0 += chunk, ++ci) {
+  for (int s0 = 0, ci = 0, len = overlap ? kOverlapFirst : chunk; s0 < a.n_steps;
+       s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 2 : chunk)) {
     const int buf = ci & 1;
+    const hipStream_t scan_on = (overlap && ci > 0) ? ctx->scan_m : ctx->scan_s;
     c4s::StreamWs w{};
     w.sum = static_cast<unsigned char*>(ctx->sum_ws) + (size_t)buf * chunk_bytes;
     w.state = static_cast<uint32_t*>(ctx->state_ws);
     w.s_begin = s0;
-    w.s_end = std::min(a.n_steps, s0 + chunk);
-    w.steps_per_group = kScanStepsPerGroup;
+    w.s_end = std::min(a.n_steps, s0 + len);
+    w.steps_per_group = overlap ? kOverlapStepsPerGroup : kScanStepsPerGroup;
     w.sortbuf = pipelined ? static_cast<uint32_t*>(ctx->ws) : nullptr;
     w.sort_stride = (int64_t)(sort_row / sizeof(uint32_t));
     hipError_t e = hipSuccess;
-    if (ci >= 2 && (e = hipStreamWaitEvent(ctx->scan_s, ctx->ev_chain[buf], 0)) != hipSuccess)
+    if (overlap && ci == 1 && (e = hipStreamWaitEvent(scan_on, ctx->ev_scan[0], 0)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream scan order");
+    if (ci >= 2 && (e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream buffer reuse");
-    e = c4s::launch_stream_scan(a, w, ctx->scan_s);
+    e = c4s::launch_stream_scan(a, w, scan_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream scan launch");
-    if ((e = hipEventRecord(ctx->ev_scan[buf], ctx->scan_s)) != hipSuccess ||
-        (e = hipStreamWaitEvent(hs, ctx->ev_scan[buf], 0)) != hipSuccess)
+    if ((e = hipEventRecord(ctx->ev_scan[buf], scan_on)) != hipSuccess ||
+        (e = hipStreamWaitEvent(chain_on, ctx->ev_scan[buf], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
     // Fast passes stop a row at a step they cannot decide; the repair kernel
     // runs that step exactly; the finisher completes whatever is left.
     for (int r = 0; r < kFastRounds; ++r) {
       w.round = r;
       if (r == 0) {   // list rows here, full-vocabulary rows on the side stream, side by side
-        if ((e = hipEventRecord(ctx->ev_fork, hs)) != hipSuccess ||
-            (e = hipStreamWaitEvent(ctx->side, ctx->ev_fork, 0)) != hipSuccess)
+        if ((e = hipEventRecord(ctx->ev_fork, chain_on)) != hipSuccess ||
+            (e = hipStreamWaitEvent(side_on, ctx->ev_fork, 0)) != hipSuccess)
           return hip_fail(ctx, e, "sample_stream fork");
-        e = launch_row_chain(w, ctx->side);
+        e = launch_row_chain(w, side_on);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream row-chain launch");
-        e = c4s::launch_stream_list(a, w, hs);
+        e = c4s::launch_stream_list(a, w, chain_on);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream list-chain launch");
-        if ((e = hipEventRecord(ctx->ev_join, ctx->side)) != hipSuccess ||
-            (e = hipStreamWaitEvent(hs, ctx->ev_join, 0)) != hipSuccess)
+        if ((e = hipEventRecord(ctx->ev_join, side_on)) != hipSuccess ||
+            (e = hipStreamWaitEvent(chain_on, ctx->ev_join, 0)) != hipSuccess)
           return hip_fail(ctx, e, "sample_stream join");
       } else {
-        e = c4s::launch_stream_list(a, w, hs);
-        if (e == hipSuccess) e = launch_row_chain(w, hs);
+        e = c4s::launch_stream_list(a, w, chain_on);
+        if (e == hipSuccess) e = launch_row_chain(w, chain_on);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
       }
-      e = c4s::launch_stream_repair(a, w, hs);
+      e = c4s::launch_stream_repair(a, w, chain_on);
       if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream repair launch");
     }
-    e = c4s::launch_stream_chain(a, w, hs);
+    e = c4s::launch_stream_chain(a, w, chain_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
-    if ((e = hipEventRecord(ctx->ev_chain[buf], hs)) != hipSuccess)
+    if ((e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream chain order");
+  }
+  if (overlap) {   // the caller's stream continues after the last chain
+    hipError_t e = hipEventRecord(ctx->ev_done, chain_on);
+    if (e == hipSuccess) e = hipStreamWaitEvent(hs, ctx->ev_done, 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream join caller");
   }
   return C4S_OK;
 }

@@ -93,6 +93,31 @@ def test_stream_two_phase_all_modes(orc, gpu_ctx, V, rows, steps):
     print("exact steps per row", st[:, 1].tolist())
 
 
+def test_stream_overlapped_chunks(orc, gpu_ctx):
+    """A stream long enough for chunks of 128 steps whose scans run beside the
+    previous chunk's chains on their own CUs: every row mode, stop tokens
+    planted in the second and third chunks, against the oracle and the
+    single-kernel stream."""
+    steps, rows, V = 300, 48, 8194
+    p = _mixed_params(4242, rows, V)
+    x = W.batch64_logits(4243, steps, rows, V)
+    stop = V - 1
+    for s, r in [(130, 0), (255, 3), (256, 9), (299, 12)]:
+        x[s, r, stop] = 80.0
+        p["top_k"][r], p["pen"][r], p["do_sample"][r] = 1, 1.0, 1
+    print(f"overlapped stream V={V} rows={rows} steps={steps}", flush=True)
+    toks, rng, st = run_stream(gpu_ctx, p, x, stop_token=stop)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
+                                    p["top_p"], p["pen"], p["do_sample"], p["rng"], stop_token=stop,
+                                    n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
+    assert np.array_equal(rng, orng)
+    assert toks[130, 0] == stop and (toks[131:, 0] == -1).all()
+    stoks, srng, _ = run_stream(gpu_ctx, p, x, stop_token=stop, sequential=True)
+    assert np.array_equal(stoks, toks) and np.array_equal(srng, rng)
+
+
 def test_stream_stop_token_and_greedy(orc, gpu_ctx):
     steps, rows, V = 40, 16, 2000
     p = W.batch64_params(seed=9, rows=rows, V=V)
