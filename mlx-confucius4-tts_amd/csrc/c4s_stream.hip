@@ -1568,7 +1568,8 @@ __device__ __forceinline__ void dma_step(const float* p, int V, const uint64_t* 
 
 // Corrections of one step over ids [lo, hi) drawn during the stream (bmN,
 // never in H0): the mass of the raw value minus that of the penalised value,
-// added to its chunk. fp32 masses with their error bound (el), or exact ones.
+// added to its chunk (unless cdelta is null: only the full-vocabulary draw
+// reads chunks). fp32 masses with their error bound (el), or exact ones.
 __device__ __forceinline__ double corrections_range(const float* val, int lo, int hi, const uint32_t* bmN,
                                                     const SumHdr& hh, const RowCfg& c, double* cdelta,
                                                     bool exact, double& el) {
@@ -1596,7 +1597,7 @@ __device__ __forceinline__ double corrections_range(const float* val, int lo, in
         d = (double)m_raw - (double)m_pen;
         el += (double)er0 + (double)er1;
       }
-      atomicAdd(&cdelta[chunk_of(id, hh.head, hh.nchunk)], d);
+      if (cdelta) atomicAdd(&cdelta[chunk_of(id, hh.head, hh.nchunk)], d);
       dl += d;
     }
   }
@@ -1635,7 +1636,8 @@ __device__ __forceinline__ int list_drawn(const uint32_t* bmN, int lo, int hi, i
 
 // fp32 corrections of one step by helper wave h over the listed drawn ids of
 // its range (n of them, all listed); returns the wave's total and (in el) its
-// error bound, in all lanes. Two ids per lane at a time.
+// error bound, in all lanes, and adds to the chunks unless cdelta is null.
+// Two ids per lane at a time.
 __device__ __forceinline__ double listed_corrections(const float* val, const int* list, int n, const SumHdr& hh,
                                                      const RowCfg& c, double* cdelta, double& el) {
   const int lane = lane_id();
@@ -1652,12 +1654,12 @@ __device__ __forceinline__ double listed_corrections(const float* val, const int
     const float a0 = mass_approx(x0, mk, e00), b0 = mass_approx(pen_approx(x0, c.pen, rpen), mk, e01);
     const float a1 = mass_approx(x1, mk, e10), b1 = mass_approx(pen_approx(x1, c.pen, rpen), mk, e11);
     const double d0 = (double)a0 - (double)b0;
-    atomicAdd(&cdelta[chunk_of(i0, hh.head, hh.nchunk)], d0);
+    if (cdelta) atomicAdd(&cdelta[chunk_of(i0, hh.head, hh.nchunk)], d0);
     dl += d0;
     ell += (double)e00 + (double)e01;
     if (v1) {
       const double d1 = (double)a1 - (double)b1;
-      atomicAdd(&cdelta[chunk_of(i1, hh.head, hh.nchunk)], d1);
+      if (cdelta) atomicAdd(&cdelta[chunk_of(i1, hh.head, hh.nchunk)], d1);
       dl += d1;
       ell += (double)e10 + (double)e11;
     }
@@ -1694,6 +1696,9 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   int s_first;
   if (!fast_begin(a, w, row, NTC, s_first)) return;
   C4S_ROW_TIME(0);
+  // Per-chunk corrections feed only the full-vocabulary draw (top_p >= 1);
+  // nucleus rows use their totals.
+  const bool dense = !(1.0 - (double)c.p > 0.0);
   const uint32_t* stw = w.state + (size_t)row * kStateWords;
   const int s_end = w.s_end;
   uint64_t* sumslots = reinterpret_cast<uint64_t*>(smem);
@@ -1727,7 +1732,8 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
     ndrawn = list_drawn(bmNb[s_first & 1], third_bound(V, hw), third_bound(V, hw + 1), ps.dlist[hw]);
     double d = 0.0, e = 0.0;
     if (c.pen_on)
-      d = helper_corrections(rowval(s_first), V, hw, bmNb[s_first & 1], hh, c, ps.cdelta[s_first & 1],
+      d = helper_corrections(rowval(s_first), V, hw, bmNb[s_first & 1], hh, c,
+                             dense ? ps.cdelta[s_first & 1] : nullptr,
                              ps.dlist[hw], ndrawn, e);
     if (lane == 0) { ps.wd[s_first & 1][hw] = d; ps.we[s_first & 1][hw] = e; }
   }
@@ -1751,10 +1757,12 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
       if (attempt == 1) {
         const int ch = (V + NTC - 1) / NTC;
         const int lo = min(V, t * ch), hi = min(V, lo + ch);
-        for (int i = t; i < kMaxChunks; i += NTC) ps.cdx[i] = 0.0;
+        if (dense)
+          for (int i = t; i < kMaxChunks; i += NTC) ps.cdx[i] = 0.0;
         __syncthreads();
         double el;
-        double d = corrections_range(rowval(s), lo, hi, bmN, hdr_from(sumslot(s)), c, ps.cdx, true, el);
+        double d = corrections_range(rowval(s), lo, hi, bmN, hdr_from(sumslot(s)), c, dense ? ps.cdx : nullptr,
+                                     true, el);
         d = wave_sum_dpp(d);
         if (lane == 0) ps.xd[wv] = d;
         __syncthreads();
@@ -1777,8 +1785,10 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
             const float m1 = mass_approx(x, mk, e0);
             const float m2 = mass_approx(pen_approx(x, c.pen, 1.0f / c.pen), mk, e1);
             const double d = (double)m1 - (double)m2;
-            if (lane == 0) cd[chunk_of(tprev, h.head, h.nchunk)] += d;
-            wave_sync();
+            if (dense) {
+              if (lane == 0) cd[chunk_of(tprev, h.head, h.nchunk)] += d;
+              wave_sync();
+            }
             ds += d;
             de += (double)e0 + (double)e1;
           }
@@ -1792,31 +1802,32 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
         const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, ps, o);
         const bool retry = attempt == 0 && !ok && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
         C4S_PHASE(2);
-        if (attempt == 0)
+        if (attempt == 0 && dense)
           for (int i = lane; i < kMaxChunks; i += kWave) ps.cdelta[par][i] = 0.0;
+        // The token joins bmN of step s+1 unless it is the stop token
+        // (text2semantic.cpp:333-334) or already penalised; both bitmap words
+        // are read by every lane at once (tok is wave-uniform).
+        const int tok = o.tok;
+        const int tc = (tok >= 0 && tok < V) ? tok : 0;
+        const uint32_t wh = bmH0[tc >> 5], wn = bmN[tc >> 5];
+        const bool fresh = ok && c.pen_on && tok != a.stop_token && tok == tc && !(((wh | wn) >> (tc & 31)) & 1u);
         if (lane == 0) {
           ps.flag[par] = ok ? 1 : (retry ? 2 : 0);
           ps.rng = rng;
           if (ok) {
-            const int tok = o.tok;
             ps.tok[par] = tok;
             acc[0] |= 64u | 1u;
             acc[2] += o.dex;
             acc[3] += o.kept;
             uint32_t* nb = bmNb[par ^ 1];   // becomes the set of step s+1
-            if (tprev >= 0) nb[tprev >> 5] |= 1u << (tprev & 31);
-            tprev = -1;
-            // text2semantic.cpp:333-334: the stop token is not appended
-            if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok) && !bit_of(bmN, tok)) {
-              nb[tok >> 5] |= 1u << (tok & 31);
-              tprev = tok;
-            }
-            ps.nt[par] = tprev;
+            if (tprev >= 0) atomicOr(&nb[tprev >> 5], 1u << (tprev & 31));
+            if (fresh) atomicOr(&nb[tok >> 5], 1u << (tok & 31));
+            ps.nt[par] = fresh ? tok : -1;
           } else if (!retry) {
             acc[0] |= 1u << (20 + o.why);
           }
         }
-        tprev = (int)readlane_u32((uint32_t)tprev, 0);
+        if (ok) tprev = fresh ? tok : -1;
       } else if (attempt == 0) {
         C4S_HELPER_PHASE(0);
         wait_loads();   // step s+1 is in LDS (this wave's range)
@@ -1835,7 +1846,8 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
           const SumHdr hh = hdr_words(hc[0], hc[1], hc[2], hc[3], hc[4]);
           double d = 0.0, e = 0.0;
           if (c.pen_on)
-            d = helper_corrections(rowval(sn), V, hw, bmN, hh, c, ps.cdelta[sn & 1], ps.dlist[hw], ndrawn, e);
+            d = helper_corrections(rowval(sn), V, hw, bmN, hh, c, dense ? ps.cdelta[sn & 1] : nullptr,
+                                   ps.dlist[hw], ndrawn, e);
           if (lane == 0) { ps.wd[sn & 1][hw] = d; ps.we[sn & 1][hw] = e; }
         }
         C4S_HELPER_PHASE(2);
