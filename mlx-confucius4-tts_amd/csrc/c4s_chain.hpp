@@ -1203,14 +1203,15 @@ __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitma
 // ---- draw over one candidate per lane ------------------------------------------
 
 // Inverse-CDF draw (text2semantic.cpp:150-165) over at most one kept entry per
-// lane: id, mass e, and slot = its rank in id order among the scan's
-// candidates (distinct, below kCandCap). The entries move to lanes in id order
+// lane: id, mass e, and slot = its rank in id order among some superset of the
+// kept entries (distinct, below 2^kBits). The entries move to lanes in id order
 // (rank by ballots over the slot bits, then a lane permute) and one prefix
 // scan forms the id-order sums. The reference sums sequentially, so the first
 // lane reaching r = u * total decides only with the margin rel_eps (plus
 // eps_add, the relative error of masses that are approximations); otherwise
 // the id-order sums are replayed sequentially (ids outside the kept set weigh
 // 0), or, when replay is false (approximate masses), -1 is returned.
+template <int kBits = 10>
 __device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, double u, int V, uint32_t& exact,
                                          double eps_add = 0.0, bool replay = true) {
   const int lane = lane_id();
@@ -1221,13 +1222,12 @@ __device__ __forceinline__ int lane_draw(bool kept, int id, int slot, double e, 
   uint64_t same = km;
   int pos = 0;
 #pragma unroll
-  for (int b = 9; b >= 0; --b) {
+  for (int b = kBits - 1; b >= 0; --b) {
     const bool bit = kept && ((slot >> b) & 1);
     const uint64_t one = __ballot(bit);
     pos += bit ? __popcll(same & ~one) : 0;
     same &= bit ? one : ~one;
   }
-  static_assert(kCandCap <= 1024, "slots have ten bits");
   const int a4 = (kept ? pos : kWave - 1) << 2;   // lanes past nk are ignored
   const uint64_t eb = (uint64_t)__double_as_longlong(e);
   const uint32_t plo = (uint32_t)__builtin_amdgcn_ds_permute(a4, (int)(uint32_t)eb);

@@ -70,7 +70,8 @@ struct SumHdr {
 static_assert(sizeof(SumHdr) == kSumHdrBytes, "summary header size");
 
 // List entry: key of z = fl(y / T) (y itself on the greedy path), then the id
-// and the id-order rank among the scan's candidates; larger entries come first
+// and an id-order rank (while the scan sorts: the candidate's position; in a
+// summary: the rank among the list's entries); larger entries come first
 // (z desc, id asc), which is the declared top_p order of equal values.
 __device__ __forceinline__ uint64_t make_entry(float y, int id, int rank) {
   return ((uint64_t)fkey(y) << 32) | ((uint32_t)(16383 - id) << 10) | (uint32_t)rank;
@@ -146,6 +147,8 @@ struct ScanSh {
   double chunk[kMaxChunks];
   double edge[8];
   uint32_t bu[4];
+  uint32_t lmark[kCandCap / 32];   // candidate positions of the list entries
+  uint32_t lpre[kCandCap / 32];    // marks before each word
 };
 
 // Block exclusive scan over the NTA threads (thread order).
@@ -440,10 +443,28 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
       // exp((double)fl(z - z_max)) as the reference computes it, in fp32.
       float* ly = reinterpret_cast<float*>(sw + kYW);
       const float zmax = kfloat(ent_key(srt[0]));
+      // The stored rank is the id-order rank among the list entries:
+      // candidates sit in id order, so it counts the list's candidate
+      // positions below the entry's own.
+      if (t < kCandCap / 32) sh.lmark[t] = 0u;
+      __syncthreads();
+      for (int i = t; i < n; i += NTA) {
+        const int ci = ent_rank(srt[i]);
+        atomicOr(&sh.lmark[ci >> 5], 1u << (ci & 31));
+      }
+      __syncthreads();
+      if (t < kWave) {
+        const uint32_t pc = (t < kCandCap / 32) ? (uint32_t)__popc(sh.lmark[t]) : 0u;
+        const uint32_t inc = wave_scan_u32(pc);
+        if (t < kCandCap / 32) sh.lpre[t] = inc - pc;
+      }
+      __syncthreads();
       for (int i = t; i < n; i += NTA) {
         const uint64_t e = srt[i];
-        lst[i] = e;
-        ly[i] = masses ? (float)exp((double)(kfloat(ent_key(e)) - zmax)) : sh.candy[ent_rank(e)];
+        const int ci = ent_rank(e);
+        const uint32_t lr = sh.lpre[ci >> 5] + (uint32_t)__popc(sh.lmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
+        lst[i] = (e & ~1023ull) | lr;
+        ly[i] = masses ? (float)exp((double)(kfloat(ent_key(e)) - zmax)) : sh.candy[ci];
       }
     }
 
@@ -541,7 +562,7 @@ __global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w
 struct ChainSh {
   uint64_t sum[kSumWords];   // this step's summary: header words, list, chunks
   double cdelta[kMaxChunks];
-  uint32_t inv[kCandCap];   // id-order slot -> (generation << 10) | unhit rank
+  uint32_t inv[kListLarge];   // id-order slot -> (generation << 10) | unhit rank
   uint32_t gen;             // generation of the last row step
   float lz[kListLarge];
   float lm[kListLarge];
@@ -564,10 +585,14 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Slot s (an id-order rank) lives at position slot_pos(s): lane l's sixteen
-// slots [16 l, 16 l + 16) are the l-th word of sixteen 64-word rows, so a wave
-// reads them without bank conflicts.
-__device__ __forceinline__ int slot_pos(int s) { return ((s & 15) << 6) | (s >> 4); }
+// Slot s (an id-order rank among the list entries) lives at position
+// slot_pos(s): lane l's eight slots [8 l, 8 l + 8) are the l-th word of eight
+// 64-word rows, so a wave reads them without bank conflicts.
+constexpr int kSlotsPerLane = kListLarge / kWave;
+constexpr int kSlotBits = 9;   // summary slots are below kListLarge
+static_assert((1 << kSlotBits) == kListLarge, "slot bits cover the list");
+static_assert(kSlotsPerLane == 8, "slot_pos assumes eight slots a lane");
+__device__ __forceinline__ int slot_pos(int s) { return ((s & 7) << 6) | (s >> 3); }
 
 __device__ __forceinline__ SumHdr hdr_words(uint64_t w0, uint64_t w1, uint64_t w2, uint64_t w3,
                                             uint64_t w4) {
@@ -709,7 +734,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   const bool kept = sv && (long long)lane < m;
   const uint64_t st = xorshift64(rng);
   C4S_LIST_PHASE(5);
-  o.tok = lane_draw(kept, ids, slot, e, unit_from_state(st), V, o.dex);
+  o.tok = lane_draw<kSlotBits>(kept, ids, slot, e, unit_from_state(st), V, o.dex);
   C4S_LIST_PHASE(6);
   o.kept = (uint32_t)__popcll(__ballot(kept));
   rng = st;
@@ -738,7 +763,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
   uint32_t gen = cs.gen + 1u;
   if (gen == 1u || gen >= (1u << 22)) {
 #pragma unroll
-    for (int i = 0; i < kCandCap / kWave; ++i) cs.inv[(i << 6) | lane] = 0u;
+    for (int i = 0; i < kSlotsPerLane; ++i) cs.inv[(i << 6) | lane] = 0u;
     gen = 1u;
   }
   if (lane == 0) cs.gen = gen;
@@ -901,15 +926,16 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
       const bool kept = lane < q;
       const int kid = kept ? cs.lid[lane] : 0, ks = kept ? cs.lslot[lane] : 0;
       int tok = -1;
-      if (approx) tok = lane_draw(kept, kid, ks, kept ? mass_of(lane, false) : 0.0, u, V, o.dex, 0x1p-22, false);
-      if (tok < 0) tok = lane_draw(kept, kid, ks, kept ? mass_of(lane, true) : 0.0, u, V, o.dex);
+      if (approx)
+        tok = lane_draw<kSlotBits>(kept, kid, ks, kept ? mass_of(lane, false) : 0.0, u, V, o.dex, 0x1p-22, false);
+      if (tok < 0) tok = lane_draw<kSlotBits>(kept, kid, ks, kept ? mass_of(lane, true) : 0.0, u, V, o.dex);
       o.tok = tok;
     } else {
       // Kept ranks [0, q) in id order: lane l reads the id-order slots
-      // [16 l, 16 l + 16); a slot tagged with this call's generation names its
+      // [8 l, 8 l + 8); a slot tagged with this call's generation names its
       // unhit rank, every other slot (no candidate, a hit, a rank past the cut)
       // weighs 0. First with the masses above, then with exact masses.
-      constexpr int kPer = kCandCap / kWave;
+      constexpr int kPer = kSlotsPerLane;
       int rks[kPer];
       uint32_t vb = 0u;   // bit i: slot 16 lane + i is kept
 #pragma unroll
@@ -978,7 +1004,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
             return ((x >> 10) == gen && rk < q) ? exp((double)(cs.lz[rk] - mt)) : 0.0;
           };
           double total = 0.0;
-          for (int sl = 0; sl < kCandCap; ++sl) {
+          for (int sl = 0; sl < kListLarge; ++sl) {
             int rk;
             total += kept_mass(sl, rk);
           }
@@ -988,7 +1014,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
             res = 0;
           } else {
             double acc = 0.0;
-            for (int sl = 0; sl < kCandCap; ++sl) {
+            for (int sl = 0; sl < kListLarge; ++sl) {
               int rk;
               const double ei = kept_mass(sl, rk);
               acc += ei;
@@ -1485,7 +1511,7 @@ struct RowPSh {
   double wd[2][4];                // helper waves' correction sums, by step parity
   double we[2][4];                // and their error bounds
   double xd[NWC];                 // exact corrections of a retried step, per wave
-  uint32_t inv[kCandCap];         // id-order slot -> (generation << 10) | unhit rank
+  uint32_t inv[kListLarge];       // id-order slot -> (generation << 10) | unhit rank
   uint32_t gen;                   // generation of the last row step
   float lz[kListLarge];
   float lm[kListLarge];
