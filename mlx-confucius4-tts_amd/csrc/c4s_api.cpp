@@ -46,6 +46,9 @@ struct c4s_ctx {
   bool cu_split_tried = false;
   hipStream_t scan_m = nullptr, chain_m = nullptr, side_m = nullptr;
   hipEvent_t ev_done = nullptr;
+  // step segments of the pipelined row chain (rows without penalty)
+  void* segres = nullptr;
+  size_t segres_bytes = 0;
 };
 
 namespace {
@@ -67,6 +70,7 @@ constexpr int kOverlapStepsPerGroup = 2;   // more, shorter scan workgroups bala
 // latter holds a whole CU's LDS).
 constexpr int kChainCusPer32 = 16;
 constexpr int kFastRounds = 3;
+constexpr int kMaxSegments = 8;   // step segments per row without penalty
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
   if (ctx) ctx->err = msg;
@@ -233,7 +237,7 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (ctx->scan_s) (void)hipStreamSynchronize(ctx->scan_s);
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamSynchronize(st);
-  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws})
+  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws, ctx->segres})
     if (p) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
@@ -355,8 +359,21 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, sort_row * (size_t)a.n_rows, "sort workspace");
     if (rc) return rc;
   }
+  // Rows without penalty split their steps into segments, one workgroup each,
+  // over the CUs the chains have (every workgroup of the pipelined chain
+  // holds a CU's LDS).
+  const int nseg = pipelined ? std::max(2, std::min(kMaxSegments, (overlap ? chain_cus : ctx->n_cus) /
+                                                                     std::max(1, a.n_rows)))
+                             : 1;
+  if (nseg > 1) {
+    rc = ensure(ctx, &ctx->segres, &ctx->segres_bytes, (size_t)a.n_rows * nseg * 4 * sizeof(uint64_t),
+                "segment results");
+    if (rc) return rc;
+  }
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
-    return pipelined ? c4s::launch_stream_rowp(a, w, on) : c4s::launch_stream_rowk(a, w, on);
+    if (!pipelined) return c4s::launch_stream_rowk(a, w, on);
+    hipError_t e = c4s::launch_stream_rowp(a, w, on);
+    return e == hipSuccess ? c4s::launch_stream_segfix(a, w, on) : e;
   };
   const hipStream_t chain_on = overlap ? ctx->chain_m : hs;
   const hipStream_t side_on = overlap ? ctx->side_m : ctx->side;
@@ -376,6 +393,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     w.steps_per_group = overlap ? kOverlapStepsPerGroup : kScanStepsPerGroup;
     w.sortbuf = pipelined ? static_cast<uint32_t*>(ctx->ws) : nullptr;
     w.sort_stride = (int64_t)(sort_row / sizeof(uint32_t));
+    w.nseg = nseg;
+    w.segres = static_cast<uint64_t*>(ctx->segres);
     hipError_t e = hipSuccess;
     if (overlap && ci == 1 && (e = hipStreamWaitEvent(scan_on, ctx->ev_scan[0], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");

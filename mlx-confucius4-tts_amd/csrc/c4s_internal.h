@@ -99,6 +99,8 @@ struct StreamWs {
   int round;               // chain rounds within the chunk (0: the first)
   uint32_t* sortbuf;       // exact steps of the pipelined row chain: per-row key buffer
   int64_t sort_stride;     // words per row
+  int nseg;                // pipelined row chain: step segments of a row without penalty
+  uint64_t* segres;        // [n_rows][nseg][4] segment results (status and stop step, RNG, statistics)
 };
 
 struct LmHeadArgs {
@@ -124,6 +126,7 @@ hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_
 hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);

@@ -1505,6 +1505,12 @@ constexpr int kDrawnList = 512;                         // drawn ids listed per 
 static_assert((size_t)kSumWordsP * 8 <= kSumStride, "whole quads stay inside a summary");
 static_assert(kHdrW % 2 == 0, "header words start a quad");
 
+// Segment results of the pipelined row chain, word 0.
+constexpr uint64_t kSegIdle = 0;                   // the row did not run in this chunk
+constexpr uint64_t kSegRan = 1ull << 62;           // ran to the segment's end
+constexpr uint64_t kSegStop = 1ull << 63;          // | stop step: ended by the stop token
+constexpr uint64_t kSegEmpty = 3ull << 60;         // no steps in this segment
+
 struct RowPSh {
   double cdelta[2][kMaxChunks];   // corrections per chunk, by step parity
   double cdx[kMaxChunks];         // exact corrections of a retried step
@@ -1719,14 +1725,38 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id(), hw = wv - 1;
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
   if (stream_mode(c, V) != kModeRow) return;
+  // A row without penalty has independent steps but for the RNG, which every
+  // step advances once: workgroup (row, g) takes the g-th of nseg segments
+  // of the steps, from the RNG state jumped ahead, and k_stream_segfix
+  // settles the stop token and the carried state. A penalty makes the steps
+  // depend on the tokens drawn: one segment.
+  const int nseg = c.pen_on ? 1 : w.nseg;
+  const int g = blockIdx.y;
+  if (g >= nseg) return;
+  uint64_t* segres = nseg > 1 ? w.segres + ((size_t)row * w.nseg + g) * 4 : nullptr;
   int s_first;
-  if (!fast_begin(a, w, row, NTC, s_first)) return;
+  if (!fast_begin(a, w, row, NTC, s_first)) {
+    if (nseg > 1 && t == 0) segres[0] = kSegIdle;
+    return;
+  }
+  int s_end = w.s_end;
+  uint64_t rng0 = a.rng[row];
+  if (nseg > 1) {
+    const int L = (s_end - s_first + nseg - 1) / nseg;
+    const int lo = min(s_end, s_first + g * L), hi = min(s_end, lo + L);
+    if (lo >= hi) {
+      if (t == 0) segres[0] = kSegEmpty;
+      return;
+    }
+    for (int i = s_first; i < lo; ++i) rng0 = xorshift64(rng0);
+    s_first = lo;
+    s_end = hi;
+  }
   C4S_ROW_TIME(0);
   // Per-chunk corrections feed only the full-vocabulary draw (top_p >= 1);
   // nucleus rows use their totals.
   const bool dense = !(1.0 - (double)c.p > 0.0);
   const uint32_t* stw = w.state + (size_t)row * kStateWords;
-  const int s_end = w.s_end;
   uint64_t* sumslots = reinterpret_cast<uint64_t*>(smem);
   float* rowslots = reinterpret_cast<float*>(smem + 3 * (size_t)kSumWordsP * 8);
   const int RS = vpad(V) + 4;
@@ -1763,10 +1793,10 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
                              ps.dlist[hw], ndrawn, e);
     if (lane == 0) { ps.wd[s_first & 1][hw] = d; ps.we[s_first & 1][hw] = e; }
   }
-  if (t == 0) ps.rng = a.rng[row];
-  uint64_t rng = a.rng[row];
-  uint32_t acc[4] = {0u, 0u, 0u, 0u};
-  if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
+  if (t == 0) ps.rng = rng0;
+  uint64_t rng = rng0;
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};   // a segment's statistics start at zero
+  if (t == 0 && nseg == 1) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
   int tprev = -1;        // wave 0: token of the previous step when it joined bmN
   bool done = false;
   __syncthreads();
@@ -1931,8 +1961,52 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   __syncthreads();
   if (t == 0 && s > s_first) a.out_tok[(int64_t)(s - 1) * a.n_rows + row] = ps.tok[(s - 1) & 1];
   for (int s2 = s + t; s2 < s_end; s2 += NTC) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
-  fast_end(a, w, row, V, NTC, s_end, false, done, ps.rng, acc, bmNb[s & 1]);
+  if (nseg > 1) {
+    if (t == 0) {
+      segres[0] = done ? (kSegStop | (uint64_t)(uint32_t)(s - 1)) : kSegRan;
+      segres[1] = ps.rng;
+      segres[2] = (uint64_t)acc[0] | ((uint64_t)acc[1] << 32);
+      segres[3] = (uint64_t)acc[2] | ((uint64_t)acc[3] << 32);
+    }
+  } else {
+    fast_end(a, w, row, V, NTC, s_end, false, done, ps.rng, acc, bmNb[s & 1]);
+  }
   C4S_ROW_TIME(1);
+}
+
+// Settles the step segments of rows without penalty: the first stop token
+// ends the row (later segments' tokens become -1), the RNG state is the one
+// after the last step decided, the statistics add up.
+__global__ __launch_bounds__(kWave) void k_stream_segfix(StreamArgs a, StreamWs w) {
+  const int row = blockIdx.x;
+  const int t = threadIdx.x;
+  const RowCfg c = make_cfg(0u, a.vocab, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (stream_mode(c, a.vocab) != kModeRow || c.pen_on || w.nseg <= 1) return;
+  const uint64_t* sr = w.segres + (size_t)row * w.nseg * 4;
+  if (sr[0] == kSegIdle) return;   // nothing ran: the row was done or had no steps here
+  uint32_t* stw = w.state + (size_t)row * kStateWords;
+  uint32_t acc[4] = {stw[1], stw[2], stw[3], stw[4]};
+  uint64_t rng = a.rng[row];
+  int stop = -1;
+  for (int g = 0; g < w.nseg && stop < 0; ++g) {
+    const uint64_t st = sr[4 * g];
+    if (st == kSegEmpty) continue;
+    rng = sr[4 * g + 1];
+    acc[0] |= (uint32_t)sr[4 * g + 2];
+    acc[1] += (uint32_t)(sr[4 * g + 2] >> 32);
+    acc[2] += (uint32_t)sr[4 * g + 3];
+    acc[3] += (uint32_t)(sr[4 * g + 3] >> 32);
+    if ((st & kSegStop) != 0u) stop = (int)(uint32_t)st;
+  }
+  if (stop >= 0)
+    for (int s = stop + 1 + t; s < w.s_end; s += kWave) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
+  if (t == 0) {
+    a.rng[row] = rng;
+    stw[kStDone] = stop >= 0 ? 1u : 0u;
+    stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
+    stw[kStNext] = (uint32_t)w.s_end;
+    stw[kStPending] = 0u;
+  }
 }
 
 // ---- repair: the pending step of each row, exactly ------------------------------------
@@ -2248,7 +2322,15 @@ size_t stream_rowp_lds_bytes(int V) {
 hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_rowp, dim3(a.n_rows), dim3(NTC), stream_rowp_lds_bytes(a.vocab), s, a, w);
+  hipLaunchKernelGGL(k_stream_rowp, dim3(a.n_rows, max(1, w.nseg)), dim3(NTC), stream_rowp_lds_bytes(a.vocab), s, a,
+                     w);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin || w.nseg <= 1) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_segfix, dim3(a.n_rows), dim3(kWave), 0, s, a, w);
   return hipGetLastError();
 }
 

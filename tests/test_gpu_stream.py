@@ -105,6 +105,11 @@ def test_stream_overlapped_chunks(orc, gpu_ctx):
     for s, r in [(130, 0), (255, 3), (256, 9), (299, 12)]:
         x[s, r, stop] = 80.0
         p["top_k"][r], p["pen"][r], p["do_sample"][r] = 1, 1.0, 1
+    # full-vocabulary rows without penalty run in step segments: stops inside
+    # a later segment, the first chunk and a segment's first step
+    for s, r in [(200, 20), (40, 21), (64, 22), (161, 23)]:
+        x[s, r, stop] = 80.0
+        p["top_k"][r], p["top_p"][r], p["pen"][r], p["do_sample"][r] = 0, 0.9, 1.0, 1
     print(f"overlapped stream V={V} rows={rows} steps={steps}", flush=True)
     toks, rng, st = run_stream(gpu_ctx, p, x, stop_token=stop)
     otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
@@ -114,6 +119,7 @@ def test_stream_overlapped_chunks(orc, gpu_ctx):
     assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
     assert np.array_equal(rng, orng)
     assert toks[130, 0] == stop and (toks[131:, 0] == -1).all()
+    assert (toks[201:, 20] == -1).all()
     stoks, srng, _ = run_stream(gpu_ctx, p, x, stop_token=stop, sequential=True)
     assert np.array_equal(stoks, toks) and np.array_equal(srng, rng)
 
