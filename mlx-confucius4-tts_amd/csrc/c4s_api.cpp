@@ -406,8 +406,11 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
         (e = hipStreamWaitEvent(chain_on, ctx->ev_scan[buf], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
     // Fast passes stop a row at a step they cannot decide; the repair kernel
-    // runs that step exactly; the finisher completes whatever is left.
-    for (int r = 0; r < kFastRounds; ++r) {
+    // runs that step exactly; the finisher completes whatever is left. With
+    // the sort buffer (pipelined) both fast chains run their exact steps
+    // themselves: one round, no repair.
+    const int rounds = pipelined ? 1 : kFastRounds;
+    for (int r = 0; r < rounds; ++r) {
       w.round = r;
       if (r == 0) {   // list rows here, full-vocabulary rows on the side stream, side by side
         if ((e = hipEventRecord(ctx->ev_fork, chain_on)) != hipSuccess ||
@@ -425,8 +428,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
         if (e == hipSuccess) e = launch_row_chain(w, chain_on);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
       }
-      e = c4s::launch_stream_repair(a, w, chain_on);
-      if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream repair launch");
+      if (!pipelined && (e = c4s::launch_stream_repair(a, w, chain_on)) != hipSuccess)
+        return hip_fail(ctx, e, "sample_stream repair launch");
     }
     e = c4s::launch_stream_chain(a, w, chain_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");

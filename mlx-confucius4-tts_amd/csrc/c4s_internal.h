@@ -123,6 +123,7 @@ size_t stream_lds_bytes(int vocab, int unused);
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
+size_t stream_list_lds_bytes(int vocab);  // candidate-list chain: a row for its exact steps
 hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s);

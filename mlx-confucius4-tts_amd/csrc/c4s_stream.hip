@@ -1182,8 +1182,28 @@ struct ListRegs {
   float y0, y1;          // their values before the temperature
 };
 
+// Penalises the ids set in bm (text2semantic.cpp:142 via sampling.cpp:26),
+// one wave: lane l takes the bitmap words l + 64 j.
+__device__ __forceinline__ void penalise_wave(float* val, const uint32_t* bm, int V, float pen) {
+  const int nwords = bitmap_words(V);
+  for (int wi = lane_id(); wi < nwords; wi += kWave) {
+    uint32_t b = bm[wi];
+    while (b) {
+      const int i = 32 * wi + __ffs(b) - 1;
+      b &= b - 1;
+      if (i < V) val[i] = pen_exact(val[i], pen);
+    }
+  }
+}
+
+// Candidate-list rows, one wave per row. A step the list cannot decide runs
+// exactly in the kernel when the per-row sort buffer exists (the row read
+// into LDS, the penalty of H0 and the stream's ids, the whole chain);
+// otherwise the row stops there with the step pending for k_stream_repair.
 __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
   __shared__ ChainSh cs;
+  __shared__ ScratchT<1> xs;   // exact steps
   __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
   const int row = blockIdx.x;
   const int V = a.vocab;
@@ -1207,7 +1227,28 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     r.y0 = sy[lane];
     r.y1 = sy[lane + kWave];
   };
-  // One step; false when it has to be run exactly (nothing changed then).
+  float* xrow = reinterpret_cast<float*>(smem);   // exact steps (with the sort buffer)
+  auto exact = [&](int s) -> int {
+    const float* p = a.logits + (int64_t)row * a.ld + (int64_t)s * a.step_stride;
+    for (int i = lane; i < V; i += kWave) xrow[i] = p[i];
+    wave_sync();
+    if (c.pen_on) {   // H0 and the stream's ids are disjoint: each id once
+      penalise_wave(xrow, bmH0, V, c.pen);
+      penalise_wave(xrow, bmN, V, c.pen);
+    }
+    __syncthreads();
+    LdsRowNC src{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
+    __syncthreads();
+    if (lane == 0) {
+      acc[0] |= xs.step_stats[0];
+      acc[1] += 1u;
+      acc[2] += xs.step_stats[2];
+      acc[3] += xs.step_stats[3];
+    }
+    return tok;
+  };
+  // One step; false when it has to be run exactly elsewhere (nothing changed then).
   auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) -> bool {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     C4S_LIST_PHASE(0);
@@ -1221,14 +1262,16 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, bmN, rng, cs, o);
     if (!ok) {
       if (lane == 0) acc[0] |= 1u << (20 + o.why);
-      return false;
+      if (!w.sortbuf) return false;
     }
-    const int tok = o.tok;
+    const int tok = ok ? o.tok : exact(s);
     if (lane == 0) {
       *outp = tok;
-      acc[0] |= 32u | 1u;
-      acc[2] += o.dex;
-      acc[3] += o.kept;
+      if (ok) {
+        acc[0] |= 32u | 1u;
+        acc[2] += o.dex;
+        acc[3] += o.kept;
+      }
       // text2semantic.cpp:333-334: the stop token is not appended
       if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
         bmN[tok >> 5] |= 1u << (tok & 31);
@@ -2295,10 +2338,13 @@ hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_
   return hipGetLastError();
 }
 
+size_t stream_list_lds_bytes(int V) { return 4 * ((size_t)vpad(V) + 4); }
+
 hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_list, dim3(a.n_rows), dim3(kWave), 0, s, a, w);
+  hipLaunchKernelGGL(k_stream_list, dim3(a.n_rows), dim3(kWave), w.sortbuf ? stream_list_lds_bytes(a.vocab) : 0, s,
+                     a, w);
   return hipGetLastError();
 }
 
