@@ -29,6 +29,13 @@
 namespace c4s {
 namespace {
 
+// LDS writes of this wave visible to its own later reads (all lanes).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 constexpr int NTA = 256;
 constexpr int NWA = NTA / kWave;
 constexpr float kLog2e = 1.44269504088896340736f;
@@ -194,17 +201,35 @@ __device__ bool hist_pick(ScanSh& sh, uint32_t m, uint32_t& bin, uint32_t& above
 }
 
 // Descending block bitonic sort of P (power of two) 64-bit entries in LDS.
+// Descending bitonic sort of v[0, P), P a power of two >= 2 NWA. A stage
+// whose pairs lie within 2 j <= P / NWA consecutive elements is run by each
+// wave on its own quarter of v, wave-synchronous; only the longer stages
+// need the workgroup barrier.
 __device__ void bitonic_desc_u64(uint64_t* v, int P) {
+  const int per_wave = P / NWA;
+  const int wpairs = per_wave >> 1;
+  const int lane = lane_id(), wv = wave_id();
+  auto cmpswap = [&](int i, int j, int k) __attribute__((always_inline)) {
+    const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+    const int hi = lo + j;
+    const uint64_t x = v[lo], y = v[hi];
+    if ((x < y) == ((lo & k) == 0)) { v[lo] = y; v[hi] = x; }
+  };
+  bool wave_stage = false;   // the last stage ran wave-locally
   for (int k = 2; k <= P; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < (P >> 1); i += NTA) {
-        const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
-        const int hi = lo + j;
-        const uint64_t x = v[lo], y = v[hi];
-        if ((x < y) == ((lo & k) == 0)) { v[lo] = y; v[hi] = x; }
+      if (2 * j <= per_wave) {
+        for (int i = lane; i < wpairs; i += kWave) cmpswap(wv * wpairs + i, j, k);
+        wave_sync();
+        wave_stage = true;
+      } else {
+        if (wave_stage) __syncthreads();
+        for (int i = threadIdx.x; i < (P >> 1); i += NTA) cmpswap(i, j, k);
+        __syncthreads();
+        wave_stage = false;
       }
-      __syncthreads();
     }
+  if (wave_stage) __syncthreads();
 }
 
 
@@ -579,11 +604,6 @@ struct ChainSh {
 // then the bitmap of ids drawn during the stream.
 enum : int { kStDone = 0, kStStats = 1, kStNext = 5, kStPending = 6, kStBits = 8 };
 
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Slot s (an id-order rank among the list entries) lives at position
 // slot_pos(s): lane l's eight slots [8 l, 8 l + 8) are the l-th word of eight
