@@ -236,7 +236,7 @@ __device__ void bitonic_desc_u64(uint64_t* v, int P) {
 // One workgroup scans steps [s0, s1) of one row. Thread t holds the float4
 // quads t + 256 j of the 16-byte aligned body and one head or tail id.
 template <int NQ>
-__global__ __launch_bounds__(NTA, 2) void k_stream_scan(StreamArgs a, StreamWs w) {
+__global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w) {
   __shared__ ScanSh sh;
   const int row = blockIdx.y;
   const int V = a.vocab;
