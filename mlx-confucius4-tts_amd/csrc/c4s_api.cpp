@@ -40,6 +40,7 @@ struct c4s_ctx {
   hipStream_t scan_s = nullptr;
   hipEvent_t ev_start = nullptr;
   hipEvent_t ev_scan[2] = {nullptr, nullptr}, ev_chain[2] = {nullptr, nullptr};
+  hipEvent_t ev_side[2] = {nullptr, nullptr};   // full-vocabulary chain of a chunk done, by buffer
   // Overlapped stream: the scan and the chains on disjoint sets of CUs (half
   // of every 32 CUs for the chains), created at first use.
   int n_cus = 0;
@@ -221,7 +222,9 @@ int c4s_create(int device, c4s_ctx** out) {
       hipEventCreateWithFlags(&ctx->ev_scan[0], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_scan[1], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_chain[0], hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->ev_chain[1], hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ctx->ev_chain[1], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_side[0], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_side[1], hipEventDisableTiming) != hipSuccess) {
     c4s_destroy(ctx);
     return C4S_EHIP;
   }
@@ -245,7 +248,7 @@ int c4s_destroy(c4s_ctx* ctx) {
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamDestroy(st);
   for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1],
-                        ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_done})
+                        ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_done, ctx->ev_side[0], ctx->ev_side[1]})
     if (ev) (void)hipEventDestroy(ev);
   delete ctx;
   return C4S_OK;
@@ -381,6 +384,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   if (e0 == hipSuccess) e0 = hipStreamWaitEvent(ctx->scan_s, ctx->ev_start, 0);
   if (e0 == hipSuccess && overlap) e0 = hipStreamWaitEvent(chain_on, ctx->ev_start, 0);
   if (e0 != hipSuccess) return hip_fail(ctx, e0, "sample_stream scan stream");
+  int last_side = -1;   // buffer of the last chunk whose full-vocabulary chain ran on the side stream
   for (int s0 = 0, ci = 0, len = overlap ? kOverlapFirst : chunk; s0 < a.n_steps;
        s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 2 : chunk)) {
     const int buf = ci & 1;
@@ -395,22 +399,36 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     w.sort_stride = (int64_t)(sort_row / sizeof(uint32_t));
     w.nseg = nseg;
     w.segres = static_cast<uint64_t*>(ctx->segres);
+    w.exact_only = pipelined ? 1 : 0;
     hipError_t e = hipSuccess;
     if (overlap && ci == 1 && (e = hipStreamWaitEvent(scan_on, ctx->ev_scan[0], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
-    if (ci >= 2 && (e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess)
+    if (ci >= 2 && ((e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess ||
+                    (pipelined && (e = hipStreamWaitEvent(scan_on, ctx->ev_side[buf], 0)) != hipSuccess)))
       return hip_fail(ctx, e, "sample_stream buffer reuse");
     e = c4s::launch_stream_scan(a, w, scan_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream scan launch");
     if ((e = hipEventRecord(ctx->ev_scan[buf], scan_on)) != hipSuccess ||
         (e = hipStreamWaitEvent(chain_on, ctx->ev_scan[buf], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
+    if (pipelined) {
+      // Both fast chains run their exact steps themselves and leave nothing
+      // pending: the full-vocabulary chain on the side stream, the list chain
+      // and then the finisher (exact-mode rows only) here, each after the scan.
+      if ((e = hipStreamWaitEvent(side_on, ctx->ev_scan[buf], 0)) != hipSuccess ||
+          (e = launch_row_chain(w, side_on)) != hipSuccess ||
+          (e = hipEventRecord(ctx->ev_side[buf], side_on)) != hipSuccess)
+        return hip_fail(ctx, e, "sample_stream row-chain launch");
+      if ((e = c4s::launch_stream_list(a, w, chain_on)) != hipSuccess ||
+          (e = c4s::launch_stream_chain(a, w, chain_on)) != hipSuccess ||
+          (e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
+        return hip_fail(ctx, e, "sample_stream chain launch");
+      last_side = buf;
+      continue;
+    }
     // Fast passes stop a row at a step they cannot decide; the repair kernel
-    // runs that step exactly; the finisher completes whatever is left. With
-    // the sort buffer (pipelined) both fast chains run their exact steps
-    // themselves: one round, no repair.
-    const int rounds = pipelined ? 1 : kFastRounds;
-    for (int r = 0; r < rounds; ++r) {
+    // runs that step exactly; the finisher completes whatever is left.
+    for (int r = 0; r < kFastRounds; ++r) {
       w.round = r;
       if (r == 0) {   // list rows here, full-vocabulary rows on the side stream, side by side
         if ((e = hipEventRecord(ctx->ev_fork, chain_on)) != hipSuccess ||
@@ -428,13 +446,17 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
         if (e == hipSuccess) e = launch_row_chain(w, chain_on);
         if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
       }
-      if (!pipelined && (e = c4s::launch_stream_repair(a, w, chain_on)) != hipSuccess)
+      if ((e = c4s::launch_stream_repair(a, w, chain_on)) != hipSuccess)
         return hip_fail(ctx, e, "sample_stream repair launch");
     }
     e = c4s::launch_stream_chain(a, w, chain_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
     if ((e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream chain order");
+  }
+  if (last_side >= 0) {   // the last full-vocabulary chain ahead of what follows on chain_on
+    hipError_t e = hipStreamWaitEvent(chain_on, ctx->ev_side[last_side], 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream join");
   }
   if (overlap) {   // the caller's stream continues after the last chain
     hipError_t e = hipEventRecord(ctx->ev_done, chain_on);

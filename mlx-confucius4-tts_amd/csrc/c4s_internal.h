@@ -99,6 +99,7 @@ struct StreamWs {
   int round;               // chain rounds within the chunk (0: the first)
   uint32_t* sortbuf;       // exact steps of the pipelined row chain: per-row key buffer
   int64_t sort_stride;     // words per row
+  int exact_only;          // finisher: exact-mode rows only (the fast chains leave nothing pending)
   int nseg;                // pipelined row chain: step segments of a row without penalty
   uint64_t* segres;        // [n_rows][nseg][4] segment results (status and stop step, RNG, statistics)
 };

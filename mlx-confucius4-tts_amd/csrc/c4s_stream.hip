@@ -1156,10 +1156,14 @@ __device__ __forceinline__ bool fast_begin(const StreamArgs& a, const StreamWs& 
                                            int& s_first) {
   uint32_t* stw = w.state + (size_t)row * kStateWords;
   s_first = (int)stw[kStNext];
-  if (stw[kStPending] != 0u || s_first >= w.s_end) return false;
-  if (stw[kStDone] != 0u) {
-    for (int s = s_first + (int)threadIdx.x; s < w.s_end; s += nthr) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
-    if (threadIdx.x == 0) stw[kStNext] = (uint32_t)w.s_end;
+  if (stw[kStPending] != 0u) return false;
+  if (stw[kStDone] != 0u || s_first >= w.s_end) {
+    if (stw[kStDone] != 0u) {
+      for (int s = s_first + (int)threadIdx.x; s < w.s_end; s += nthr) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
+      if (threadIdx.x == 0) stw[kStNext] = (uint32_t)w.s_end;
+    }
+    if (threadIdx.x == 0 && a.stats && w.s_end == a.n_steps)   // nothing left: the final statistics
+      for (int i = 0; i < 4; ++i) a.stats[4 * (int64_t)row + i] = stw[kStStats + i];
     return false;
   }
   return true;
@@ -1192,6 +1196,10 @@ __device__ __forceinline__ void fast_end(const StreamArgs& a, const StreamWs& w,
     stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
     stw[kStNext] = (uint32_t)s;
     stw[kStPending] = pending ? 1u : 0u;
+    if (a.stats && !pending && s >= a.n_steps) {   // the row's last step: its statistics
+      uint32_t* o = a.stats + 4 * (int64_t)row;
+      o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
+    }
   }
   const int nwords = bitmap_words(V);
   for (int i = threadIdx.x; i < nwords; i += nthr) stw[kStBits + i] = bmN[i];
@@ -2069,6 +2077,10 @@ __global__ __launch_bounds__(kWave) void k_stream_segfix(StreamArgs a, StreamWs 
     stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
     stw[kStNext] = (uint32_t)w.s_end;
     stw[kStPending] = 0u;
+    if (a.stats && w.s_end == a.n_steps) {
+      uint32_t* o = a.stats + 4 * (int64_t)row;
+      o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
+    }
   }
 }
 
@@ -2129,6 +2141,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
   const int mode = stream_mode(c, V);
+  if (w.exact_only && mode != kModeExact) return;   // the fast chains finish these rows
   LdsLayout L = lds_layout(smem, V);
   const int nwords = bitmap_words(V);
   uint32_t* bmH0 = L.bitmap + nwords;
