@@ -7,10 +7,11 @@ own temperature / top_k / top_p / repetition penalty; the full processor chain
 and the xorshift64 draw for every row-step. Inputs (2.1 GB of logits) are
 resident in HBM before timing starts. One call of the stream entry point
 processes the whole job: the scan kernel reads every (step, row) once and
-writes candidate summaries, then the per-row chain kernels walk the steps on
-them (exact repair steps where a decision needs the full row). `value` is
-sampled rows per second over that call; --sequential times the single-kernel
-stream instead.
+writes candidate summaries, the per-row chain kernels walk the steps on them
+(exact steps where a decision needs the full row), and chunks of steps are
+scanned beside the chains of the previous chunk. The calls are issued back to
+back on a stream of the bench's own. `value` is sampled rows per second over
+that call; --sequential times the single-kernel stream instead.
 
 Also reported: the same chain as one launch per AR step (per_call), an HBM
 copy probe, bit-exact parity of the first AR steps against the CPU oracle, and
@@ -105,10 +106,15 @@ def main():
     stats = torch.zeros((R, 4), dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
 
+    # The calls go on a stream of their own, as an AR loop would issue them: on
+    # the legacy default stream the scan's CU-masked (blocking) stream would
+    # add implicit synchronisation to every call.
+    work = torch.cuda.Stream()
+
     def launch(stats_ptr=None):
         ctx.sample_stream(logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out,
                           do_sample=do_sample, stop_token=-1, out_stats=stats_ptr,
-                          sequential=args.sequential)
+                          sequential=args.sequential, stream=work)
 
     # ---- warmup (the first launch starts from the seeded RNG: kept for parity) ------
     log(f"warmup x{args.warmup}")
@@ -125,10 +131,10 @@ def main():
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    ev0.record()
+    ev0.record(work)
     for _ in range(args.steps):
         launch()
-    ev1.record()
+    ev1.record(work)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     ms = ev0.elapsed_time(ev1) / args.steps
@@ -223,8 +229,8 @@ def main():
                                "one stream call per bench step",
                    "rows": R, "vocab": V, "ar_steps": T,
                    "launch": ("k_stream_lds" if args.sequential else
-                              "k_stream_scan, then k_stream_list | k_stream_rowp side by side, "
-                              "then k_stream_repair / k_stream_chain for what is left")},
+                              "chunks of 64-256 steps: k_stream_scan of the next chunk on half the CUs beside "
+                              "k_stream_list + k_stream_chain | k_stream_rowp + k_stream_segfix on the other half")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic,
