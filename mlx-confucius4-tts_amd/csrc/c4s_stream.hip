@@ -37,6 +37,7 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 constexpr int NTA = 256;
+constexpr int kLanesHint = 48;   // nucleus cuts within this many entries take the chain's register path
 constexpr int NWA = NTA / kWave;
 constexpr float kLog2e = 1.44269504088896340736f;
 
@@ -72,7 +73,9 @@ struct SumHdr {
   int head;         // ids before the first 16-byte boundary of the row
   double err;       // absolute error bound of the chunk masses, summed over the row
   double s0;        // sum of the chunk masses
-  int pad[6];
+  int qhint;        // nucleus rows: kLanesHint (or 256) when the cut without hits and corrections
+                    // lies within that many first entries, else kListLarge (a hint)
+  int pad[5];
 };
 static_assert(sizeof(SumHdr) == kSumHdrBytes, "summary header size");
 
@@ -154,6 +157,7 @@ struct ScanSh {
   double chunk[kMaxChunks];
   double edge[8];
   uint32_t bu[4];
+  double redh[NWA];                // per wave: mass of its list positions below NTA
   uint32_t lmark[kCandCap / 32];   // candidate positions of the list entries
   uint32_t lpre[kCandCap / 32];    // marks before each word
 };
@@ -459,6 +463,8 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
     const bool bad = overflow || n == 0;
 
     uint64_t* sw = reinterpret_cast<uint64_t*>(w.sum + ((size_t)(s - w.s_begin) * a.n_rows + row) * kSumStride);
+    double top_mass = 0.0;   // wave 0: mass of the list's first kLanesHint entries
+    double first_mass = 0.0; // the thread's list position below NTA
     uint64_t* lst = sw;
     SumHdr* hdr = reinterpret_cast<SumHdr*>(sw + kHdrW);
     double* chk = reinterpret_cast<double*>(sw + kChunkW);
@@ -489,14 +495,26 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
         const int ci = ent_rank(e);
         const uint32_t lr = sh.lpre[ci >> 5] + (uint32_t)__popc(sh.lmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
         lst[i] = (e & ~1023ull) | lr;
-        ly[i] = masses ? (float)exp((double)(kfloat(ent_key(e)) - zmax)) : sh.candy[ci];
+        if (masses) {
+          const float m = (float)exp((double)(kfloat(ent_key(e)) - zmax));
+          ly[i] = m;
+          if (i < kLanesHint) top_mass += (double)m;   // wave 0, first pass
+          if (i < NTA) first_mass = (double)m;
+        } else {
+          ly[i] = sh.candy[ci];
+        }
+      }
+      if (masses) {
+        if (wv == 0) top_mass = wave_sum_f64(top_mass);
+        const double fm = wave_sum_f64(first_mass);
+        if (lane == 0) sh.redh[wv] = fm;   // read after the barriers of the chunk masses
       }
     }
 
     C4S_SCAN_PHASE(6);
     // Chunk masses of the whole row (rows without top-k).
     float m0 = 0.f;
-    int nchunk = 0;
+    int nchunk = 0, qhint = kListLarge;   // qhint: read by thread 0 (wave 0 holds top_mass)
     double err = 0.0, s0 = 0.0;
     if (masses && !bad) {
       m0 = kfloat(ent_key(srt[0]));
@@ -562,6 +580,16 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       double cl = 0.0;
       for (int i = t; i < nchunk; i += NTA) { chk[i] = sh.chunk[i]; cl += sh.chunk[i]; }
       s0 = block_sum_f64<NTA>(cl, sh.redd);
+      // Cut hint for the chains (nucleus rows): the list's first kLanesHint
+      // (or NTA) entries hold p * s0 of the mass, so the cut lies among them
+      // unless hits or corrections move it.
+      if (1.0 - (double)c.p > 0.0) {
+        double top_nta = 0.0;
+#pragma unroll
+        for (int ww = 0; ww < NWA; ++ww) top_nta += sh.redh[ww];
+        const double pS0 = (double)c.p * s0;
+        qhint = top_mass >= pS0 ? kLanesHint : (top_nta >= pS0 ? NTA : kListLarge);
+      }
     }
     C4S_SCAN_PHASE(7);
     if (t == 0) {
@@ -574,6 +602,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       h.head = rs.head;
       h.err = err + 0x1p-100;
       h.s0 = s0;
+      h.qhint = qhint;
       *hdr = h;
     }
     __syncthreads();
@@ -757,6 +786,420 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   o.tok = lane_draw<kSlotBits>(kept, ids, slot, e, unit_from_state(st), V, o.dex);
   C4S_LIST_PHASE(6);
   o.kept = (uint32_t)__popcll(__ballot(kept));
+  rng = st;
+  return true;
+}
+
+// Dense draw (top_p keeps every id of nonzero mass; zero masses never win),
+// text2semantic.cpp:150-165: r = u * S, the chunk prefixes (summary chunk
+// masses less the corrections, times rho) locate r, the chunk's masses are
+// recomputed exactly from the staged row. False when r is not inside its
+// chunk by the error margin.
+__device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int V, const float* val,
+                                           const uint32_t* bmN, const uint32_t* bmH0, const uint64_t* sum,
+                                           const double* cdelta, double u, double S, double rho, double err,
+                                           float mt, StepOut& o) {
+  const int lane = lane_id();
+  const float ninf = neg_inf();
+  const double eps = rel_eps(V);
+  o.why = kWhyDraw;
+  const int nchunk = h.nchunk;
+  double cv[4];
+  double cs_l = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 4 * lane + i;
+    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)sum[kChunkW + ci]) - cdelta[ci] : 0.0;
+    cs_l += cv[i];
+  }
+  const double r = u * S;
+  const double inc = wave_scan_f64(cs_l);
+  double run = (inc - cs_l) * rho;
+  int cstar = -1;
+  double pstar = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 4 * lane + i;
+    const double nx = run + cv[i] * rho;
+    if (cstar < 0 && ci < nchunk && nx >= r) { cstar = ci; pstar = run; }
+    run = nx;
+  }
+  const uint64_t hmk = __ballot(cstar >= 0);
+  if (!hmk || !(r > 0.0)) return false;
+  const int fl = __ffsll((unsigned long long)hmk) - 1;
+  cstar = (int)readlane_u32((uint32_t)cstar, fl);
+  pstar = readlane_f64(pstar, fl);
+  const int lo = cstar == 0 ? 0 : h.head + kChunkIds * cstar;
+  const int hi = (cstar == nchunk - 1) ? V : h.head + kChunkIds * (cstar + 1);
+  double ea = 0.0, eb = 0.0;
+  const int ia = lo + lane, ib = lo + kWave + lane;
+  auto mass_at = [&](int id) -> double {
+    const float x = val[id];
+    const float y = (c.pen_on && (bit_of(bmH0, id) || bit_of(bmN, id))) ? pen_exact(x, c.pen) : x;
+    const float z = c.temp_on ? y / c.temp : y;
+    return (z == ninf) ? 0.0 : exp((double)(z - mt));
+  };
+  if (ia < hi) ea = mass_at(ia);
+  if (ib < hi) eb = mass_at(ib);
+  const double sa = wave_scan_f64(ea) + pstar;
+  const double ta = readlane_f64(sa, kWave - 1);
+  const double sb = wave_scan_f64(eb) + ta;
+  const double mg = 2.0 * err;
+  const uint64_t fa = __ballot(ia < hi && ea > 0.0 && sa >= r);
+  const uint64_t fb = __ballot(ib < hi && eb > 0.0 && sb >= r);
+  double af, pf;
+  int tok;
+  if (fa) {
+    const int f = __ffsll((unsigned long long)fa) - 1;
+    af = readlane_f64(sa, f);
+    pf = af - readlane_f64(ea, f);
+    tok = lo + f;
+  } else if (fb) {
+    const int f = __ffsll((unsigned long long)fb) - 1;
+    af = readlane_f64(sb, f);
+    pf = af - readlane_f64(eb, f);
+    tok = lo + kWave + f;
+  } else {
+    return false;
+  }
+  if (!((af - r > mg + eps * af) && (r - pf > mg + eps * r))) return false;
+  o.tok = tok;
+  o.kept = (uint32_t)V;
+  o.dex = 0;
+  return true;
+}
+
+// row_step in registers for a step decided within the first 64 list entries
+// (one per lane): a nucleus of at most 64 unhit ranks, or the dense draw. The
+// unhit entries move to lanes 0..nu-1 in rank order by one lane permute; the
+// cut is one prefix scan, the draw the lane draw. Same decisions and margins
+// as row_step; false, with rng and o unchanged, when the step needs row_step.
+__device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c, int V, const float* val,
+                                               const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
+                                               const uint64_t* sum, const double* cdelta, uint64_t& rng,
+                                               StepOut& o) {
+  const int lane = lane_id();
+  if (h.flags & 1u) return false;
+  const int n = h.n;
+  const float ninf = neg_inf();
+  const bool v = lane < n;
+  const uint64_t e = v ? sum[lane] : 0ull;
+  const float m32 = v ? reinterpret_cast<const float*>(sum + kYW)[lane] : 0.0f;
+  const int id = v ? ent_id(e) : 0;
+  const bool hit = c.pen_on && v && bit_of(bmN, id);
+  // a drawn id is never in H0: its value is the raw one (the penalty and the
+  // temperature are monotone, so the largest penalised hit comes from the largest raw one)
+  const float hraw = (c.pen_on && hit) ? val[id] : ninf;
+  const bool un = v && !hit;
+  const uint64_t ub = __ballot(un);
+  const int nu = __popcll(ub);
+  if (nu == 0) return false;
+  // lane permutation: unhit entries to their ranks, the others after them
+  const int dst = (un ? __popcll(ub & lanemask_lt()) : nu + __popcll(~ub & lanemask_lt())) << 2;
+  const uint32_t pk = (uint32_t)__builtin_amdgcn_ds_permute(dst, (int)ent_key(e));
+  const float pm = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(m32)));
+  const int pid = __builtin_amdgcn_ds_permute(dst, id);
+  const int pslot = __builtin_amdgcn_ds_permute(dst, ent_rank(e));
+  const bool in = lane < nu;
+  const float z = in ? kfloat(pk) : ninf;
+  const float mt = readlane_f32(z, 0);
+  const float zo = (h.tout != 0u) ? kfloat(h.tout) : ninf;
+  if (!(mt > ninf) || !(zo < mt)) return false;
+  // entries past the first 64 are at or below entry 63
+  const float zend = (n > kWave) ? kfloat(readlane_u32(ent_key(e), kWave - 1)) : ninf;
+  if (!(zend < mt)) return false;
+  const float hx = wave_max_dpp(hraw);
+  const float hy = pen_exact(hx, c.pen);   // sampling.cpp:26, then :16
+  const float hm = c.temp_on ? hy / c.temp : hy;
+  if (!(hm < mt)) return false;
+
+  const double eps = rel_eps(V);
+  const double dm = (double)h.m0 - (double)mt;
+  const double rho = (dm == 0.0) ? 1.0 : exp(dm);
+  const double S = (h.s0 - dsum) * rho;
+  const double err = (h.err + derr + fabs(dsum) * 0x1p-50) * rho +
+                     (dm > 0.0 ? 0x1p-23 * ((40.0 + dm) * S + (double)V * 0x1p-50) : 0.0) + eps * S;
+  const double thr = 1.0 - (double)c.p;
+  const uint64_t st = xorshift64(rng);
+  const double u = unit_from_state(st);
+  if (!(thr > 0.0)) {
+    if (!dense_draw(h, c, V, val, bmN, bmH0, sum, cdelta, u, S, rho, err, mt, o)) return false;
+    rng = st;
+    return true;
+  }
+  // nucleus cut on the unhit ranks: removed iff above >= p * S (as row_step)
+  const double pS = (double)c.p * S;
+  const double marg = (double)c.p * err + eps * S;
+  const bool approx = dm == 0.0;
+  const double dmass = approx ? 0x1p-23 : 0.0;
+  const bool stored = approx && pm >= 0x1p-100f;
+  double em = (in && stored) ? (double)pm : 0.0;
+  if (__ballot(in && !stored)) em = (in && !stored) ? exp((double)(z - mt)) : em;
+  const double inc = wave_scan_f64(em);
+  const double above = inc - em;
+  const double D = above - pS;
+  if (__ballot(in && lane >= c.min_keep && !(fabs(D) > marg + (eps + dmass) * above))) return false;
+  if (__ballot(in && D < 0.0 && em < 0x1p-1000)) return false;   // subnormal kept masses
+  const uint64_t qm = __ballot(in && D >= 0.0);
+  if (!qm) return false;   // the cut lies past these ranks
+  const int q = max(__ffsll((unsigned long long)qm) - 1, c.min_keep);
+  if (q > nu) return false;
+  const float zq1 = readlane_f32(z, q - 1);
+  if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
+  // the draw on the kept ranks [0, q): first with the masses above, then exact
+  const bool kept = lane < q;
+  uint32_t dex = 0;
+  int tok = -1;
+  if (approx) tok = lane_draw<kSlotBits>(kept, pid, pslot, kept ? em : 0.0, u, V, dex, 0x1p-22, false);
+  if (tok < 0) {
+    const double ex = kept ? exp((double)(z - mt)) : 0.0;
+    tok = lane_draw<kSlotBits>(kept, pid, pslot, ex, u, V, dex);
+  }
+  o.tok = tok;
+  o.kept = (uint32_t)q;
+  o.dex = dex;
+  rng = st;
+  return true;
+}
+
+// Draw over the kept unhit ranks [0, q) in id order (text2semantic.cpp:150-165):
+// cs.inv maps the id-order slots to the ranks tagged with generation gen,
+// cs.lz/lm/lid hold the ranks' values, stored fp32 masses and ids. Sets o.dex.
+template <class CS>
+__device__ __forceinline__ int inv_draw(CS& cs, uint32_t gen, int q, bool approx, float mt, double u, int V,
+                                        StepOut& o) {
+  const int lane = lane_id();
+  // Kept ranks [0, q) in id order: lane l reads the id-order slots
+  // [8 l, 8 l + 8); a slot tagged with this call's generation names its
+  // unhit rank, every other slot (no candidate, a hit, a rank past the cut)
+  // weighs 0. First with the masses above, then with exact masses.
+  constexpr int kPer = kSlotsPerLane;
+  int rks[kPer];
+  uint32_t vb = 0u;   // bit i: slot 8 lane + i is kept
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t x = cs.inv[(i << 6) | lane];
+    rks[i] = (int)(x & 1023u);
+    vb |= (((x >> 10) == gen && rks[i] < q) ? 1u : 0u) << i;
+  }
+  float mf[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) mf[i] = cs.lm[rks[i]];   // tagged ranks are below kListLarge
+  C4S_PHASE(13);
+  auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
+    // in-lane inclusive prefix p[i], then one scan over the lanes
+    double e[kPer], p[kPer];
+    bool need = false;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const bool v = (vb >> i) & 1u;
+      const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
+      e[i] = (v && st) ? (double)mf[i] : 0.0;
+      need |= v && !st;
+    }
+    if (__ballot(need)) {   // exp for every slot (no per-slot branches), kept where needed
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const double x = exp((double)(cs.lz[rks[i]] - mt));
+        const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
+        e[i] = (((vb >> i) & 1u) && !st) ? x : e[i];
+      }
+    }
+    p[0] = e[0];
+#pragma unroll
+    for (int i = 1; i < kPer; ++i) p[i] = p[i - 1] + e[i];
+    const double inc = wave_scan_f64(p[kPer - 1]);
+    const double r = u * readlane_f64(inc, kWave - 1);
+    const double base = inc - p[kPer - 1];
+    double ha = 0.0, hp = 0.0;
+    int hrk = -1;
+#pragma unroll
+    for (int i = kPer - 1; i >= 0; --i) {   // the first slot reaching r wins
+      const double nx = base + p[i];
+      if (e[i] > 0.0 && nx >= r) { hrk = rks[i]; ha = nx; hp = i ? base + p[i - 1] : base; }
+    }
+    const uint64_t hb = __ballot(hrk >= 0);
+    if (!hb) return -1;
+    const int f = __ffsll((unsigned long long)hb) - 1;
+    const double af = readlane_f64(ha, f), pf = readlane_f64(hp, f);
+    const double eps = rel_eps(V) + eps_add;
+    if (!(r > 0.0 && (af - r > eps * af) && (r - pf > eps * r))) return -1;
+    return cs.lid[readlane_u32((uint32_t)hrk, f)];
+  };
+  int tok = -1;
+  o.dex = 0;
+  if (approx) tok = draw(false, 0x1p-22);
+  C4S_PHASE(14);
+  if (tok < 0) tok = draw(true, 0.0);
+  if (tok < 0) {
+    // text2semantic.cpp:152-164 sequentially in id order with exact masses
+    o.dex = 1;
+    int res = 0;
+    if (lane == 0) {
+      auto kept_mass = [&](int sl, int& rk) -> double {
+        const uint32_t x = cs.inv[slot_pos(sl)];
+        rk = (int)(x & 1023u);
+        return ((x >> 10) == gen && rk < q) ? exp((double)(cs.lz[rk] - mt)) : 0.0;
+      };
+      double total = 0.0;
+      for (int sl = 0; sl < kListLarge; ++sl) {
+        int rk;
+        total += kept_mass(sl, rk);
+      }
+      const double rr = u * total;
+      res = V - 1;
+      if (rr <= 0.0) {
+        res = 0;
+      } else {
+        double acc = 0.0;
+        for (int sl = 0; sl < kListLarge; ++sl) {
+          int rk;
+          const double ei = kept_mass(sl, rk);
+          acc += ei;
+          if (ei > 0.0 && rr <= acc) { res = cs.lid[rk]; break; }
+        }
+      }
+    }
+    tok = (int)readlane_u32((uint32_t)res, 0);
+  }
+  return tok;
+}
+
+// row_step in registers for a nucleus within the first 256 list entries, four
+// consecutive ones per lane: unhit ranks from one scan of the lane counts, the
+// cut from one prefix scan of the lane masses, no list compaction; the kept
+// ranks then go to LDS for the id-order draw (inv_draw). Same decisions and
+// margins as row_step; false, with rng and o unchanged, when the step needs
+// row_step (its generation counter may have moved, which is harmless).
+template <class CS>
+__device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c, int V, const float* val,
+                                                const uint32_t* bmN, double dsum, double derr, const uint64_t* sum,
+                                                uint64_t& rng, CS& cs, StepOut& o) {
+  constexpr int K = 4;
+  const int lane = lane_id();
+  if (h.flags & 1u) return false;
+  const int n = h.n;
+  const float ninf = neg_inf();
+  const int p0 = K * lane;
+  const float* ly = reinterpret_cast<const float*>(sum + kYW);
+  uint64_t e[K];
+  float mk[K], z[K];
+  bool un[K];
+  uint32_t cnt = 0;
+  float hraw = ninf;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const bool v = p0 + i < n;
+    e[i] = v ? sum[p0 + i] : 0ull;
+    mk[i] = v ? ly[p0 + i] : 0.0f;
+    const int id = v ? ent_id(e[i]) : 0;
+    const bool hit = c.pen_on & v & bit_of(bmN, id);
+    // a drawn id is never in H0: its value is the raw one
+    if (c.pen_on) hraw = hit ? fmaxf(hraw, val[id]) : hraw;
+    un[i] = v & !hit;
+    z[i] = un[i] ? kfloat(ent_key(e[i])) : ninf;
+    cnt += un[i] ? 1u : 0u;
+  }
+  const uint32_t cinc = wave_scan_u32(cnt);
+  const int nu = (int)readlane_u32(cinc, kWave - 1);
+  if (nu == 0) return false;
+  int rk[K];
+  {
+    int r = (int)(cinc - cnt);
+#pragma unroll
+    for (int i = 0; i < K; ++i) { rk[i] = r; r += un[i] ? 1 : 0; }
+  }
+  // the largest unhit value is rank 0: the first lane with an unhit entry
+  float zf = ninf;
+#pragma unroll
+  for (int i = K - 1; i >= 0; --i) zf = un[i] ? z[i] : zf;
+  const float mt = readlane_f32(zf, __ffsll((unsigned long long)__ballot(cnt != 0u)) - 1);
+  const float zo = (h.tout != 0u) ? kfloat(h.tout) : ninf;
+  if (!(mt > ninf) || !(zo < mt)) return false;
+  const float zend = (n > K * kWave) ? kfloat(readlane_u32(ent_key(e[K - 1]), kWave - 1)) : ninf;
+  if (!(zend < mt)) return false;
+  const float hy = pen_exact(wave_max_dpp(hraw), c.pen);   // sampling.cpp:26, then :16
+  const float hm = c.temp_on ? hy / c.temp : hy;
+  if (!(hm < mt)) return false;
+
+  const double eps = rel_eps(V);
+  const double dm = (double)h.m0 - (double)mt;
+  const double rho = (dm == 0.0) ? 1.0 : exp(dm);
+  const double S = (h.s0 - dsum) * rho;
+  const double err = (h.err + derr + fabs(dsum) * 0x1p-50) * rho +
+                     (dm > 0.0 ? 0x1p-23 * ((40.0 + dm) * S + (double)V * 0x1p-50) : 0.0) + eps * S;
+  if (!(1.0 - (double)c.p > 0.0)) return false;   // dense rows take the other paths
+  const uint64_t st = xorshift64(rng);
+  const double u = unit_from_state(st);
+  const double pS = (double)c.p * S;
+  const double marg = (double)c.p * err + eps * S;
+  const bool approx = dm == 0.0;
+  const double dmass = approx ? 0x1p-23 : 0.0;
+  double em[K];
+  bool need = false;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const bool stored = approx && mk[i] >= 0x1p-100f;
+    em[i] = (un[i] && stored) ? (double)mk[i] : 0.0;
+    need |= un[i] && !stored;
+  }
+  if (__ballot(need)) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const double x = exp((double)(z[i] - mt));
+      const bool stored = approx && mk[i] >= 0x1p-100f;
+      em[i] = (un[i] && !stored) ? x : em[i];
+    }
+  }
+  double ls = 0.0;
+#pragma unroll
+  for (int i = 0; i < K; ++i) ls += em[i];
+  const double inc = wave_scan_f64(ls);
+  double ab = inc - ls;
+  bool unsure = false, tiny = false;
+  int qloc = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const double D = ab - pS;
+    unsure |= un[i] && rk[i] >= c.min_keep && !(fabs(D) > marg + (eps + dmass) * ab);
+    tiny |= un[i] && D < 0.0 && em[i] < 0x1p-1000;
+    if (un[i] && D >= 0.0) qloc = min(qloc, rk[i]);
+    ab += em[i];
+  }
+  if (__ballot(unsure) || __ballot(tiny)) return false;
+  const uint64_t qb = __ballot(qloc != 0x7fffffff);
+  if (!qb) return false;   // the cut lies past these ranks
+  const int q = max((int)readlane_u32((uint32_t)qloc, __ffsll((unsigned long long)qb) - 1), c.min_keep);
+  if (q > nu) return false;
+  float zs = ninf;
+  bool has = false;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const bool m = un[i] && rk[i] == q - 1;
+    zs = m ? z[i] : zs;
+    has |= m;
+  }
+  const float zq1 = readlane_f32(zs, __ffsll((unsigned long long)__ballot(has)) - 1);
+  if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
+  // kept ranks to LDS, tagged with this call's generation, then the id-order draw
+  uint32_t gen = cs.gen + 1u;
+  if (gen == 1u || gen >= (1u << 22)) {
+#pragma unroll
+    for (int i = 0; i < kSlotsPerLane; ++i) cs.inv[(i << 6) | lane] = 0u;
+    gen = 1u;
+  }
+  if (lane == 0) cs.gen = gen;
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    if (un[i] && rk[i] < q) {
+      cs.lz[rk[i]] = z[i];
+      cs.lm[rk[i]] = mk[i];
+      cs.lid[rk[i]] = ent_id(e[i]);
+      cs.inv[slot_pos(ent_rank(e[i]))] = (gen << 10) | (uint32_t)rk[i];
+    }
+  wave_sync();
+  o.tok = inv_draw(cs, gen, q, approx, mt, u, V, o);
+  o.kept = (uint32_t)q;
   rng = st;
   return true;
 }
@@ -951,100 +1394,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
       if (tok < 0) tok = lane_draw<kSlotBits>(kept, kid, ks, kept ? mass_of(lane, true) : 0.0, u, V, o.dex);
       o.tok = tok;
     } else {
-      // Kept ranks [0, q) in id order: lane l reads the id-order slots
-      // [8 l, 8 l + 8); a slot tagged with this call's generation names its
-      // unhit rank, every other slot (no candidate, a hit, a rank past the cut)
-      // weighs 0. First with the masses above, then with exact masses.
-      constexpr int kPer = kSlotsPerLane;
-      int rks[kPer];
-      uint32_t vb = 0u;   // bit i: slot 16 lane + i is kept
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const uint32_t x = cs.inv[(i << 6) | lane];
-        rks[i] = (int)(x & 1023u);
-        vb |= (((x >> 10) == gen && rks[i] < q) ? 1u : 0u) << i;
-      }
-      float mf[kPer];
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) mf[i] = cs.lm[rks[i]];   // tagged ranks are below kListLarge
-      C4S_PHASE(13);
-      auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
-        // in-lane inclusive prefix p[i], then one scan over the lanes
-        double e[kPer], p[kPer];
-        bool need = false;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const bool v = (vb >> i) & 1u;
-          const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
-          e[i] = (v && st) ? (double)mf[i] : 0.0;
-          need |= v && !st;
-        }
-        if (__ballot(need)) {   // exp for every slot (no per-slot branches), kept where needed
-#pragma unroll
-          for (int i = 0; i < kPer; ++i) {
-            const double x = exp((double)(cs.lz[rks[i]] - mt));
-            const bool st = approx && !exact_only && mf[i] >= 0x1p-100f;
-            e[i] = (((vb >> i) & 1u) && !st) ? x : e[i];
-          }
-        }
-        p[0] = e[0];
-#pragma unroll
-        for (int i = 1; i < kPer; ++i) p[i] = p[i - 1] + e[i];
-        const double inc = wave_scan_f64(p[kPer - 1]);
-        const double r = u * readlane_f64(inc, kWave - 1);
-        const double base = inc - p[kPer - 1];
-        double ha = 0.0, hp = 0.0;
-        int hrk = -1;
-#pragma unroll
-        for (int i = kPer - 1; i >= 0; --i) {   // the first slot reaching r wins
-          const double nx = base + p[i];
-          if (e[i] > 0.0 && nx >= r) { hrk = rks[i]; ha = nx; hp = i ? base + p[i - 1] : base; }
-        }
-        const uint64_t hb = __ballot(hrk >= 0);
-        if (!hb) return -1;
-        const int f = __ffsll((unsigned long long)hb) - 1;
-        const double af = readlane_f64(ha, f), pf = readlane_f64(hp, f);
-        const double eps = rel_eps(V) + eps_add;
-        if (!(r > 0.0 && (af - r > eps * af) && (r - pf > eps * r))) return -1;
-        return cs.lid[readlane_u32((uint32_t)hrk, f)];
-      };
-      int tok = -1;
-      o.dex = 0;
-      if (approx) tok = draw(false, 0x1p-22);
-      C4S_PHASE(14);
-      if (tok < 0) tok = draw(true, 0.0);
-      if (tok < 0) {
-        // text2semantic.cpp:152-164 sequentially in id order with exact masses
-        o.dex = 1;
-        int res = 0;
-        if (lane == 0) {
-          auto kept_mass = [&](int sl, int& rk) -> double {
-            const uint32_t x = cs.inv[slot_pos(sl)];
-            rk = (int)(x & 1023u);
-            return ((x >> 10) == gen && rk < q) ? exp((double)(cs.lz[rk] - mt)) : 0.0;
-          };
-          double total = 0.0;
-          for (int sl = 0; sl < kListLarge; ++sl) {
-            int rk;
-            total += kept_mass(sl, rk);
-          }
-          const double rr = u * total;
-          res = V - 1;
-          if (rr <= 0.0) {
-            res = 0;
-          } else {
-            double acc = 0.0;
-            for (int sl = 0; sl < kListLarge; ++sl) {
-              int rk;
-              const double ei = kept_mass(sl, rk);
-              acc += ei;
-              if (ei > 0.0 && rr <= acc) { res = cs.lid[rk]; break; }
-            }
-          }
-        }
-        tok = (int)readlane_u32((uint32_t)res, 0);
-      }
-      o.tok = tok;
+      o.tok = inv_draw(cs, gen, q, approx, mt, u, V, o);
     }
     C4S_PHASE(12);
     o.kept = (uint32_t)q;
@@ -1052,72 +1402,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
     return true;
   }
 
-  const int nchunk = h.nchunk;
-  double cv[4];
-  double cs_l = 0.0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ci = 4 * lane + i;
-    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)sum[kChunkW + ci]) - cdelta[ci] : 0.0;
-    cs_l += cv[i];
-  }
-  // Dense draw (top_p keeps every id of nonzero mass; zero masses never win):
-  // r = u * S, chunk prefixes locate r, the chunk is recomputed exactly.
-  const double r = u * S;
-  const double inc = wave_scan_f64(cs_l);
-  double run = (inc - cs_l) * rho;
-  int cstar = -1;
-  double pstar = 0.0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ci = 4 * lane + i;
-    const double nx = run + cv[i] * rho;
-    if (cstar < 0 && ci < nchunk && nx >= r) { cstar = ci; pstar = run; }
-    run = nx;
-  }
-  const uint64_t hmk = __ballot(cstar >= 0);
-  o.why = kWhyDraw;
-  if (!hmk || !(r > 0.0)) return false;
-  const int fl = __ffsll((unsigned long long)hmk) - 1;
-  cstar = (int)readlane_u32((uint32_t)cstar, fl);
-  pstar = readlane_f64(pstar, fl);
-  const int lo = cstar == 0 ? 0 : h.head + kChunkIds * cstar;
-  const int hi = (cstar == nchunk - 1) ? V : h.head + kChunkIds * (cstar + 1);
-  double ea = 0.0, eb = 0.0;
-  const int ia = lo + lane, ib = lo + kWave + lane;
-  auto mass_at = [&](int id) -> double {
-    const float x = val[id];
-    const float y = (c.pen_on && (bit_of(bmH0, id) || bit_of(bmN, id))) ? pen_exact(x, c.pen) : x;
-    const float z = c.temp_on ? y / c.temp : y;
-    return (z == ninf) ? 0.0 : exp((double)(z - mt));
-  };
-  if (ia < hi) ea = mass_at(ia);
-  if (ib < hi) eb = mass_at(ib);
-  const double sa = wave_scan_f64(ea) + pstar;
-  const double ta = readlane_f64(sa, kWave - 1);
-  const double sb = wave_scan_f64(eb) + ta;
-  const double mg = 2.0 * err;
-  const uint64_t fa = __ballot(ia < hi && ea > 0.0 && sa >= r);
-  const uint64_t fb = __ballot(ib < hi && eb > 0.0 && sb >= r);
-  double af, pf;
-  int tok;
-  if (fa) {
-    const int f = __ffsll((unsigned long long)fa) - 1;
-    af = readlane_f64(sa, f);
-    pf = af - readlane_f64(ea, f);
-    tok = lo + f;
-  } else if (fb) {
-    const int f = __ffsll((unsigned long long)fb) - 1;
-    af = readlane_f64(sb, f);
-    pf = af - readlane_f64(eb, f);
-    tok = lo + kWave + f;
-  } else {
-    return false;
-  }
-  if (!((af - r > mg + eps * af) && (r - pf > mg + eps * r))) return false;
-  o.tok = tok;
-  o.kept = (uint32_t)V;
-  o.dex = 0;
+  if (!dense_draw(h, c, V, val, bmN, bmH0, sum, cdelta, u, S, rho, err, mt, o)) return false;
   rng = st;
   return true;
 }
@@ -1926,7 +2211,11 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
         }
         C4S_PHASE(1);
         StepOut o{0, 0u, 0u, 0u};
-        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, ps, o);
+        // the register path when the scan's cut hint leaves room for hits within 64 ranks
+        const int hint = (int)(uint32_t)sw[kHdrW + 5];
+        const bool ok = ((dense || hint <= kLanesHint) && row_step_lanes(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, o)) ||
+                        (!dense && hint <= 4 * kWave && row_step_lanes4(h, c, V, val, bmN, ds, de, sw, rng, ps, o)) ||
+                        row_step(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, ps, o);
         const bool retry = attempt == 0 && !ok && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
         C4S_PHASE(2);
         if (attempt == 0 && dense)
