@@ -616,11 +616,11 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
 struct ChainSh {
   uint64_t sum[kSumWords];   // this step's summary: header words, list, chunks
   double cdelta[kMaxChunks];
-  uint32_t inv[kListLarge];   // id-order slot -> (generation << 10) | unhit rank
+  uint32_t inv[kListLarge + 1];   // id-order slot -> (generation << 10) | unhit rank; + a trash word
   uint32_t gen;             // generation of the last row step
-  float lz[kListLarge];
-  float lm[kListLarge];
-  int lid[kListLarge];
+  float lz[kListLarge + 1];   // by unhit rank; + a trash entry
+  float lm[kListLarge + 1];
+  int lid[kListLarge + 1];
   int lslot[kListLarge];
   double wd[NW];
   double we[NW];
@@ -1094,12 +1094,16 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     mk[i] = v ? ly[p0 + i] : 0.0f;
     const int id = v ? ent_id(e[i]) : 0;
     const bool hit = c.pen_on & v & bit_of(bmN, id);
-    // a drawn id is never in H0: its value is the raw one
-    if (c.pen_on) hraw = hit ? fmaxf(hraw, val[id]) : hraw;
+    // a drawn id is never in H0: its value is the raw one (read without a branch)
+    if (c.pen_on) {
+      const float x = val[id];
+      hraw = hit ? fmaxf(hraw, x) : hraw;
+    }
     un[i] = v & !hit;
     z[i] = un[i] ? kfloat(ent_key(e[i])) : ninf;
     cnt += un[i] ? 1u : 0u;
   }
+  C4S_PHASE(4);
   const uint32_t cinc = wave_scan_u32(cnt);
   const int nu = (int)readlane_u32(cinc, kWave - 1);
   if (nu == 0) return false;
@@ -1118,10 +1122,14 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   if (!(mt > ninf) || !(zo < mt)) return false;
   const float zend = (n > K * kWave) ? kfloat(readlane_u32(ent_key(e[K - 1]), kWave - 1)) : ninf;
   if (!(zend < mt)) return false;
-  const float hy = pen_exact(wave_max_dpp(hraw), c.pen);   // sampling.cpp:26, then :16
-  const float hm = c.temp_on ? hy / c.temp : hy;
+  float hm = ninf;   // the largest penalised hit: sampling.cpp:26, then :16
+  if (__ballot(hraw > ninf)) {
+    const float hy = pen_exact(wave_max_dpp(hraw), c.pen);
+    hm = c.temp_on ? hy / c.temp : hy;
+  }
   if (!(hm < mt)) return false;
 
+  C4S_PHASE(5);
   const double eps = rel_eps(V);
   const double dm = (double)h.m0 - (double)mt;
   const double rho = (dm == 0.0) ? 1.0 : exp(dm);
@@ -1135,6 +1143,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   const double marg = (double)c.p * err + eps * S;
   const bool approx = dm == 0.0;
   const double dmass = approx ? 0x1p-23 : 0.0;
+  C4S_PHASE(6);
   double em[K];
   bool need = false;
 #pragma unroll
@@ -1166,6 +1175,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     if (un[i] && D >= 0.0) qloc = min(qloc, rk[i]);
     ab += em[i];
   }
+  C4S_PHASE(7);
   if (__ballot(unsure) || __ballot(tiny)) return false;
   const uint64_t qb = __ballot(qloc != 0x7fffffff);
   if (!qb) return false;   // the cut lies past these ranks
@@ -1189,15 +1199,19 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     gen = 1u;
   }
   if (lane == 0) cs.gen = gen;
+  // every entry writes (no branches): an unhit one its rank and tag, a hit its
+  // slot untagged, an entry past the list the trash words
 #pragma unroll
-  for (int i = 0; i < K; ++i)
-    if (un[i] && rk[i] < q) {
-      cs.lz[rk[i]] = z[i];
-      cs.lm[rk[i]] = mk[i];
-      cs.lid[rk[i]] = ent_id(e[i]);
-      cs.inv[slot_pos(ent_rank(e[i]))] = (gen << 10) | (uint32_t)rk[i];
-    }
+  for (int i = 0; i < K; ++i) {
+    const bool v = p0 + i < n;
+    const int r = un[i] ? rk[i] : kListLarge;
+    cs.lz[r] = z[i];
+    cs.lm[r] = mk[i];
+    cs.lid[r] = ent_id(e[i]);
+    cs.inv[v ? slot_pos(ent_rank(e[i])) : kListLarge] = un[i] ? ((gen << 10) | (uint32_t)rk[i]) : 0u;
+  }
   wave_sync();
+  C4S_PHASE(8);
   o.tok = inv_draw(cs, gen, q, approx, mt, u, V, o);
   o.kept = (uint32_t)q;
   rng = st;
@@ -1873,11 +1887,11 @@ struct RowPSh {
   double wd[2][4];                // helper waves' correction sums, by step parity
   double we[2][4];                // and their error bounds
   double xd[NWC];                 // exact corrections of a retried step, per wave
-  uint32_t inv[kListLarge];       // id-order slot -> (generation << 10) | unhit rank
+  uint32_t inv[kListLarge + 1];   // id-order slot -> (generation << 10) | unhit rank; + a trash word
   uint32_t gen;                   // generation of the last row step
-  float lz[kListLarge];
-  float lm[kListLarge];
-  int lid[kListLarge];
+  float lz[kListLarge + 1];   // by unhit rank; + a trash entry
+  float lm[kListLarge + 1];
+  int lid[kListLarge + 1];
   int lslot[kListLarge];
   alignas(16) uint64_t hdr[2][3][8];   // per parity and helper wave: header copy
   int dlist[3][kDrawnList];       // per helper wave: drawn ids of its range (while they fit)
