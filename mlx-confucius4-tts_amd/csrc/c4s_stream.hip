@@ -1191,28 +1191,112 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   }
   const float zq1 = readlane_f32(zs, __ffsll((unsigned long long)__ballot(has)) - 1);
   if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
-  // kept ranks to LDS, tagged with this call's generation, then the id-order draw
-  uint32_t gen = cs.gen + 1u;
-  if (gen == 1u || gen >= (1u << 22)) {
-#pragma unroll
-    for (int i = 0; i < kSlotsPerLane; ++i) cs.inv[(i << 6) | lane] = 0u;
-    gen = 1u;
-  }
-  if (lane == 0) cs.gen = gen;
-  // every entry writes (no branches): an unhit one its rank and tag, a hit its
-  // slot untagged, an entry past the list the trash words
+  // Id-order draw (text2semantic.cpp:150-165) over the kept ranks: a bitmap of
+  // their id-order slots and its prefix counts give each kept entry its place
+  // among them; masses, values and ids go there, and four places a lane, one
+  // prefix scan, decide. First with the masses above, then exact, then replayed.
+  constexpr int kWords = kListLarge / 32;
+  if (lane < kWords) cs.kbits[lane] = 0u;
+  wave_sync();
+  bool kp[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    const bool v = p0 + i < n;
-    const int r = un[i] ? rk[i] : kListLarge;
-    cs.lz[r] = z[i];
-    cs.lm[r] = mk[i];
-    cs.lid[r] = ent_id(e[i]);
-    cs.inv[v ? slot_pos(ent_rank(e[i])) : kListLarge] = un[i] ? ((gen << 10) | (uint32_t)rk[i]) : 0u;
+    kp[i] = un[i] && rk[i] < q;
+    const int sl = ent_rank(e[i]);
+    if (kp[i]) atomicOr(&cs.kbits[sl >> 5], 1u << (sl & 31));
   }
   wave_sync();
+  {
+    const uint32_t wb = lane < kWords ? cs.kbits[lane] : 0u;
+    const uint32_t pc = (uint32_t)__popc(wb);
+    const uint32_t pinc = wave_scan_u32(pc);
+    if (lane < kWords) cs.kpre[lane] = pinc - pc;
+  }
+  wave_sync();
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const int sl = ent_rank(e[i]);
+    const int w = sl >> 5;
+    const int pos = kp[i] ? (int)(cs.kpre[w] + (uint32_t)__popc(cs.kbits[w] & ((1u << (sl & 31)) - 1u))) : kListLarge;
+    cs.lm[pos] = mk[i];
+    cs.lz[pos] = z[i];
+    cs.lid[pos] = ent_id(e[i]);
+  }
+  wave_sync();
+  float pm[K], pz[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const int pp = min(K * lane + i, kListLarge);
+    pm[i] = cs.lm[pp];
+    pz[i] = cs.lz[pp];
+  }
   C4S_PHASE(8);
-  o.tok = inv_draw(cs, gen, q, approx, mt, u, V, o);
+  auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
+    double ed[K], pr[K];
+    bool need2 = false;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const bool v = K * lane + i < q;
+      const bool stp = approx && !exact_only && pm[i] >= 0x1p-100f;
+      ed[i] = (v && stp) ? (double)pm[i] : 0.0;
+      need2 |= v && !stp;
+    }
+    if (__ballot(need2)) {
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        const bool v = K * lane + i < q;
+        const bool stp = approx && !exact_only && pm[i] >= 0x1p-100f;
+        const double x = exp((double)(pz[i] - mt));
+        ed[i] = (v && !stp) ? x : ed[i];
+      }
+    }
+    pr[0] = ed[0];
+#pragma unroll
+    for (int i = 1; i < K; ++i) pr[i] = pr[i - 1] + ed[i];
+    const double sinc = wave_scan_f64(pr[K - 1]);
+    const double r = u * readlane_f64(sinc, kWave - 1);
+    const double base = sinc - pr[K - 1];
+    double ha = 0.0, hp = 0.0;
+    int hpos = -1;
+#pragma unroll
+    for (int i = K - 1; i >= 0; --i) {   // the first place reaching r wins
+      const double nx = base + pr[i];
+      if (ed[i] > 0.0 && nx >= r) { hpos = K * lane + i; ha = nx; hp = i ? base + pr[i - 1] : base; }
+    }
+    const uint64_t hb = __ballot(hpos >= 0);
+    if (!hb) return -1;
+    const int f = __ffsll((unsigned long long)hb) - 1;
+    const double af = readlane_f64(ha, f), pf = readlane_f64(hp, f);
+    const double eps2 = rel_eps(V) + eps_add;
+    if (!(r > 0.0 && (af - r > eps2 * af) && (r - pf > eps2 * r))) return -1;
+    return cs.lid[readlane_u32((uint32_t)hpos, f)];
+  };
+  int tok = -1;
+  o.dex = 0;
+  if (approx) tok = draw(false, 0x1p-22);
+  if (tok < 0) tok = draw(true, 0.0);
+  if (tok < 0) {   // text2semantic.cpp:152-164 sequentially in id order with exact masses
+    o.dex = 1;
+    int res = 0;
+    if (lane == 0) {
+      double total = 0.0;
+      for (int pp = 0; pp < q; ++pp) total += exp((double)(cs.lz[pp] - mt));
+      const double rr = u * total;
+      res = V - 1;
+      if (rr <= 0.0) {
+        res = 0;
+      } else {
+        double acc = 0.0;
+        for (int pp = 0; pp < q; ++pp) {
+          const double ei = exp((double)(cs.lz[pp] - mt));
+          acc += ei;
+          if (ei > 0.0 && rr <= acc) { res = cs.lid[pp]; break; }
+        }
+      }
+    }
+    tok = (int)readlane_u32((uint32_t)res, 0);
+  }
+  o.tok = tok;
   o.kept = (uint32_t)q;
   rng = st;
   return true;
@@ -1893,6 +1977,8 @@ struct RowPSh {
   float lm[kListLarge + 1];
   int lid[kListLarge + 1];
   int lslot[kListLarge];
+  uint32_t kbits[kListLarge / 32];   // four-per-lane draw: id-order slots of the kept ranks
+  uint32_t kpre[kListLarge / 32];    // and their counts before each word
   alignas(16) uint64_t hdr[2][3][8];   // per parity and helper wave: header copy
   int dlist[3][kDrawnList];       // per helper wave: drawn ids of its range (while they fit)
   int nt[2];                      // token of step s when it joined bmN, else -1, at [s & 1]
