@@ -61,15 +61,16 @@ constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's stat
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
 // Chunks of the overlapped stream: the first is short (its scan is not
-// hidden), each next one 1.5 times longer (its scan, on half the CUs, must end
+// hidden), each next one 1.5 times longer (its scan, on its share of the CUs, must end
 // before the chain of the previous one), up to kOverlapChunk steps.
 constexpr int kOverlapFirst = 64;
 constexpr int kOverlapChunk = 256;
 constexpr int kOverlapStepsPerGroup = 2;   // more, shorter scan workgroups balance a short chunk
-// Of every 32 CUs, the chains' share in the overlapped stream: room for one
-// list workgroup and one full-vocabulary workgroup per row side by side (the
-// latter holds a whole CU's LDS).
-constexpr int kChainCusPer32 = 16;
+// Of every 32 CUs, the chains' shares in the overlapped stream: the
+// full-vocabulary chain (a workgroup holds a whole CU's LDS) and the list
+// chain (two workgroups a CU); the scans take the rest.
+constexpr int kRowCusPer32 = 6;
+constexpr int kListCusPer32 = 4;
 constexpr int kFastRounds = 3;
 constexpr int kMaxSegments = 8;   // step segments per row without penalty
 
@@ -265,22 +266,40 @@ int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream) {
   return launch_rows_checked(ctx, rows, static_cast<hipStream_t>(stream));
 }
 
-// Streams of the overlapped stream, created once: the two chain streams on
-// CUs 32 j + i, i < kChainCusPer32 (the runtime spreads them evenly over the
-// XCDs), the scan on the others. False when the device or the runtime cannot
-// split.
+// Streams of the overlapped stream, created once, on disjoint CU sets: the
+// full-vocabulary chain (side_m), the list chain (chain_m) and the scans
+// (scan_m). Mask bit c is CU c, and CU c sits on XCD c % 8. Within an XCD the
+// CUs go to the sets in bit-reversed order of their index (mod 32), so that
+// each set spreads evenly over the XCD's blocks of CUs. False when the device
+// or the runtime cannot split.
+static int cu_set(int cu) {   // 0: full-vocabulary chain, 1: list chain, 2: scan
+  const uint32_t k = (uint32_t)(cu / 8) & 31u;
+  const int rev = (int)(((k & 1u) << 4) | ((k & 2u) << 2) | (k & 4u) | ((k & 8u) >> 2) | ((k & 16u) >> 4));
+  return rev < kRowCusPer32 ? 0 : (rev < kRowCusPer32 + kListCusPer32 ? 1 : 2);
+}
+static int cus_in_set(const c4s_ctx* ctx, int set) {
+  int c = 0;
+  for (int cu = 0; cu < ctx->n_cus; ++cu) c += cu_set(cu) == set ? 1 : 0;
+  return c;
+}
+static int row_cus(const c4s_ctx* ctx) { return cus_in_set(ctx, 0); }
+static int list_cus(const c4s_ctx* ctx) { return cus_in_set(ctx, 1); }
 static bool cu_split(c4s_ctx* ctx) {
   if (ctx->chain_m) return true;
   if (ctx->cu_split_tried) return false;
   ctx->cu_split_tried = true;
   const int n = ctx->n_cus;
   if (n < 64 || n % 32 != 0) return false;
-  std::vector<uint32_t> chain_mask((size_t)n / 32, (1u << kChainCusPer32) - 1u), scan_mask((size_t)n / 32);
-  for (size_t i = 0; i < scan_mask.size(); ++i) scan_mask[i] = ~chain_mask[i];
-  const uint32_t nw = (uint32_t)chain_mask.size();
-  if (hipExtStreamCreateWithCUMask(&ctx->scan_m, nw, scan_mask.data()) != hipSuccess ||
-      hipExtStreamCreateWithCUMask(&ctx->chain_m, nw, chain_mask.data()) != hipSuccess ||
-      hipExtStreamCreateWithCUMask(&ctx->side_m, nw, chain_mask.data()) != hipSuccess ||
+  const size_t nw = (size_t)n / 32;
+  std::vector<uint32_t> row_mask(nw, 0u), list_mask(nw, 0u), scan_mask(nw, 0u);
+  for (int cu = 0; cu < n; ++cu) {
+    const int set = cu_set(cu);
+    std::vector<uint32_t>& m = set == 0 ? row_mask : (set == 1 ? list_mask : scan_mask);
+    m[(size_t)cu / 32] |= 1u << (cu % 32);
+  }
+  if (hipExtStreamCreateWithCUMask(&ctx->scan_m, (uint32_t)nw, scan_mask.data()) != hipSuccess ||
+      hipExtStreamCreateWithCUMask(&ctx->chain_m, (uint32_t)nw, list_mask.data()) != hipSuccess ||
+      hipExtStreamCreateWithCUMask(&ctx->side_m, (uint32_t)nw, row_mask.data()) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_done, hipEventDisableTiming) != hipSuccess) {
     for (hipStream_t* st : {&ctx->scan_m, &ctx->chain_m, &ctx->side_m})
       if (*st) { (void)hipStreamDestroy(*st); *st = nullptr; }
@@ -334,15 +353,14 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     return C4S_OK;
   }
   // Steps go in chunks; the chain carries its per-row state from chunk to
-  // chunk. Overlapped (rows at most half the chains' CUs, steps for two
+  // chunk. Overlapped (rows at most the chains' CUs, steps for four
   // chunks or more): the scan of chunk c+1 runs on its own CUs beside the chain of chunk
   // c, summaries are double-buffered and a scan waits for the chain that last
   // read its buffer; the first chunk's scan, which nothing hides, runs on every
   // CU. Otherwise the whole stream is one chunk where the budget allows, each
   // phase on every CU.
   const size_t per_step = (size_t)a.n_rows * c4s::kSumStride;
-  const int chain_cus = ctx->n_cus / 32 * kChainCusPer32;
-  const bool overlap = 2 * a.n_rows <= chain_cus && a.n_steps >= 4 * kOverlapFirst &&
+  const bool overlap = a.n_rows <= row_cus(ctx) + list_cus(ctx) && a.n_steps >= 4 * kOverlapFirst &&
                        (size_t)kOverlapChunk * 2 * per_step <= kSumBudget && cu_split(ctx);
   size_t chunk_sz = std::min<size_t>((size_t)a.n_steps, kSumBudget / per_step);
   if (overlap) chunk_sz = std::min<size_t>((size_t)a.n_steps, kOverlapChunk);
@@ -365,7 +383,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // Rows without penalty split their steps into segments, one workgroup each,
   // over the CUs the chains have (every workgroup of the pipelined chain
   // holds a CU's LDS).
-  const int nseg = pipelined ? std::max(2, std::min(kMaxSegments, (overlap ? chain_cus : ctx->n_cus) /
+  const int nseg = pipelined ? std::max(2, std::min(kMaxSegments, (overlap ? row_cus(ctx) : ctx->n_cus) /
                                                                      std::max(1, a.n_rows)))
                              : 1;
   if (nseg > 1) {

@@ -93,12 +93,16 @@ __device__ __forceinline__ int ent_rank(uint64_t e) { return (int)((uint32_t)e &
 // Summary words: list entries [0, kListLarge); from kYW one float per entry:
 // its value before the temperature (greedy and top-k rows) or its mass
 // exp((double)fl(z - m0)) rounded to fp32 (full-vocabulary rows); header
-// [kHdrW, kHdrW + 8); chunk masses from kChunkW. List entry i sits in lane i % 64 of a wave's i / 64-th
-// load, so list rows read their entries straight into registers.
+// [kHdrW, kHdrW + 8); chunk masses from kChunkW; from kPlaceW (full-vocabulary
+// rows) one byte per entry of the list's first NTA: its id-order place among
+// them. List entry i sits in lane i % 64 of a wave's i / 64-th load, so list
+// rows read their entries straight into registers.
 constexpr int kYW = kListLarge;
 constexpr int kHdrW = kYW + kListLarge / 2;
 constexpr int kChunkW = kHdrW + kSumHdrBytes / 8;
-constexpr int kSumWords = kChunkW + kMaxChunks;
+constexpr int kPlaceW = kChunkW + kMaxChunks;
+constexpr int kSumWords = kPlaceW + NTA / 8;
+static_assert(NTA <= 256, "places fit a byte");
 static_assert((size_t)kSumWords * 8 <= kSumStride, "summary fits its stride");
 
 __device__ __forceinline__ const uint64_t* sum_words(const StreamWs& w, int n_rows, int s, int row) {
@@ -160,6 +164,8 @@ struct ScanSh {
   double redh[NWA];                // per wave: mass of its list positions below NTA
   uint32_t lmark[kCandCap / 32];   // candidate positions of the list entries
   uint32_t lpre[kCandCap / 32];    // marks before each word
+  uint32_t fmark[kCandCap / 32];   // the same for the list's first NTA entries
+  uint32_t fpre[kCandCap / 32];
 };
 
 // Block exclusive scan over the NTA threads (thread order).
@@ -476,20 +482,28 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       const float zmax = kfloat(ent_key(srt[0]));
       // The stored rank is the id-order rank among the list entries:
       // candidates sit in id order, so it counts the list's candidate
-      // positions below the entry's own.
-      if (t < kCandCap / 32) sh.lmark[t] = 0u;
+      // positions below the entry's own. Full-vocabulary rows also get each
+      // of the first NTA entries' id-order place among those NTA.
+      if (t < kCandCap / 32) { sh.lmark[t] = 0u; sh.fmark[t] = 0u; }
       __syncthreads();
       for (int i = t; i < n; i += NTA) {
         const int ci = ent_rank(srt[i]);
         atomicOr(&sh.lmark[ci >> 5], 1u << (ci & 31));
+        if (i < NTA) atomicOr(&sh.fmark[ci >> 5], 1u << (ci & 31));
       }
       __syncthreads();
-      if (t < kWave) {
-        const uint32_t pc = (t < kCandCap / 32) ? (uint32_t)__popc(sh.lmark[t]) : 0u;
+      if (wv < 2) {
+        const uint32_t* mk = wv ? sh.fmark : sh.lmark;
+        const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(mk[lane]) : 0u;
         const uint32_t inc = wave_scan_u32(pc);
-        if (t < kCandCap / 32) sh.lpre[t] = inc - pc;
+        if (lane < kCandCap / 32) (wv ? sh.fpre : sh.lpre)[lane] = inc - pc;
       }
       __syncthreads();
+      if (masses && t < n) {
+        const int ci = ent_rank(srt[t]);
+        const uint32_t pw = sh.fpre[ci >> 5] + (uint32_t)__popc(sh.fmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
+        reinterpret_cast<uint8_t*>(sw + kPlaceW)[t] = (uint8_t)pw;
+      }
       for (int i = t; i < n; i += NTA) {
         const uint64_t e = srt[i];
         const int ci = ent_rank(e);
@@ -829,6 +843,7 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   const int fl = __ffsll((unsigned long long)hmk) - 1;
   cstar = (int)readlane_u32((uint32_t)cstar, fl);
   pstar = readlane_f64(pstar, fl);
+  C4S_PHASE(13);
   const int lo = cstar == 0 ? 0 : h.head + kChunkIds * cstar;
   const int hi = (cstar == nchunk - 1) ? V : h.head + kChunkIds * (cstar + 1);
   double ea = 0.0, eb = 0.0;
@@ -841,6 +856,7 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   };
   if (ia < hi) ea = mass_at(ia);
   if (ib < hi) eb = mass_at(ib);
+  C4S_PHASE(14);
   const double sa = wave_scan_f64(ea) + pstar;
   const double ta = readlane_f64(sa, kWave - 1);
   const double sb = wave_scan_f64(eb) + ta;
@@ -900,6 +916,7 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const float pm = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(m32)));
   const int pid = __builtin_amdgcn_ds_permute(dst, id);
   const int pslot = __builtin_amdgcn_ds_permute(dst, ent_rank(e));
+  C4S_PHASE(4);
   const bool in = lane < nu;
   const float z = in ? kfloat(pk) : ninf;
   const float mt = readlane_f32(z, 0);
@@ -912,6 +929,7 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const float hy = pen_exact(hx, c.pen);   // sampling.cpp:26, then :16
   const float hm = c.temp_on ? hy / c.temp : hy;
   if (!(hm < mt)) return false;
+  C4S_PHASE(5);
 
   const double eps = rel_eps(V);
   const double dm = (double)h.m0 - (double)mt;
@@ -922,6 +940,7 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const double thr = 1.0 - (double)c.p;
   const uint64_t st = xorshift64(rng);
   const double u = unit_from_state(st);
+  C4S_PHASE(6);
   if (!(thr > 0.0)) {
     if (!dense_draw(h, c, V, val, bmN, bmH0, sum, cdelta, u, S, rho, err, mt, o)) return false;
     rng = st;
@@ -946,6 +965,7 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   if (q > nu) return false;
   const float zq1 = readlane_f32(z, q - 1);
   if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
+  C4S_PHASE(7);
   // the draw on the kept ranks [0, q): first with the masses above, then exact
   const bool kept = lane < q;
   uint32_t dex = 0;
@@ -1082,6 +1102,8 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   const float ninf = neg_inf();
   const int p0 = K * lane;
   const float* ly = reinterpret_cast<const float*>(sum + kYW);
+  // id-order places of this lane's entries among the list's first K * 64, one byte each
+  const uint32_t pl = reinterpret_cast<const uint32_t*>(sum + kPlaceW)[lane];
   uint64_t e[K];
   float mk[K], z[K];
   bool un[K];
@@ -1191,44 +1213,31 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   }
   const float zq1 = readlane_f32(zs, __ffsll((unsigned long long)__ballot(has)) - 1);
   if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
-  // Id-order draw (text2semantic.cpp:150-165) over the kept ranks: a bitmap of
-  // their id-order slots and its prefix counts give each kept entry its place
-  // among them; masses, values and ids go there, and four places a lane, one
-  // prefix scan, decide. First with the masses above, then exact, then replayed.
-  constexpr int kWords = kListLarge / 32;
-  if (lane < kWords) cs.kbits[lane] = 0u;
-  wave_sync();
-  bool kp[K];
+  // Id-order draw (text2semantic.cpp:150-165) over the kept ranks: every entry
+  // of the list's first np writes its stored mass, value and id (-1 unless
+  // kept) at its id-order place among them (the scan's place bytes); four
+  // places a lane, one prefix scan, decide. First with the masses above, then
+  // exact, then replayed.
+  const int np = min(n, K * kWave);
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    kp[i] = un[i] && rk[i] < q;
-    const int sl = ent_rank(e[i]);
-    if (kp[i]) atomicOr(&cs.kbits[sl >> 5], 1u << (sl & 31));
+    if (p0 + i < np) {
+      const int pp = (int)((pl >> (8 * i)) & 255u);
+      cs.lm[pp] = mk[i];
+      cs.lz[pp] = z[i];
+      cs.lid[pp] = (un[i] && rk[i] < q) ? ent_id(e[i]) : -1;
+    }
   }
   wave_sync();
-  {
-    const uint32_t wb = lane < kWords ? cs.kbits[lane] : 0u;
-    const uint32_t pc = (uint32_t)__popc(wb);
-    const uint32_t pinc = wave_scan_u32(pc);
-    if (lane < kWords) cs.kpre[lane] = pinc - pc;
-  }
-  wave_sync();
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-    const int sl = ent_rank(e[i]);
-    const int w = sl >> 5;
-    const int pos = kp[i] ? (int)(cs.kpre[w] + (uint32_t)__popc(cs.kbits[w] & ((1u << (sl & 31)) - 1u))) : kListLarge;
-    cs.lm[pos] = mk[i];
-    cs.lz[pos] = z[i];
-    cs.lid[pos] = ent_id(e[i]);
-  }
-  wave_sync();
+  C4S_PHASE(11);
   float pm[K], pz[K];
+  int pid[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    const int pp = min(K * lane + i, kListLarge);
+    const int pp = K * lane + i;
     pm[i] = cs.lm[pp];
     pz[i] = cs.lz[pp];
+    pid[i] = pp < np ? cs.lid[pp] : -1;
   }
   C4S_PHASE(8);
   auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
@@ -1236,7 +1245,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     bool need2 = false;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const bool v = K * lane + i < q;
+      const bool v = pid[i] >= 0;
       const bool stp = approx && !exact_only && pm[i] >= 0x1p-100f;
       ed[i] = (v && stp) ? (double)pm[i] : 0.0;
       need2 |= v && !stp;
@@ -1244,7 +1253,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     if (__ballot(need2)) {
 #pragma unroll
       for (int i = 0; i < K; ++i) {
-        const bool v = K * lane + i < q;
+        const bool v = pid[i] >= 0;
         const bool stp = approx && !exact_only && pm[i] >= 0x1p-100f;
         const double x = exp((double)(pz[i] - mt));
         ed[i] = (v && !stp) ? x : ed[i];
@@ -1269,7 +1278,10 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     const double af = readlane_f64(ha, f), pf = readlane_f64(hp, f);
     const double eps2 = rel_eps(V) + eps_add;
     if (!(r > 0.0 && (af - r > eps2 * af) && (r - pf > eps2 * r))) return -1;
-    return cs.lid[readlane_u32((uint32_t)hpos, f)];
+    int hid = -1;
+#pragma unroll
+    for (int i = 0; i < K; ++i) hid = (hpos == K * lane + i) ? pid[i] : hid;
+    return (int)readlane_u32((uint32_t)hid, f);
   };
   int tok = -1;
   o.dex = 0;
@@ -1280,14 +1292,16 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     int res = 0;
     if (lane == 0) {
       double total = 0.0;
-      for (int pp = 0; pp < q; ++pp) total += exp((double)(cs.lz[pp] - mt));
+      for (int pp = 0; pp < np; ++pp)
+        if (cs.lid[pp] >= 0) total += exp((double)(cs.lz[pp] - mt));
       const double rr = u * total;
       res = V - 1;
       if (rr <= 0.0) {
         res = 0;
       } else {
         double acc = 0.0;
-        for (int pp = 0; pp < q; ++pp) {
+        for (int pp = 0; pp < np; ++pp) {
+          if (cs.lid[pp] < 0) continue;
           const double ei = exp((double)(cs.lz[pp] - mt));
           acc += ei;
           if (ei > 0.0 && rr <= acc) { res = cs.lid[pp]; break; }
@@ -1977,8 +1991,6 @@ struct RowPSh {
   float lm[kListLarge + 1];
   int lid[kListLarge + 1];
   int lslot[kListLarge];
-  uint32_t kbits[kListLarge / 32];   // four-per-lane draw: id-order slots of the kept ranks
-  uint32_t kpre[kListLarge / 32];    // and their counts before each word
   alignas(16) uint64_t hdr[2][3][8];   // per parity and helper wave: header copy
   int dlist[3][kDrawnList];       // per helper wave: drawn ids of its range (while they fit)
   int nt[2];                      // token of step s when it joined bmN, else -1, at [s & 1]
