@@ -166,6 +166,7 @@ struct ScanSh {
   uint32_t lpre[kCandCap / 32];    // marks before each word
   uint32_t fmark[kCandCap / 32];   // the same for the list's first NTA entries
   uint32_t fpre[kCandCap / 32];
+  uint32_t place4[NTA / 4];        // their id-order places, a byte each, stored as words
 };
 
 // Block exclusive scan over the NTA threads (thread order).
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       if (masses && t < n) {
         const int ci = ent_rank(srt[t]);
         const uint32_t pw = sh.fpre[ci >> 5] + (uint32_t)__popc(sh.fmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
-        reinterpret_cast<uint8_t*>(sw + kPlaceW)[t] = (uint8_t)pw;
+        reinterpret_cast<uint8_t*>(sh.place4)[t] = (uint8_t)pw;   // to the summary as words below
       }
       for (int i = t; i < n; i += NTA) {
         const uint64_t e = srt[i];
@@ -606,6 +607,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       }
     }
     C4S_SCAN_PHASE(7);
+    if (masses && !bad && t < NTA / 4) reinterpret_cast<uint32_t*>(sw + kPlaceW)[t] = sh.place4[t];   // places (above)
     if (t == 0) {
       SumHdr h{};
       h.n = bad ? 0 : n;
