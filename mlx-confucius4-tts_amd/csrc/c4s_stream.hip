@@ -6,18 +6,23 @@
 // and its RNG advances once per sampled step whatever was drawn
 // (text2semantic.cpp:158). So the bulk of the work is split off:
 //
-//  scan  (k_stream_scan, all CUs, every (step, row) independently)
+//  scan  (k_stream_scan, every (step, row) independently)
 //        reads the row once from HBM, applies the initial history H0 and writes
 //        a summary: the top of the row sorted by (value desc, id asc), a key
-//        bound on everything left out, and, for rows without top-k, chunk masses
-//        exp(z - m0) of the whole row in 64-id chunks with an absolute error
-//        bound (fp32 exp2 with a per-element relative bound).
-//  chain (k_stream_chain, one workgroup per row, steps in order)
-//        applies the penalty of ids drawn during the stream to the summary
-//        (only those ids change), then decides top-k / top-p / the draw on
-//        the candidates. Every decision is accepted only with a margin larger
-//        than the error bounds; otherwise the step runs the exact chain on the
-//        full row (fetched into LDS), as the single-kernel stream does.
+//        bound on everything left out, and, for rows without top-k, the chunk
+//        masses exp((double)fl(z - m0)) of the whole row in 64-id chunks, their
+//        sum, the list entries' fp32 masses, a cut hint and the first 256
+//        entries' id-order places.
+//  chains (one per row, steps in order) apply the penalty of ids drawn during
+//        the stream to the summary (only those ids change), then decide top-k /
+//        top-p / the draw on the candidates: k_stream_list (greedy and top-k
+//        rows, one wave), k_stream_rowp (full-vocabulary rows, a CU each,
+//        pipelined with helper waves; rows without penalty in step segments
+//        settled by k_stream_segfix), k_stream_chain (the exact chain, for
+//        rows the fast chains do not take), k_stream_rowk / k_stream_repair
+//        (where the pipelined chain does not fit). Every decision is accepted
+//        only with a margin larger than the error bounds; otherwise the step
+//        runs the exact chain on the full row staged in LDS.
 //
 // Row modes (stream_mode): greedy rows and top-k rows with k <= 64 use the
 // candidate list alone; full-vocabulary rows (top-k off) also use the chunk
@@ -1321,7 +1326,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
 // Full-vocabulary step (wave 0). The summary words are in LDS at `sum`; also
 // needs the correction of the masses for ids drawn during the stream (dsum,
 // its error derr; per chunk in `cdelta`) and the raw row in LDS (`val`). The
-// list is compacted lazily, 64 entries at a time, only as deep as the decision
+// list is compacted lazily, 256 entries at a time, only as deep as the decision
 // needs; cs provides the compaction and slot arrays.
 template <class CS>
 __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
@@ -1346,8 +1351,8 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
   if (lane == 0) cs.gen = gen;
   int nb = 0, nu = 0;
   float hm = ninf;
-  // list block [nb, nb + 64): unhit entries to their ranks, penalised hits into hm
-  // (256 entries a call, four consecutive ones per lane)
+  // list block [nb, nb + 256): unhit entries to their ranks, penalised hits into
+  // hm (four consecutive entries per lane)
   auto compact = [&]() __attribute__((always_inline)) {
     const int p0 = nb + 4 * lane;
     uint64_t e[4];
