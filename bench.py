@@ -13,7 +13,8 @@ scanned beside the chains of the previous chunk. The calls are issued back to
 back on a stream of the bench's own. `value` is sampled rows per second over
 that call; --sequential times the single-kernel stream instead.
 
-Also reported: the same chain as one launch per AR step (per_call), an HBM
+Also reported: the same chain as one launch per AR step (per_call; with the
+history as CSR ids, and kept on the device as a set that each call extends), an HBM
 copy probe, bit-exact parity of the first AR steps against the CPU oracle, and
 the oracle timed on host cores as the CPU baseline (kind "port").
 
@@ -166,9 +167,25 @@ def main():
     torch.cuda.synchronize()
     call_us = e0.elapsed_time(e1) * 1e3 / n_calls
     call_bytes = R * (4 * V + 4) + 4 * h0.sum()
+    # the same loop with the history kept on the device as a set (grows by each token)
+    bits = torch.zeros((R, (V + 31) // 32), dtype=torch.int32, device=dev)
+    ctx.hist_bits_init(hist_ids, hist_off, R, V, bits)
+    rng2 = rng0.clone()
+    torch.cuda.synchronize()
+    e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e2.record()
+    for t in range(n_calls):
+        ctx.sample_rows(logits[t % T], None, None, temp, top_k, top_p, pen, rng2, tok1,
+                        do_sample=do_sample, hist_bits=bits, stop_token=V - 1)
+    e3.record()
+    torch.cuda.synchronize()
+    bits_us = e2.elapsed_time(e3) * 1e3 / n_calls
+    bits_bytes = R * (4 * V + 4 + 4 * ((V + 31) // 32) + 4)
     per_call = {"us_per_call": round(call_us, 3), "rows_per_s": round(R / (call_us * 1e-6), 1),
-                "achieved_GBps": round(call_bytes / (call_us * 1e-6) / 1e9, 1)}
-    log(f"per-call: {call_us:.2f} us per 64-row step")
+                "achieved_GBps": round(call_bytes / (call_us * 1e-6) / 1e9, 1),
+                "hist_bits_us_per_call": round(bits_us, 3),
+                "hist_bits_achieved_GBps": round(bits_bytes / (bits_us * 1e-6) / 1e9, 1)}
+    log(f"per-call: {call_us:.2f} us per 64-row step ({bits_us:.2f} us with the history kept as a set)")
 
     # ---- HBM probe ------------------------------------------------------------------------
     nb = 1 << 30

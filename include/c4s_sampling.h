@@ -98,6 +98,14 @@ typedef struct c4s_rows {
   float* out_masked;            /* [n_rows][vocab] or NULL: row state before argmax/draw */
   uint32_t* out_stats;          /* [n_rows][4] or NULL */
   uint32_t mode;                /* C4S_MODE_CHAIN or C4S_MODE_CUSTOM | ... */
+  /* The AR loop's history gen[b] kept on the device across steps, as a set:
+   * [n_rows][(vocab + 31) / 32] bit words or NULL. When set it is the penalty's
+   * history in place of hist_ids/hist_offsets (sampling.cpp:22 applies each
+   * distinct id once, so the set is the history), and after the step every
+   * active row's token joins it unless it equals stop_token
+   * (text2semantic.cpp:333-334). Fill it once with c4s_hist_bits_init. */
+  uint32_t* hist_bits;
+  int32_t stop_token;           /* with hist_bits: the token that does not join (-1: none) */
 } c4s_rows;
 
 /* Many AR steps of a batch whose logits are already known (synthetic or
@@ -159,6 +167,12 @@ int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);
 /* head(cur) then the chain on its logits (text2semantic.cpp:297-337 in one
  * call); rows->logits/ld/dtype/vocab/n_rows are taken from `head`. */
 int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);
+
+/* hist_bits[b] = the set of row b's CSR history ids in [0, vocab) (ids
+ * outside are skipped, sampling.cpp:24); the starting state of
+ * c4s_rows.hist_bits (text2semantic.cpp:196-372 keeps gen[b] across steps). */
+int c4s_hist_bits_init(c4s_ctx* ctx, const int32_t* hist_ids, const int64_t* hist_offsets, int32_t n_rows,
+                       int32_t vocab, uint32_t* hist_bits, void* stream);
 
 /* Seeds (host only): text2semantic.cpp:109 and :292-294. */
 uint64_t c4s_seed_single(uint64_t seed);

@@ -32,7 +32,8 @@ class Rows(C.Structure):
                 ("vocab", C.c_int32), ("hist_ids", _vp), ("hist_offsets", _vp),
                 ("temperature", _vp), ("top_k", _vp), ("top_p", _vp), ("rep_penalty", _vp),
                 ("min_keep", _vp), ("do_sample", _vp), ("row_active", _vp), ("rng_state", _vp),
-                ("out_token", _vp), ("out_masked", _vp), ("out_stats", _vp), ("mode", C.c_uint32)]
+                ("out_token", _vp), ("out_masked", _vp), ("out_stats", _vp), ("mode", C.c_uint32),
+                ("hist_bits", _vp), ("stop_token", C.c_int32)]
 
 
 class Stream(C.Structure):
@@ -87,6 +88,7 @@ def lib() -> C.CDLL:
     L.c4s_version.restype = C.c_char_p
     L.c4s_sample_rows.argtypes = [_vp, C.POINTER(Rows), _vp]
     L.c4s_sample_stream.argtypes = [_vp, C.POINTER(Stream), _vp]
+    L.c4s_hist_bits_init.argtypes = [_vp, _vp, _vp, C.c_int32, C.c_int32, _vp, _vp]
     L.c4s_lmhead.argtypes = [_vp, C.POINTER(Head), _vp]
     L.c4s_lmhead_sample.argtypes = [_vp, C.POINTER(Head), C.POINTER(Rows), _vp]
     L.c4s_seed_single.argtypes = [C.c_uint64]
@@ -155,7 +157,8 @@ class Context:
     # ---- device entry points (torch tensors on the GPU) ------------------------
     def sample_rows(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_token,
                     do_sample=None, min_keep=None, row_active=None, out_masked=None,
-                    out_stats=None, mode=MODE_CHAIN, vocab=None, stream=None):
+                    out_stats=None, mode=MODE_CHAIN, vocab=None, stream=None, hist_bits=None,
+                    stop_token=-1):
         import torch
         n_rows, ld = logits.shape
         r = Rows(logits=_p(logits), ld=ld, dtype=BF16 if logits.dtype == torch.bfloat16 else F32,
@@ -163,8 +166,13 @@ class Context:
                  temperature=_p(temp), top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen),
                  min_keep=_p(min_keep), do_sample=_p(do_sample), row_active=_p(row_active),
                  rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
-                 out_stats=_p(out_stats), mode=mode)
+                 out_stats=_p(out_stats), mode=mode, hist_bits=_p(hist_bits), stop_token=stop_token)
         self._check(lib().c4s_sample_rows(self._h, C.byref(r), _stream_handle(stream)), "sample_rows")
+
+    def hist_bits_init(self, hist_ids, hist_off, n_rows, vocab, hist_bits, stream=None):
+        """hist_bits[b] (int32 words, [n_rows][(vocab+31)//32]) = the set of row b's CSR history."""
+        self._check(lib().c4s_hist_bits_init(self._h, _p(hist_ids), _p(hist_off), n_rows, vocab, _p(hist_bits),
+                                             _stream_handle(stream)), "hist_bits_init")
 
     def sample_stream(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_tokens,
                       do_sample=None, stop_token=-1, out_stats=None, stream=None, sequential=False):

@@ -138,8 +138,8 @@ int validate_rows(c4s_ctx* ctx, const c4s_rows* r) {
   if (custom && (m & C4S_T_ARGMAX) && (m & C4S_T_DRAW))
     return fail(ctx, C4S_EINVAL, "argmax and draw are exclusive");
   const bool pen = !custom || (m & C4S_P_PENALTY);
-  if (pen && (!r->rep_penalty || !r->hist_offsets))
-    return fail(ctx, C4S_EINVAL, "penalty needs rep_penalty and hist_offsets");
+  if (pen && (!r->rep_penalty || (!r->hist_offsets && !r->hist_bits)))
+    return fail(ctx, C4S_EINVAL, "penalty needs rep_penalty and hist_offsets or hist_bits");
   if (pen && !r->hist_ids) {
     // allowed only when every history is empty; the kernel never reads ids then
   }
@@ -173,6 +173,8 @@ c4s::RowsArgs to_args(const c4s_rows* r) {
   a.out_masked = r->out_masked;
   a.stats = r->out_stats;
   a.mode = r->mode;
+  a.hist_bits = r->hist_bits;
+  a.stop_token = r->stop_token;
   return a;
 }
 
@@ -307,6 +309,21 @@ static bool cu_split(c4s_ctx* ctx) {
     return false;
   }
   return true;
+}
+
+int c4s_hist_bits_init(c4s_ctx* ctx, const int32_t* hist_ids, const int64_t* hist_offsets, int32_t n_rows,
+                       int32_t vocab, uint32_t* hist_bits, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (n_rows < 0) return fail(ctx, C4S_EINVAL, "n_rows < 0");
+  if (n_rows == 0) return C4S_OK;
+  if (vocab < 1 || vocab > c4s::kMaxVocab) return fail(ctx, C4S_EINVAL, "vocab out of range");
+  if (!hist_bits || !hist_offsets) return fail(ctx, C4S_EINVAL, "hist_bits/hist_offsets is NULL");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  const hipError_t e = c4s::launch_hist_bits_init(hist_ids, hist_offsets, n_rows, vocab, hist_bits,
+                                                  static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(ctx, e, "hist_bits_init launch");
+  return C4S_OK;
 }
 
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {

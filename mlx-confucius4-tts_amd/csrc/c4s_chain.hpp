@@ -1121,6 +1121,8 @@ struct LdsLayout {
 
 __host__ __device__ __forceinline__ int vpad(int V) { return (V + 3) & ~3; }
 __host__ __device__ __forceinline__ int bitmap_words(int V) { return ((V + 31) / 32 + 1 + 3) & ~3; }
+// Words of a caller's per-row history set (c4s_rows.hist_bits).
+__host__ __device__ __forceinline__ int hist_words(int V) { return (V + 31) / 32; }
 
 // `val` is the row buffer base (vpad(V) + 4 floats); a row is stored at
 // val + shift so that its float4 body is 16-byte aligned in LDS.

@@ -53,6 +53,8 @@ struct RowsArgs {
   uint32_t mode;        // kCustom | processor bits, or 0 for the reference chain
   uint32_t* sort_ws;    // large-vocab exact pass: per-row key buffer
   int64_t sort_ws_stride;
+  uint32_t* hist_bits;  // per-row history set kept across steps, or null
+  int stop_token;       // with hist_bits: the token that does not join it
 };
 
 struct StreamArgs {
@@ -122,6 +124,8 @@ size_t rows_global_lds_bytes(int vocab);
 size_t stream_lds_bytes(int vocab, int unused);
 
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s);
+hipError_t launch_hist_bits_init(const int32_t* ids, const int64_t* off, int n_rows, int V, uint32_t* bits,
+                                 hipStream_t s);
 hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_list_lds_bytes(int vocab);  // candidate-list chain: a row for its exact steps

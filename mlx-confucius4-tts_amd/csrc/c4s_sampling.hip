@@ -31,6 +31,13 @@ namespace {
 
 // ---- kernels -------------------------------------------------------------------
 
+// The drawn token joins the row's kept history set unless it is the stop token
+// (text2semantic.cpp:333-334: a finished row appends nothing).
+__device__ __forceinline__ void join_history(const RowsArgs& a, int row, int tok) {
+  if (a.hist_bits && tok >= 0 && tok < a.vocab && tok != a.stop_token)
+    atomicOr(&a.hist_bits[(int64_t)row * hist_words(a.vocab) + (tok >> 5)], 1u << (tok & 31));
+}
+
 __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ Scratch sh;
@@ -54,13 +61,18 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
   }
   if (c.pen_on) {
     const int nw = bitmap_words(V);
-    for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
-    __syncthreads();
-    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-    for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
-      const int id = a.hist_ids[j];
-      if (id < 0 || id >= V) continue;   // sampling.cpp:24
-      atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
+    if (a.hist_bits) {   // the history set kept across steps
+      const uint32_t* hb = a.hist_bits + (int64_t)row * hist_words(V);
+      for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = w < hist_words(V) ? hb[w] : 0u;
+    } else {
+      for (int w = threadIdx.x; w < nw; w += NT) L.bitmap[w] = 0u;
+      __syncthreads();
+      const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+      for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+        const int id = a.hist_ids[j];
+        if (id < 0 || id >= V) continue;   // sampling.cpp:24
+        atomicOr(&L.bitmap[id >> 5], 1u << (id & 31));
+      }
     }
     __syncthreads();
     penalise_chunk(L.val, L.bitmap, V, c.pen);
@@ -77,6 +89,7 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
   if (threadIdx.x == 0) {
     a.out_tok[row] = tok;
     if (c.draw && a.rng) a.rng[row] = rng;
+    join_history(a, row, tok);
   }
 }
 
@@ -96,11 +109,16 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
   for (int w = threadIdx.x; w < nw; w += NT) bitmap[w] = 0u;
   __syncthreads();
   if (c.pen_on) {
-    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-    for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
-      const int id = a.hist_ids[j];
-      if (id < 0 || id >= V) continue;
-      atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    if (a.hist_bits) {   // the history set kept across steps
+      const uint32_t* hb = a.hist_bits + (int64_t)row * hist_words(V);
+      for (int w = threadIdx.x; w < nw; w += NT) bitmap[w] = hb[w];
+    } else {
+      const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+      for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+        const int id = a.hist_ids[j];
+        if (id < 0 || id >= V) continue;
+        atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+      }
     }
     __syncthreads();
   }
@@ -124,6 +142,22 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
   if (threadIdx.x == 0) {
     a.out_tok[row] = tok;
     if (c.draw && a.rng) a.rng[row] = rng;
+    join_history(a, row, tok);
+  }
+}
+
+// hist_bits[b] = the ids in [0, V) of row b's CSR history (sampling.cpp:24).
+__global__ __launch_bounds__(NT) void k_hist_bits_init(const int32_t* ids, const int64_t* off, int V,
+                                                       uint32_t* bits) {
+  const int row = blockIdx.x;
+  const int W = hist_words(V);
+  uint32_t* b = bits + (int64_t)row * W;
+  for (int w = threadIdx.x; w < W; w += NT) b[w] = 0u;
+  __syncthreads();
+  if (!ids) return;
+  for (int64_t j = off[row] + threadIdx.x; j < off[row + 1]; j += NT) {
+    const int id = ids[j];
+    if (id >= 0 && id < V) atomicOr(&b[id >> 5], 1u << (id & 31));
   }
 }
 
@@ -219,6 +253,14 @@ size_t rows_lds_bytes(int V) {
 size_t stream_lds_bytes(int V, int) { return rows_lds_bytes(V); }
 
 size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
+
+hipError_t launch_hist_bits_init(const int32_t* ids, const int64_t* off, int n_rows, int V, uint32_t* bits,
+                                 hipStream_t s) {
+  if (n_rows <= 0) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_hist_bits_init, dim3(n_rows), dim3(NT), 0, s, ids, off, V, bits);
+  return hipGetLastError();
+}
 
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;

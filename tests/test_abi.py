@@ -43,6 +43,7 @@ def test_null_context_is_einval():
     assert L.c4s_sample_rows(None, None, None) == c4s.EINVAL
     assert L.c4s_sample_stream(None, None, None) == c4s.EINVAL
     assert L.c4s_lmhead(None, None, None) == c4s.EINVAL
+    assert L.c4s_hist_bits_init(None, None, None, 0, 0, None, None) == c4s.EINVAL
     v = np.zeros(4, np.float32)
     assert L.c4s_host_top_k(None, v.ctypes.data, 4, 2) == c4s.EINVAL
     assert L.c4s_create(0, None) == c4s.EINVAL
@@ -69,3 +70,25 @@ def test_cpp_mirror_exports_reference_signatures():
                 "c4::t2s::sampling::top_p(std::vector<float, std::allocator<float> >&, float, int)",
                 "c4::t2s::sampling::argmax(std::vector<float, std::allocator<float> > const&)"]:
         assert sig in out, sig
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """The binding's struct layouts (size, every field's offset) equal what a C
+    compiler makes of the public header."""
+    structs = {"c4s_rows": c4s.Rows, "c4s_stream": c4s.Stream, "c4s_head": c4s.Head}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{c4s.HEADER}"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(src)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, got):
+        cname, what, val = line.split()
+        py = structs[cname]
+        want = C.sizeof(py) if what == "size" else getattr(py, what).offset
+        assert int(val) == want, (cname, what, int(val), want)
