@@ -124,6 +124,27 @@ def test_stream_overlapped_chunks(orc, gpu_ctx):
     assert np.array_equal(stoks, toks) and np.array_equal(srng, rng)
 
 
+@pytest.mark.parametrize("rows,steps", [(80, 260), (81, 260), (1, 300)])
+def test_stream_row_counts(orc, gpu_ctx, rows, steps):
+    """Row counts around the overlapped stream's limit on a 256-CU device (80
+    rows: chains and scans on their CU sets; 81: one chunk on every CU) and a
+    single row, every row mode, against the oracle."""
+    V = 8194
+    p = _mixed_params(5151 + rows, rows, V)
+    x = W.batch64_logits(5152 + rows, steps, rows, V)
+    stop = V - 1
+    for s, r in [(steps - 1, 0), (100, rows - 1), (200, rows // 2)]:
+        x[s, r, stop] = 80.0
+    print(f"stream V={V} rows={rows} steps={steps}", flush=True)
+    toks, rng, st = run_stream(gpu_ctx, p, x, stop_token=stop)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
+                                    p["top_p"], p["pen"], p["do_sample"], p["rng"], stop_token=stop,
+                                    n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
+    assert np.array_equal(rng, orng)
+
+
 def test_stream_stop_token_and_greedy(orc, gpu_ctx):
     steps, rows, V = 40, 16, 2000
     p = W.batch64_params(seed=9, rows=rows, V=V)
