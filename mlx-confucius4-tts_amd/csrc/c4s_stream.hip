@@ -906,13 +906,16 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const int n = h.n;
   const float ninf = neg_inf();
   const bool v = lane < n;
-  const uint64_t e = v ? sum[lane] : 0ull;
-  const float m32 = v ? reinterpret_cast<const float*>(sum + kYW)[lane] : 0.0f;
+  // reads unconditional and in bounds (entry and bitmap word, raw value, issued together)
+  const uint64_t e = sum[lane];
+  const float m32 = reinterpret_cast<const float*>(sum + kYW)[lane];
   const int id = v ? ent_id(e) : 0;
-  const bool hit = c.pen_on && v && bit_of(bmN, id);
+  const uint32_t bw = bmN[id >> 5];
+  const float xr = val[id];
+  const bool hit = c.pen_on && v && ((bw >> (id & 31)) & 1u);
   // a drawn id is never in H0: its value is the raw one (the penalty and the
   // temperature are monotone, so the largest penalised hit comes from the largest raw one)
-  const float hraw = (c.pen_on && hit) ? val[id] : ninf;
+  const float hraw = hit ? xr : ninf;
   const bool un = v && !hit;
   const uint64_t ub = __ballot(un);
   const int nu = __popcll(ub);
@@ -1116,18 +1119,30 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   bool un[K];
   uint32_t cnt = 0;
   float hraw = ninf;
+  // All reads unconditional, from addresses that are always in bounds (list
+  // positions below K * 64 <= kListLarge; id 0 for positions past n), so that
+  // the four entries' reads go out together: entries, then bitmap words and
+  // raw values. A drawn id is never in H0: its value is the raw one.
+  int id[K];
+  uint32_t bw[K];
+  float xr[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    e[i] = sum[p0 + i];
+    mk[i] = ly[p0 + i];
+  }
+#pragma unroll
+  for (int i = 0; i < K; ++i) id[i] = (p0 + i < n) ? ent_id(e[i]) : 0;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    bw[i] = bmN[id[i] >> 5];
+    xr[i] = val[id[i]];
+  }
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     const bool v = p0 + i < n;
-    e[i] = v ? sum[p0 + i] : 0ull;
-    mk[i] = v ? ly[p0 + i] : 0.0f;
-    const int id = v ? ent_id(e[i]) : 0;
-    const bool hit = c.pen_on & v & bit_of(bmN, id);
-    // a drawn id is never in H0: its value is the raw one (read without a branch)
-    if (c.pen_on) {
-      const float x = val[id];
-      hraw = hit ? fmaxf(hraw, x) : hraw;
-    }
+    const bool hit = c.pen_on & v & (((bw[i] >> (id[i] & 31)) & 1u) != 0u);
+    hraw = hit ? fmaxf(hraw, xr[i]) : hraw;
     un[i] = v & !hit;
     z[i] = un[i] ? kfloat(ent_key(e[i])) : ninf;
     cnt += un[i] ? 1u : 0u;
@@ -1227,13 +1242,11 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   // exact, then replayed.
   const int np = min(n, K * kWave);
 #pragma unroll
-  for (int i = 0; i < K; ++i) {
-    if (p0 + i < np) {
-      const int pp = (int)((pl >> (8 * i)) & 255u);
-      cs.lm[pp] = mk[i];
-      cs.lz[pp] = z[i];
-      cs.lid[pp] = (un[i] && rk[i] < q) ? ent_id(e[i]) : -1;
-    }
+  for (int i = 0; i < K; ++i) {   // positions past np write the trash entry
+    const int pp = (p0 + i < np) ? (int)((pl >> (8 * i)) & 255u) : kListLarge;
+    cs.lm[pp] = mk[i];
+    cs.lz[pp] = z[i];
+    cs.lid[pp] = (un[i] && rk[i] < q) ? ent_id(e[i]) : -1;
   }
   wave_sync();
   C4S_PHASE(11);
@@ -1244,7 +1257,8 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     const int pp = K * lane + i;
     pm[i] = cs.lm[pp];
     pz[i] = cs.lz[pp];
-    pid[i] = pp < np ? cs.lid[pp] : -1;
+    const int rid = cs.lid[pp];
+    pid[i] = pp < np ? rid : -1;
   }
   C4S_PHASE(8);
   auto draw = [&](bool exact_only, double eps_add) __attribute__((always_inline)) -> int {
