@@ -827,10 +827,19 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   const int nchunk = h.nchunk;
   double cv[4];
   double cs_l = 0.0;
+  // chunk words read unconditionally (in bounds: index clamped), then selected
+  uint64_t cw[4];
+  double cd[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int cr = min(4 * lane + i, kMaxChunks - 1);
+    cw[i] = sum[kChunkW + cr];
+    cd[i] = cdelta[cr];
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ci = 4 * lane + i;
-    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)sum[kChunkW + ci]) - cdelta[ci] : 0.0;
+    cv[i] = (ci < nchunk) ? __longlong_as_double((long long)cw[i]) - cd[i] : 0.0;
     cs_l += cv[i];
   }
   const double r = u * S;
@@ -853,16 +862,19 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   C4S_PHASE(13);
   const int lo = cstar == 0 ? 0 : h.head + kChunkIds * cstar;
   const int hi = (cstar == nchunk - 1) ? V : h.head + kChunkIds * (cstar + 1);
-  double ea = 0.0, eb = 0.0;
   const int ia = lo + lane, ib = lo + kWave + lane;
-  auto mass_at = [&](int id) -> double {
-    const float x = val[id];
-    const float y = (c.pen_on && (bit_of(bmH0, id) || bit_of(bmN, id))) ? pen_exact(x, c.pen) : x;
+  // the chunk's values and bitmap words read unconditionally (ids clamped into
+  // the chunk), so that both reads of each id go out together
+  const int ja = min(ia, hi - 1), jb = min(ib, hi - 1);
+  const float xa = val[ja], xb = val[jb];
+  const uint32_t ha = bmH0[ja >> 5] | bmN[ja >> 5], hb = bmH0[jb >> 5] | bmN[jb >> 5];
+  auto mass_of = [&](float x, uint32_t hw, int id) -> double {
+    const float y = (c.pen_on && ((hw >> (id & 31)) & 1u)) ? pen_exact(x, c.pen) : x;
     const float z = c.temp_on ? y / c.temp : y;
     return (z == ninf) ? 0.0 : exp((double)(z - mt));
   };
-  if (ia < hi) ea = mass_at(ia);
-  if (ib < hi) eb = mass_at(ib);
+  const double ea = ia < hi ? mass_of(xa, ha, ja) : 0.0;
+  const double eb = ib < hi ? mass_of(xb, hb, jb) : 0.0;
   C4S_PHASE(14);
   const double sa = wave_scan_f64(ea) + pstar;
   const double ta = readlane_f64(sa, kWave - 1);
