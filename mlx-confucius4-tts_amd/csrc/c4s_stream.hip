@@ -2181,7 +2181,8 @@ __device__ __forceinline__ double listed_corrections(const float* val, const int
   double dl = 0.0, ell = 0.0;
   for (int j = lane; j < n; j += 2 * kWave) {
     const bool v1 = j + kWave < n;
-    const int i0 = list[j], i1 = v1 ? list[j + kWave] : i0;
+    const int i0 = list[j], i1r = list[min(j + kWave, kDrawnList - 1)];   // both reads together
+    const int i1 = v1 ? i1r : i0;
     const float x0 = val[i0], x1 = val[i1];
     float e00, e01, e10, e11;
     const float a0 = mass_approx(x0, mk, e00), b0 = mass_approx(pen_approx(x0, c.pen, rpen), mk, e01);
@@ -2306,6 +2307,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
   for (; s < s_end; ++s) {
     const int par = s & 1;
     const uint32_t* bmN = bmNb[par];
+    int sflag = 0, stok = -1;   // the step's outcome, read after its barrier
     // Attempt 0: wave 0 decides with the fp32 corrections while the helpers
     // prepare step s+1. Attempt 1 (a decision inside their error bound): all
     // four wavefronts compute the exact corrections of step s, wave 0 decides
@@ -2331,12 +2333,13 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
         const SumHdr h = hdr_from(sw);
         double ds, de;
         double* cd;
+        const float xprev = val[tprev >= 0 ? tprev : 0];   // read with the header words
         if (attempt == 0) {
           cd = ps.cdelta[par];
           ds = ps.wd[par][0] + ps.wd[par][1] + ps.wd[par][2];
           de = ps.we[par][0] + ps.we[par][1] + ps.we[par][2];
           if (tprev >= 0 && !(h.flags & 1u)) {   // step s-1's token, not in the helpers' sums
-            const float x = val[tprev];
+            const float x = xprev;
             const MassCoef mk = mass_coef(c, h.m0);
             float e0, e1;
             const float m1 = mass_approx(x, mk, e0);
@@ -2421,9 +2424,11 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
       lds_barrier();
       C4S_PHASE(3);
       C4S_HELPER_PHASE(4);
-      if (ps.flag[par] != 2) break;
+      sflag = ps.flag[par];   // read together with the token
+      stok = ps.tok[par];
+      if (sflag != 2) break;
     }
-    if (!ps.flag[par]) {
+    if (!sflag) {
       // text2semantic.cpp:142-166 on the whole staged row: penalty over H0 and
       // the stream's ids (disjoint sets, so each id once), then the chain.
       rng = ps.rng;
@@ -2454,8 +2459,9 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
       }
       tprev = (int)readlane_u32((uint32_t)tprev, 0);
       __syncthreads();
+      stok = ps.tok[par];
     }
-    if (ps.tok[par] == a.stop_token) {
+    if (stok == a.stop_token) {
       done = true;
       ++s;
       break;
