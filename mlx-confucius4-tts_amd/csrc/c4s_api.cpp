@@ -61,7 +61,7 @@ constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's stat
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
 // Chunks of the overlapped stream: the first is short (its scan is not
-// hidden), each next one 1.5 times longer (its scan, on its share of the CUs, must end
+// hidden), each next one 4/3 times longer (its scan, on its share of the CUs, must end
 // before the chain of the previous one), up to kOverlapChunk steps.
 constexpr int kOverlapFirst = 64;
 constexpr int kOverlapChunk = 256;
@@ -421,7 +421,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   if (e0 != hipSuccess) return hip_fail(ctx, e0, "sample_stream scan stream");
   int last_side = -1;   // buffer of the last chunk whose full-vocabulary chain ran on the side stream
   for (int s0 = 0, ci = 0, len = overlap ? kOverlapFirst : chunk; s0 < a.n_steps;
-       s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 2 : chunk)) {
+       s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 3 : chunk)) {
     const int buf = ci & 1;
     const hipStream_t scan_on = (overlap && ci > 0) ? ctx->scan_m : ctx->scan_s;
     c4s::StreamWs w{};

@@ -94,10 +94,9 @@ def test_stream_two_phase_all_modes(orc, gpu_ctx, V, rows, steps):
 
 
 def test_stream_overlapped_chunks(orc, gpu_ctx):
-    """A stream long enough for chunks of 128 steps whose scans run beside the
+    """A stream long enough for several chunks whose scans run beside the
     previous chunk's chains on their own CUs: every row mode, stop tokens
-    planted in the second and third chunks, against the oracle and the
-    single-kernel stream."""
+    planted in later chunks, against the oracle and the single-kernel stream."""
     steps, rows, V = 300, 48, 8194
     p = _mixed_params(4242, rows, V)
     x = W.batch64_logits(4243, steps, rows, V)
