@@ -505,24 +505,33 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
         if (lane < kCandCap / 32) (wv ? sh.fpre : sh.lpre)[lane] = inc - pc;
       }
       __syncthreads();
-      if (masses && t < n) {
-        const int ci = ent_rank(srt[t]);
-        const uint32_t pw = sh.fpre[ci >> 5] + (uint32_t)__popc(sh.fmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
-        reinterpret_cast<uint8_t*>(sh.place4)[t] = (uint8_t)pw;   // to the summary as words below
-      }
-      for (int i = t; i < n; i += NTA) {
-        const uint64_t e = srt[i];
-        const int ci = ent_rank(e);
-        const uint32_t lr = sh.lpre[ci >> 5] + (uint32_t)__popc(sh.lmark[ci >> 5] & ((1u << (ci & 31)) - 1u));
-        lst[i] = (e & ~1023ull) | lr;
+      // Entries t and t + NTA (n <= 2 NTA): every LDS read first, at clamped
+      // positions, so that each dependent group goes out together.
+      static_assert(kListLarge <= 2 * NTA, "two list entries a thread");
+      const bool v0 = t < n, v1 = t + NTA < n;
+      const uint64_t e0 = srt[v0 ? t : 0], e1 = srt[v1 ? t + NTA : 0];
+      const int c0 = ent_rank(e0), c1 = ent_rank(e1);
+      const uint32_t below0 = (1u << (c0 & 31)) - 1u, below1 = (1u << (c1 & 31)) - 1u;
+      const uint32_t lp0 = sh.lpre[c0 >> 5], lk0 = sh.lmark[c0 >> 5];
+      const uint32_t lp1 = sh.lpre[c1 >> 5], lk1 = sh.lmark[c1 >> 5];
+      const uint32_t fp0 = sh.fpre[c0 >> 5], fk0 = sh.fmark[c0 >> 5];
+      const float y0 = sh.candy[c0], y1 = sh.candy[c1];
+      if (masses && v0)   // the place among the first NTA, to the summary as words below
+        reinterpret_cast<uint8_t*>(sh.place4)[t] = (uint8_t)(fp0 + (uint32_t)__popc(fk0 & below0));
+      if (v0) {
+        lst[t] = (e0 & ~1023ull) | (lp0 + (uint32_t)__popc(lk0 & below0));
         if (masses) {
-          const float m = (float)exp((double)(kfloat(ent_key(e)) - zmax));
-          ly[i] = m;
-          if (i < kLanesHint) top_mass += (double)m;   // wave 0, first pass
-          if (i < NTA) first_mass = (double)m;
+          const float m = (float)exp((double)(kfloat(ent_key(e0)) - zmax));
+          ly[t] = m;
+          if (t < kLanesHint) top_mass += (double)m;   // wave 0
+          first_mass = (double)m;
         } else {
-          ly[i] = sh.candy[ci];
+          ly[t] = y0;
         }
+      }
+      if (v1) {
+        lst[t + NTA] = (e1 & ~1023ull) | (lp1 + (uint32_t)__popc(lk1 & below1));
+        ly[t + NTA] = masses ? (float)exp((double)(kfloat(ent_key(e1)) - zmax)) : y1;
       }
       if (masses) {
         if (wv == 0) top_mass = wave_sum_f64(top_mass);
@@ -542,14 +551,19 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       const bool exm = exact_masses(c);
       nchunk = max(1, (rs.nq + 15) >> 4);
       double el = 0.0;
+      // the quads' H0 bits first, all reads at once (quad index clamped into the row)
+      uint32_t hq[NQ];
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int id = rs.head + 4 * max(0, min(t + NTA * j, rs.nq - 1));
+        hq[j] = (uint32_t)(((uint64_t)sh.bm[id >> 5] | ((uint64_t)sh.bm[(id >> 5) + 1] << 32)) >> (id & 31)) & 15u;
+      }
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
         const int q = t + NTA * j;
         double qd = 0.0;
         if (q < rs.nq) {
-          const int id = rs.head + 4 * q;
-          const uint32_t hb = (uint32_t)(((uint64_t)sh.bm[id >> 5] | ((uint64_t)sh.bm[(id >> 5) + 1] << 32)) >>
-                                         (id & 31)) & 15u;
+          const uint32_t hb = hq[j];
           const bool pon = c.pen_on;
           if (exm) {
             qd = mass_exact((pon && (hb & 1u)) ? pen_exact(xv[j].x, pen) : xv[j].x, c, m0) +
