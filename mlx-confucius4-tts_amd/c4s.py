@@ -199,12 +199,12 @@ class Context:
 
     def lmhead_sample(self, hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k,
                       top_p, pen, rng, out_token, logits=None, do_sample=None, out_masked=None,
-                      out_stats=None, eps=1e-5, stream=None):
+                      out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1):
         h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
         r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp),
                  top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
                  rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
-                 out_stats=_p(out_stats), mode=MODE_CHAIN)
+                 out_stats=_p(out_stats), mode=MODE_CHAIN, hist_bits=_p(hist_bits), stop_token=stop_token)
         self._check(lib().c4s_lmhead_sample(self._h, C.byref(h), C.byref(r), _stream_handle(stream)),
                     "lmhead_sample")
 

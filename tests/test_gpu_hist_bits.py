@@ -70,3 +70,54 @@ def test_step_loop_with_hist_bits(orc, gpu_ctx, V, R, T):
         h0 = p["hist_ids"][p["hist_off"][r]:p["hist_off"][r + 1]]
         drawn = [t for t in got[:, r] if t >= 0 and t != stop]
         assert np.array_equal(fin[r], _words(list(h0) + drawn, V)), r
+
+
+def test_hist_bits_bf16_and_lmhead_match_csr(orc, gpu_ctx):
+    """The kept set gives the same tokens, masked rows and RNG states as the CSR
+    history it was filled from: bf16 logits, and the fused LM head + chain."""
+    import torch
+    b = W.batch64(seed=23)
+    R, V = b.n_rows, b.logits.shape[1]
+    bits = torch.zeros((R, (V + 31) // 32), dtype=torch.int32, device="cuda")
+    ids, off = dev(b.hist_ids, torch), dev(b.hist_off, torch)
+    gpu_ctx.hist_bits_init(ids, off, R, V, bits)
+    x16 = dev(W.f32_to_bf16_bits(b.logits), torch)
+    args = [dev(getattr(b, k), torch) for k in ("temp", "top_k", "top_p", "pen")]
+    outs = []
+    for use_bits in (False, True):
+        rng = dev(b.rng, torch)
+        tok = torch.full((R,), -7, dtype=torch.int32, device="cuda")
+        m = torch.zeros((R, V), dtype=torch.float32, device="cuda")
+        print("bf16 rows, history", "set" if use_bits else "CSR", flush=True)
+        gpu_ctx.sample_rows(x16, None if use_bits else ids, None if use_bits else off, *args, rng, tok,
+                            do_sample=dev(b.do_sample, torch), out_masked=m,
+                            hist_bits=bits if use_bits else None, stop_token=-1)
+        torch.cuda.synchronize()
+        outs.append((tok.cpu().numpy(), rng.cpu().numpy(), m.cpu().numpy().view(np.uint32)))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(outs[0][2], outs[1][2])
+
+    head, p = W.lmhead(seed=5)
+    M = head.hidden.shape[0]
+    hb = torch.zeros((M, (V + 31) // 32), dtype=torch.int32, device="cuda")
+    hids, hoff = dev(p["hist_ids"], torch), dev(p["hist_off"], torch)
+    gpu_ctx.hist_bits_init(hids, hoff, M, V, hb)
+    res = []
+    for use_bits in (False, True):
+        rng = dev(p["rng"], torch)
+        tok = torch.full((M,), -7, dtype=torch.int32, device="cuda")
+        print("lmhead_sample, history", "set" if use_bits else "CSR", flush=True)
+        gpu_ctx.lmhead_sample(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch),
+                              dev(head.weight, torch), dev(head.bias, torch), None if use_bits else hids,
+                              None if use_bits else hoff, dev(p["temp"], torch), dev(p["top_k"], torch),
+                              dev(p["top_p"], torch), dev(p["pen"], torch), rng, tok,
+                              do_sample=dev(p["do_sample"], torch), hist_bits=hb if use_bits else None)
+        torch.cuda.synchronize()
+        res.append((tok.cpu().numpy(), rng.cpu().numpy()))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+    # the tokens joined the set: it now holds the history and each row's token
+    fin = hb.cpu().numpy().view(np.uint32)
+    for r in range(M):
+        h0 = p["hist_ids"][p["hist_off"][r]:p["hist_off"][r + 1]]
+        assert np.array_equal(fin[r], _words(list(h0) + [res[1][0][r]], V)), r
