@@ -160,7 +160,11 @@ const char* c4s_version(void);
 
 /* text2semantic.cpp:303-337 (batched) / :142-166 (single row). */
 int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream);
-/* text2semantic.cpp:296-337 over n_steps with precomputed logits. */
+/* text2semantic.cpp:296-337 over n_steps with precomputed logits. Queued on
+ * `stream` like the other entry points, except that with the overlapped
+ * schedule (rows at most the chains' CUs, 256 steps or more) the calling
+ * thread first waits until the previous such call of this context has ended
+ * on the GPU: one call in flight per context. */
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream);
 /* text2semantic.cpp:118-121 / :283-286 (head(cur)). */
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);

@@ -61,8 +61,9 @@ constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's stat
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
 // Chunks of the overlapped stream: the first is short (its scan is not
-// hidden), each next one 4/3 times longer (its scan, on its share of the CUs, must end
-// before the chain of the previous one), up to kOverlapChunk steps.
+// hidden), each next one 6/5 times longer (its scan, on its share of the CUs, must end
+// before the chain of the previous one: the scan takes about 2.9 us a step
+// there, the row chain 3.55), up to kOverlapChunk steps.
 constexpr int kOverlapFirst = 64;
 constexpr int kOverlapChunk = 256;
 constexpr int kOverlapStepsPerGroup = 2;   // more, shorter scan workgroups balance a short chunk
@@ -415,13 +416,23 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   };
   const hipStream_t chain_on = overlap ? ctx->chain_m : hs;
   const hipStream_t side_on = overlap ? ctx->side_m : ctx->side;
+  // One overlapped call in flight per context: the host waits for the
+  // previous one to end before it queues this one. A call's packets queued
+  // behind the running one (its first scan's wait at the head of a queue)
+  // slowed the running call's kernels by about 7% (dispatches of the short
+  // kernels 5 -> 32 us); queuing takes about 1.5 ms of the 4 ms call, so the
+  // first scan still starts within tens of microseconds.
+  if (overlap) {
+    hipError_t ew = hipEventSynchronize(ctx->ev_done);
+    if (ew != hipSuccess) return hip_fail(ctx, ew, "sample_stream previous call");
+  }
   hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
   if (e0 == hipSuccess) e0 = hipStreamWaitEvent(ctx->scan_s, ctx->ev_start, 0);
   if (e0 == hipSuccess && overlap) e0 = hipStreamWaitEvent(chain_on, ctx->ev_start, 0);
   if (e0 != hipSuccess) return hip_fail(ctx, e0, "sample_stream scan stream");
   int last_side = -1;   // buffer of the last chunk whose full-vocabulary chain ran on the side stream
   for (int s0 = 0, ci = 0, len = overlap ? kOverlapFirst : chunk; s0 < a.n_steps;
-       s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 3 : chunk)) {
+       s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 5 : chunk)) {
     const int buf = ci & 1;
     const hipStream_t scan_on = (overlap && ci > 0) ? ctx->scan_m : ctx->scan_s;
     c4s::StreamWs w{};
