@@ -66,7 +66,7 @@ constexpr int kScanStepsPerGroup = 8;
 // there, the row chain 3.55), up to kOverlapChunk steps.
 constexpr int kOverlapFirst = 64;
 constexpr int kOverlapChunk = 256;
-constexpr int kOverlapStepsPerGroup = 2;   // more, shorter scan workgroups balance a short chunk
+constexpr int kOverlapStepsPerGroup = 1;   // one step a scan workgroup: the shortest chunk ends on time
 // Of every 32 CUs, the chains' shares in the overlapped stream: the
 // full-vocabulary chain (a workgroup holds a whole CU's LDS) and the list
 // chain (two workgroups a CU); the scans take the rest.
