@@ -187,6 +187,47 @@ def main():
                 "hist_bits_achieved_GBps": round(bits_bytes / (bits_us * 1e-6) / 1e9, 1)}
     log(f"per-call: {call_us:.2f} us per 64-row step ({bits_us:.2f} us with the history kept as a set)")
 
+    # ---- LM head (LN -> bf16 MFMA GEMM + bias) alone and fused with the chain, 64 rows x D=1280 ----
+    D = 1280
+    gh = torch.Generator(device=dev)
+    gh.manual_seed(77)
+    hidden = torch.randn((R, D), generator=gh, device=dev).to(torch.bfloat16)
+    weight = (0.02 * torch.randn((V, D), generator=gh, device=dev)).to(torch.bfloat16)
+    gamma = 1.0 + 0.02 * torch.randn(D, generator=gh, device=dev)
+    beta = 0.02 * torch.randn(D, generator=gh, device=dev)
+    bias = 0.02 * torch.randn(V, generator=gh, device=dev)
+    head_out = torch.empty((R, V), dtype=torch.float32, device=dev)
+    rng3 = rng0.clone()
+
+    def head_only():
+        ctx.lmhead(hidden, gamma, beta, weight, bias, head_out)
+
+    def head_sample():
+        ctx.lmhead_sample(hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k, top_p, pen,
+                          rng3, tok1, logits=head_out, do_sample=do_sample)
+
+    head_us = {}
+    for name, fn in (("lmhead", head_only), ("lmhead_sample", head_sample)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n_calls):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        head_us[name] = e0.elapsed_time(e1) * 1e3 / n_calls
+    # weight, hidden, bias, gamma/beta read once; logits written once
+    head_bytes = 2 * V * D + 2 * R * D + 4 * V + 8 * D + 4 * R * V
+    head_gbs = head_bytes / (head_us["lmhead"] * 1e-6) / 1e9
+    per_call.update({"lmhead_us_per_call": round(head_us["lmhead"], 3),
+                     "lmhead_achieved_GBps": round(head_gbs, 1),
+                     "lmhead_frac_of_hbm_peak": round(head_gbs / PEAK_HBM_GBS, 4),
+                     "lmhead_sample_us_per_call": round(head_us["lmhead_sample"], 3)})
+    log(f"lm head: {head_us['lmhead']:.2f} us ({head_gbs:.0f} GB/s); with the chain "
+        f"{head_us['lmhead_sample']:.2f} us per 64-row step")
+    del hidden, weight, head_out
+
     # ---- HBM probe ------------------------------------------------------------------------
     nb = 1 << 30
     src = torch.empty(nb // 4, dtype=torch.float32, device=dev).fill_(1.0)

@@ -19,7 +19,7 @@ ATOL = 2e-3
 RTOL = 1e-3
 
 
-@pytest.mark.parametrize("M,D,V", [(64, 1280, 8194), (5, 64, 100), (70, 256, 1000)])
+@pytest.mark.parametrize("M,D,V", [(64, 1280, 8194), (5, 64, 100), (70, 256, 1000), (3, 2080, 300), (9, 4096, 130)])
 def test_lmhead_logits(orc, gpu_ctx, M, D, V):
     import torch
     head, _ = W.lmhead(seed=M + D, M=M, D=D, V=V)
