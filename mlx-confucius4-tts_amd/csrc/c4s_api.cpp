@@ -39,8 +39,9 @@ struct c4s_ctx {
   // third stream: the scan of the next chunk of steps beside the chain of this one
   hipStream_t scan_s = nullptr;
   hipEvent_t ev_start = nullptr;
-  hipEvent_t ev_scan[2] = {nullptr, nullptr}, ev_chain[2] = {nullptr, nullptr};
-  hipEvent_t ev_side[2] = {nullptr, nullptr};   // full-vocabulary chain of a chunk done, by buffer
+  // by summary buffer: its scan done, its list chain done, its full-vocabulary chain done
+  hipEvent_t ev_scan[3] = {nullptr, nullptr, nullptr}, ev_chain[3] = {nullptr, nullptr, nullptr};
+  hipEvent_t ev_side[3] = {nullptr, nullptr, nullptr};
   // Overlapped stream: the scan and the chains on disjoint sets of CUs (half
   // of every 32 CUs for the chains), created at first use.
   int n_cus = 0;
@@ -66,6 +67,10 @@ constexpr int kScanStepsPerGroup = 8;
 // there, the row chain 3.55), up to kOverlapChunk steps.
 constexpr int kOverlapFirst = 64;
 constexpr int kOverlapChunk = 256;
+// Summary buffers of the overlapped stream: the scans depend on nothing but
+// the inputs, so with three buffers a scan waits only for the chains of the
+// chunk three back and runs ahead of the chains instead of in step with them.
+constexpr int kOverlapBufs = 3;
 constexpr int kOverlapStepsPerGroup = 1;   // one step a scan workgroup: the shortest chunk ends on time
 // Of every 32 CUs, the chains' shares in the overlapped stream: the
 // full-vocabulary chain (a workgroup holds a whole CU's LDS) and the list
@@ -225,10 +230,13 @@ int c4s_create(int device, c4s_ctx** out) {
       hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_scan[0], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_scan[1], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_scan[2], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_chain[0], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_chain[1], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_chain[2], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_side[0], hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->ev_side[1], hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ctx->ev_side[1], hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->ev_side[2], hipEventDisableTiming) != hipSuccess) {
     c4s_destroy(ctx);
     return C4S_EHIP;
   }
@@ -251,8 +259,9 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (ctx->scan_s) (void)hipStreamDestroy(ctx->scan_s);
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamDestroy(st);
-  for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1],
-                        ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_done, ctx->ev_side[0], ctx->ev_side[1]})
+  for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1], ctx->ev_scan[2],
+                        ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_chain[2], ctx->ev_done, ctx->ev_side[0],
+                        ctx->ev_side[1], ctx->ev_side[2]})
     if (ev) (void)hipEventDestroy(ev);
   delete ctx;
   return C4S_OK;
@@ -372,20 +381,20 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   }
   // Steps go in chunks; the chain carries its per-row state from chunk to
   // chunk. Overlapped (rows at most the chains' CUs, steps for four
-  // chunks or more): the scan of chunk c+1 runs on its own CUs beside the chain of chunk
-  // c, summaries are double-buffered and a scan waits for the chain that last
-  // read its buffer; the first chunk's scan, which nothing hides, runs on every
-  // CU. Otherwise the whole stream is one chunk where the budget allows, each
-  // phase on every CU.
+  // chunks or more): the scans of later chunks run on their own CUs beside the
+  // chains, summaries rotate through kOverlapBufs buffers and a scan waits for
+  // the chains that last read its buffer; the first chunk's scan, which nothing
+  // hides, runs on every CU. Otherwise the whole stream is one chunk where the
+  // budget allows (else two buffers), each phase on every CU.
   const size_t per_step = (size_t)a.n_rows * c4s::kSumStride;
   const bool overlap = a.n_rows <= row_cus(ctx) + list_cus(ctx) && a.n_steps >= 4 * kOverlapFirst &&
-                       (size_t)kOverlapChunk * 2 * per_step <= kSumBudget && cu_split(ctx);
+                       (size_t)kOverlapChunk * kOverlapBufs * per_step <= kSumBudget && cu_split(ctx);
   size_t chunk_sz = std::min<size_t>((size_t)a.n_steps, kSumBudget / per_step);
   if (overlap) chunk_sz = std::min<size_t>((size_t)a.n_steps, kOverlapChunk);
   else if (chunk_sz < (size_t)a.n_steps) chunk_sz = std::min(chunk_sz, kSumBudget / 2 / per_step);   // two buffers
   const int chunk = (int)std::max<size_t>(1, chunk_sz);   // the longest chunk
   const size_t chunk_bytes = per_step * (size_t)chunk;
-  const int n_bufs = chunk < a.n_steps ? 2 : 1;
+  const int n_bufs = chunk >= a.n_steps ? 1 : overlap ? kOverlapBufs : 2;
   int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, (size_t)n_bufs * chunk_bytes, "stream summaries");
   if (rc) return rc;
   rc = ensure(ctx, &ctx->state_ws, &ctx->state_bytes, (size_t)a.n_rows * c4s::kStateWords * 4, "stream state");
@@ -433,7 +442,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   int last_side = -1;   // buffer of the last chunk whose full-vocabulary chain ran on the side stream
   for (int s0 = 0, ci = 0, len = overlap ? kOverlapFirst : chunk; s0 < a.n_steps;
        s0 += len, ++ci, len = std::min(chunk, overlap ? len + len / 5 : chunk)) {
-    const int buf = ci & 1;
+    const int buf = ci % n_bufs;
     const hipStream_t scan_on = (overlap && ci > 0) ? ctx->scan_m : ctx->scan_s;
     c4s::StreamWs w{};
     w.sum = static_cast<unsigned char*>(ctx->sum_ws) + (size_t)buf * chunk_bytes;
@@ -449,7 +458,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     hipError_t e = hipSuccess;
     if (overlap && ci == 1 && (e = hipStreamWaitEvent(scan_on, ctx->ev_scan[0], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
-    if (ci >= 2 && ((e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess ||
+    if (ci >= n_bufs && ((e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess ||
                     (pipelined && (e = hipStreamWaitEvent(scan_on, ctx->ev_side[buf], 0)) != hipSuccess)))
       return hip_fail(ctx, e, "sample_stream buffer reuse");
     e = c4s::launch_stream_scan(a, w, scan_on);
