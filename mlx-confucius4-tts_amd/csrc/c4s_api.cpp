@@ -431,8 +431,12 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // slowed the running call's kernels by about 7% (dispatches of the short
   // kernels 5 -> 32 us); queuing takes about 1.5 ms of the 4 ms call, so the
   // first scan still starts within tens of microseconds.
+  // (Not while the caller's stream is being captured into a graph: a host
+  // wait is not allowed there, and a graph's replays are ordered by its user.)
   if (overlap) {
-    hipError_t ew = hipEventSynchronize(ctx->ev_done);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t ew = hipStreamIsCapturing(hs, &cap);
+    if (ew == hipSuccess && cap == hipStreamCaptureStatusNone) ew = hipEventSynchronize(ctx->ev_done);
     if (ew != hipSuccess) return hip_fail(ctx, ew, "sample_stream previous call");
   }
   hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
