@@ -164,7 +164,8 @@ int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream);
  * `stream` like the other entry points, except that with the overlapped
  * schedule (rows at most the chains' CUs, 256 steps or more) the calling
  * thread first waits until the previous such call of this context has ended
- * on the GPU: one call in flight per context. */
+ * on the GPU (not while `stream` is being captured into a graph): one call in
+ * flight per context. */
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream);
 /* text2semantic.cpp:118-121 / :283-286 (head(cur)). */
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);
