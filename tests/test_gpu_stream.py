@@ -43,6 +43,38 @@ def test_stream_10k_rows_bit_exact(orc):
     ctx.close()
 
 
+def test_stream_bench_workload_bit_exact(orc, gpu_ctx):
+    """The whole headline workload: 64 rows x 1000 AR steps at V = 8194 with the
+    inputs the bench builds (batch-64 parameters of seed 2, logits drawn on the
+    device from seed 1002 with five spikes a row-step), 64,000 sampled rows
+    against the oracle, tokens and final RNG states bit for bit."""
+    import torch
+    T, R, V = 1000, 64, W.V_SEMANTIC
+    p = W.batch64_params(seed=2, rows=R, V=V)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1002)
+    logits = torch.randn((T, R, V), generator=g, device="cuda", dtype=torch.float32) * 3.0
+    spikes = torch.randint(0, V, (T, R, 5), generator=g, device="cuda")
+    logits.scatter_(2, spikes, 12.0)
+    out = torch.full((T, R), -9, dtype=torch.int32, device="cuda")
+    rng = dev(p["rng"], torch)
+    print("bench workload: gpu", flush=True)
+    gpu_ctx.sample_stream(logits, dev(p["hist_ids"], torch), dev(p["hist_off"], torch), dev(p["temp"], torch),
+                          dev(p["top_k"], torch), dev(p["top_p"], torch), dev(p["pen"], torch), rng, out,
+                          do_sample=dev(p["do_sample"], torch))
+    torch.cuda.synchronize()
+    toks, grng = out.cpu().numpy(), rng.cpu().numpy().view(np.uint64)
+    x = logits.cpu().numpy()
+    del logits
+    print("bench workload: oracle", flush=True)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"], p["top_p"],
+                                    p["pen"], p["do_sample"], p["rng"], n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first (step, row) {bad[:5].tolist()}"
+    assert np.array_equal(grng, orng)
+    assert toks.size == 64000 and (toks >= 0).all()
+
+
 def _mixed_params(seed, rows, V):
     """Every row mode of the two-phase stream: greedy, top-k (list), top-k > 64
     and penalty < 1 (exact every step), full vocabulary with p < 1, p = 1, p > 1
