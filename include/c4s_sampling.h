@@ -23,6 +23,11 @@
  *   - Device entry points are asynchronous on the given stream; the caller
  *     owns every input/output buffer (device memory); the context owns its
  *     workspace. A context is not thread-safe: use one per host thread.
+ *   - Workspaces grow on first use (hipMalloc, which synchronises the device).
+ *     c4s_sample_rows with vocab <= 12288 uses none. While the stream is being
+ *     captured into a graph a workspace never grows (C4S_EINVAL): make one call
+ *     of the same shape outside the capture first. Once a captured call used a
+ *     workspace, a later growth keeps the old buffer alive until c4s_destroy.
  *   - Input contract: logits are finite or -inf (no +inf/NaN), temperature is
  *     1, <= 0, or keeps logits/temperature finite.
  *   - top_p tie order: when the nucleus cut falls inside a group of equal
@@ -164,8 +169,8 @@ int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream);
  * `stream` like the other entry points, except that with the overlapped
  * schedule (rows at most the chains' CUs, 256 steps or more) the calling
  * thread first waits until the previous such call of this context has ended
- * on the GPU (not while `stream` is being captured into a graph): one call in
- * flight per context. */
+ * on the GPU: one call in flight per context. Not capturable: returns
+ * C4S_EINVAL while `stream` is being captured into a graph. */
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream);
 /* text2semantic.cpp:118-121 / :283-286 (head(cur)). */
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);

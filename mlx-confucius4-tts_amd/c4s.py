@@ -6,9 +6,11 @@ present: there is no CPU fallback in this package.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import re
+import weakref
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
@@ -127,6 +129,24 @@ class C4SError(RuntimeError):
     pass
 
 
+# Contexts still open when the interpreter exits are closed by an atexit hook:
+# Python runs atexit hooks before it tears down modules and before the C
+# runtime's exit handlers unload the HIP runtime (and, under a profiler, the
+# profiler's tool library), so c4s_destroy's stream syncs and frees still find
+# a live runtime. Leaving them to __del__ during module teardown would run
+# those HIP calls in whatever order the garbage collector picks.
+_live_contexts: "weakref.WeakSet[Context]" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_contexts() -> None:
+    for ctx in list(_live_contexts):
+        try:
+            ctx.close()
+        except Exception:
+            pass
+
+
 class Context:
     """One library context on one device (not thread-safe)."""
 
@@ -137,11 +157,13 @@ class Context:
             raise C4SError(f"c4s_create(device={device}) failed with code {rc} "
                            "(no gfx950 device visible?)")
         self.device = device
+        _live_contexts.add(self)
 
     def close(self):
         if self._h:
-            lib().c4s_destroy(self._h)
-            self._h = _vp()
+            h, self._h = self._h, _vp()
+            lib().c4s_destroy(h)
+        _live_contexts.discard(self)
 
     def __del__(self):
         try:

@@ -35,7 +35,6 @@ struct c4s_ctx {
   size_t state_bytes = 0;
   // second stream: the two fast chain kernels run side by side
   hipStream_t side = nullptr;
-  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   // third stream: the scan of the next chunk of steps beside the chain of this one
   hipStream_t scan_s = nullptr;
   hipEvent_t ev_start = nullptr;
@@ -51,6 +50,11 @@ struct c4s_ctx {
   // step segments of the pipelined row chain (rows without penalty)
   void* segres = nullptr;
   size_t segres_bytes = 0;
+  // Set once a call on a capturing stream used a workspace: from then on a
+  // workspace that grows is retired (freed at c4s_destroy) instead of freed,
+  // because a captured graph may still write the old buffer when replayed.
+  bool graph_used = false;
+  std::vector<void*> retired;
 };
 
 namespace {
@@ -77,7 +81,6 @@ constexpr int kOverlapStepsPerGroup = 1;   // one step a scan workgroup: the sho
 // chain (two workgroups a CU); the scans take the rest.
 constexpr int kRowCusPer32 = 6;
 constexpr int kListCusPer32 = 4;
-constexpr int kFastRounds = 3;
 constexpr int kMaxSegments = 8;   // step segments per row without penalty
 
 int fail(c4s_ctx* ctx, int code, const std::string& msg) {
@@ -102,13 +105,35 @@ struct DeviceGuard {
   }
 };
 
-int ensure(c4s_ctx* ctx, void** buf, size_t* have, size_t need, const char* what) {
-  if (need <= *have) return C4S_OK;
+bool is_capturing(hipStream_t s) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+}
+
+// Workspace of at least `need` bytes for a call queued on `s`. A workspace
+// never grows while `s` is being captured into a graph (allocation is not
+// allowed there): a first call of the same shape outside the capture sizes it.
+int ensure(c4s_ctx* ctx, void** buf, size_t* have, size_t need, const char* what, hipStream_t s) {
+  const bool cap = is_capturing(s);
+  if (need <= *have) {
+    if (cap) ctx->graph_used = true;
+    return C4S_OK;
+  }
+  if (cap)
+    return fail(ctx, C4S_EINVAL, std::string(what) +
+                                     ": the workspace would grow during graph capture; make one call of "
+                                     "this shape (or larger) outside the capture first");
   if (*buf) {
-    hipError_t e = hipFree(*buf);
-    *buf = nullptr;
-    *have = 0;
-    if (e != hipSuccess) return hip_fail(ctx, e, what);
+    if (ctx->graph_used) {   // a graph may still use it: keep it until c4s_destroy
+      ctx->retired.push_back(*buf);
+      *buf = nullptr;
+      *have = 0;
+    } else {
+      hipError_t e = hipFree(*buf);
+      *buf = nullptr;
+      *have = 0;
+      if (e != hipSuccess) return hip_fail(ctx, e, what);
+    }
   }
   hipError_t e = hipMalloc(buf, need);
   if (e != hipSuccess) {
@@ -188,7 +213,7 @@ int launch_rows_checked(c4s_ctx* ctx, const c4s_rows* r, hipStream_t s) {
   c4s::RowsArgs a = to_args(r);
   if (r->vocab > c4s::kLdsVocabMax) {
     const size_t per_row = pow2_at_least((size_t)r->vocab) * sizeof(uint32_t);
-    int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, per_row * (size_t)r->n_rows, "sort workspace");
+    int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, per_row * (size_t)r->n_rows, "sort workspace", s);
     if (rc) return rc;
     a.sort_ws = static_cast<uint32_t*>(ctx->ws);
     a.sort_ws_stride = (int64_t)(per_row / sizeof(uint32_t));
@@ -225,8 +250,6 @@ int c4s_create(int device, c4s_ctx** out) {
   if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->scan_s, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_start, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_scan[0], hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->ev_scan[1], hipEventDisableTiming) != hipSuccess ||
@@ -254,12 +277,13 @@ int c4s_destroy(c4s_ctx* ctx) {
     if (st) (void)hipStreamSynchronize(st);
   for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws, ctx->segres})
     if (p) (void)hipFree(p);
+  for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->scan_s) (void)hipStreamDestroy(ctx->scan_s);
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamDestroy(st);
-  for (hipEvent_t ev : {ctx->ev_fork, ctx->ev_join, ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1], ctx->ev_scan[2],
+  for (hipEvent_t ev : {ctx->ev_start, ctx->ev_scan[0], ctx->ev_scan[1], ctx->ev_scan[2],
                         ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_chain[2], ctx->ev_done, ctx->ev_side[0],
                         ctx->ev_side[1], ctx->ev_side[2]})
     if (ev) (void)hipEventDestroy(ev);
@@ -371,9 +395,16 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   const hipStream_t hs = static_cast<hipStream_t>(stream);
+  // The stream call waits on the host for the previous call and may grow its
+  // workspaces, so it is not capturable: a graph would also keep pointers to
+  // summary buffers that the next eager call reuses.
+  if (is_capturing(hs)) return fail(ctx, C4S_EINVAL, "sample_stream: not allowed while the stream is captured");
+  // The two-phase stream needs the pipelined full-vocabulary chain (three
+  // rows and summaries in LDS, V <= 8232); larger vocabularies, and callers
+  // that ask for it, take the single-kernel stream.
   const bool two_phase = !(st->flags & C4S_STREAM_SEQUENTIAL) &&
                          c4s::stream_chain_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit &&
-                         c4s::stream_rowk_lds_bytes(a.vocab) + kChainStaticLds <= kLdsLimit;
+                         c4s::stream_rowp_lds_bytes(a.vocab) + kRowPStaticLds <= kLdsLimit;
   if (!two_phase) {
     hipError_t e = c4s::launch_stream(a, hs);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream launch");
@@ -395,31 +426,22 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   const int chunk = (int)std::max<size_t>(1, chunk_sz);   // the longest chunk
   const size_t chunk_bytes = per_step * (size_t)chunk;
   const int n_bufs = chunk >= a.n_steps ? 1 : overlap ? kOverlapBufs : 2;
-  int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, (size_t)n_bufs * chunk_bytes, "stream summaries");
+  int rc = ensure(ctx, &ctx->sum_ws, &ctx->sum_bytes, (size_t)n_bufs * chunk_bytes, "stream summaries", hs);
   if (rc) return rc;
-  rc = ensure(ctx, &ctx->state_ws, &ctx->state_bytes, (size_t)a.n_rows * c4s::kStateWords * 4, "stream state");
+  rc = ensure(ctx, &ctx->state_ws, &ctx->state_bytes, (size_t)a.n_rows * c4s::kStateWords * 4, "stream state", hs);
   if (rc) return rc;
-  // Full-vocabulary rows: the pipelined chain (three rows and summaries in LDS)
-  // where it fits; its exact steps sort in a per-row global key buffer.
-  const bool pipelined = c4s::stream_rowp_lds_bytes(a.vocab) + kRowPStaticLds <= kLdsLimit;
+  // The chains' exact steps sort in a per-row global key buffer.
   const size_t sort_row = pow2_at_least((size_t)a.vocab) * sizeof(uint32_t);
-  if (pipelined) {
-    rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, sort_row * (size_t)a.n_rows, "sort workspace");
-    if (rc) return rc;
-  }
+  rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, sort_row * (size_t)a.n_rows, "sort workspace", hs);
+  if (rc) return rc;
   // Rows without penalty split their steps into segments, one workgroup each,
   // over the CUs the chains have (every workgroup of the pipelined chain
   // holds a CU's LDS).
-  const int nseg = pipelined ? std::max(2, std::min(kMaxSegments, (overlap ? row_cus(ctx) : ctx->n_cus) /
-                                                                     std::max(1, a.n_rows)))
-                             : 1;
-  if (nseg > 1) {
-    rc = ensure(ctx, &ctx->segres, &ctx->segres_bytes, (size_t)a.n_rows * nseg * 4 * sizeof(uint64_t),
-                "segment results");
-    if (rc) return rc;
-  }
+  const int nseg = std::max(2, std::min(kMaxSegments, (overlap ? row_cus(ctx) : ctx->n_cus) / std::max(1, a.n_rows)));
+  rc = ensure(ctx, &ctx->segres, &ctx->segres_bytes, (size_t)a.n_rows * nseg * 4 * sizeof(uint64_t),
+              "segment results", hs);
+  if (rc) return rc;
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
-    if (!pipelined) return c4s::launch_stream_rowk(a, w, on);
     hipError_t e = c4s::launch_stream_rowp(a, w, on);
     return e == hipSuccess ? c4s::launch_stream_segfix(a, w, on) : e;
   };
@@ -431,12 +453,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // slowed the running call's kernels by about 7% (dispatches of the short
   // kernels 5 -> 32 us); queuing takes about 1.5 ms of the 4 ms call, so the
   // first scan still starts within tens of microseconds.
-  // (Not while the caller's stream is being captured into a graph: a host
-  // wait is not allowed there, and a graph's replays are ordered by its user.)
   if (overlap) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    hipError_t ew = hipStreamIsCapturing(hs, &cap);
-    if (ew == hipSuccess && cap == hipStreamCaptureStatusNone) ew = hipEventSynchronize(ctx->ev_done);
+    const hipError_t ew = hipEventSynchronize(ctx->ev_done);
     if (ew != hipSuccess) return hip_fail(ctx, ew, "sample_stream previous call");
   }
   hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
@@ -454,64 +472,33 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
     w.s_begin = s0;
     w.s_end = std::min(a.n_steps, s0 + len);
     w.steps_per_group = overlap ? kOverlapStepsPerGroup : kScanStepsPerGroup;
-    w.sortbuf = pipelined ? static_cast<uint32_t*>(ctx->ws) : nullptr;
+    w.sortbuf = static_cast<uint32_t*>(ctx->ws);
     w.sort_stride = (int64_t)(sort_row / sizeof(uint32_t));
     w.nseg = nseg;
     w.segres = static_cast<uint64_t*>(ctx->segres);
-    w.exact_only = pipelined ? 1 : 0;
     hipError_t e = hipSuccess;
     if (overlap && ci == 1 && (e = hipStreamWaitEvent(scan_on, ctx->ev_scan[0], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
     if (ci >= n_bufs && ((e = hipStreamWaitEvent(scan_on, ctx->ev_chain[buf], 0)) != hipSuccess ||
-                    (pipelined && (e = hipStreamWaitEvent(scan_on, ctx->ev_side[buf], 0)) != hipSuccess)))
+                    (e = hipStreamWaitEvent(scan_on, ctx->ev_side[buf], 0)) != hipSuccess))
       return hip_fail(ctx, e, "sample_stream buffer reuse");
     e = c4s::launch_stream_scan(a, w, scan_on);
     if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream scan launch");
     if ((e = hipEventRecord(ctx->ev_scan[buf], scan_on)) != hipSuccess ||
         (e = hipStreamWaitEvent(chain_on, ctx->ev_scan[buf], 0)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream scan order");
-    if (pipelined) {
-      // Both fast chains run their exact steps themselves and leave nothing
-      // pending: the full-vocabulary chain on the side stream, the list chain
-      // and then the finisher (exact-mode rows only) here, each after the scan.
-      if ((e = hipStreamWaitEvent(side_on, ctx->ev_scan[buf], 0)) != hipSuccess ||
-          (e = launch_row_chain(w, side_on)) != hipSuccess ||
-          (e = hipEventRecord(ctx->ev_side[buf], side_on)) != hipSuccess)
-        return hip_fail(ctx, e, "sample_stream row-chain launch");
-      if ((e = c4s::launch_stream_list(a, w, chain_on)) != hipSuccess ||
-          (e = c4s::launch_stream_chain(a, w, chain_on)) != hipSuccess ||
-          (e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
-        return hip_fail(ctx, e, "sample_stream chain launch");
-      last_side = buf;
-      continue;
-    }
-    // Fast passes stop a row at a step they cannot decide; the repair kernel
-    // runs that step exactly; the finisher completes whatever is left.
-    for (int r = 0; r < kFastRounds; ++r) {
-      w.round = r;
-      if (r == 0) {   // list rows here, full-vocabulary rows on the side stream, side by side
-        if ((e = hipEventRecord(ctx->ev_fork, chain_on)) != hipSuccess ||
-            (e = hipStreamWaitEvent(side_on, ctx->ev_fork, 0)) != hipSuccess)
-          return hip_fail(ctx, e, "sample_stream fork");
-        e = launch_row_chain(w, side_on);
-        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream row-chain launch");
-        e = c4s::launch_stream_list(a, w, chain_on);
-        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream list-chain launch");
-        if ((e = hipEventRecord(ctx->ev_join, side_on)) != hipSuccess ||
-            (e = hipStreamWaitEvent(chain_on, ctx->ev_join, 0)) != hipSuccess)
-          return hip_fail(ctx, e, "sample_stream join");
-      } else {
-        e = c4s::launch_stream_list(a, w, chain_on);
-        if (e == hipSuccess) e = launch_row_chain(w, chain_on);
-        if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
-      }
-      if ((e = c4s::launch_stream_repair(a, w, chain_on)) != hipSuccess)
-        return hip_fail(ctx, e, "sample_stream repair launch");
-    }
-    e = c4s::launch_stream_chain(a, w, chain_on);
-    if (e != hipSuccess) return hip_fail(ctx, e, "sample_stream chain launch");
-    if ((e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
-      return hip_fail(ctx, e, "sample_stream chain order");
+    // Both fast chains run their exact steps themselves: the full-vocabulary
+    // chain on the side stream, the list chain and then the finisher
+    // (exact-mode rows only) here, each after the scan.
+    if ((e = hipStreamWaitEvent(side_on, ctx->ev_scan[buf], 0)) != hipSuccess ||
+        (e = launch_row_chain(w, side_on)) != hipSuccess ||
+        (e = hipEventRecord(ctx->ev_side[buf], side_on)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream row-chain launch");
+    if ((e = c4s::launch_stream_list(a, w, chain_on)) != hipSuccess ||
+        (e = c4s::launch_stream_chain(a, w, chain_on)) != hipSuccess ||
+        (e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
+      return hip_fail(ctx, e, "sample_stream chain launch");
+    last_side = buf;
   }
   if (last_side >= 0) {   // the last full-vocabulary chain ahead of what follows on chain_on
     hipError_t e = hipStreamWaitEvent(chain_on, ctx->ev_side[last_side], 0);
@@ -535,7 +522,7 @@ static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t l
   if ((reinterpret_cast<uintptr_t>(h->hidden) | reinterpret_cast<uintptr_t>(h->weight)) & 15u)
     return fail(ctx, C4S_EINVAL, "lmhead: hidden and weight must be 16-byte aligned");
   const size_t mpad = (size_t)((h->M + 63) / 64 * 64);
-  int rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, mpad * (size_t)h->D * 2, "lmhead workspace");
+  int rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, mpad * (size_t)h->D * 2, "lmhead workspace", s);
   if (rc) return rc;
   c4s::LmHeadArgs a{};
   a.hidden = h->hidden;
@@ -574,7 +561,8 @@ int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, 
   int64_t ld = head->ld_out;
   if (!logits) {
     int rc = ensure(ctx, &ctx->logits_ws, &ctx->logits_bytes,
-                    (size_t)std::max(head->M, 1) * (size_t)std::max(head->V, 1) * 4, "logits workspace");
+                    (size_t)std::max(head->M, 1) * (size_t)std::max(head->V, 1) * 4, "logits workspace",
+                    static_cast<hipStream_t>(stream));
     if (rc) return rc;
     logits = static_cast<float*>(ctx->logits_ws);
     ld = head->V;
@@ -619,7 +607,7 @@ int stage_for(c4s_ctx* ctx, int32_t n, int64_t n_ids, Stage* st) {
   auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t b_logits = al((size_t)n * 4), b_ids = al((size_t)std::max<int64_t>(n_ids, 1) * 4);
   const size_t need = b_logits + b_ids + al(16) + al(12) + al(8) + al(8) + al(4);
-  int rc = ensure(ctx, &ctx->stage, &ctx->stage_bytes, need, "staging");
+  int rc = ensure(ctx, &ctx->stage, &ctx->stage_bytes, need, "staging", ctx->host_stream);
   if (rc) return rc;
   char* p = static_cast<char*>(ctx->stage);
   st->logits = reinterpret_cast<float*>(p); p += b_logits;

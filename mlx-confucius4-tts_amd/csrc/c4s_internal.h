@@ -98,10 +98,8 @@ struct StreamWs {
   uint32_t* state;         // [n_rows][kStateWords] carried across kernels and chunks
   int s_begin, s_end;      // steps of this chunk
   int steps_per_group;     // scan: steps per workgroup
-  int round;               // chain rounds within the chunk (0: the first)
   uint32_t* sortbuf;       // exact steps of the pipelined row chain: per-row key buffer
   int64_t sort_stride;     // words per row
-  int exact_only;          // finisher: exact-mode rows only (the fast chains leave nothing pending)
   int nseg;                // pipelined row chain: step segments of a row without penalty
   uint64_t* segres;        // [n_rows][nseg][4] segment results (status and stop step, RNG, statistics)
 };
@@ -130,13 +128,10 @@ hipError_t launch_stream(const StreamArgs& a, hipStream_t s);
 hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_list_lds_bytes(int vocab);  // candidate-list chain: a row for its exact steps
 hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_t s);
-hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStream_t s);
-hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
-size_t stream_rowk_lds_bytes(int vocab);
 size_t stream_rowp_lds_bytes(int vocab);  // 0 when the pipelined row chain does not fit
 hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);

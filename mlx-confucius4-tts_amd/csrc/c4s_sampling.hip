@@ -162,11 +162,6 @@ __global__ __launch_bounds__(NT) void k_hist_bits_init(const int32_t* ids, const
 }
 
 // Multi-step AR stream for rows staged in LDS: one persistent workgroup per
-// row walks all steps; the row's distinct penalised ids live in LDS (bitmap +
-// list) and grow with every sampled token that is not the stop token
-// (text2semantic.cpp:333-334). A stopped row reports -1 afterwards and its RNG
-// stays frozen.
-// Multi-step AR stream for rows staged in LDS: one persistent workgroup per
 // row walks all steps. The row's distinct penalised ids live in an LDS bitmap
 // that gains every sampled token that is not the stop token
 // (text2semantic.cpp:333-334). While step s runs, the logits of step s+1 are

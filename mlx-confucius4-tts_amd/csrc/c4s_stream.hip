@@ -19,10 +19,10 @@
 //        rows, one wave), k_stream_rowp (full-vocabulary rows, a CU each,
 //        pipelined with helper waves; rows without penalty in step segments
 //        settled by k_stream_segfix), k_stream_chain (the exact chain, for
-//        rows the fast chains do not take), k_stream_rowk / k_stream_repair
-//        (where the pipelined chain does not fit). Every decision is accepted
-//        only with a margin larger than the error bounds; otherwise the step
-//        runs the exact chain on the full row staged in LDS.
+//        rows the fast chains do not take). Every decision is accepted only
+//        with a margin larger than the error bounds; otherwise the step runs
+//        the exact chain on the full row staged in LDS. Vocabularies whose
+//        pipelined chain does not fit in LDS take the single-kernel stream.
 //
 // Row modes (stream_mode): greedy rows and top-k rows with k <= 64 use the
 // candidate list alone; full-vocabulary rows (top-k off) also use the chunk
@@ -59,11 +59,6 @@ __device__ __forceinline__ int stream_mode(const RowCfg& c, int V) {
 __device__ __forceinline__ int list_cap(const RowCfg& c) {
   return (!c.greedy && !c.topk_on && c.p > 0.0f && c.p < 1.0f) ? kListLarge : kListSmall;
 }
-
-// Chunk masses are computed as the reference does, exp((double)fl(fl(y/T) - m0)):
-// the nucleus cut and the full-vocabulary draw are then decided with margins of
-// a few ulp (the fp32 exp2 variant below is kept for rows that opt out).
-__device__ __forceinline__ bool exact_masses(const RowCfg&) { return true; }
 
 __device__ __forceinline__ float pen_exact(float s, float pen) {
   return (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
@@ -283,7 +278,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
     }
   }
   __syncthreads();
-  const float pen = c.pen, rpen = 1.0f / c.pen;
+  const float pen = c.pen;
 
   for (int s = s0; s < s1; ++s) {
     C4S_SCAN_PHASE(0);
@@ -546,11 +541,11 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
     int nchunk = 0, qhint = kListLarge;   // qhint: read by thread 0 (wave 0 holds top_mass)
     double err = 0.0, s0 = 0.0;
     if (masses && !bad) {
+      // Chunk masses as the reference computes them, exp((double)fl(fl(y/T) - m0)):
+      // the nucleus cut and the full-vocabulary draw are then decided with
+      // margins of a few ulp, and the masses carry no error term (err = 0).
       m0 = kfloat(ent_key(srt[0]));
-      const MassCoef mk = mass_coef(c, m0);
-      const bool exm = exact_masses(c);
       nchunk = max(1, (rs.nq + 15) >> 4);
-      double el = 0.0;
       // the quads' H0 bits first, all reads at once (quad index clamped into the row)
       uint32_t hq[NQ];
 #pragma unroll
@@ -565,21 +560,10 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
         if (q < rs.nq) {
           const uint32_t hb = hq[j];
           const bool pon = c.pen_on;
-          if (exm) {
-            qd = mass_exact((pon && (hb & 1u)) ? pen_exact(xv[j].x, pen) : xv[j].x, c, m0) +
-                 mass_exact((pon && (hb & 2u)) ? pen_exact(xv[j].y, pen) : xv[j].y, c, m0) +
-                 mass_exact((pon && (hb & 4u)) ? pen_exact(xv[j].z, pen) : xv[j].z, c, m0) +
-                 mass_exact((pon && (hb & 8u)) ? pen_exact(xv[j].w, pen) : xv[j].w, c, m0);
-          } else {
-            float er, qs = 0.f, qe = 0.f;
-            qs += mass_approx((pon && (hb & 1u)) ? pen_approx(xv[j].x, pen, rpen) : xv[j].x, mk, er); qe += er;
-            qs += mass_approx((pon && (hb & 2u)) ? pen_approx(xv[j].y, pen, rpen) : xv[j].y, mk, er); qe += er;
-            qs += mass_approx((pon && (hb & 4u)) ? pen_approx(xv[j].z, pen, rpen) : xv[j].z, mk, er); qe += er;
-            qs += mass_approx((pon && (hb & 8u)) ? pen_approx(xv[j].w, pen, rpen) : xv[j].w, mk, er); qe += er;
-            qe += qs * 0x1p-22f;   // fp32 sum of four
-            el += (double)qe;
-            qd = (double)qs;
-          }
+          qd = mass_exact((pon && (hb & 1u)) ? pen_exact(xv[j].x, pen) : xv[j].x, c, m0) +
+               mass_exact((pon && (hb & 2u)) ? pen_exact(xv[j].y, pen) : xv[j].y, c, m0) +
+               mass_exact((pon && (hb & 4u)) ? pen_exact(xv[j].z, pen) : xv[j].z, c, m0) +
+               mass_exact((pon && (hb & 8u)) ? pen_exact(xv[j].w, pen) : xv[j].w, c, m0);
         }
         // 16 consecutive lanes hold the 16 quads of one chunk
         double d = qd;
@@ -594,15 +578,8 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       __syncthreads();
       if (eh || et) {
         const bool pb = c.pen_on && bit_of(sh.bm, eid);
-        if (exm) {
-          sh.edge[t] = mass_exact(pb ? pen_exact(xe, pen) : xe, c, m0);   // t < 6
-        } else {
-          float er;
-          sh.edge[t] = (double)mass_approx(pb ? pen_approx(xe, pen, rpen) : xe, mk, er);
-          el += (double)er;
-        }
+        sh.edge[t] = mass_exact(pb ? pen_exact(xe, pen) : xe, c, m0);   // t < 6
       }
-      err = block_sum_f64<NTA>(el, sh.redd);
       if (t == 0) {
         double hs = 0.0, ts = 0.0;
         for (int i = 0; i < rs.head; ++i) hs += sh.edge[i];
@@ -666,7 +643,7 @@ struct ChainSh {
 // Per-row state carried across the chain kernels and across chunks of steps
 // (kStateWords words): done flag, statistics, next step, pending exact step,
 // then the bitmap of ids drawn during the stream.
-enum : int { kStDone = 0, kStStats = 1, kStNext = 5, kStPending = 6, kStBits = 8 };
+enum : int { kStDone = 0, kStStats = 1, kStNext = 5, kStBits = 8 };
 
 
 // Slot s (an id-order rank among the list entries) lives at position
@@ -1584,23 +1561,21 @@ __device__ __forceinline__ int exact_step(float* val, double* E, const uint32_t*
 }
 
 
-// ---- fast chain kernels: candidate steps only -------------------------------------------
+// ---- fast chain kernels ------------------------------------------------------------------
 //
-// No exact code here (its register demand would spill the hot loops): a step
-// they cannot decide marks the row pending and ends the row's pass; the repair
-// kernel then runs that one step exactly and the next pass resumes. Greedy and
-// top-k rows need only their candidate list: one wavefront per row, no
-// barriers, summaries four steps ahead in registers. Full-vocabulary rows also
-// stream their raw row for the corrections: four wavefronts per row.
+// Greedy and top-k rows need only their candidate list: one wavefront per
+// row, no barriers, summaries four steps ahead in registers. Full-vocabulary
+// rows also stream their raw row for the corrections: four wavefronts per
+// row. A step the summary cannot settle runs the exact chain inside the
+// kernel, on the row read into LDS.
 
 // State load shared by both: returns false when the row has nothing to do in
-// this pass (pending, finished, or stopped; a stopped row reports -1 for the
-// rest of the chunk, text2semantic.cpp:304).
+// this chunk (finished, or stopped; a stopped row reports -1 for the rest of
+// the chunk, text2semantic.cpp:304).
 __device__ __forceinline__ bool fast_begin(const StreamArgs& a, const StreamWs& w, int row, int nthr,
                                            int& s_first) {
   uint32_t* stw = w.state + (size_t)row * kStateWords;
   s_first = (int)stw[kStNext];
-  if (stw[kStPending] != 0u) return false;
   if (stw[kStDone] != 0u || s_first >= w.s_end) {
     if (stw[kStDone] != 0u) {
       for (int s = s_first + (int)threadIdx.x; s < w.s_end; s += nthr) a.out_tok[(int64_t)s * a.n_rows + row] = -1;
@@ -1631,7 +1606,7 @@ __device__ __forceinline__ void fast_bitmaps(const StreamArgs& a, const uint32_t
 }
 
 __device__ __forceinline__ void fast_end(const StreamArgs& a, const StreamWs& w, int row, int V, int nthr,
-                                         int s, bool pending, bool done, uint64_t rng, const uint32_t* acc,
+                                         int s, bool done, uint64_t rng, const uint32_t* acc,
                                          const uint32_t* bmN) {
   uint32_t* stw = w.state + (size_t)row * kStateWords;
   if (threadIdx.x == 0) {
@@ -1639,8 +1614,7 @@ __device__ __forceinline__ void fast_end(const StreamArgs& a, const StreamWs& w,
     stw[kStDone] = done ? 1u : 0u;
     stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
     stw[kStNext] = (uint32_t)s;
-    stw[kStPending] = pending ? 1u : 0u;
-    if (a.stats && !pending && s >= a.n_steps) {   // the row's last step: its statistics
+    if (a.stats && s >= a.n_steps) {   // the row's last step: its statistics
       uint32_t* o = a.stats + 4 * (int64_t)row;
       o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
     }
@@ -1669,9 +1643,9 @@ __device__ __forceinline__ void penalise_wave(float* val, const uint32_t* bm, in
 }
 
 // Candidate-list rows, one wave per row. A step the list cannot decide runs
-// exactly in the kernel when the per-row sort buffer exists (the row read
-// into LDS, the penalty of H0 and the stream's ids, the whole chain);
-// otherwise the row stops there with the step pending for k_stream_repair.
+// exactly in the kernel: the row read into LDS, the penalty of H0 and the
+// stream's ids, the whole chain (its top_p exact pass sorts in the per-row
+// key buffer).
 __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ ChainSh cs;
@@ -1720,8 +1694,7 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     }
     return tok;
   };
-  // One step; false when it has to be run exactly elsewhere (nothing changed then).
-  auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) -> bool {
+  auto step = [&](int s, ListRegs& r) __attribute__((always_inline)) {
     int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
     C4S_LIST_PHASE(0);
     const SumHdr h = hdr_lanes(r.hw);
@@ -1732,10 +1705,7 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     C4S_LIST_PHASE(1);
     StepOut o{0, 0u, 0u, 0u};
     const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, bmN, rng, cs, o);
-    if (!ok) {
-      if (lane == 0) acc[0] |= 1u << (20 + o.why);
-      if (!w.sortbuf) return false;
-    }
+    if (!ok && lane == 0) acc[0] |= 1u << (20 + o.why);
     const int tok = ok ? o.tok : exact(s);
     if (lane == 0) {
       *outp = tok;
@@ -1751,7 +1721,6 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     wave_sync();
     C4S_LIST_PHASE(7);
     if (tok == a.stop_token) done = true;
-    return true;
   };
 
   ListRegs P0{}, P1{}, P2{}, P3{};
@@ -1762,241 +1731,25 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
   // A stopped row leaves the loop (no step path skips its prefetch) and
   // reports -1 afterwards.
   int s = s_first;
-  bool pending = false;
   while (s < w.s_end) {
-    if (!step(s, P0)) { pending = true; break; }
+    step(s, P0);
     if (++s >= w.s_end || done) break;
-    if (!step(s, P1)) { pending = true; break; }
+    step(s, P1);
     if (++s >= w.s_end || done) break;
-    if (!step(s, P2)) { pending = true; break; }
+    step(s, P2);
     if (++s >= w.s_end || done) break;
-    if (!step(s, P3)) { pending = true; break; }
+    step(s, P3);
     if (++s >= w.s_end || done) break;
   }
   if (done) {
     for (int s2 = s + lane; s2 < w.s_end; s2 += kWave) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
     s = w.s_end;
   }
-  fast_end(a, w, row, V, kWave, s, pending, done, rng, acc, bmN);
+  fast_end(a, w, row, V, kWave, s, done, rng, acc, bmN);
 }
 
 constexpr int NTC = 256;
 constexpr int NWC = NTC / kWave;
-constexpr int kQuadsC = kLdsVocabMax / 4 / NTC;
-static_assert(kQuadsC * 4 * NTC == kLdsVocabMax, "row fetch covers the LDS rows");
-
-// A row of up to NQC * 4 * 256 body ids plus edge ids, in registers.
-template <int NQC>
-struct RowRegsC {
-  float4 q[NQC];
-  float e;
-};
-struct SumRegsC {
-  uint64_t w[4];
-};
-static_assert(4 * NTC >= kSumWords && 4 * NTC * 8 <= (int)kSumStride, "four words a thread cover a summary");
-
-template <int NQC>
-__device__ __forceinline__ void fetch_row_c(const float* p, int V, RowRegsC<NQC>& f) {
-  const RowShape r = row_shape(p, V);
-  const float4* p4 = reinterpret_cast<const float4*>(p + r.head);
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int j = 0; j < NQC; ++j) {
-    const int q = t + NTC * j;
-    f.q[j] = (q < r.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  f.e = (t < r.head) ? p[t] : ((t < r.head + r.tail) ? p[r.head + 4 * r.nq + (t - r.head)] : 0.f);
-}
-
-template <int NQC>
-__device__ __forceinline__ float* store_row_c(const float* p, int V, const RowRegsC<NQC>& f, float* buf) {
-  const RowShape r = row_shape(p, V);
-  float* val = buf + ((4 - r.head) & 3);
-  const int t = threadIdx.x;
-  float4* body = reinterpret_cast<float4*>(val + r.head);
-#pragma unroll
-  for (int j = 0; j < NQC; ++j) {
-    const int q = t + NTC * j;
-    if (q < r.nq) body[q] = f.q[j];
-  }
-  if (t < r.head) val[t] = f.e;
-  else if (t < r.head + r.tail) val[r.head + 4 * r.nq + (t - r.head)] = f.e;
-  return val;
-}
-
-template <int NQC>
-__global__ __launch_bounds__(NTC) void k_stream_rowk(StreamArgs a, StreamWs w) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ ChainSh cs;
-  __shared__ ScratchT<NWC> xs;   // exact steps
-  __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
-  const int row = blockIdx.x;
-  const int V = a.vocab;
-  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
-  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
-  if (stream_mode(c, V) != kModeRow) return;
-  int s_first;
-  if (!fast_begin(a, w, row, NTC, s_first)) return;
-  const uint32_t* stw = w.state + (size_t)row * kStateWords;
-  for (int i = t; i < kMaxChunks; i += NTC) cs.cdelta[i] = 0.0;
-  if (t == 0) cs.gen = 0u;
-  fast_bitmaps(a, stw, row, V, NTC, bmH0, bmN, true);
-  double* E = reinterpret_cast<double*>(smem);   // exact steps: masses by id, sort keys
-  float* vbuf = reinterpret_cast<float*>(smem + 8 * (size_t)vpad(V));
-  uint64_t rng = a.rng[row];
-  uint32_t acc[4] = {0u, 0u, 0u, 0u};
-  if (t == 0) { acc[0] = stw[1]; acc[1] = stw[2]; acc[2] = stw[3]; acc[3] = stw[4]; }
-  bool done = false;
-  const float* base = a.logits + (int64_t)row * a.ld;
-  const float rpen = 1.0f / c.pen;
-  const int ch = ((V + NTC - 1) / NTC) | 1;   // corrections: ids [t ch, t ch + ch)
-
-  auto load_sum = [&](int s, SumRegsC& Sg) __attribute__((always_inline)) {
-    const uint64_t* sw = sum_words(w, a.n_rows, s, row);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) Sg.w[i] = sw[t + NTC * i];   // inside the 1024-word stride
-  };
-  // One step; false when the summary cannot settle it (nothing changed then,
-  // and the raw row of step s stays staged in LDS).
-  auto step = [&](int s, SumRegsC& Sg, RowRegsC<NQC>& R) __attribute__((always_inline)) -> bool {
-    int32_t* outp = a.out_tok + (int64_t)s * a.n_rows + row;
-    const float* cur = base + (int64_t)s * a.step_stride;
-    C4S_PHASE(0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (t + NTC * i < kSumWords) cs.sum[t + NTC * i] = Sg.w[i];
-    float* val = store_row_c(cur, V, R, vbuf);
-    C4S_PHASE(1);
-    if (s + 1 < w.s_end) fetch_row_c(cur + a.step_stride, V, R);
-    if (s + 2 < w.s_end) load_sum(s + 2, Sg);
-    C4S_PHASE(2);
-    __syncthreads();
-    C4S_PHASE(3);
-    const SumHdr h = hdr_from(cs.sum);
-    // Corrections for ids drawn during the stream (never in H0): fp32 masses
-    // first; a decision that falls inside their error bound is retried once
-    // with the reference's double masses.
-    for (int attempt = 0; attempt < 2; ++attempt) {
-      const bool exact = attempt == 1;
-      double dl = 0.0, el = 0.0;
-      if (!(h.flags & 1u) && c.pen_on) {
-        const MassCoef mk = mass_coef(c, h.m0);
-        const int lo = min(V, t * ch), hi = min(V, lo + ch);
-        if (lo < hi) {
-          const int w0 = lo >> 5;
-          uint64_t bits = (uint64_t)bmN[w0] | ((uint64_t)bmN[w0 + 1] << 32);
-          bits >>= (lo - 32 * w0);
-          bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
-          while (bits) {
-            const int id = lo + __ffsll((unsigned long long)bits) - 1;
-            bits &= bits - 1;
-            const float x = val[id];
-            double d;
-            if (exact) {
-              d = mass_exact(x, c, h.m0) - mass_exact(pen_exact(x, c.pen), c, h.m0);
-            } else {
-              float er0, er1;
-              const float m_raw = mass_approx(x, mk, er0);
-              const float m_pen = mass_approx(pen_approx(x, c.pen, rpen), mk, er1);
-              d = (double)m_raw - (double)m_pen;
-              el += (double)er0 + (double)er1;
-            }
-            atomicAdd(&cs.cdelta[chunk_of(id, h.head, h.nchunk)], d);
-            dl += d;
-          }
-        }
-      }
-      dl = wave_sum_dpp(dl);
-      el = wave_sum_dpp(el);
-      if (lane == 0) { cs.wd[wv] = dl; cs.we[wv] = el; }
-      __syncthreads();
-      C4S_PHASE(4);
-      if (wv == 0) {
-        double ds = 0.0, de = 0.0;
-        for (int i = 0; i < NWC; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-        StepOut o{0, 0u, 0u, 0u};
-        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, cs.sum, cs.cdelta, rng, cs, o);
-        for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
-        const bool retry = !ok && !exact && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
-        if (lane == 0) {
-          cs.bi[0] = ok ? 1 : (retry ? 2 : 0); cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why;
-          cs.bi[3] = (int)o.dex; cs.rng = rng;
-          if (ok) {
-            const int tok = o.tok;
-            *outp = tok;
-            acc[0] |= 64u | 1u;
-            acc[2] += o.dex;
-            acc[3] += o.kept;
-            // text2semantic.cpp:333-334: the stop token is not appended
-            if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
-              bmN[tok >> 5] |= 1u << (tok & 31);
-          } else if (!retry) {
-            acc[0] |= 1u << (20 + o.why);
-          }
-        }
-      }
-      __syncthreads();
-      if (cs.bi[0] != 2) break;
-    }
-    C4S_PHASE(5);
-    rng = cs.rng;
-    if (cs.bi[0] == 0) return false;
-    if (cs.bi[1] == a.stop_token) done = true;
-    return true;
-  };
-
-  // The fast loop stops at a step the summary cannot settle; that step runs
-  // the exact chain here, outside the loop, so that no prefetch is live across
-  // it (its register demand would otherwise spill the loop), and the loop is
-  // primed again from the next step.
-  RowRegsC<NQC> R;
-  SumRegsC SA, SB;
-  // A stopped row leaves the loop (no step path skips its prefetch, so the
-  // loop never waits on loads still in flight) and reports -1 afterwards.
-  int s = s_first;
-  while (s < w.s_end && !done) {
-    load_sum(s, SA);
-    if (s + 1 < w.s_end) load_sum(s + 1, SB);
-    fetch_row_c(base + (int64_t)s * a.step_stride, V, R);
-    bool bail = false;
-    while (s < w.s_end) {
-      if (!step(s, SA, R)) { bail = true; break; }
-      if (++s >= w.s_end || done) break;
-      if (!step(s, SB, R)) { bail = true; break; }
-      if (++s >= w.s_end || done) break;
-    }
-    if (!bail) break;
-    // text2semantic.cpp:142-166 on the whole staged row: penalty over H0 and
-    // the stream's ids (disjoint sets, so each id once), then the chain.
-    const float* cur = base + (int64_t)s * a.step_stride;
-    float* val = vbuf + ((4 - row_shape(cur, V).head) & 3);
-    __syncthreads();
-    if (c.pen_on) {
-      penalise_chunk<NTC>(val, bmH0, V, c.pen);
-      penalise_chunk<NTC>(val, bmN, V, c.pen);
-    }
-    __syncthreads();
-    LdsRow src{val, E, V, 0u, false};
-    const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
-    if (t == 0) {
-      const uint32_t* stp = xs.step_stats;
-      a.out_tok[(int64_t)s * a.n_rows + row] = tok;
-      acc[0] |= stp[0];
-      acc[1] += 1u;
-      acc[2] += stp[2];
-      acc[3] += stp[3];
-      if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0, tok))
-        bmN[tok >> 5] |= 1u << (tok & 31);
-    }
-    __syncthreads();
-    if (tok == a.stop_token) done = true;
-    ++s;
-  }
-  for (int s2 = s + t; s2 < w.s_end; s2 += NTC) a.out_tok[(int64_t)s2 * a.n_rows + row] = -1;
-  s = w.s_end;
-  fast_end(a, w, row, V, NTC, s, false, done, rng, acc, bmN);
-}
 
 // ---- pipelined full-vocabulary chain ------------------------------------------------
 //
@@ -2494,7 +2247,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
       segres[3] = (uint64_t)acc[2] | ((uint64_t)acc[3] << 32);
     }
   } else {
-    fast_end(a, w, row, V, NTC, s_end, false, done, ps.rng, acc, bmNb[s & 1]);
+    fast_end(a, w, row, V, NTC, s_end, done, ps.rng, acc, bmNb[s & 1]);
   }
   C4S_ROW_TIME(1);
 }
@@ -2530,58 +2283,10 @@ __global__ __launch_bounds__(kWave) void k_stream_segfix(StreamArgs a, StreamWs 
     stw[kStDone] = stop >= 0 ? 1u : 0u;
     stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
     stw[kStNext] = (uint32_t)w.s_end;
-    stw[kStPending] = 0u;
     if (a.stats && w.s_end == a.n_steps) {
       uint32_t* o = a.stats + 4 * (int64_t)row;
       o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
     }
-  }
-}
-
-// ---- repair: the pending step of each row, exactly ------------------------------------
-__global__ __launch_bounds__(NT) void k_stream_repair(StreamArgs a, StreamWs w) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ Scratch sh;
-  const int row = blockIdx.x;
-  const int V = a.vocab;
-  const int t = threadIdx.x;
-  uint32_t* stw = w.state + (size_t)row * kStateWords;
-  if (stw[kStPending] == 0u) return;
-  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
-  const int s = (int)stw[kStNext];
-  LdsLayout L = lds_layout(smem, V);
-  const int nwords = bitmap_words(V);
-  uint32_t* bmH0r = L.bitmap + nwords;
-  for (int i = t; i < nwords; i += NT) bmH0r[i] = 0u;
-  __syncthreads();
-  {
-    const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-    for (int64_t j = h0 + t; j < h1; j += NT) {
-      const int id = a.hist_ids[j];
-      if (id >= 0 && id < V) atomicOr(&bmH0r[id >> 5], 1u << (id & 31));   // sampling.cpp:24
-    }
-  }
-  __syncthreads();
-  for (int i = t; i < nwords; i += NT) L.bitmap[i] = bmH0r[i] | stw[kStBits + i];
-  const float* cur = a.logits + (int64_t)row * a.ld + (int64_t)s * a.step_stride;
-  RowFetch f;
-  fetch_row(cur, V, f);
-  float* val = store_row(cur, V, f, L.val);
-  __syncthreads();
-  uint64_t rng = a.rng[row];
-  uint32_t* stp = a.stats ? sh.step_stats : nullptr;
-  const int tok = exact_step(val, L.E, L.bitmap, c, V, sh, rng, stp);
-  if (t == 0) {
-    a.out_tok[(int64_t)s * a.n_rows + row] = tok;
-    if (stp) { stw[1] |= stp[0]; stw[3] += stp[2]; stw[4] += stp[3]; }
-    stw[2] += 1u;
-    // the stop token is not appended (text2semantic.cpp:333-334); H0 ids are not kept in the state
-    if (c.pen_on && tok != a.stop_token && tok >= 0 && tok < V && !bit_of(bmH0r, tok))
-      stw[kStBits + (tok >> 5)] |= 1u << (tok & 31);
-    stw[kStDone] = (tok == a.stop_token) ? 1u : 0u;
-    stw[kStNext] = (uint32_t)(s + 1);
-    stw[kStPending] = 0u;
-    a.rng[row] = rng;
   }
 }
 
@@ -2595,7 +2300,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
   const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
   const int mode = stream_mode(c, V);
-  if (w.exact_only && mode != kModeExact) return;   // the fast chains finish these rows
+  if (mode != kModeExact) return;   // the fast chains finish these rows
   LdsLayout L = lds_layout(smem, V);
   const int nwords = bitmap_words(V);
   uint32_t* bmH0 = L.bitmap + nwords;
@@ -2795,7 +2500,6 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
     stw[kStDone] = done ? 1u : 0u;
     stw[1] = acc[0]; stw[2] = acc[1]; stw[3] = acc[2]; stw[4] = acc[3];
     stw[kStNext] = (uint32_t)w.s_end;
-    stw[kStPending] = 0u;
     if (a.stats && w.s_end == a.n_steps) {
       uint32_t* o = a.stats + 4 * (int64_t)row;
       o[0] = acc[0]; o[1] = acc[1]; o[2] = acc[2]; o[3] = acc[3];
@@ -2835,19 +2539,6 @@ hipError_t launch_stream_list(const StreamArgs& a, const StreamWs& w, hipStream_
   return hipGetLastError();
 }
 
-size_t stream_rowk_lds_bytes(int V) { return 8 * (size_t)vpad(V) + 4 * ((size_t)vpad(V) + 4); }
-
-hipError_t launch_stream_rowk(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
-  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
-  (void)hipGetLastError();
-  const size_t lds = stream_rowk_lds_bytes(a.vocab);
-  if ((a.vocab >> 2) <= 8 * NTC)   // body quads of any alignment fit 8 per thread
-    hipLaunchKernelGGL(k_stream_rowk<8>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
-  else
-    hipLaunchKernelGGL(k_stream_rowk<kQuadsC>, dim3(a.n_rows), dim3(NTC), lds, s, a, w);
-  return hipGetLastError();
-}
-
 size_t stream_rowp_lds_bytes(int V) {
   return 3 * (size_t)kSumWordsP * 8 + 3 * 4 * ((size_t)vpad(V) + 4);
 }
@@ -2864,13 +2555,6 @@ hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStrea
   if (a.n_rows <= 0 || w.s_end <= w.s_begin || w.nseg <= 1) return hipSuccess;
   (void)hipGetLastError();
   hipLaunchKernelGGL(k_stream_segfix, dim3(a.n_rows), dim3(kWave), 0, s, a, w);
-  return hipGetLastError();
-}
-
-hipError_t launch_stream_repair(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
-  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
-  (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_repair, dim3(a.n_rows), dim3(NT), stream_chain_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 

@@ -25,8 +25,9 @@
 // orc_top_p_literal keeps the reference's value-only comparator for measuring
 // how often the two differ.
 //
-// Pinning (what checks each function) is listed in oracle/README.md and is
-// enforced by tests/test_oracle_*.py.
+// Pinning (what checks each function) is enforced by tests/test_oracle_pins.py
+// (closed forms, invariants, exact rational top_p, the xorshift64 shift
+// matrices) and tests/test_oracle_golden.py (HF processor goldens).
 
 #include <algorithm>
 #include <cmath>

@@ -47,30 +47,16 @@ def test_batch64_general_rows(orc, gpu_ctx):
 
 @pytest.mark.parametrize("sweep", ["greedy", "top_k1", "top_p"])
 def test_bf16_ties(orc, gpu_ctx, sweep):
-    b = W.bf16_ties(seed=3, rows=512, sweep=sweep)
+    b = W.bf16_ties(seed=3, rows=1024, sweep=sweep)
     print(f"bf16_ties {sweep}", flush=True)
     tok, st = compare_with_oracle(orc, gpu_ctx, b)
     if sweep == "top_k1":
         assert (st[:, 3] > 1).all()      # the tied maxima all survive top_k=1
 
 
-def test_bf16_ties_literal_sort_divergence(orc):
-    """How often the reference's value-only std::sort (this host's libstdc++)
-    keeps different ids than the declared order inside a cut tie group."""
-    b = W.bf16_ties(seed=3, rows=64, sweep="top_p")
-    x = W.bf16_bits_to_f32(b.logits)
-    differ = 0
-    for r in range(b.n_rows):
-        a = orc.top_p(x[r], 0.5)
-        lit = orc.top_p(x[r], 0.5, literal=True)
-        assert np.isfinite(a).sum() == np.isfinite(lit).sum()   # same count, maybe other ids
-        differ += int(not np.array_equal(np.isfinite(a), np.isfinite(lit)))
-    print(f"literal std::sort keeps other ids in {differ}/{b.n_rows} rows")
-
-
 def test_large_vocab(orc, gpu_ctx):
-    b = W.large_vocab(seed=4, rows=64)
-    print("large_vocab 64 rows", flush=True)
+    b = W.large_vocab(seed=4, rows=256)
+    print("large_vocab 256 rows", flush=True)
     compare_with_oracle(orc, gpu_ctx, b, masked=True)
 
 

@@ -40,6 +40,12 @@ def test_stream_10k_rows_bit_exact(orc):
     assert np.array_equal(rng, orng)
     print("rows", toks.size, "exact steps", int(st[:, 1].sum()), "exact draws", int(st[:, 2].sum()))
     assert int(st[:, 1].sum()) < toks.size // 50      # the candidate summaries decide almost every step
+    # Every sampled row advanced its xorshift64 state once per step: the GPU's
+    # final states against the shift-matrix construction (text2semantic.cpp:158),
+    # independently of the oracle.
+    from xorshift_pin import advance
+    for r in np.flatnonzero(p["do_sample"]):
+        assert int(rng[r]) == advance(int(p["rng"][r]), steps), r
     ctx.close()
 
 
@@ -108,7 +114,11 @@ def _mixed_params(seed, rows, V):
     return p
 
 
-@pytest.mark.parametrize("V,rows,steps", [(8194, 40, 60), (1000, 30, 80), (37, 20, 50), (3000, 25, 70)])
+# 8194: the two-phase stream with the pipelined row chain; from 8233 on the
+# pipelined chain no longer fits in LDS and the single-kernel stream runs.
+@pytest.mark.parametrize("V,rows,steps", [(8194, 40, 60), (1000, 30, 80), (37, 20, 50), (3000, 25, 70),
+                                          (8233, 24, 40), (9216, 30, 60), (10092, 20, 40), (10093, 12, 30),
+                                          (12288, 20, 40)])
 def test_stream_two_phase_all_modes(orc, gpu_ctx, V, rows, steps):
     p = _mixed_params(V + rows, rows, V)
     x = W.batch64_logits(V + 7, steps, rows, V)
@@ -125,13 +135,15 @@ def test_stream_two_phase_all_modes(orc, gpu_ctx, V, rows, steps):
     print("exact steps per row", st[:, 1].tolist())
 
 
-def test_stream_overlapped_chunks(orc, gpu_ctx):
+@pytest.mark.parametrize("V", [8194, 9216, 12288])
+def test_stream_overlapped_chunks(orc, gpu_ctx, V):
     """A stream long enough for several chunks whose scans run beside the
     previous chunk's chains on their own CUs: every row mode, stop tokens
-    planted in later chunks, against the oracle and the single-kernel stream."""
-    steps, rows, V = 300, 48, 8194
-    p = _mixed_params(4242, rows, V)
-    x = W.batch64_logits(4243, steps, rows, V)
+    planted in later chunks, against the oracle and the single-kernel stream
+    (at 9216 and 12288 the single-kernel stream runs for both calls)."""
+    steps, rows = 300, 48
+    p = _mixed_params(4242 + V, rows, V)
+    x = W.batch64_logits(4243 + V, steps, rows, V)
     stop = V - 1
     for s, r in [(130, 0), (255, 3), (256, 9), (299, 12)]:
         x[s, r, stop] = 80.0

@@ -4,9 +4,13 @@ Each check comes from mathematics or from an independent computation, chosen
 so that a plausible mistake (a wrong shift or direction, an off-by-one rank,
 a reversed sort, a dropped min_keep, a draw in the wrong order) fails:
 
-* xorshift64 (text2semantic.cpp:158): the map is linear over GF(2); its matrix,
-  read off the oracle on the 64 basis vectors, must have order exactly 2^64-1
-  (the published full-period property of the (13, 7, 17) triple).
+* xorshift64 (text2semantic.cpp:158: x ^= x << 13; x ^= x >> 7; x ^= x << 17):
+  the map is linear over GF(2). Its matrix, read off the oracle on the 64
+  basis vectors, must equal the product (I + L^17)(I + R^7)(I + L^13) built
+  from explicit shift matrices, and must differ from every other order and
+  direction of the same three shifts (Marsaglia's eight line variants of a
+  full-period triple all have order 2^64-1, so the period alone cannot tell
+  them apart). The period check stays as a second, independent property.
 * seeds (text2semantic.cpp:109, :292-294): literal constants.
 * top_k (sampling.cpp:30-40): threshold by full sort, ties kept.
 * top_p (sampling.cpp:42-71): exact rational arithmetic on tiny rows, and the
@@ -22,6 +26,9 @@ from fractions import Fraction
 
 import numpy as np
 import pytest
+
+from xorshift_pin import REF_STEPS, advance, to_bits, from_bits
+from xorshift_pin import xorshift_matrix as _xorshift_matrix
 
 U64 = (1 << 64) - 1
 
@@ -45,6 +52,37 @@ def _matpow(M, e):
         B = (B @ B) % 2
         e >>= 1
     return R
+
+
+def test_xorshift_shift_order_and_directions(orc):
+    import itertools
+    M = _gf2_matrix(orc)
+    assert (M == _xorshift_matrix(REF_STEPS)).all()
+    same = []
+    for perm in itertools.permutations([13, 7, 17]):
+        for dirs in itertools.product([True, False], repeat=3):
+            steps = list(zip(perm, dirs))
+            if (_xorshift_matrix(steps) == M).all():
+                same.append(steps)
+    assert same == [REF_STEPS], same
+    # wrong amounts fail as well
+    for steps in ([(12, True), (7, False), (17, True)], [(13, True), (8, False), (17, True)]):
+        assert not (_xorshift_matrix(steps) == M).all()
+
+
+def test_xorshift_known_answers(orc):
+    """The seeds' streams (text2semantic.cpp:109, :292-294) from the shift-matrix
+    construction, 2000 steps each, against the oracle step by step."""
+    A = _xorshift_matrix(REF_STEPS)
+    for seed in [0x9E3779B97F4A7C15, 1234, (0x9E3779B97F4A7C15 + 63 * 0x100000001B3) & U64, 1]:
+        v = to_bits(seed)
+        t = seed
+        for n in range(2000):
+            v = (A @ v) % 2
+            t = orc.xorshift64(t)
+            if n % 97 == 0 or n == 1999:
+                assert from_bits(v) == t
+        assert advance(seed, 2000) == t
 
 
 def test_xorshift_linear(orc):
@@ -199,6 +237,28 @@ def test_top_p_ties_lower_id_survives(orc):
     x = np.zeros(10, dtype=np.float32)
     got = orc.top_p(x, 0.35)      # 10 equal weights: 4 survive (cum of 6 removed = 0.6 <= 0.65)
     assert list(np.flatnonzero(~np.isneginf(got))) == [0, 1, 2, 3]
+
+
+def test_top_p_literal_sort_differs_only_inside_the_cut_tie_group(orc):
+    """The reference's value-only std::sort (this host's libstdc++) against the
+    declared order (lower id survives) on the tie-heavy bf16 workload: the same
+    number of ids survive, and the kept sets differ only among ids whose value
+    equals the smallest kept value (the tie group the nucleus cut falls in)."""
+    import c4s_workloads as W
+    b = W.bf16_ties(seed=3, rows=64, sweep="top_p")
+    x = W.bf16_bits_to_f32(b.logits)
+    differ = 0
+    for r in range(b.n_rows):
+        a = orc.top_p(x[r], 0.5)
+        lit = orc.top_p(x[r], 0.5, literal=True)
+        ka, kl = np.isfinite(a), np.isfinite(lit)
+        assert ka.sum() == kl.sum()
+        if not np.array_equal(ka, kl):
+            differ += 1
+            cut = x[r][ka].min()
+            assert x[r][ka].min() == x[r][kl].min() == cut
+            assert (x[r][ka ^ kl] == cut).all()
+    print(f"literal std::sort keeps other ids in {differ}/{b.n_rows} rows")
 
 
 def test_argmax_first_max(orc):
