@@ -72,7 +72,8 @@ enum {
 
 /* Per-row statistics (c4s_rows.out_stats, 4 words per row). */
 enum {
-  C4S_STAT_PATH = 0,       /* bit0 drawn, bit1 top-k applied, bit2 top-p applied, bit3 greedy */
+  C4S_STAT_PATH = 0,       /* bit0 drawn, bit1 top-k applied, bit2 top-p applied, bit3 greedy,
+                              bit4 decided without the multi-pass chain */
   C4S_STAT_TOPP_EXACT = 1, /* nucleus cut fell inside the error bound -> exact pass ran */
   C4S_STAT_DRAW_EXACT = 2, /* draw fell inside the error bound -> exact pass ran */
   C4S_STAT_KEPT = 3        /* ids left with nonzero weight before the draw */

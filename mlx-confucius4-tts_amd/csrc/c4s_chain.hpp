@@ -1188,16 +1188,19 @@ __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitma
   const int ch = odd_chunk<NTX>(V);
   const int lo = min(V, (int)threadIdx.x * ch);
   const int hi = min(V, lo + ch);
-  if (lo >= hi) return;
-  const int w0 = lo >> 5;
-  uint64_t bits = (uint64_t)bitmap[w0] | ((uint64_t)bitmap[w0 + 1] << 32);
-  bits >>= (lo - 32 * w0);
-  bits &= (hi - lo >= 64) ? ~0ull : ((1ull << (hi - lo)) - 1ull);
-  while (bits) {
-    const int i = lo + __ffsll((unsigned long long)bits) - 1;
-    bits &= bits - 1;
-    const float s = val[i];
-    val[i] = (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
+  // the chunk's bits, 32 ids at a time (a chunk may span several words)
+  for (int b0 = lo; b0 < hi; b0 += 32) {
+    const int w0 = b0 >> 5;
+    uint64_t bits = (uint64_t)bitmap[w0] | ((uint64_t)bitmap[w0 + 1] << 32);
+    bits >>= (b0 - 32 * w0);
+    const int len = min(32, hi - b0);
+    bits &= (1ull << len) - 1ull;
+    while (bits) {
+      const int i = b0 + __ffsll((unsigned long long)bits) - 1;
+      bits &= bits - 1;
+      const float s = val[i];
+      val[i] = (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
+    }
   }
 }
 

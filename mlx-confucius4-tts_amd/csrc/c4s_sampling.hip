@@ -24,7 +24,7 @@
 // bitmap, temperature re-applied on the fly).
 
 
-#include "c4s_chain.hpp"
+#include "c4s_step.hpp"
 
 namespace c4s {
 namespace {
@@ -91,6 +91,457 @@ __global__ __launch_bounds__(NT) void k_rows_lds(RowsArgs a) {
     if (c.draw && a.rng) a.rng[row] = rng;
     join_history(a, row, tok);
   }
+}
+
+// Writes one row's result: token, RNG state, history set (text2semantic.cpp:
+// 333-334: the stop token does not join), statistics.
+__device__ __forceinline__ void step_out(const StepIO& io, int V, int tok, uint64_t rng, bool draw,
+                                         uint32_t s0, uint32_t s1, uint32_t s2, uint32_t s3) {
+  *io.out_tok = tok;
+  if (draw && io.rng) *io.rng = rng;
+  if (io.join && tok >= 0 && tok < V && tok != io.stop_token) atomicOr(&io.join[tok >> 5], 1u << (tok & 31));
+  if (io.stats) { io.stats[0] = s0; io.stats[1] = s1; io.stats[2] = s2; io.stats[3] = s3; }
+}
+
+// The draw of the one-pass step (text2semantic.cpp:150-165) once the kept set
+// is known: e[] are this thread's kept fp32 masses (0 elsewhere), ds the
+// workgroup scan of their sums with the error bound in tot2. The thread whose
+// interval holds r decides; inside the margin its wave recomputes the draw in
+// double (draw_replay).
+template <int PT>
+__device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, const KeptRule& kr, const float (&z)[PT],
+                                            int lo, int n, float m, const Scan2& ds, uint32_t n_kept,
+                                            uint32_t st_path, uint32_t st_exact) {
+  const int t = threadIdx.x;
+  const uint64_t st2 = xorshift64(*io.rng);
+  const double u = unit_from_state(st2);
+  const double K = ds.tot;
+  const double r = u * K;
+  const double margin = 2.0 * ds.tot2 + rel_eps(c.V) * K;
+  if (!(r > 0.0)) {   // r == 0: the first id satisfies r <= acc (text2semantic.cpp:161-162)
+    if (t == 0) step_out(io, c.V, 0, st2, true, st_path, st_exact, 0u, n_kept);
+    return;
+  }
+  const bool owner = (ds.ex < r && r <= ds.in) || (t == kStepThreads - 1 && r > ds.in);
+  int found = -1;
+  bool certain = false;
+  if (owner) {
+    double acc = ds.ex, prev = ds.ex;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      bool kp;
+      const float ej = j < n ? kept_mass32(kr, z[j], m, lo + j, kp) : 0.0f;
+      if (found < 0 && ej > 0.0f) {
+        const double na = acc + (double)ej;
+        if (na >= r) { found = lo + j; prev = acc; }
+        acc = na;
+      }
+    }
+    certain = found >= 0 && (acc - r > margin) && (r - prev > margin);
+  }
+  if (__ballot(owner && !certain)) {
+    const int tk = draw_replay(io, c, kr, m, u);
+    if (owner) { found = tk; }
+  }
+  if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, certain ? 0u : 1u, n_kept);
+}
+
+// The multi-pass chain (c4s_chain.hpp) on the penalised row staged in LDS
+// (`val`), for the rows the one pass leaves; kept out of line so that its
+// registers do not weigh on the one-pass path.
+__device__ __noinline__ void chain_fallback(const StepIO& io, const RowCfg& c, unsigned char* work, float* val,
+                                            StepScratch& sh) {
+  const int V = c.V, t = threadIdx.x;
+  uint64_t rng = *io.rng;
+  LdsRow src{val, reinterpret_cast<double*>(work), V, 0u, false};
+  const int tok = run_chain(src, sh, c, rng, io.masked, sh.step_stats);
+  if (t == 0) {
+    const uint32_t* sp = sh.step_stats;
+    step_out(io, V, tok, rng, true, sp[0], sp[1], sp[2], sp[3]);
+  }
+}
+
+// One AR step of the reference chain (C4S_MODE_CHAIN) for one row per
+// workgroup, in one pass where it can (c4s_step.hpp), else the multi-pass
+// chain on the row staged in LDS. PT >= the ids a thread owns.
+template <int PT>
+__global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ StepScratch sh;
+  __shared__ StepSh ss;
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  if (a.row_active && !a.row_active[row]) {
+    if (t == 0) a.out_tok[row] = -1;
+    return;
+  }
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, a.min_keep, a.do_sample);
+  C4S_PHASE(0);
+  unsigned char* work = smem;
+  float* vbuf = reinterpret_cast<float*>(smem + step_work_bytes(V));
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(vbuf + vpad(V) + 4);
+  uint32_t* hc = reinterpret_cast<uint32_t*>(work);   // [waves][kNB] bucket counts
+  unsigned long long* hm = reinterpret_cast<unsigned long long*>(work + kHistBytes);   // [waves][kNB] masses, 2^-32 units
+  uint64_t* sbuf = reinterpret_cast<uint64_t*>(work + 3 * kHistBytes);
+  uint64_t* list = sbuf + 2 * kSortCap;
+  const int P = odd_chunk<kStepThreads>(V);
+  const int lo = min(V, t * P), n = min(V, lo + P) - lo;
+  const int64_t roff = (int64_t)row * a.ld;
+  const bool csr = c.pen_on && !a.hist_bits;
+  StepIO io;
+  io.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
+  io.xb = a.dtype == 1 ? static_cast<const uint16_t*>(a.logits) + roff : nullptr;
+  io.bitmap = csr ? bitmap : nullptr;
+  io.hbits = (c.pen_on && a.hist_bits) ? a.hist_bits + (int64_t)row * hist_words(V) : nullptr;
+  io.out_tok = a.out_tok + row;
+  io.rng = a.rng ? a.rng + row : nullptr;
+  io.masked = a.out_masked ? a.out_masked + (int64_t)row * V : nullptr;
+  io.stats = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
+  io.join = a.hist_bits ? a.hist_bits + (int64_t)row * hist_words(V) : nullptr;
+  io.stop_token = a.stop_token;
+  const float ninf = neg_inf();
+
+  // history offsets first (the ids depend on them), then the row into LDS
+  // with coalesced 16-byte loads, then the first history ids
+  int64_t h0 = 0, h1 = 0;
+  if (csr) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
+  }
+  float* val;
+  if (io.xf) {
+    StepFetch f;
+    step_fetch(io.xf, V, f);
+    val = step_store(io.xf, V, f, vbuf);
+  } else {
+    val = stage_row_bf16(io.xb, V, vbuf);
+  }
+  const int hid = (csr && h0 + t < h1) ? a.hist_ids[h0 + t] : -1;
+  // penalty bits of this thread's ids: words lo/32 .. lo/32 + 2 (up to 65 ids
+  // from bit lo % 32 span at most three words)
+  static_assert(PT <= 65, "a thread's ids span at most three bitmap words");
+  uint32_t pw[3] = {0u, 0u, 0u};
+  if (io.hbits && n > 0) {
+    const int w0 = lo >> 5, hwn = hist_words(V);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) pw[q] = (w0 + q < hwn) ? io.hbits[w0 + q] : 0u;
+  }
+  // LDS: the history bitmap and the histograms start at zero
+  const int nw = bitmap_words(V);
+  if (csr)
+    for (int i = t; i < nw; i += kStepThreads) bitmap[i] = 0u;
+  if (!c.greedy)
+    for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
+  __syncthreads();
+  if (csr) {
+    if (hid >= 0 && hid < V) atomicOr(&bitmap[hid >> 5], 1u << (hid & 31));   // sampling.cpp:24
+    for (int64_t j = h0 + t + kStepThreads; j < h1; j += kStepThreads) {
+      const int id = a.hist_ids[j];
+      if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    if (n > 0) {
+      const int w0 = lo >> 5;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) pw[q] = (w0 + q < nw) ? bitmap[w0 + q] : 0u;
+    }
+  }
+  C4S_PHASE(1);
+  if (c.pen_on) {
+    // sampling.cpp:19-28 on this thread's ids in LDS, one set bit at a time
+    // (each distinct id once); the row in LDS is the penalised row from here on
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int b0 = (lo & ~31) + 32 * q;
+      uint32_t bits = pw[q];
+      if (b0 < lo) bits &= ~0u << (lo - b0);
+      if (b0 + 32 > lo + n) bits &= (lo + n - b0 <= 0) ? 0u : (lo + n - b0 >= 32 ? ~0u : (1u << (lo + n - b0)) - 1u);
+      while (bits) {
+        const int i = b0 + __ffs(bits) - 1;
+        bits &= bits - 1;
+        const float x = val[i];
+        val[i] = (x < 0) ? x * c.pen : x / c.pen;   // sampling.cpp:26
+      }
+    }
+  }
+  float y[PT];   // this thread's ids (odd stride: no LDS bank conflicts)
+#pragma unroll
+  for (int j = 0; j < PT; ++j) y[j] = (j < n) ? val[lo + j] : ninf;
+
+  if (c.greedy) {   // text2semantic.cpp:144-145: argmax of the penalised row, first maximum
+    float bv = ninf;
+    int bi = INT_MAX;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      if (j < n) argmax_merge(bv, bi, y[j], lo + j);
+    block_argmax<kStepThreads>(bv, bi, sh.redf, sh.redi);
+    if (io.masked)
+#pragma unroll
+      for (int j = 0; j < PT; ++j)
+        if (j < n) io.masked[lo + j] = y[j];
+    if (t == 0) step_out(io, V, bi, 0ull, false, 8u | 16u, 0u, 0u, (uint32_t)V);
+    return;
+  }
+
+  // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----
+  float z[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? y[j] / c.temp : y[j];
+  {
+    float lm = ninf;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) lm = fmaxf(lm, z[j]);
+    lm = wave_max_dpp(lm);
+    if (lane == 0) ss.wmax[w] = lm;
+  }
+  C4S_PHASE(2);
+  __syncthreads();
+  C4S_PHASE(3);
+  float m = ninf;
+#pragma unroll
+  for (int i = 0; i < kStepWaves; ++i) m = fmaxf(m, ss.wmax[i]);
+  const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 removes while cum <= 1 - p
+  const bool topk = c.topk_on;
+  const bool dense = !topk && thr <= 0.0;
+  // The draw's maximum starts from -1e30f (text2semantic.cpp:150): below it, or
+  // for an all -inf row, or with p <= 0, the multi-pass chain decides.
+  bool one_pass = !(m < -1e30f) && thr < 1.0;
+  int verdict = 0;
+  bool tp_exact = false;
+  if (one_pass) {
+    // fp32 masses; the dense rows' kept set; the histogram (counts for top_k,
+    // masses for top_p). Sums per thread in fp32: bound (2^-20 + PT 2^-24)
+    // relative (terms and summation) + 2^-125 a term (underflow).
+    float s32 = 0.0f;
+    uint32_t flags = 0, kc = 0, nf = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      if (j < n && z[j] != ninf) {
+        const float tt = z[j] - m;
+        float ej = topk ? 0.0f : mass32(tt);
+        if (dense) {
+          // p == 1 removes the zero-mass positions: exp((double)tt) == 0 below
+          // about -745.13; near that, and for subnormal kept masses, the chain decides
+          const bool kp = thr < 0.0 || tt > -745.0f;
+          if ((thr == 0.0 && tt <= -745.0f && tt >= -745.25f) || (kp && tt < -690.0f)) flags = 1u;
+          if (!kp) ej = 0.0f;
+          kc += kp ? 1u : 0u;
+        }
+        s32 += ej;
+        ++nf;
+        if (!dense) {
+          const int b = bucket_of(z[j], m);
+          if (b < kNB - 1) {
+            if (topk) atomicAdd(&hc[w * kNB + b], 1u);
+            else atomicAdd(&hm[w * kNB + b], (unsigned long long)(ej * 0x1p32f));
+          }
+        }
+      }
+    }
+    const double s = (double)s32;
+    const double er = s * (0x1p-20 + PT * 0x1p-24) + (double)nf * 0x1p-125;
+    C4S_PHASE(4);
+    const Scan2 sc = block_scan2(s, er, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
+    C4S_PHASE(5);
+    const uint32_t n_pos = sc.utot & 0xFFFFu;   // dense rows: kept ids with a finite value
+    // p == 1 with min_keep above the positive-mass count keeps zero-mass values
+    // unmasked (sampling.cpp:67-68): the multi-pass chain handles that
+    if ((sc.utot >> 16) || (dense && thr == 0.0 && n_pos < (uint32_t)max(0, c.min_keep))) {
+      one_pass = false;
+    } else if (dense) {
+      // nothing to cut: the draw over the fp32 masses scanned above
+      const KeptRule kr{true, thr < 0.0, 0ull};
+      if (io.masked)
+#pragma unroll
+        for (int j = 0; j < PT; ++j)
+          if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
+      C4S_PHASE(10);
+      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u);
+      C4S_PHASE(15);
+      return;
+    } else {
+      const double S = sc.tot, errS = sc.tot2;
+      // boundary buckets: threads 0..255 merge one bucket each over the waves,
+      // then wave 0 scans them (lane l holds buckets 4l .. 4l+3)
+      uint32_t* bcnt = reinterpret_cast<uint32_t*>(sbuf);           // sort buffers are free here
+      double* bmass = reinterpret_cast<double*>(sbuf) + kNB;
+      if (t < kNB) {
+        uint32_t cn = 0;
+        unsigned long long ms = 0ull;
+#pragma unroll
+        for (int i = 0; i < kStepWaves; ++i) {
+          cn += hc[i * kNB + t];
+          ms += hm[i * kNB + t];
+        }
+        bcnt[t] = cn;
+        bmass[t] = (double)ms * 0x1p-32;
+      }
+      __syncthreads();
+      if (w == 0) {
+        uint32_t c4[4], lc = 0;
+        double m4[4], lmass = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          c4[q] = bcnt[4 * lane + q];
+          m4[q] = bmass[4 * lane + q];
+          lc += c4[q];
+          lmass += m4[q];
+        }
+        const uint32_t ci = wave_scan_u32(lc);
+        const double mi = wave_scan_f64(lmass);
+        uint32_t crun = ci - lc;
+        double mrun = mi - lmass;
+        int blo = -1, bhi = -1;
+        uint32_t above = 0;
+        const double B = S - thr * S;   // the mass the kept entries hold
+        const double Blo = B * (1.0 - 1e-3) - errS, Bhi = B * (1.0 + 1e-3) + errS;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int b = 4 * lane + q;
+          const double nx = mrun + m4[q];
+          if (topk) {
+            if (blo < 0 && crun + c4[q] >= (uint32_t)c.k) { blo = b; bhi = b; above = crun; }
+          } else {
+            if (blo < 0 && nx >= Blo) { blo = b; above = crun; }
+            if (bhi < 0 && nx >= Bhi) bhi = b;
+          }
+          mrun = nx;
+          crun += c4[q];
+        }
+        const uint64_t hl = __ballot(blo >= 0), hh = __ballot(bhi >= 0);
+        int rlo = -1, rhi = -1, rab = 0;
+        if (hl) {
+          const int f = __ffsll((unsigned long long)hl) - 1;
+          rlo = (int)readlane_u32((uint32_t)blo, f);
+          rab = (int)readlane_u32(above, f);
+        }
+        if (hh) rhi = (int)readlane_u32((uint32_t)bhi, __ffsll((unsigned long long)hh) - 1);
+        if (lane == 0) { ss.bsel[0] = rlo; ss.bsel[1] = rhi; ss.bsel[2] = rab; ss.nx = 0u; }
+      }
+      __syncthreads();
+      C4S_PHASE(6);
+      const int blo = ss.bsel[0], bhi = ss.bsel[1];
+      if (blo < 0 || bhi < 0) {
+        one_pass = false;
+      } else {
+        // X: the entries to sort. top_k: every bucket up to the k-th value (the
+        // survivors then are a prefix of X). top_p: the boundary buckets (every
+        // entry above them is kept, every entry below removed).
+        const int xlo = topk ? 0 : blo, xhi = bhi;
+        float ma32 = 0.0f;
+        uint32_t na = 0;   // entries above the boundary buckets
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+          if (j < n) {
+            const int b = bucket_of(z[j], m);
+            if (b >= xlo && b <= xhi) {
+              const uint32_t slot = atomicAdd(&ss.nx, 1u);
+              if (slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
+            } else if (b < xlo) {
+              ma32 += mass32(z[j] - m);
+              ++na;
+            }
+          }
+        }
+        double ma = (double)ma32;
+        double ema = ma * (0x1p-20 + PT * 0x1p-24) + (double)na * 0x1p-125;
+        ma = wave_sum_dpp(ma);
+        ema = wave_sum_dpp(ema);
+        na = wave_sum_u32(na);
+        if (lane == 0) { ss.wc[w] = ma; ss.wd[w] = ema; ss.wv[w] = na; }
+        __syncthreads();
+        C4S_PHASE(7);
+        const int nX = (int)ss.nx;
+        double Ma = 0.0, eMa = 0.0;
+        uint32_t n_above = 0;
+#pragma unroll
+        for (int i = 0; i < kStepWaves; ++i) { Ma += ss.wc[i]; eMa += ss.wd[i]; n_above += ss.wv[i]; }
+        if (nX > kSortCap) {
+          one_pass = false;
+        } else {
+          int P2 = 1;
+          while (P2 < nX) P2 <<= 1;
+          const bool block = P2 > kWave;
+          uint64_t v = 0ull;
+          if (block) {
+            v = t < nX ? list[t] : 0ull;
+            v = sort_desc(v, P2, sbuf);
+            if (t < nX) list[t] = v;
+            __syncthreads();
+            C4S_PHASE(8);
+            decide_cut<true>(c, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+          } else if (w == 0) {
+            v = lane < nX ? list[lane] : 0ull;
+            v = sort_desc(v, P2, sbuf);
+            C4S_PHASE(8);
+            decide_cut<false>(c, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+          }
+          __syncthreads();
+          verdict = ss.verdict;
+          if (verdict == 2) {
+            // decide again with every mass in double (S and the mass above the boundary)
+            tp_exact = true;
+            double se = 0.0, sa = 0.0;
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+              if (j < n && z[j] != ninf) {
+                const double ed = exp((double)(z[j] - m));
+                se += ed;
+                if (bucket_of(z[j], m) < xlo) sa += ed;
+              }
+            }
+            se = wave_sum_dpp(se);
+            sa = wave_sum_dpp(sa);
+            if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; }
+            __syncthreads();
+            double Se = 0.0, Mae = 0.0;
+#pragma unroll
+            for (int i = 0; i < kStepWaves; ++i) { Se += ss.wc[i]; Mae += ss.wd[i]; }
+            if (block) decide_cut<true>(c, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            else if (w == 0) decide_cut<false>(c, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            __syncthreads();
+            verdict = ss.verdict;
+          }
+          C4S_PHASE(9);
+          if (verdict != 1) one_pass = false;
+        }
+      }
+    }
+  }
+  if (one_pass) {
+    // the draw over the kept set: key >= the last kept key
+    const uint64_t kthr = ss.kthr;
+    const KeptRule kr{false, false, kthr};
+    float ks32 = 0.0f;
+    uint32_t kc = 0, flags = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      if (j < n) {
+        bool kp;
+        const float ej = kept_mass32(kr, z[j], m, lo + j, kp);
+        if (kp && z[j] != ninf) {
+          if (z[j] - m < -690.0f) flags = 1u;   // subnormal kept masses: libm implementations may disagree
+          ++kc;
+        }
+        ks32 += ej;
+        if (io.masked) io.masked[lo + j] = kp ? z[j] : ninf;
+      }
+    }
+    const double ks = (double)ks32;
+    const double ek = ks * (0x1p-20 + PT * 0x1p-24) + (double)kc * 0x1p-125;
+    const Scan2 ds = block_scan2(ks, ek, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
+    C4S_PHASE(10);
+    if ((ds.utot >> 16) == 0u) {
+      draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
+                      tp_exact ? 1u : 0u);
+      C4S_PHASE(15);
+      return;
+    }
+  }
+  // ---- the multi-pass chain on the row staged in LDS (c4s_chain.hpp) ----
+  __syncthreads();   // every thread is done with the work area
+  chain_fallback(io, c, work, val, sh);
 }
 
 __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
@@ -249,6 +700,10 @@ size_t stream_lds_bytes(int V, int) { return rows_lds_bytes(V); }
 
 size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
 
+size_t rows_step_lds_bytes(int V) {
+  return step_work_bytes(V) + 4 * ((size_t)vpad(V) + 4) + 4 * (size_t)bitmap_words(V);
+}
+
 hipError_t launch_hist_bits_init(const int32_t* ids, const int64_t* off, int n_rows, int V, uint32_t* bits,
                                  hipStream_t s) {
   if (n_rows <= 0) return hipSuccess;
@@ -260,7 +715,14 @@ hipError_t launch_hist_bits_init(const int32_t* ids, const int64_t* off, int n_r
 hipError_t launch_rows(const RowsArgs& a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
   (void)hipGetLastError();  // report only this launch's status
-  if (a.vocab <= kLdsVocabMax) {
+  if (a.vocab <= kLdsVocabMax && a.mode == 0u) {
+    const size_t lds = rows_step_lds_bytes(a.vocab);
+    const int P = ((a.vocab + kStepThreads - 1) / kStepThreads) | 1;   // ids a thread owns (odd_chunk)
+    const dim3 g(a.n_rows), b(kStepThreads);
+    if (P <= 9) hipLaunchKernelGGL(k_rows_step<9>, g, b, lds, s, a);
+    else if (P <= 17) hipLaunchKernelGGL(k_rows_step<17>, g, b, lds, s, a);
+    else hipLaunchKernelGGL(k_rows_step<25>, g, b, lds, s, a);
+  } else if (a.vocab <= kLdsVocabMax) {
     const size_t lds = rows_lds_bytes(a.vocab);
     hipLaunchKernelGGL(k_rows_lds, dim3(a.n_rows), dim3(NT), lds, s, a);
   } else {

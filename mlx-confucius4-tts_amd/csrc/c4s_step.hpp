@@ -1,0 +1,411 @@
+// One AR step of the reference chain for one row, decided in one pass over
+// the row (k_rows_step).
+//
+// The chain is the reference's (text2semantic.cpp:142-166, sampling.cpp:14-76):
+// penalty -> greedy ? argmax : temperature -> top_k -> top_p -> draw. Thread t of
+// the step workgroup owns the ids [t*P, t*P + P) (P odd) and keeps their values in
+// registers (the row is staged in LDS with coalesced 16-byte loads). After the
+// row maximum m:
+//
+//  * masses exp(t), t = fl(z - m), are first taken in fp32 (mass32, with an
+//    error bound per term); every value falls in a bucket of (m - z) (four
+//    buckets per unit, the last one unbounded), and one histogram pass (per-wave
+//    counters in LDS, masses in 2^-32 fixed point) locates the bucket of the k-th largest
+//    value (top_k) or the nucleus boundary (top_p: a window of +-1e-3 relative
+//    around the kept mass p * S, far wider than the fp32 errors);
+//  * only the entries of the boundary buckets (every bucket up to the k-th
+//    value for top_k) are sorted, by (value desc, id asc), with a bitonic
+//    network (lane shuffles inside a wave, LDS across waves), and their masses
+//    are the reference's exp((double)t) (sampling.cpp:55);
+//  * the cut is taken on the sorted entries with sums formed in parallel, each
+//    decision with the margin rel_eps(V) * S plus the fp32 error bounds; a
+//    decision inside it is taken again with every mass in double;
+//  * the kept set is then every id whose key (value, then lower id first) is
+//    at or above the last kept key; the draw is one workgroup scan of the
+//    kept fp32 masses in id order (thread order) and a walk of the one thread
+//    whose range holds r = u * K, accepted when r is farther than the error
+//    bounds from both ends of the chosen id's interval. Otherwise that
+//    thread's wave recomputes the whole draw in double from the row
+//    (text2semantic.cpp:150-165; sequentially when even that is too close).
+//
+// Rows the one pass cannot settle (an all -inf row or one below the draw's
+// -1e30 floor, p <= 0, a boundary of more than 1024 entries or in the
+// unbounded bucket, a cut inside the margin even in double, subnormal kept
+// masses) return false before the RNG or any output changes; the kernel then
+// runs the multi-pass chain (run_chain) on the row staged in LDS.
+
+#pragma once
+
+#include "c4s_chain.hpp"
+
+namespace c4s {
+namespace {
+
+constexpr int kNB = 256;                 // buckets of (m - z) * kBucketScale; the last is unbounded
+constexpr float kBucketScale = 4.0f;
+// Threads of the workgroup that owns a row in the one-pass step.
+constexpr int kStepThreads = 512;
+constexpr int kStepWaves = kStepThreads / kWave;
+static_assert(kStepThreads >= kNB && kStepThreads <= NT, "one bucket per thread in the merge");
+constexpr int kSortCap = kStepThreads;   // boundary entries one sort handles (one per thread)
+// Work area of the one-pass step (aliases the mass cache of the fallback
+// chain): per-wave bucket counters and masses (64-bit fixed point, 2^-32
+// units: integer LDS atomics), two sort exchange buffers, the boundary entries.
+constexpr size_t kHistBytes = (size_t)kStepWaves * kNB * 4;
+constexpr size_t kStepWorkBytes = 3 * kHistBytes + 3 * (size_t)kSortCap * 8;
+
+__host__ __device__ __forceinline__ size_t step_work_bytes(int V) {
+  const size_t e = 8 * (size_t)vpad(V);
+  return e > kStepWorkBytes ? e : kStepWorkBytes;
+}
+
+using StepScratch = ScratchT<kStepWaves>;
+
+// Coalesced fetch of an f32 row (V <= kLdsVocabMax) by the step workgroup into
+// registers, then into LDS (the layout of fetch_row / store_row).
+constexpr int kStepQuads = (kLdsVocabMax / 4 + kStepThreads - 1) / kStepThreads;
+struct StepFetch {
+  float4 body[kStepQuads];
+  float edge;
+};
+__device__ __forceinline__ void step_fetch(const float* p, int V, StepFetch& f) {
+  const RowShape r = row_shape(p, V);
+  const float4* p4 = reinterpret_cast<const float4*>(p + r.head);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kStepQuads; ++j) {
+    const int q = t + kStepThreads * j;
+    f.body[j] = (q < r.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  f.edge = (t < r.head) ? p[t] : ((t < r.head + r.tail) ? p[r.head + 4 * r.nq + (t - r.head)] : 0.f);
+}
+__device__ __forceinline__ float* step_store(const float* p, int V, const StepFetch& f, float* buf) {
+  const RowShape r = row_shape(p, V);
+  float* val = buf + ((4 - r.head) & 3);
+  const int t = threadIdx.x;
+  float4* body = reinterpret_cast<float4*>(val + r.head);
+#pragma unroll
+  for (int j = 0; j < kStepQuads; ++j) {
+    const int q = t + kStepThreads * j;
+    if (q < r.nq) body[q] = f.body[j];
+  }
+  if (t < r.head) val[t] = f.edge;
+  else if (t < r.head + r.tail) val[r.head + 4 * r.nq + (t - r.head)] = f.edge;
+  return val;
+}
+
+struct StepSh {
+  float wmax[NW];
+  // per-wave partials of the workgroup scans; each set is written again only
+  // after a barrier that follows every read of its previous contents
+  double wa[NW], wb[NW], wc[NW], wd[NW], we[NW], wf[NW];
+  uint32_t wu[NW], wv[NW], ww[NW];
+  int bsel[3];       // first boundary bucket, last boundary bucket, entries above the first
+  uint32_t nx;       // boundary entries (compaction counter)
+  uint64_t kthr;     // kept iff key64 >= kthr
+  int verdict;       // 1 decided, 2 decide again with every mass in double, 0 multi-pass chain
+};
+
+constexpr float kStepLog2e = 1.44269502162933349609375f;   // fp32(log2 e)
+constexpr float kStepLog2eLo = 1.925963033500011e-8f;       // log2 e - kStepLog2e
+constexpr float kStepLn2 = 0.693147180559945309f;
+
+// exp(t) for a finite t <= 0 in fp32, as 2^th * 2^tl with th + tl = t log2 e
+// carried in two parts. Its error against exp((double)t) is below
+// mass32_err(e) (v_exp_f32 to about an ulp, the rest below 2^-24 relative;
+// fp32 underflow below 2^-126 absolute).
+__device__ __forceinline__ float mass32(float t) {
+  const float th = t * kStepLog2e;
+  const float tl = fmaf(t, kStepLog2e, -th) + t * kStepLog2eLo;
+  const float e = __builtin_amdgcn_exp2f(th);
+  return fmaf(e * kStepLn2, tl, e);
+}
+__device__ __forceinline__ double mass32_err(float e) { return (double)e * 0x1p-20 + 0x1p-125; }
+
+__device__ __forceinline__ int bucket_of(float z, float m) {
+  const float q = (m - z) * kBucketScale;   // monotone in z; +inf for z = -inf
+  return q < (float)(kNB - 1) ? (int)q : kNB - 1;
+}
+
+// Strict total order of the chain: value descending, then lower id first
+// (the declared top_p tie order).
+__device__ __forceinline__ uint64_t key64(float z, int id) {
+  return ((uint64_t)fkey(z) << 32) | (uint64_t)(~(uint32_t)id);
+}
+__device__ __forceinline__ float key_value(uint64_t k) { return kfloat((uint32_t)(k >> 32)); }
+
+// Workgroup scan (thread order) of a double v: exclusive and inclusive prefix
+// and total, with a second double summed and a u32 summed over the
+// workgroup, one barrier. The inclusive prefix of thread t is bitwise the
+// exclusive prefix of thread t + 1 and the last thread's is the total, so the
+// intervals (ex, in] tile (0, total].
+struct Scan2 {
+  double ex, in, tot, tot2;
+  uint32_t utot;
+};
+__device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, double* wa, double* wb,
+                                             uint32_t* wu) {
+  const int lane = lane_id(), w = wave_id();
+  const double inc = wave_scan_f64(v);
+  double exc = __shfl_up(inc, 1, kWave);
+  if (lane == 0) exc = 0.0;
+  const double s2 = wave_sum_dpp(v2);
+  const uint32_t us = wave_sum_u32(u);
+  if (lane == kWave - 1) wa[w] = inc;
+  if (lane == 0) { wb[w] = s2; wu[w] = us; }
+  __syncthreads();
+  Scan2 r;
+  double base = 0.0, run = 0.0, t2 = 0.0;
+  uint32_t ut = 0;
+#pragma unroll
+  for (int i = 0; i < kStepWaves; ++i) {
+    if (i == w) base = run;
+    run += wa[i];
+    t2 += wb[i];
+    ut += wu[i];
+  }
+  r.ex = base + exc;
+  r.in = base + inc;
+  r.tot = run;
+  r.tot2 = t2;
+  r.utot = ut;
+  return r;
+}
+
+// Descending bitonic sort of P2 (a power of two, <= kSortCap) distinct keys,
+// one per thread t < P2 (threads at or above P2 carry padding among
+// themselves). Stages across waves exchange through `buf` (two halves of
+// kSortCap keys, one barrier each), stages inside a wave through lane
+// shuffles. For P2 <= 64 only wave 0 calls it and no barrier runs.
+__device__ __forceinline__ uint64_t sort_desc(uint64_t v, int P2, uint64_t* buf) {
+  const int t = threadIdx.x;
+  int half = 0;
+  for (int k = 2; k <= P2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint64_t p;
+      if (j >= kWave) {
+        buf[half * kSortCap + t] = v;
+        __syncthreads();
+        p = buf[half * kSortCap + (t ^ j)];
+        half ^= 1;
+      } else {
+        p = __shfl_xor(v, j, kWave);
+      }
+      const bool take_max = ((t & j) == 0) == ((t & k) == 0);
+      v = take_max ? (v > p ? v : p) : (v < p ? v : p);
+    }
+  }
+  return v;
+}
+
+// Where one row's inputs and outputs are (the kernel's view of c4s_rows).
+struct StepIO {
+  const float* xf;           // f32 row or null
+  const uint16_t* xb;        // bf16 row or null
+  const uint32_t* bitmap;    // penalised ids: LDS bitmap (CSR history) or null
+  const uint32_t* hbits;     // penalised ids: the caller's history set or null
+  int32_t* out_tok;          // this row's token
+  uint64_t* rng;             // this row's state
+  float* masked;             // row or null
+  uint32_t* stats;           // 4 words or null
+  uint32_t* join;            // the history set that the token joins, or null
+  int stop_token;
+};
+
+// The value of id i as the chain sees it before the temperature (penalty applied).
+__device__ __forceinline__ float step_value(const StepIO& io, const RowCfg& c, int i) {
+  float x = io.xf ? io.xf[i] : __uint_as_float((uint32_t)io.xb[i] << 16);
+  if (c.pen_on) {
+    const uint32_t wd = io.bitmap ? io.bitmap[i >> 5] : io.hbits[i >> 5];
+    if ((wd >> (i & 31)) & 1u) x = (x < 0) ? x * c.pen : x / c.pen;   // sampling.cpp:26
+  }
+  return x;
+}
+
+// The kept set of the draw, as the one pass decided it.
+struct KeptRule {
+  bool dense;      // every id with a positive mass (thr == 0) or every id (thr < 0)
+  bool all;        // thr < 0
+  uint64_t kthr;   // otherwise: key64 >= kthr
+};
+__device__ __forceinline__ bool kept_by(const KeptRule& kr, float z, float m, int id) {
+  if (kr.dense) return kr.all || (z != neg_inf() && exp((double)(z - m)) > 0.0);
+  return key64(z, id) >= kr.kthr;
+}
+// The same test in the one pass (dense rows whose t = fl(z - m) lies within
+// [-745.25, -745] leave it, so `t > -745` decides there), and the fp32 mass.
+__device__ __forceinline__ float kept_mass32(const KeptRule& kr, float z, float m, int id, bool& kept) {
+  const bool fin = z != neg_inf();
+  kept = kr.dense ? (kr.all || (fin && z - m > -745.0f)) : key64(z, id) >= kr.kthr;
+  return (kept && fin) ? mass32(z - m) : 0.0f;
+}
+
+// The draw recomputed in double by one wave from the row (text2semantic.cpp:
+// 150-165): the kept masses exp((double)fl(z - m)) summed in parallel and the
+// first id whose prefix reaches r = u * sum taken when both ends of its
+// interval are farther than rel_eps from r; otherwise the reference's
+// sequential sums in id order.
+__device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const KeptRule& kr, float m, double u) {
+  const int lane = lane_id();
+  const int V = c.V;
+  auto mass_at = [&](int i) -> double {
+    if (i >= V) return 0.0;
+    const float y = step_value(io, c, i);
+    const float z = c.temp_on ? y / c.temp : y;
+    return (z != neg_inf() && kept_by(kr, z, m, i)) ? exp((double)(z - m)) : 0.0;
+  };
+  double tot = 0.0;
+  for (int base = 0; base < V; base += kWave) tot += wave_sum_dpp(mass_at(base + lane));
+  const double r = u * tot;
+  const double eps = rel_eps(V);
+  if (!(r > 0.0)) return 0;
+  double carry = 0.0;
+  for (int base = 0; base < V; base += kWave) {
+    const double e = mass_at(base + lane);
+    const double inc = wave_scan_f64(e) + carry;
+    const uint64_t hit = __ballot(e > 0.0 && inc >= r);
+    if (hit) {
+      const int f = __ffsll((unsigned long long)hit) - 1;
+      const double af = readlane_f64(inc, f), pf = af - readlane_f64(e, f);
+      if ((af - r > eps * af) && (r - pf > eps * r)) return base + f;
+      break;
+    }
+    carry = readlane_f64(inc, kWave - 1);
+  }
+  // sequential, in id order, as the reference sums
+  double total = 0.0;
+  for (int base = 0; base < V; base += kWave) {
+    const double e = mass_at(base + lane);
+    const int cnt = min(kWave, V - base);
+    for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+  }
+  const double rr = u * total;
+  if (!(rr > 0.0)) return 0;
+  double acc = 0.0;
+  for (int base = 0; base < V; base += kWave) {
+    const double e = mass_at(base + lane);
+    const int cnt = min(kWave, V - base);
+    for (int q = 0; q < cnt; ++q) {
+      acc += __shfl(e, q, kWave);
+      if (rr <= acc) return base + q;
+    }
+  }
+  return V - 1;
+}
+
+// The nucleus / top-k cut on the sorted boundary entries, by the whole
+// workgroup (kBlock, more than 64 entries) or by wave 0. v: this thread's
+// sorted entry (valid below nX). S, errS: the sum of all masses and its error
+// bound (rows without top-k); Ma, errMa: the mass above the boundary buckets
+// and its bound. Writes sh.kthr and sh.verdict (1; 2 when a decision falls
+// inside the margin while fp32 errors remain; 0).
+template <bool kBlock>
+__device__ __noinline__ void decide_cut(const RowCfg& c, uint64_t v, int nX, float m, double thr, double S, double errS,
+                           double Ma, double errMa, uint32_t n_above, const uint64_t* list, StepSh& sh) {
+  const int t = threadIdx.x, lane = lane_id();
+  const bool topk = c.topk_on;
+  const bool valid = t < nX;
+  const float ninf = neg_inf();
+  const float zt = valid ? key_value(v) : ninf;
+  // top_k (sampling.cpp:30-40): survivors are the entries >= the k-th largest value
+  uint32_t kkey = 0;
+  if (topk) kkey = kBlock ? (uint32_t)(list[c.k - 1] >> 32) : readlane_u32((uint32_t)(v >> 32), c.k - 1);
+  const bool surv = valid && (!topk || (uint32_t)(v >> 32) >= kkey);
+  const double et = (surv && zt != ninf) ? exp((double)(zt - m)) : 0.0;
+  double ex, tot;
+  if (kBlock) {
+    const Scan2 sc = block_scan2(et, 0.0, 0u, sh.we, sh.wf, sh.wv);
+    ex = sc.ex;
+    tot = sc.tot;
+  } else {
+    const double inc = wave_scan_f64(et);
+    ex = __shfl_up(inc, 1, kWave);
+    if (lane == 0) ex = 0.0;
+    tot = readlane_f64(inc, kWave - 1);
+  }
+  // entry removed iff the mass at or below it in ascending order,
+  // M = S - (mass above it), is <= (1 - p) S (sampling.cpp:60-65)
+  const double Sx = topk ? tot : S;   // after top_k only the survivors carry mass
+  const double err = topk ? 0.0 : 2.0 * errS + errMa;
+  const double above = topk ? ex : Ma + ex;
+  const double A = thr * Sx;
+  const double M = Sx - above;
+  bool kept, unsure;
+  if (thr <= 0.0) {   // p >= 1 (top_k rows only here): only zero-mass positions can go
+    kept = surv && (thr < 0.0 || et > 0.0);
+    unsure = false;
+  } else {
+    kept = surv && M > A;
+    unsure = surv && !(fabs(M - A) > rel_eps(c.V) * Sx + err);
+  }
+  uint32_t nk, ns, nuns;
+  if (kBlock) {
+    const Scan2 cn = block_scan2(0.0, 0.0, (kept ? 1u : 0u) | (surv ? 1u << 11 : 0u) | (unsure ? 1u << 22 : 0u),
+                                 sh.wc, sh.wd, sh.ww);
+    nk = cn.utot & 2047u;
+    ns = (cn.utot >> 11) & 2047u;
+    nuns = cn.utot >> 22;
+  } else {
+    nk = (uint32_t)__popcll(__ballot(kept));
+    ns = (uint32_t)__popcll(__ballot(surv));
+    nuns = (uint32_t)__popcll(__ballot(unsure));
+  }
+  // min_tokens_to_keep (sampling.cpp:67-68): the top min_keep positions stay
+  const uint32_t mk = (uint32_t)max(0, c.min_keep);
+  int verdict = 1;
+  if (nuns) {
+    verdict = err > 0.0 ? 2 : 0;
+  } else if (topk) {
+    if (nk < mk) nk = min(mk, ns);
+  } else if (n_above + nk < mk) {
+    if (mk > n_above + (uint32_t)nX) verdict = 0;
+    else nk = mk - n_above;
+  }
+  if (t == 0) sh.verdict = verdict;
+  // the last kept entry; with none kept here, everything above the boundary buckets
+  if (verdict == 1 && t == (nk > 0 ? (int)nk - 1 : 0)) sh.kthr = nk > 0 ? v : v + 1ull;
+}
+
+}  // namespace
+}  // namespace c4s
+
+namespace c4s {
+namespace {
+
+// Stages a bf16 row in LDS as fp32 with 16-byte loads (eight ids each): the
+// 0-7 ids before the first 16-byte boundary and the 0-7 after the last one go
+// one per thread. Returns where the row starts (buf + 0..3, the body 16-byte
+// aligned). V <= kLdsVocabMax.
+constexpr int kStepOcts = (kLdsVocabMax / 8 + kStepThreads - 1) / kStepThreads;
+__device__ __forceinline__ float* stage_row_bf16(const uint16_t* p, int V, float* buf) {
+  const int head = min(V, (int)(((16u - ((uint32_t)(uintptr_t)p & 15u)) & 15u) >> 1));
+  const int nq = (V - head) >> 3;
+  const int tail = V - head - 8 * nq;
+  float* val = buf + ((4 - (head & 3)) & 3);
+  const uint4* p8 = reinterpret_cast<const uint4*>(p + head);
+  const int t = threadIdx.x;
+  uint4 q[kStepOcts];
+#pragma unroll
+  for (int j = 0; j < kStepOcts; ++j) {
+    const int i = t + kStepThreads * j;
+    q[j] = (i < nq) ? p8[i] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  const int eidx = (t < head) ? t : ((t < head + tail) ? head + 8 * nq + (t - head) : -1);
+  const uint16_t ev = (eidx >= 0) ? p[eidx] : (uint16_t)0;
+  auto lo16 = [](uint32_t x) { return __uint_as_float(x << 16); };
+  auto hi16 = [](uint32_t x) { return __uint_as_float(x & 0xFFFF0000u); };
+#pragma unroll
+  for (int j = 0; j < kStepOcts; ++j) {
+    const int i = t + kStepThreads * j;
+    if (i < nq) {
+      float4* d = reinterpret_cast<float4*>(val + head + 8 * i);
+      d[0] = make_float4(lo16(q[j].x), hi16(q[j].x), lo16(q[j].y), hi16(q[j].y));
+      d[1] = make_float4(lo16(q[j].z), hi16(q[j].z), lo16(q[j].w), hi16(q[j].w));
+    }
+  }
+  if (eidx >= 0) val[eidx] = __uint_as_float((uint32_t)ev << 16);
+  return val;
+}
+
+}  // namespace
+}  // namespace c4s

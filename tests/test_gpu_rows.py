@@ -29,11 +29,9 @@ def test_batch64_one_step(orc, gpu_ctx, seed):
     print(f"batch64 seed={seed}", flush=True)
     tok, st = compare_with_oracle(orc, gpu_ctx, b)
     print("exact top_p passes", int(st[:, 1].sum()), "exact draws", int(st[:, 2].sum()))
-    fast = (st[:, 0] & 16) != 0
-    topk = (b.top_k > 0) & (b.top_k <= 64)
-    print("fast path rows", int(fast.sum()), "of", int(topk.sum()), "top-k rows")
-    assert not fast[~topk].any()
-    assert fast[topk].mean() > 0.8
+    one_pass = (st[:, 0] & 16) != 0
+    print("rows decided in one pass", int(one_pass.sum()), "of", b.n_rows)
+    assert one_pass.mean() > 0.9
 
 
 def test_batch64_general_rows(orc, gpu_ctx):
