@@ -179,6 +179,18 @@ int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);
  * call); rows->logits/ld/dtype/vocab/n_rows are taken from `head`. */
 int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);
 
+/* c4s_lmhead_sample without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The same kernels as
+ * c4s_lmhead_sample; the normalised rows and, when head->logits is NULL, the
+ * logits live in a static device array of 8 MiB that the library holds on each
+ * GPU until the process ends. Limits: M x D x 2 (M rounded up to 64) plus, with
+ * no logits buffer, M x V x 4 bytes within 8 MiB, and vocab <= 12288;
+ * otherwise C4S_EINVAL. Every call on one GPU shares that GPU's array (the
+ * kernels overwrite all of it that they read; nothing needs clearing): calls
+ * that overlap on one GPU, from any context or stream, race. */
+int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);
+
 /* hist_bits[b] = the set of row b's CSR history ids in [0, vocab) (ids
  * outside are skipped, sampling.cpp:24); the starting state of
  * c4s_rows.hist_bits (text2semantic.cpp:196-372 keeps gen[b] across steps). */

@@ -93,6 +93,7 @@ def lib() -> C.CDLL:
     L.c4s_hist_bits_init.argtypes = [_vp, _vp, _vp, C.c_int32, C.c_int32, _vp, _vp]
     L.c4s_lmhead.argtypes = [_vp, C.POINTER(Head), _vp]
     L.c4s_lmhead_sample.argtypes = [_vp, C.POINTER(Head), C.POINTER(Rows), _vp]
+    L.c4s_lmhead_sample_noalloc.argtypes = [_vp, C.POINTER(Head), C.POINTER(Rows), _vp]
     L.c4s_seed_single.argtypes = [C.c_uint64]
     L.c4s_seed_single.restype = C.c_uint64
     L.c4s_seed_batch.argtypes = [C.c_uint64, C.c_int32, _vp]
@@ -229,6 +230,18 @@ class Context:
                  out_stats=_p(out_stats), mode=MODE_CHAIN, hist_bits=_p(hist_bits), stop_token=stop_token)
         self._check(lib().c4s_lmhead_sample(self._h, C.byref(h), C.byref(r), _stream_handle(stream)),
                     "lmhead_sample")
+
+    def lmhead_sample_noalloc(self, hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k,
+                              top_p, pen, rng, out_token, logits=None, do_sample=None, out_masked=None,
+                              out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1):
+        """c4s_lmhead_sample with its workspace in the library's static device scratch."""
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+        r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp),
+                 top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
+                 rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
+                 out_stats=_p(out_stats), mode=MODE_CHAIN, hist_bits=_p(hist_bits), stop_token=stop_token)
+        self._check(lib().c4s_lmhead_sample_noalloc(self._h, C.byref(h), C.byref(r), _stream_handle(stream)),
+                    "lmhead_sample_noalloc")
 
     def hbm_probe(self, src, dst, nbytes, mode=0, stream=None):
         self._check(lib().c4s_hbm_probe(self._h, _p(src), _p(dst), nbytes, mode,

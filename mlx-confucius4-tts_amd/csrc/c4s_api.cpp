@@ -55,6 +55,9 @@ struct c4s_ctx {
   // because a captured graph may still write the old buffer when replayed.
   bool graph_used = false;
   std::vector<void*> retired;
+  // this device's address of the no-allocation entry point's static scratch
+  // (null when the runtime could not give it)
+  void* noalloc = nullptr;
 };
 
 namespace {
@@ -246,6 +249,12 @@ int c4s_create(int device, c4s_ctx** out) {
     // The code objects are built for gfx950 only.
     delete ctx;
     return C4S_EINVAL;
+  }
+  // The static scratch of c4s_lmhead_sample_noalloc: its address on this
+  // device, asked for once, with the device current.
+  if (c4s::noalloc_scratch(&ctx->noalloc) != hipSuccess) {
+    ctx->noalloc = nullptr;
+    (void)hipGetLastError();
   }
   if (hipStreamCreateWithFlags(&ctx->host_stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
@@ -512,18 +521,26 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   return C4S_OK;
 }
 
-static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out,
-                       hipStream_t s) {
-  if (!h->hidden || !h->gamma || !h->beta || !h->weight || !h->bias || !logits)
+static int lmhead_check(c4s_ctx* ctx, const c4s_head* h) {
+  if (!h->hidden || !h->gamma || !h->beta || !h->weight || !h->bias)
     return fail(ctx, C4S_EINVAL, "lmhead: required pointer is NULL");
   if (h->M < 1 || h->D < 32 || h->V < 1 || (h->D % 32) != 0)
     return fail(ctx, C4S_EINVAL, "lmhead: needs M >= 1, V >= 1, D a positive multiple of 32");
-  if (ld_out < h->V) return fail(ctx, C4S_EINVAL, "lmhead: ld_out < V");
   if ((reinterpret_cast<uintptr_t>(h->hidden) | reinterpret_cast<uintptr_t>(h->weight)) & 15u)
     return fail(ctx, C4S_EINVAL, "lmhead: hidden and weight must be 16-byte aligned");
-  const size_t mpad = (size_t)((h->M + 63) / 64 * 64);
-  int rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, mpad * (size_t)h->D * 2, "lmhead workspace", s);
-  if (rc) return rc;
+  return C4S_OK;
+}
+
+// Bytes of normalised rows the LM head stages (rows padded to the 64-row tile).
+static size_t lmhead_hnorm_bytes(const c4s_head* h) {
+  return (size_t)((h->M + 63) / 64 * 64) * (size_t)h->D * 2;
+}
+
+// The LM head with its normalised-row workspace `hnorm` (lmhead_hnorm_bytes).
+static int lmhead_launch(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out, void* hnorm,
+                         hipStream_t s) {
+  if (!logits) return fail(ctx, C4S_EINVAL, "lmhead: logits is NULL");
+  if (ld_out < h->V) return fail(ctx, C4S_EINVAL, "lmhead: ld_out < V");
   c4s::LmHeadArgs a{};
   a.hidden = h->hidden;
   a.gamma = h->gamma;
@@ -536,12 +553,20 @@ static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t l
   a.M = h->M;
   a.D = h->D;
   a.V = h->V;
-  a.hnorm = static_cast<uint16_t*>(ctx->hnorm);
+  a.hnorm = static_cast<uint16_t*>(hnorm);
   hipError_t e = c4s::launch_layernorm_bf16(a, s);
   if (e != hipSuccess) return hip_fail(ctx, e, "layernorm launch");
   e = c4s::launch_lmhead_gemm(a, s);
   if (e != hipSuccess) return hip_fail(ctx, e, "lmhead gemm launch");
   return C4S_OK;
+}
+
+static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out, hipStream_t s) {
+  int rc = lmhead_check(ctx, h);
+  if (rc) return rc;
+  rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, lmhead_hnorm_bytes(h), "lmhead workspace", s);
+  if (rc) return rc;
+  return lmhead_launch(ctx, h, logits, ld_out, ctx->hnorm, s);
 }
 
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream) {
@@ -569,6 +594,40 @@ int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, 
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = lmhead_impl(ctx, head, logits, ld, s);
+  if (rc) return rc;
+  c4s_rows r = *rows;
+  r.logits = logits;
+  r.ld = ld;
+  r.dtype = C4S_DTYPE_F32;
+  r.n_rows = head->M;
+  r.vocab = head->V;
+  rc = validate_rows(ctx, &r);
+  if (rc) return rc;
+  return launch_rows_checked(ctx, &r, s);
+}
+
+int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!head || !rows) return fail(ctx, C4S_EINVAL, "descriptor is NULL");
+  if (!ctx->noalloc) return fail(ctx, C4S_EHIP, "lmhead_sample_noalloc: the static scratch has no address on this device");
+  int rc = lmhead_check(ctx, head);
+  if (rc) return rc;
+  // One AR step at a vocabulary the sampler stages in LDS needs no sampler
+  // workspace; larger vocabularies need the context's sort buffers.
+  if (head->V > c4s::kLdsVocabMax)
+    return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: vocab above 12288 needs a workspace");
+  const size_t hbytes = (lmhead_hnorm_bytes(head) + 255) & ~(size_t)255;
+  const size_t lbytes = head->logits ? 0 : (size_t)head->M * (size_t)head->V * 4;
+  if (hbytes + lbytes > c4s::kNoAllocBytes)
+    return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: M x D x 2 (rows padded to 64) + M x V x 4 (without a "
+                                 "logits buffer) exceeds the 8 MiB static scratch");
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  unsigned char* base = static_cast<unsigned char*>(ctx->noalloc);
+  float* logits = head->logits ? head->logits : reinterpret_cast<float*>(base + hbytes);
+  const int64_t ld = head->logits ? head->ld_out : head->V;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = lmhead_launch(ctx, head, logits, ld, base, s);
   if (rc) return rc;
   c4s_rows r = *rows;
   r.logits = logits;

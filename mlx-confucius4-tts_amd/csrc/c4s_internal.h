@@ -117,6 +117,11 @@ struct LmHeadArgs {
   uint16_t* hnorm;         // [M][D] bf16 scratch (normalised rows)
 };
 
+// Static device scratch of the no-allocation entry point (per device).
+constexpr size_t kNoAllocBytes = (size_t)8 << 20;
+// This device's address of that scratch (the current device).
+hipError_t noalloc_scratch(void** ptr);
+
 size_t rows_lds_bytes(int vocab);
 size_t rows_global_lds_bytes(int vocab);
 size_t stream_lds_bytes(int vocab, int unused);
