@@ -51,6 +51,11 @@ enum {
 };
 
 enum { C4S_DTYPE_F32 = 0, C4S_DTYPE_BF16 = 1 };
+/* LM head weight storage: bf16; fp32 (the reference's .npy weights load as
+ * float32, include/c4tts/npy.h:202-206); 8-bit affine groups along the input
+ * dimension, codes 0..255 as bytes (the quantized_matmul layout of
+ * src/t2s/gpt2.cpp:49-62 at 8 bits). */
+enum { C4S_W_BF16 = 0, C4S_W_F32 = 1, C4S_W_Q8 = 2 };
 
 /* Processor selection (c4s_rows.mode).
  * C4S_MODE_CHAIN runs the reference chain per row (text2semantic.cpp:142-166):
@@ -152,11 +157,15 @@ typedef struct c4s_head {
   const float* gamma;           /* [D] */
   const float* beta;            /* [D] */
   float eps;                    /* 1e-5 in the reference (nn.h:49-50) */
-  const uint16_t* weight;       /* [V][D] bf16 */
+  const void* weight;           /* [V][D] in wdtype (semantic_head.weight, [out][in]) */
   const float* bias;            /* [V] */
   int32_t M, D, V;
   float* logits;                /* [M][ld_out] f32 */
   int64_t ld_out;
+  int32_t wdtype;               /* C4S_W_*; 0 (zero-initialised descriptor) is bf16 */
+  int32_t group;                /* C4S_W_Q8: inputs per scale group: 32, 64 or 128 */
+  const float* wscale;          /* C4S_W_Q8: [V][D / group] */
+  const float* wbias;           /* C4S_W_Q8: [V][D / group]; w[n][k] = wscale * q[n][k] + wbias */
 } c4s_head;
 
 int c4s_create(int device, c4s_ctx** out);
@@ -182,11 +191,10 @@ int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, 
 /* c4s_lmhead_sample without any allocation: no counterpart in the reference.
  * For callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). The same kernels as
- * c4s_lmhead_sample; the normalised rows and, when head->logits is NULL, the
- * logits live in a static device array of 8 MiB that the library holds on each
- * GPU until the process ends. Limits: M x D x 2 (M rounded up to 64) plus, with
- * no logits buffer, M x V x 4 bytes within 8 MiB, and vocab <= 12288;
- * otherwise C4S_EINVAL. Every call on one GPU shares that GPU's array (the
+ * c4s_lmhead_sample; when head->logits is NULL the logits live in a static
+ * device array of 8 MiB that the library holds on each GPU until the process
+ * ends. Limits: M x V x 4 bytes within 8 MiB when no logits buffer is given,
+ * and vocab <= 12288; otherwise C4S_EINVAL. Every call on one GPU shares that GPU's array (the
  * kernels overwrite all of it that they read; nothing needs clearing): calls
  * that overlap on one GPU, from any context or stream, race. */
 int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);

@@ -25,6 +25,7 @@ T_ARGMAX, T_DRAW = 16, 32
 MODE_CUSTOM = 256
 STAT_PATH, STAT_TOPP_EXACT, STAT_DRAW_EXACT, STAT_KEPT = 0, 1, 2, 3
 STREAM_SEQUENTIAL = 1
+W_BF16, W_F32, W_Q8 = 0, 1, 2   # c4s_head.wdtype
 
 _vp = C.c_void_p
 
@@ -50,7 +51,8 @@ class Stream(C.Structure):
 class Head(C.Structure):
     _fields_ = [("hidden", _vp), ("gamma", _vp), ("beta", _vp), ("eps", C.c_float),
                 ("weight", _vp), ("bias", _vp), ("M", C.c_int32), ("D", C.c_int32),
-                ("V", C.c_int32), ("logits", _vp), ("ld_out", C.c_int64)]
+                ("V", C.c_int32), ("logits", _vp), ("ld_out", C.c_int64), ("wdtype", C.c_int32),
+                ("group", C.c_int32), ("wscale", _vp), ("wbias", _vp)]
 
 
 def header_functions() -> list[str]:
@@ -209,21 +211,32 @@ class Context:
         self._check(lib().c4s_sample_stream(self._h, C.byref(s), _stream_handle(stream)),
                     "sample_stream")
 
-    def _head(self, hidden, gamma, beta, weight, bias, logits, eps):
+    @staticmethod
+    def _head(hidden, gamma, beta, weight, bias, logits, eps, quant=None):
+        """quant: None for bf16 or fp32 weights (from weight's dtype), else
+        (scales, biases, group) of 8-bit codes (uint8 weight)."""
         M, D = hidden.shape
         V = weight.shape[0]
+        kind = {"torch.bfloat16": W_BF16, "torch.int16": W_BF16, "torch.float32": W_F32,
+                "torch.uint8": W_Q8}.get(str(weight.dtype))
+        if kind is None:
+            raise ValueError(f"lmhead: unsupported weight dtype {weight.dtype}")
+        if (kind == W_Q8) != (quant is not None):
+            raise ValueError("lmhead: 8-bit weights need quant=(scales, biases, group), others none")
+        ws, wb, group = quant if quant is not None else (None, None, 0)
         return Head(hidden=_p(hidden), gamma=_p(gamma), beta=_p(beta), eps=eps, weight=_p(weight),
                     bias=_p(bias), M=M, D=D, V=V, logits=_p(logits),
-                    ld_out=(logits.shape[1] if logits is not None else V))
+                    ld_out=(logits.shape[1] if logits is not None else V), wdtype=kind, group=group,
+                    wscale=_p(ws), wbias=_p(wb))
 
-    def lmhead(self, hidden, gamma, beta, weight, bias, logits, eps=1e-5, stream=None):
-        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+    def lmhead(self, hidden, gamma, beta, weight, bias, logits, eps=1e-5, stream=None, quant=None):
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps, quant)
         self._check(lib().c4s_lmhead(self._h, C.byref(h), _stream_handle(stream)), "lmhead")
 
     def lmhead_sample(self, hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k,
                       top_p, pen, rng, out_token, logits=None, do_sample=None, out_masked=None,
-                      out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1):
-        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+                      out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1, quant=None):
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps, quant)
         r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp),
                  top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
                  rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),
@@ -233,9 +246,9 @@ class Context:
 
     def lmhead_sample_noalloc(self, hidden, gamma, beta, weight, bias, hist_ids, hist_off, temp, top_k,
                               top_p, pen, rng, out_token, logits=None, do_sample=None, out_masked=None,
-                              out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1):
+                              out_stats=None, eps=1e-5, stream=None, hist_bits=None, stop_token=-1, quant=None):
         """c4s_lmhead_sample with its workspace in the library's static device scratch."""
-        h = self._head(hidden, gamma, beta, weight, bias, logits, eps)
+        h = self._head(hidden, gamma, beta, weight, bias, logits, eps, quant)
         r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp),
                  top_k=_p(top_k), top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
                  rng_state=_p(rng), out_token=_p(out_token), out_masked=_p(out_masked),

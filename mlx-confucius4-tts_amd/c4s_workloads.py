@@ -187,3 +187,21 @@ def lmhead(seed: int = 5, M: int = 64, D: int = 1280, V: int = V_SEMANTIC) -> tu
     weight = f32_to_bf16_bits((0.02 * g.standard_normal((V, D), dtype=np.float32)).astype(np.float32))
     bias = (0.02 * g.standard_normal(V)).astype(np.float32)
     return LMHead(hidden, gamma, beta, weight, bias), batch64_params(seed + 1, M, V)
+
+
+def head_weight_f32(seed: int, V: int, D: int) -> np.ndarray:
+    """semantic_head.weight [V, D] in float32 (the reference's dtype)."""
+    return (0.02 * np.random.default_rng(seed).standard_normal((V, D))).astype(np.float32)
+
+
+def quantize_affine8(w: np.ndarray, group: int = 64) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """8-bit affine groups along the input dimension: codes q in 0..255 with
+    w ~ scale * q + bias per group of `group` inputs (bias = the group's
+    minimum, scale = its range / 255)."""
+    V, D = w.shape
+    g = w.astype(np.float64).reshape(V, D // group, group)
+    lo, hi = g.min(axis=2), g.max(axis=2)
+    scale = np.where(hi > lo, (hi - lo) / 255.0, 1.0)
+    q = np.clip(np.rint((g - lo[..., None]) / scale[..., None]), 0, 255).astype(np.uint8).reshape(V, D)
+    return q, scale.astype(np.float32), lo.astype(np.float32)
+

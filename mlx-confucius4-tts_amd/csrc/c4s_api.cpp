@@ -21,8 +21,6 @@ struct c4s_ctx {
   hipStream_t host_stream = nullptr;  // used by the synchronous host helpers
   void* ws = nullptr;                 // large-vocab exact-pass key buffers
   size_t ws_bytes = 0;
-  void* hnorm = nullptr;              // LM head: normalised bf16 rows
-  size_t hnorm_bytes = 0;
   void* logits_ws = nullptr;          // LM head + sample: logits when the caller gives none
   size_t logits_bytes = 0;
   // host-helper staging (device)
@@ -284,7 +282,7 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (ctx->scan_s) (void)hipStreamSynchronize(ctx->scan_s);
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamSynchronize(st);
-  for (void* p : {ctx->ws, ctx->hnorm, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws, ctx->segres})
+  for (void* p : {ctx->ws, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws, ctx->segres})
     if (p) (void)hipFree(p);
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
@@ -526,19 +524,23 @@ static int lmhead_check(c4s_ctx* ctx, const c4s_head* h) {
     return fail(ctx, C4S_EINVAL, "lmhead: required pointer is NULL");
   if (h->M < 1 || h->D < 32 || h->V < 1 || (h->D % 32) != 0)
     return fail(ctx, C4S_EINVAL, "lmhead: needs M >= 1, V >= 1, D a positive multiple of 32");
-  if ((reinterpret_cast<uintptr_t>(h->hidden) | reinterpret_cast<uintptr_t>(h->weight)) & 15u)
-    return fail(ctx, C4S_EINVAL, "lmhead: hidden and weight must be 16-byte aligned");
+  if (h->wdtype != C4S_W_BF16 && h->wdtype != C4S_W_F32 && h->wdtype != C4S_W_Q8)
+    return fail(ctx, C4S_EINVAL, "lmhead: unknown weight dtype");
+  if (h->wdtype == C4S_W_Q8) {
+    if (!h->wscale || !h->wbias) return fail(ctx, C4S_EINVAL, "lmhead: 8-bit weights need wscale and wbias");
+    if ((h->group != 32 && h->group != 64 && h->group != 128) || h->D % h->group != 0)
+      return fail(ctx, C4S_EINVAL, "lmhead: group must be 32, 64 or 128 and divide D");
+  }
+  const uintptr_t al16 = reinterpret_cast<uintptr_t>(h->hidden) | reinterpret_cast<uintptr_t>(h->gamma) |
+                         reinterpret_cast<uintptr_t>(h->beta) |
+                         (h->wdtype == C4S_W_Q8 ? 0 : reinterpret_cast<uintptr_t>(h->weight));
+  if ((al16 & 15u) || (reinterpret_cast<uintptr_t>(h->weight) & 7u))
+    return fail(ctx, C4S_EINVAL, "lmhead: hidden, gamma, beta and weight must be 16-byte aligned (8-bit weight: 8)");
   return C4S_OK;
 }
 
-// Bytes of normalised rows the LM head stages (rows padded to the 64-row tile).
-static size_t lmhead_hnorm_bytes(const c4s_head* h) {
-  return (size_t)((h->M + 63) / 64 * 64) * (size_t)h->D * 2;
-}
-
-// The LM head with its normalised-row workspace `hnorm` (lmhead_hnorm_bytes).
-static int lmhead_launch(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out, void* hnorm,
-                         hipStream_t s) {
+// The LM head into `logits` (row stride ld_out): one kernel, no workspace.
+static int lmhead_launch(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out, hipStream_t s) {
   if (!logits) return fail(ctx, C4S_EINVAL, "lmhead: logits is NULL");
   if (ld_out < h->V) return fail(ctx, C4S_EINVAL, "lmhead: ld_out < V");
   c4s::LmHeadArgs a{};
@@ -547,26 +549,25 @@ static int lmhead_launch(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t
   a.beta = h->beta;
   a.eps = h->eps;
   a.weight = h->weight;
+  a.wkind = h->wdtype;
+  a.group = h->group;
+  a.wscale = h->wscale;
+  a.wbias = h->wbias;
   a.bias = h->bias;
   a.logits = logits;
   a.ld_out = ld_out;
   a.M = h->M;
   a.D = h->D;
   a.V = h->V;
-  a.hnorm = static_cast<uint16_t*>(hnorm);
-  hipError_t e = c4s::launch_layernorm_bf16(a, s);
-  if (e != hipSuccess) return hip_fail(ctx, e, "layernorm launch");
-  e = c4s::launch_lmhead_gemm(a, s);
-  if (e != hipSuccess) return hip_fail(ctx, e, "lmhead gemm launch");
+  hipError_t e = c4s::launch_lmhead_fused(a, s);
+  if (e != hipSuccess) return hip_fail(ctx, e, "lmhead launch");
   return C4S_OK;
 }
 
 static int lmhead_impl(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t ld_out, hipStream_t s) {
   int rc = lmhead_check(ctx, h);
   if (rc) return rc;
-  rc = ensure(ctx, &ctx->hnorm, &ctx->hnorm_bytes, lmhead_hnorm_bytes(h), "lmhead workspace", s);
-  if (rc) return rc;
-  return lmhead_launch(ctx, h, logits, ld_out, ctx->hnorm, s);
+  return lmhead_launch(ctx, h, logits, ld_out, s);
 }
 
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream) {
@@ -616,18 +617,17 @@ int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows
   // workspace; larger vocabularies need the context's sort buffers.
   if (head->V > c4s::kLdsVocabMax)
     return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: vocab above 12288 needs a workspace");
-  const size_t hbytes = (lmhead_hnorm_bytes(head) + 255) & ~(size_t)255;
   const size_t lbytes = head->logits ? 0 : (size_t)head->M * (size_t)head->V * 4;
-  if (hbytes + lbytes > c4s::kNoAllocBytes)
-    return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: M x D x 2 (rows padded to 64) + M x V x 4 (without a "
-                                 "logits buffer) exceeds the 8 MiB static scratch");
+  if (lbytes > c4s::kNoAllocBytes)
+    return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: M x V x 4 logits (no logits buffer given) exceed the "
+                                 "8 MiB static scratch");
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   unsigned char* base = static_cast<unsigned char*>(ctx->noalloc);
-  float* logits = head->logits ? head->logits : reinterpret_cast<float*>(base + hbytes);
+  float* logits = head->logits ? head->logits : reinterpret_cast<float*>(base);
   const int64_t ld = head->logits ? head->ld_out : head->V;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = lmhead_launch(ctx, head, logits, ld, base, s);
+  rc = lmhead_launch(ctx, head, logits, ld, s);
   if (rc) return rc;
   c4s_rows r = *rows;
   r.logits = logits;

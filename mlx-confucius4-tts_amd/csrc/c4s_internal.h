@@ -104,17 +104,22 @@ struct StreamWs {
   uint64_t* segres;        // [n_rows][nseg][4] segment results (status and stop step, RNG, statistics)
 };
 
+// LM head weight kinds (values of c4s_head.wdtype).
+enum : int { kLmW_BF16 = 0, kLmW_F32 = 1, kLmW_Q8 = 2 };
+
 struct LmHeadArgs {
   const uint16_t* hidden;  // [M][D] bf16
   const float* gamma;
   const float* beta;
   float eps;
-  const uint16_t* weight;  // [V][D] bf16
+  const void* weight;      // [V][D] bf16, f32 or 8-bit codes (wkind)
+  const float* wscale;     // 8-bit: [V][D / group] scales
+  const float* wbias;      // 8-bit: [V][D / group] offsets
+  int wkind, group;
   const float* bias;       // [V]
   float* logits;           // [M][V] f32 (row stride ld_out)
   int64_t ld_out;
   int M, D, V;
-  uint16_t* hnorm;         // [M][D] bf16 scratch (normalised rows)
 };
 
 // Static device scratch of the no-allocation entry point (per device).
@@ -138,8 +143,7 @@ hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStrea
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
 size_t stream_rowp_lds_bytes(int vocab);  // 0 when the pipelined row chain does not fit
-hipError_t launch_layernorm_bf16(const LmHeadArgs& a, hipStream_t s);
-hipError_t launch_lmhead_gemm(const LmHeadArgs& a, hipStream_t s);
+hipError_t launch_lmhead_fused(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);
 
 }  // namespace c4s

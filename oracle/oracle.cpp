@@ -270,16 +270,20 @@ void orc_sample_stream(const float* logits, int64_t ld, int n_steps, int n_rows,
 }
 
 // ---- LM head (config with the fused LN + linear) ---------------------------
-// hidden: [M][D] bf16, gamma/beta: [D] f32, W: [V][D] bf16 (nn.cpp:11-16 takes
-// weight as (out, in)), bias: [V] f32. LayerNorm over D with biased variance
-// and eps (nn.cpp:73-83; eps default 1e-5, nn.h:49-50), computed in double.
-// `h_out` (optional, [M][D]) receives the normalised row rounded to bf16,
-// which is what a bf16 matrix engine consumes; logits use that rounded row and
-// are accumulated in double.
-void orc_ln_lmhead(const uint16_t* hidden, int M, int D, const float* gamma, const float* beta,
-                   float eps, const uint16_t* W, const float* bias, int V, float* logits,
-                   uint16_t* h_out, int n_threads) {
-  std::vector<uint16_t> hn(static_cast<size_t>(M) * D);
+// hidden: [M][D] bf16, gamma/beta: [D] f32, W: [V][D] (nn.cpp:11-16 takes the
+// weight as (out, in)) in one of three kinds: bf16, f32, or 8-bit affine groups
+// along D as the reference's quantized projections use them (gpt2.cpp:53-62,
+// group 64: w = scale * q + bias per group; q one byte per element, scales and
+// biases [V][D / group]); bias: [V] f32. LayerNorm over D with biased variance
+// and eps (nn.cpp:73-83; eps default 1e-5, nn.h:49-50). Everything in double:
+// the exact values that an fp32 LayerNorm + linear approximates. `y_out`
+// (optional, [M][D]) receives the normalised rows as f32.
+enum { ORC_W_BF16 = 0, ORC_W_F32 = 1, ORC_W_Q8 = 2 };
+
+void orc_ln_lmhead(const uint16_t* hidden, int M, int D, const float* gamma, const float* beta, float eps,
+                   const void* W, int wkind, const float* wscale, const float* wbias, int group,
+                   const float* bias, int V, float* logits, float* y_out, int n_threads) {
+  std::vector<double> y(static_cast<size_t>(M) * D);
   for (int m = 0; m < M; ++m) {
     const uint16_t* x = hidden + static_cast<int64_t>(m) * D;
     double mean = 0.0;
@@ -292,18 +296,28 @@ void orc_ln_lmhead(const uint16_t* hidden, int M, int D, const float* gamma, con
     }
     var /= D;
     const double inv = 1.0 / std::sqrt(var + static_cast<double>(eps));
-    for (int d = 0; d < D; ++d) {
-      const double y = (bf16_to_f32(x[d]) - mean) * inv * gamma[d] + beta[d];
-      hn[static_cast<size_t>(m) * D + d] = f32_to_bf16_rne(static_cast<float>(y));
-    }
+    for (int d = 0; d < D; ++d)
+      y[static_cast<size_t>(m) * D + d] = (bf16_to_f32(x[d]) - mean) * inv * gamma[d] + beta[d];
   }
-  if (h_out) std::copy(hn.begin(), hn.end(), h_out);
+  if (y_out)
+    for (size_t i = 0; i < y.size(); ++i) y_out[i] = static_cast<float>(y[i]);
   parallel_rows(V, n_threads, [&](int v) {
-    const uint16_t* w = W + static_cast<int64_t>(v) * D;
+    std::vector<double> w(D);
+    for (int d = 0; d < D; ++d) {
+      const int64_t i = static_cast<int64_t>(v) * D + d;
+      if (wkind == ORC_W_BF16) {
+        w[d] = bf16_to_f32(static_cast<const uint16_t*>(W)[i]);
+      } else if (wkind == ORC_W_F32) {
+        w[d] = static_cast<const float*>(W)[i];
+      } else {
+        const int64_t gi = static_cast<int64_t>(v) * (D / group) + d / group;
+        w[d] = static_cast<double>(wscale[gi]) * static_cast<const uint8_t*>(W)[i] + wbias[gi];
+      }
+    }
     for (int m = 0; m < M; ++m) {
       double acc = 0.0;
-      const uint16_t* h = hn.data() + static_cast<size_t>(m) * D;
-      for (int d = 0; d < D; ++d) acc += static_cast<double>(bf16_to_f32(h[d])) * bf16_to_f32(w[d]);
+      const double* h = y.data() + static_cast<size_t>(m) * D;
+      for (int d = 0; d < D; ++d) acc += h[d] * w[d];
       logits[static_cast<int64_t>(m) * V + v] = static_cast<float>(acc + bias[v]);
     }
   });

@@ -60,8 +60,8 @@ def lib():
         L.orc_sample_stream.argtypes = [
             _f32p, C.c_int64, C.c_int, C.c_int, C.c_int, _i32p, _i64p, _f32p, _i32p, _f32p, _f32p,
             _u8p, C.c_int, _u64p, _i32p, C.c_int]
-        L.orc_ln_lmhead.argtypes = [_u16p, C.c_int, C.c_int, _f32p, _f32p, C.c_float, _u16p, _f32p,
-                                    C.c_int, _f32p, C.c_void_p, C.c_int]
+        L.orc_ln_lmhead.argtypes = [_u16p, C.c_int, C.c_int, _f32p, _f32p, C.c_float, C.c_void_p, C.c_int,
+                                    C.c_void_p, C.c_void_p, C.c_int, _f32p, C.c_int, _f32p, C.c_void_p, C.c_int]
         _lib = L
     return _lib
 
@@ -166,14 +166,24 @@ def sample_stream(logits, hist_ids, hist_off, temp, top_k, top_p, pen, do_sample
     return out, rng
 
 
-def ln_lmhead(hidden_bf16, gamma, beta, W_bf16, bias, eps=1e-5, n_threads=1, want_h=False):
+W_BF16, W_F32, W_Q8 = 0, 1, 2
+
+
+def ln_lmhead(hidden_bf16, gamma, beta, W, bias, eps=1e-5, n_threads=1, want_h=False, wkind=W_BF16,
+              wscale=None, wbias=None, group=64):
+    """LayerNorm + linear in double. W: [V][D] bf16 bits (uint16), f32, or
+    8-bit affine groups (uint8 codes with f32 scales/biases [V][D/group])."""
     hidden_bf16 = np.ascontiguousarray(hidden_bf16, dtype=np.uint16)
-    W_bf16 = np.ascontiguousarray(W_bf16, dtype=np.uint16)
+    dt = {W_BF16: np.uint16, W_F32: np.float32, W_Q8: np.uint8}[wkind]
+    W = np.ascontiguousarray(W, dtype=dt)
     M, D = hidden_bf16.shape
-    V = W_bf16.shape[0]
+    V = W.shape[0]
     out = np.zeros((M, V), dtype=np.float32)
-    h = np.zeros((M, D), dtype=np.uint16) if want_h else None
+    h = np.zeros((M, D), dtype=np.float32) if want_h else None
+    ws = None if wscale is None else np.ascontiguousarray(wscale, dtype=np.float32)
+    wb = None if wbias is None else np.ascontiguousarray(wbias, dtype=np.float32)
     lib().orc_ln_lmhead(hidden_bf16, M, D, np.ascontiguousarray(gamma, dtype=np.float32),
-                        np.ascontiguousarray(beta, dtype=np.float32), eps, W_bf16,
-                        np.ascontiguousarray(bias, dtype=np.float32), V, out, _ptr(h), n_threads)
+                        np.ascontiguousarray(beta, dtype=np.float32), eps, W.ctypes.data_as(C.c_void_p), wkind,
+                        _ptr(ws), _ptr(wb), group, np.ascontiguousarray(bias, dtype=np.float32), V, out, _ptr(h),
+                        n_threads)
     return (out, h) if want_h else out

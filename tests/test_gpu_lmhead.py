@@ -1,54 +1,98 @@
-"""LM head (LayerNorm -> bf16 MFMA GEMM + bias) and LM head + sampling.
+"""LM head (LayerNorm folded into one MFMA kernel, + bias) for bf16, fp32 and
+8-bit affine weights, and LM head + sampling.
 
-Logits differ from the oracle's float64 accumulation by rounding only (fp32
-LayerNorm statistics and MFMA accumulation order), so they are compared with a
-tolerance; the tokens are then checked bit for bit by running the oracle
-chain on the GPU's own logits.
+Logits differ from the oracle's float64 LayerNorm + linear by rounding only
+(the activations enter the matrix engine as hi + lo bf16 pairs, fp32 weights
+too; fp32 accumulation), so they are compared with a tolerance; the tokens
+are then checked bit for bit by running the oracle chain on the GPU's own
+logits.
 """
 import numpy as np
 import pytest
 
+import c4s
 import c4s_workloads as W
 from gpu_util import dev
 
 pytestmark = pytest.mark.gpu
 
-# |logit| ~ 1 here; fp32 LN vs double LN can move one bf16 rounding of a
-# normalised element (2^-8 relative of that element) -> ~1e-3 absolute at most.
 ATOL = 2e-3
 RTOL = 1e-3
 
 
-@pytest.mark.parametrize("M,D,V", [(64, 1280, 8194), (5, 64, 100), (70, 256, 1000), (3, 2080, 300), (9, 4096, 130)])
-def test_lmhead_logits(orc, gpu_ctx, M, D, V):
+def _weights(kind, head, seed, group):
+    """(device weight, quant, oracle weight, oracle kwargs) of one kind."""
+    import torch
+    V, D = head.weight.shape
+    if kind == "bf16":
+        return dev(head.weight, torch), None, head.weight, {}
+    wf = W.head_weight_f32(seed, V, D)
+    if kind == "f32":
+        return dev(wf, torch), None, wf, {"wkind": 1}
+    q, sc, bi = W.quantize_affine8(wf, group)
+    quant = (dev(sc, torch), dev(bi, torch), group)
+    return dev(q, torch), quant, q, {"wkind": 2, "wscale": sc, "wbias": bi, "group": group}
+
+
+CASES = [("bf16", 64, 1280, 8194, 64, 0.0), ("bf16", 5, 64, 100, 64, 0.0), ("bf16", 70, 256, 1000, 64, 0.0),
+         ("bf16", 3, 2080, 300, 64, 0.0), ("bf16", 9, 4096, 130, 64, 0.0), ("bf16", 16, 1280, 1000, 64, 4.0),
+         ("f32", 64, 1280, 8194, 64, 0.0), ("f32", 70, 96, 517, 64, 0.0), ("f32", 16, 1280, 1000, 64, 4.0),
+         ("q8", 64, 1280, 8194, 64, 0.0), ("q8", 5, 64, 100, 32, 0.0), ("q8", 70, 256, 1000, 128, 0.0),
+         ("q8", 33, 1280, 777, 32, 4.0)]
+
+
+@pytest.mark.parametrize("kind,M,D,V,group,shift", CASES)
+def test_lmhead_logits(orc, gpu_ctx, kind, M, D, V, group, shift):
     import torch
     head, _ = W.lmhead(seed=M + D, M=M, D=D, V=V)
+    if shift:   # hidden rows with mean `shift`: the folded LayerNorm's cancellation case
+        head.hidden = W.f32_to_bf16_bits(W.bf16_bits_to_f32(head.hidden) + np.float32(shift))
+    wdev, quant, worc, kw = _weights(kind, head, M + D + 1, group)
+    print(f"lmhead {kind} M={M} D={D} V={V} group={group} shift={shift}", flush=True)
     logits = torch.zeros((M, V), dtype=torch.float32, device="cuda")
-    gpu_ctx.lmhead(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch),
-                   dev(head.weight, torch), dev(head.bias, torch), logits)
+    gpu_ctx.lmhead(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch), wdev,
+                   dev(head.bias, torch), logits, quant=quant)
     torch.cuda.synchronize()
     got = logits.cpu().numpy()
-    want = orc.ln_lmhead(head.hidden, head.gamma, head.beta, head.weight, head.bias, n_threads=16)
-    err = np.abs(got - want)
-    print(f"M={M} D={D} V={V} max abs err {err.max():.3e}")
+    want = orc.ln_lmhead(head.hidden, head.gamma, head.beta, worc, head.bias, n_threads=16, **kw)
+    err = np.abs(got.astype(np.float64) - want)
+    print(f"  max abs err {err.max():.3e}  max |logit| {np.abs(want).max():.3f}", flush=True)
     assert np.all(err <= ATOL + RTOL * np.abs(want))
 
 
-def test_lmhead_sample_tokens(orc, gpu_ctx):
+@pytest.mark.parametrize("kind", ["bf16", "f32", "q8"])
+def test_lmhead_sample_tokens(orc, gpu_ctx, kind):
     import torch
     head, p = W.lmhead(seed=5)
     M, V = 64, 8194
+    wdev, quant, _, _ = _weights(kind, head, 11, 64)
+    print(f"lmhead_sample {kind}", flush=True)
     logits = torch.zeros((M, V), dtype=torch.float32, device="cuda")
     rng = dev(p["rng"], torch)
     tok = torch.zeros(M, dtype=torch.int32, device="cuda")
-    gpu_ctx.lmhead_sample(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch),
-                          dev(head.weight, torch), dev(head.bias, torch), dev(p["hist_ids"], torch),
+    gpu_ctx.lmhead_sample(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch), wdev,
+                          dev(head.bias, torch), dev(p["hist_ids"], torch),
                           dev(p["hist_off"], torch), dev(p["temp"], torch), dev(p["top_k"], torch),
                           dev(p["top_p"], torch), dev(p["pen"], torch), rng, tok, logits=logits,
-                          do_sample=dev(p["do_sample"], torch))
+                          do_sample=dev(p["do_sample"], torch), quant=quant)
     torch.cuda.synchronize()
     L = logits.cpu().numpy()
     otok, orng, _ = orc.sample_rows(L, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
                                     p["top_p"], p["pen"], p["do_sample"], p["rng"], n_threads=16)
     assert np.array_equal(tok.cpu().numpy(), otok)
     assert np.array_equal(rng.cpu().numpy().view(np.uint64), orng)
+
+
+def test_lmhead_rejects_bad_descriptors(gpu_ctx):
+    import torch
+    head, _ = W.lmhead(seed=1, M=2, D=64, V=10)
+    h, g, b, bias = (dev(x, torch) for x in (head.hidden, head.gamma, head.beta, head.bias))
+    out = torch.zeros((2, 10), dtype=torch.float32, device="cuda")
+    q = torch.zeros((10, 64), dtype=torch.uint8, device="cuda")
+    sc = torch.ones((10, 2), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError):
+        gpu_ctx.lmhead(h, g, b, q, bias, out)                          # 8-bit without scales
+    with pytest.raises(c4s.C4SError, match="code 1"):
+        gpu_ctx.lmhead(h, g, b, q, bias, out, quant=(sc, sc, 48))      # group not 32/64/128
+    with pytest.raises(c4s.C4SError, match="code 1"):
+        gpu_ctx.lmhead(h, g, b, q, bias, out, quant=(sc, sc, 128))     # group does not divide D

@@ -355,15 +355,28 @@ def test_stream_is_repeated_steps(orc):
 
 
 def test_lmhead_vs_numpy(orc):
+    """LayerNorm (biased variance, eps) + linear (x @ W^T + b) against numpy in
+    float64 (nn.cpp:73-83, :11-16), for each weight kind."""
     import c4s_workloads as W
-    head, _ = W.lmhead(seed=3, M=4, D=64, V=50)
-    logits, h = orc.ln_lmhead(head.hidden, head.gamma, head.beta, head.weight, head.bias,
-                              want_h=True)
+    head, _ = W.lmhead(seed=3, M=4, D=128, V=50)
     x = W.bf16_bits_to_f32(head.hidden).astype(np.float64)
     mu = x.mean(axis=1, keepdims=True)
     var = ((x - mu) ** 2).mean(axis=1, keepdims=True)
     y = (x - mu) / np.sqrt(var + 1e-5) * head.gamma + head.beta
-    hb = W.bf16_bits_to_f32(W.f32_to_bf16_bits(y.astype(np.float32))).astype(np.float64)
-    assert np.array_equal(W.f32_to_bf16_bits(hb.astype(np.float32)), h)
-    want = hb @ W.bf16_bits_to_f32(head.weight).astype(np.float64).T + head.bias
+    logits, h = orc.ln_lmhead(head.hidden, head.gamma, head.beta, head.weight, head.bias, want_h=True)
+    assert np.allclose(h, y, rtol=1e-6, atol=1e-7)
+    want = y @ W.bf16_bits_to_f32(head.weight).astype(np.float64).T + head.bias
     assert np.allclose(logits, want, rtol=1e-6, atol=1e-6)
+    # f32 weights
+    g = np.random.default_rng(9)
+    wf = (0.02 * g.standard_normal((50, 128))).astype(np.float32)
+    got = orc.ln_lmhead(head.hidden, head.gamma, head.beta, wf, head.bias, wkind=orc.W_F32)
+    assert np.allclose(got, y @ wf.astype(np.float64).T + head.bias, rtol=1e-6, atol=1e-6)
+    # 8-bit affine groups of 64 along D: w = scale * q + bias per group
+    q = g.integers(0, 256, size=(50, 128)).astype(np.uint8)
+    sc = (0.001 * (1 + g.random((50, 2)))).astype(np.float32)
+    bi = (-0.1 * g.random((50, 2))).astype(np.float32)
+    wq = q.astype(np.float64) * np.repeat(sc, 64, axis=1) + np.repeat(bi, 64, axis=1)
+    got = orc.ln_lmhead(head.hidden, head.gamma, head.beta, q, head.bias, wkind=orc.W_Q8, wscale=sc, wbias=bi,
+                        group=64)
+    assert np.allclose(got, y @ wq.T + head.bias, rtol=1e-6, atol=1e-6)
