@@ -559,7 +559,7 @@ static int lmhead_launch(c4s_ctx* ctx, const c4s_head* h, float* logits, int64_t
   a.M = h->M;
   a.D = h->D;
   a.V = h->V;
-  hipError_t e = c4s::launch_lmhead_fused(a, s);
+  hipError_t e = c4s::launch_lmhead(a, s);
   if (e != hipSuccess) return hip_fail(ctx, e, "lmhead launch");
   return C4S_OK;
 }

@@ -143,7 +143,7 @@ hipError_t launch_stream_segfix(const StreamArgs& a, const StreamWs& w, hipStrea
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
 size_t stream_rowp_lds_bytes(int vocab);  // 0 when the pipelined row chain does not fit
-hipError_t launch_lmhead_fused(const LmHeadArgs& a, hipStream_t s);
+hipError_t launch_lmhead(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);
 
 }  // namespace c4s

@@ -1,10 +1,10 @@
 // LM head ahead of the sampler: final LayerNorm + semantic_head linear
 // (src/t2s/text2semantic.cpp:118-121 -> src/nn/nn.cpp:73-83 and :11-16) in one
-// kernel, k_lmhead_fused, for weights in bf16, fp32 (the reference's own
-// dtype: its .npy weights load as float32, include/c4tts/npy.h:202-206) or
-// 8-bit affine groups (the quantized_matmul layout the reference uses for its
-// projections, src/t2s/gpt2.cpp:49-62: w = scale * q + bias per group of
-// `group` consecutive input elements).
+// kernel, k_lmhead, for weights in bf16, fp32 (the reference's own dtype: its
+// .npy weights load as float32, include/c4tts/npy.h:202-206) or 8-bit affine
+// groups (the quantized_matmul layout the reference uses for its projections,
+// src/t2s/gpt2.cpp:49-62: w = scale * q + bias per group of `group`
+// consecutive input elements).
 // k_hbm_probe: streaming copy / read kernels for the achievable-bandwidth line.
 
 #include <hip/hip_runtime.h>
@@ -16,100 +16,75 @@ namespace c4s {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileM = 64;
 constexpr int kTileN = 32;
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
-  return __uint_as_float(static_cast<uint32_t>(b) << 16);
-}
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x7fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
 
 // ---- LayerNorm folded into the GEMM (one kernel) -------------------------------------
 //
 // With y = (x - mu) * inv * gamma + beta (nn.cpp:73-83, inv = 1/sqrt(var + eps),
 // biased variance) the head's output W y + b (nn.cpp:11-16) is
 //   logits[m][n] = inv_m * (G[m][n] - mu_m * c[n]) + d[n] + b[n],
-//   G[m][n] = sum_k W[n][k] gamma_k x[m][k],  c[n] = sum_k W[n][k] gamma_k,
+//   G[m][n] = sum_k (W[n][k] gamma_k) x[m][k],  c[n] = sum_k W[n][k] gamma_k,
 //   d[n] = sum_k W[n][k] beta_k,  mu_m and var_m from sum_k x and sum_k x^2.
-// So one pass reads W and x once and needs the statistics only in the
-// epilogue. The MFMA operands are bf16: gamma_k x[m][k] (fp32) and gamma, beta
-// enter as a hi + lo pair of bf16 (two MFMAs), which keeps them to about
-// 2^-17 relative, so the logits follow the reference's fp32 LayerNorm + linear
-// instead of a bf16-rounded activation. c and d come from a fifth row block
-// whose rows 0 and 1 are gamma and beta.
+// One pass reads W and x once and needs the statistics only in the epilogue.
 //
-// Weights: bf16 enter the MFMA as they are. fp32 weights are split into hi + lo
-// bf16 as well; the products hi*hi + lo*hi + hi*lo (three MFMAs) leave out only
-// lo*lo, about 2^-16 of 2^-8 relative. 8-bit codes are exact in bf16; a group
-// of `group` inputs (SPU = group / 32 k-steps) accumulates sum q * a in a
-// partial tile P and sum a in Q (an MFMA against ones), and the group adds
-// scale[n] * P + bias[n] * Q to the tile.
+// x is bf16, so it enters the matrix engine as it is. gamma goes to the weight
+// side: each lane forms W[n][k] gamma_k in fp32 for its eight k and splits it
+// into hi + lo bf16 (two MFMAs; the pair keeps about 2^-17 relative), adding c
+// and d in fp32 on the way; every weight element is converted once on the whole
+// chip. fp32 weights take the same path; 8-bit codes q are converted to fp32,
+// each step's partial tiles P = sum (q gamma) x and Q = sum gamma x (gamma
+// against every column) enter the tile as scale[n] P + bias[n] Q. The row
+// statistics come from the matrix engine too: sum_k x against a block of ones,
+// sum_k x^2 as the diagonal of the 16x16 Gram block x x^T (bf16 products are
+// exact in fp32).
 //
-// A workgroup owns 32 columns (vocabulary entries) and 64 rows; its four waves
-// split K round-robin in units of SPU steps of 32 and issue every weight load
-// of up to kSteps steps before the first MFMA; the waves' partial sums meet in
-// LDS in a fixed order, so results are run-to-run stable.
-constexpr int kFuseThreads = 256;
-constexpr int kFuseWaves = kFuseThreads / kWave;
+// A workgroup owns 32 columns (vocabulary entries) and 64 rows. K goes in
+// chunks of eight steps of 32 (256 inputs): the workgroup stages the chunk's
+// rows of x in LDS with 16-byte loads that cover whole cache lines (32 KB, two
+// buffers), and wave w takes the chunk's steps w and w + 4. The first two
+// chunks' loads are issued before the weights (loads complete in issue order,
+// so the first chunk does not wait behind the weight window); each later
+// chunk's loads are issued one chunk ahead. Each wave keeps the weights of its
+// next kSteps steps in flight (all of them for D = 1280). Reading x straight
+// from global memory in MFMA fragment order instead (16 rows, 64 bytes each,
+// per load) stalled the L1 on tag conflicts and cost three times as long. The
+// waves' partial sums meet in LDS (over the staging buffers) in a fixed order,
+// so results are run-to-run stable. At most 256 registers a wave and 66 KB of
+// LDS: two workgroups fit on a CU, so a grid of a few more tiles than CUs
+// (V = 8194: 257) does not take a second round.
+constexpr int kLmThreads = 256;
+constexpr int kLmWaves = kLmThreads / kWave;
+constexpr int kWaveSteps = 2;                                     // steps a wave takes per chunk
+constexpr int kChunkK = kLmWaves * kWaveSteps * 32;               // inputs per chunk
+constexpr int kXPitch = kChunkK * 2 + 16;                         // bytes per staged row (+16: conflict-free reads)
+constexpr int kXLoads = kTileM * kChunkK * 2 / 16 / kLmThreads;   // 16-byte loads per thread per chunk
+constexpr int kRowPieces = kChunkK / 8;                           // 16-byte pieces per staged row
+constexpr size_t kXBytes = (size_t)kTileM * kXPitch;
+constexpr size_t kRedBytes = (size_t)kLmWaves * kTileM * (kTileN + 1) * 4;
+static_assert(kRedBytes <= 2 * kXBytes, "the partial sums fit over the staging buffers");
 
-// v = hi + lo as two bf16 (round to nearest even), packed: the low halfword
-// holds the first of a pair.
+// Two floats to two bf16, round to nearest even (v_cvt_pk_bf16_f32); the
+// low halfword holds the first.
+__device__ __forceinline__ uint32_t pack_bf16(float v0, float v1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{v0, v1}), bf16x2));
+}
+
+// v = hi + lo as two bf16 each, packed: lo rounds the exact residual v - hi.
 __device__ __forceinline__ void split2(float v0, float v1, uint32_t& hi, uint32_t& lo) {
-  const uint16_t h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1);
-  const uint16_t l0 = f32_to_bf16_rne(v0 - bf16_to_f32(h0)), l1 = f32_to_bf16_rne(v1 - bf16_to_f32(h1));
-  hi = (uint32_t)h0 | ((uint32_t)h1 << 16);
-  lo = (uint32_t)l0 | ((uint32_t)l1 << 16);
+  hi = pack_bf16(v0, v1);
+  lo = pack_bf16(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xFFFF0000u));
 }
 
-// Eight bf16 of x (one 16-byte fragment) times gamma: the hi and lo fragments
-// of the products, and the sums of x and x^2 (zeros when the row is absent).
-__device__ __forceinline__ void scaled_split(uint4 xq, float4 ga, float4 gb, bool in, uint4& hi, uint4& lo,
-                                             float& s1, float& s2) {
-  const uint32_t xw[4] = {xq.x, xq.y, xq.z, xq.w};
-  const float gm[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-  uint32_t h[4], o[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const float x0 = in ? __uint_as_float(xw[q] << 16) : 0.0f;
-    const float x1 = in ? __uint_as_float(xw[q] & 0xFFFF0000u) : 0.0f;
-    s1 += x0;
-    s1 += x1;
-    s2 += x0 * x0;
-    s2 += x1 * x1;
-    split2(x0 * gm[2 * q], x1 * gm[2 * q + 1], h[q], o[q]);
-  }
-  hi = make_uint4(h[0], h[1], h[2], h[3]);
-  lo = make_uint4(o[0], o[1], o[2], o[3]);
-}
-
-__device__ __forceinline__ void split_vec(float4 va, float4 vb, uint4& hi, uint4& lo) {
-  split2(va.x, va.y, hi.x, lo.x);
-  split2(va.z, va.w, hi.y, lo.y);
-  split2(vb.x, vb.y, hi.z, lo.z);
-  split2(vb.z, vb.w, hi.w, lo.w);
-}
-
-// Eight 8-bit codes as bf16 (exact: integers below 256 have at most 8
-// significant bits).
-__device__ __forceinline__ uint4 codes_bf16(uint2 q) {
-  uint32_t o[4];
-  const uint32_t wd[2] = {q.x, q.y};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t v = wd[i >> 1] >> (16 * (i & 1));
-    const uint32_t lo = __float_as_uint((float)(v & 0xFFu)) >> 16;
-    const uint32_t hi = __float_as_uint((float)((v >> 8) & 0xFFu)) >> 16;
-    o[i] = lo | (hi << 16);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
+__device__ __forceinline__ void split8(const float (&v)[8], uint4& hi, uint4& lo) {
+  split2(v[0], v[1], hi.x, lo.x);
+  split2(v[2], v[3], hi.y, lo.y);
+  split2(v[4], v[5], hi.z, lo.z);
+  split2(v[6], v[7], hi.w, lo.w);
 }
 
 __device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
@@ -117,11 +92,20 @@ __device__ __forceinline__ f32x4 mfma_bf16(uint4 a, uint4 b, f32x4 c) {
                                                  0, 0, 0);
 }
 
-// One lane's raw weight fragment: 8 consecutive k of one column.
+// One lane's raw weight fragment (8 consecutive k of one column) and its
+// values as fp32: the weight (bf16, fp32) or the code (8-bit).
 template <int WK> struct WRaw;
 template <> struct WRaw<kLmW_BF16> {
   uint4 v;
   __device__ void load(const void* w, int64_t off) { v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + off); }
+  __device__ void get(float (&o)[8]) const {
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(q[i] << 16);
+      o[2 * i + 1] = __uint_as_float(q[i] & 0xFFFF0000u);
+    }
+  }
 };
 template <> struct WRaw<kLmW_F32> {
   float4 a, b;
@@ -130,178 +114,244 @@ template <> struct WRaw<kLmW_F32> {
     a = *reinterpret_cast<const float4*>(p);
     b = *reinterpret_cast<const float4*>(p + 4);
   }
+  __device__ void get(float (&o)[8]) const {
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
 };
 template <> struct WRaw<kLmW_Q8> {
   uint2 v;
   __device__ void load(const void* w, int64_t off) { v = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(w) + off); }
-};
-
-// c += a * w for one 16x16x32 block: a as hi + lo, w as the raw fragment.
-template <int WK>
-__device__ __forceinline__ f32x4 mac(uint4 ah, uint4 al, const WRaw<WK>& w, f32x4 c) {
-  if constexpr (WK == kLmW_F32) {
-    uint4 wh, wl;
-    split_vec(w.a, w.b, wh, wl);
-    c = mfma_bf16(ah, wh, c);
-    c = mfma_bf16(al, wh, c);
-    return mfma_bf16(ah, wl, c);
-  } else {
-    uint4 b;
-    if constexpr (WK == kLmW_Q8) b = codes_bf16(w.v); else b = w.v;
-    c = mfma_bf16(ah, b, c);
-    return mfma_bf16(al, b, c);
+  __device__ void get(float (&o)[8]) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (float)(((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFFu);
   }
-}
+};
 
 // WK: weight kind; SPU: k-steps of 32 per scale group (1 unless 8-bit).
 template <int WK, int SPU>
-__global__ __launch_bounds__(kFuseThreads) void k_lmhead_fused(LmHeadArgs a) {
-  constexpr int kSteps = WK == kLmW_F32 ? 4 : 8;   // weight k-steps a wave keeps in flight (registers)
-  constexpr int kUnits = kSteps / SPU;
+__global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_lmhead(LmHeadArgs a) {
   constexpr bool kQ = WK == kLmW_Q8;
-  __shared__ float red[kFuseWaves][kTileM + 2][kTileN + 1];
-  __shared__ float st1[kFuseWaves][kTileM], st2[kFuseWaves][kTileM];
+  // chunks whose weights a wave keeps in flight (kWaveSteps steps each)
+  constexpr int kWin = WK == kLmW_F32 ? 2 : (WK == kLmW_Q8 && SPU > 1 ? 2 : 5);
+  __shared__ __align__(16) unsigned char xs[2 * kXBytes];
+  __shared__ float st1[kLmWaves][kTileM], st2[kLmWaves][kTileM];
+  __shared__ float scd[kLmWaves][2][kTileN];
+  __shared__ double rmu[kTileM], rinv[kTileM], ccol[kTileN], dcol[kTileN];
+  float (*red)[kTileM][kTileN + 1] = reinterpret_cast<float (*)[kTileM][kTileN + 1]>(xs);
   const int n0 = blockIdx.x * kTileN;
   const int m0 = blockIdx.y * kTileM;
   const int D = a.D, V = a.V, M = a.M;
-  const int w = wave_id(), l = lane_id();
+  const int t = threadIdx.x, w = wave_id(), l = lane_id();
   const int r = l & 15, g = l >> 4;
-  // acc[0..3][nt]: row blocks of x; acc[4][nt]: rows 0 (gamma) and 1 (beta)
-  f32x4 acc[5][2];
+  const int nsteps = D / 32, nchunks = (nsteps + kLmWaves * kWaveSteps - 1) / (kLmWaves * kWaveSteps);
+  // per row block: the two column blocks, then the ones and the Gram products
+  f32x4 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 5; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float cp[2] = {0.f, 0.f}, dp[2] = {0.f, 0.f};   // this lane's parts of c and d (its k, its columns)
   const int col[2] = {min(n0 + r, V - 1), min(n0 + 16 + r, V - 1)};
   const int64_t woff[2] = {(int64_t)col[0] * D + 8 * g, (int64_t)col[1] * D + 8 * g};
-  const uint16_t* xrow[4];
-  bool xin[4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int m = m0 + mt * 16 + r;
-    xin[mt] = m < M;
-    xrow[mt] = a.hidden + (int64_t)min(m, M - 1) * D + 8 * g;
-  }
-  const int ngroups = D / (32 * SPU);
-  const int mine = (ngroups - w + kFuseWaves - 1) / kFuseWaves;   // this wave's units: w, w + 4, ...
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-  for (int base = 0; base < mine; base += kUnits) {
-    // every weight fragment of these units in flight first
-    WRaw<WK> wr[kUnits][SPU][2];
-    float qs[kUnits][2], qb[kUnits][2];
+  // staging: piece j of this thread is row (kLmThreads / kRowPieces) j + t / kRowPieces,
+  // 16-byte column t % kRowPieces
+  constexpr int kRowsPerLoad = kLmThreads / kRowPieces;
+  static_assert(kRowsPerLoad * kXLoads == kTileM, "staging layout");
+  const int tr = t / kRowPieces, tc = (t % kRowPieces) * 8;
+  // chunk ch's piece j of this thread (past D, a partial last chunk: an
+  // in-bounds piece that is not used)
+  auto x_piece = [&](int ch, int j) {
+    const int k = ch * kChunkK + tc;
+    return *reinterpret_cast<const uint4*>(a.hidden + (int64_t)min(m0 + kRowsPerLoad * j + tr, M - 1) * D +
+                                           (k < D ? k : 0));
+  };
+  auto x_lds = [&](int buf, int j) {
+    return reinterpret_cast<uint4*>(&xs[buf * kXBytes + (kRowsPerLoad * j + tr) * kXPitch + tc * 2]);
+  };
+  // the first two chunks' rows, then the weight window (slot i: the steps of chunk i)
+  uint4 xv[kXLoads];
 #pragma unroll
-    for (int i = 0; i < kUnits; ++i) {
-      const int u = w + kFuseWaves * min(base + i, mine - 1);   // past the end: a repeated unit, not used
+  for (int j = 0; j < kXLoads; ++j) *x_lds(0, j) = x_piece(0, j);
 #pragma unroll
-      for (int j = 0; j < SPU; ++j)
+  for (int j = 0; j < kXLoads; ++j) xv[j] = x_piece(min(1, nchunks - 1), j);
+  WRaw<WK> wr[kWin][kWaveSteps][2];
+  auto w_load = [&](int i, int ch) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) wr[i][j][nt].load(a.weight, woff[nt] + (u * SPU + j) * 32);
-      if constexpr (kQ) {
+    for (int h = 0; h < kWaveSteps; ++h) {
+      const int k0 = min(ch * kLmWaves * kWaveSteps + h * kLmWaves + w, nsteps - 1) * 32;   // past the end: unused
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          qs[i][nt] = a.wscale[(int64_t)col[nt] * ngroups + u];
-          qb[i][nt] = a.wbias[(int64_t)col[nt] * ngroups + u];
-        }
-      }
+      for (int nt = 0; nt < 2; ++nt) wr[i][h][nt].load(a.weight, woff[nt] + k0);
     }
+  };
 #pragma unroll
-    for (int i = 0; i < kUnits; ++i) {
-      if (base + i < mine) {
-        const int u = w + kFuseWaves * (base + i);
-        f32x4 P[5][2], Q[5];
-        if constexpr (kQ) {
+  for (int i = 0; i < kWin; ++i) w_load(i, i);
+  __syncthreads();
+  for (int base = 0; base < nchunks; base += kWin) {
 #pragma unroll
-          for (int mt = 0; mt < 5; ++mt) {
-            Q[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            P[mt][0] = P[mt][1] = Q[mt];
-          }
+    for (int i = 0; i < kWin; ++i) {
+      const int ch = base + i;
+      if (ch < nchunks) {   // uniform over the workgroup
+        // the next chunk into the other buffer (last read before the previous
+        // barrier), then the chunk after it in flight
+        if (ch + 1 < nchunks) {
+#pragma unroll
+          for (int j = 0; j < kXLoads; ++j) *x_lds((ch + 1) & 1, j) = xv[j];
         }
 #pragma unroll
-        for (int j = 0; j < SPU; ++j) {
-          const int k0 = (u * SPU + j) * 32;
-          const int kk = k0 + 8 * g;
-          const float4 ga = *reinterpret_cast<const float4*>(a.gamma + kk);
-          const float4 gb = *reinterpret_cast<const float4*>(a.gamma + kk + 4);
+        for (int j = 0; j < kXLoads; ++j) xv[j] = x_piece(min(ch + 2, nchunks - 1), j);
 #pragma unroll
-          for (int mt = 0; mt < 5; ++mt) {
-            uint4 ah, al;
-            if (mt < 4) {
-              scaled_split(*reinterpret_cast<const uint4*>(xrow[mt] + k0), ga, gb, xin[mt], ah, al, s1[mt], s2[mt]);
-            } else {
-              ah = make_uint4(0u, 0u, 0u, 0u);
-              al = ah;
-              if (r == 0) {
-                split_vec(ga, gb, ah, al);
-              } else if (r == 1) {
-                split_vec(*reinterpret_cast<const float4*>(a.beta + kk),
-                          *reinterpret_cast<const float4*>(a.beta + kk + 4), ah, al);
+        for (int h = 0; h < kWaveSteps; ++h) {
+          const int step = ch * kLmWaves * kWaveSteps + h * kLmWaves + w;
+          if (step < nsteps) {
+            const int k0 = step * 32, kk = k0 + 8 * g;
+            const float4 ga = *reinterpret_cast<const float4*>(a.gamma + kk), gb = *reinterpret_cast<const float4*>(a.gamma + kk + 4);
+            const float4 ba = *reinterpret_cast<const float4*>(a.beta + kk), bb = *reinterpret_cast<const float4*>(a.beta + kk + 4);
+            const float gm[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+            const float bt[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+            uint4 bh[2], bl[2];
+            float cq[2], dq[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              float wv[8], wg[8];
+              wr[i][h][nt].get(wv);
+              float c1 = 0.f, d1 = 0.f;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                wg[e] = wv[e] * gm[e];
+                c1 += wg[e];
+                d1 = __builtin_fmaf(wv[e], bt[e], d1);
+              }
+              split8(wg, bh[nt], bl[nt]);
+              cq[nt] = c1;
+              dq[nt] = d1;
+            }
+            uint4 gh, gl;
+            float cg = 0.f, db = 0.f;
+            float qsc[2], qbi[2];
+            if constexpr (kQ) {
+              split8(gm, gh, gl);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                cg += gm[e];
+                db += bt[e];
+              }
+              const int grp = step / SPU, ng = nsteps / SPU;
+#pragma unroll
+              for (int nt = 0; nt < 2; ++nt) {
+                qsc[nt] = a.wscale[(int64_t)col[nt] * ng + grp];
+                qbi[nt] = a.wbias[(int64_t)col[nt] * ng + grp];
               }
             }
-            if constexpr (kQ) {
-              P[mt][0] = mac<WK>(ah, al, wr[i][j][0], P[mt][0]);
-              P[mt][1] = mac<WK>(ah, al, wr[i][j][1], P[mt][1]);
-              Q[mt] = mfma_bf16(ah, ones, Q[mt]);
-              Q[mt] = mfma_bf16(al, ones, Q[mt]);
-            } else {
-              acc[mt][0] = mac<WK>(ah, al, wr[i][j][0], acc[mt][0]);
-              acc[mt][1] = mac<WK>(ah, al, wr[i][j][1], acc[mt][1]);
+            const unsigned char* xb = &xs[(ch & 1) * kXBytes + ((h * kLmWaves + w) * 32 + 8 * g) * 2];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+              const uint4 xa = *reinterpret_cast<const uint4*>(xb + (mt * 16 + r) * kXPitch);
+              if constexpr (kQ) {
+                f32x4 P0 = f32x4{0.f, 0.f, 0.f, 0.f}, P1 = P0, Q = P0;
+                P0 = mfma_bf16(xa, bh[0], P0);
+                P0 = mfma_bf16(xa, bl[0], P0);
+                P1 = mfma_bf16(xa, bh[1], P1);
+                P1 = mfma_bf16(xa, bl[1], P1);
+                Q = mfma_bf16(xa, gh, Q);
+                Q = mfma_bf16(xa, gl, Q);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  acc[mt][0][e] = __builtin_fmaf(qsc[0], P0[e], __builtin_fmaf(qbi[0], Q[e], acc[mt][0][e]));
+                  acc[mt][1][e] = __builtin_fmaf(qsc[1], P1[e], __builtin_fmaf(qbi[1], Q[e], acc[mt][1][e]));
+                }
+              } else {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                  acc[mt][nt] = mfma_bf16(xa, bh[nt], acc[mt][nt]);
+                  acc[mt][nt] = mfma_bf16(xa, bl[nt], acc[mt][nt]);
+                }
+              }
+              acc[mt][2] = mfma_bf16(xa, ones, acc[mt][2]);
+              acc[mt][3] = mfma_bf16(xa, xa, acc[mt][3]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+              if constexpr (kQ) {
+                cp[nt] = __builtin_fmaf(qsc[nt], cq[nt], __builtin_fmaf(qbi[nt], cg, cp[nt]));
+                dp[nt] = __builtin_fmaf(qsc[nt], dq[nt], __builtin_fmaf(qbi[nt], db, dp[nt]));
+              } else {
+                cp[nt] += cq[nt];
+                dp[nt] += dq[nt];
+              }
             }
           }
         }
-        if constexpr (kQ) {
-#pragma unroll
-          for (int mt = 0; mt < 5; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) acc[mt][nt][e] += qs[i][nt] * P[mt][nt][e] + qb[i][nt] * Q[mt][e];
-        }
+        // refill this slot with the steps kWin chunks later
+        if (ch + kWin < nchunks) w_load(i, ch + kWin);
+        __syncthreads();
       }
     }
   }
-  // row statistics: the four lanes of a row (g = 0..3) hold its k sub-ranges
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    s1[mt] += __shfl_xor(s1[mt], 16, kWave);
-    s1[mt] += __shfl_xor(s1[mt], 32, kWave);
-    s2[mt] += __shfl_xor(s2[mt], 16, kWave);
-    s2[mt] += __shfl_xor(s2[mt], 32, kWave);
-    if (g == 0) { st1[w][mt * 16 + r] = s1[mt]; st2[w][mt * 16 + r] = s2[mt]; }
-  }
+  // (the last barrier: every wave is done with the staging buffers)
   // 16x16 accumulator layout: lane l holds rows 4*(l/16)+i, column l%16.
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[w][mt * 16 + 4 * g + i][nt * 16 + r] = acc[mt][nt][i];
-  if (g == 0) {   // rows 0 (c) and 1 (d) of the fifth block
+    if (r == 0)   // every column of the ones product holds the row sums
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      red[w][kTileM][nt * 16 + r] = acc[4][nt][0];
-      red[w][kTileM + 1][nt * 16 + r] = acc[4][nt][1];
+      for (int i = 0; i < 4; ++i) st1[w][mt * 16 + 4 * g + i] = acc[mt][2][i];
+    if ((r >> 2) == g) {   // the Gram diagonal: row r at column r
+      const int i = r & 3;
+      const float dg = i == 0 ? acc[mt][3][0] : (i == 1 ? acc[mt][3][1] : (i == 2 ? acc[mt][3][2] : acc[mt][3][3]));
+      st2[w][mt * 16 + r] = dg;
+    }
+  }
+  // c and d: the four lanes of a column (g = 0..3) hold its k sub-ranges
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    float cc = cp[nt], dd = dp[nt];
+    cc += __shfl_xor(cc, 16, kWave);
+    cc += __shfl_xor(cc, 32, kWave);
+    dd += __shfl_xor(dd, 16, kWave);
+    dd += __shfl_xor(dd, 32, kWave);
+    if (g == 0) {
+      scd[w][0][nt * 16 + r] = cc;
+      scd[w][1][nt * 16 + r] = dd;
     }
   }
   __syncthreads();
-  const double invD = 1.0 / (double)D;
-  for (int o = threadIdx.x; o < kTileM * kTileN; o += kFuseThreads) {
+  // per row: mean and 1/sqrt(var + eps); per column: c and d + bias
+  if (t < kTileM) {
+    double S1 = 0.0, S2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < kLmWaves; ++i) {
+      S1 += (double)st1[i][t];
+      S2 += (double)st2[i][t];
+    }
+    const double invD = 1.0 / (double)D;
+    const double mu = S1 * invD;
+    rmu[t] = mu;
+    rinv[t] = 1.0 / sqrt(fmax(S2 * invD - mu * mu, 0.0) + (double)a.eps);
+  } else if (t < kTileM + kTileN) {
+    const int cl = t - kTileM;
+    double cc = 0.0, dd = 0.0;
+#pragma unroll
+    for (int i = 0; i < kLmWaves; ++i) {
+      cc += (double)scd[i][0][cl];
+      dd += (double)scd[i][1][cl];
+    }
+    ccol[cl] = cc;
+    dcol[cl] = dd + (double)a.bias[min(n0 + cl, V - 1)];
+  }
+  __syncthreads();
+  for (int o = t; o < kTileM * kTileN; o += kLmThreads) {
     const int row = o / kTileN, cl = o % kTileN;
     const int n = n0 + cl, m = m0 + row;
     if (n < V && m < M) {
-      double G = 0.0, cc = 0.0, dd = 0.0, S1 = 0.0, S2 = 0.0;
+      double G = 0.0;
 #pragma unroll
-      for (int i = 0; i < kFuseWaves; ++i) {
-        G += (double)red[i][row][cl];
-        cc += (double)red[i][kTileM][cl];
-        dd += (double)red[i][kTileM + 1][cl];
-        S1 += (double)st1[i][row];
-        S2 += (double)st2[i][row];
-      }
-      const double mu = S1 * invD;
-      const double var = fmax(S2 * invD - mu * mu, 0.0);
-      const double inv = 1.0 / sqrt(var + (double)a.eps);
-      a.logits[(int64_t)m * a.ld_out + n] = (float)(inv * (G - mu * cc) + dd + (double)a.bias[n]);
+      for (int i = 0; i < kLmWaves; ++i) G += (double)red[i][row][cl];
+      a.logits[(int64_t)m * a.ld_out + n] = (float)(rinv[row] * (G - rmu[row] * ccol[cl]) + dcol[cl]);
     }
   }
 }
@@ -347,20 +397,20 @@ __global__ __launch_bounds__(kProbeThreads) void k_hbm_read(const f32x4* src, fl
 }  // namespace
 
 template <int WK, int SPU>
-static hipError_t launch_fused(const LmHeadArgs& a, hipStream_t s) {
+static hipError_t launch_k(const LmHeadArgs& a, hipStream_t s) {
   const dim3 grid((a.V + kTileN - 1) / kTileN, (a.M + kTileM - 1) / kTileM);
-  hipLaunchKernelGGL((k_lmhead_fused<WK, SPU>), grid, dim3(kFuseThreads), 0, s, a);
+  hipLaunchKernelGGL((k_lmhead<WK, SPU>), grid, dim3(kLmThreads), 0, s, a);
   return hipGetLastError();
 }
 
-hipError_t launch_lmhead_fused(const LmHeadArgs& a, hipStream_t s) {
+hipError_t launch_lmhead(const LmHeadArgs& a, hipStream_t s) {
   switch (a.wkind) {
-    case kLmW_BF16: return launch_fused<kLmW_BF16, 1>(a, s);
-    case kLmW_F32: return launch_fused<kLmW_F32, 1>(a, s);
+    case kLmW_BF16: return launch_k<kLmW_BF16, 1>(a, s);
+    case kLmW_F32: return launch_k<kLmW_F32, 1>(a, s);
     case kLmW_Q8:
-      if (a.group == 32) return launch_fused<kLmW_Q8, 1>(a, s);
-      if (a.group == 64) return launch_fused<kLmW_Q8, 2>(a, s);
-      if (a.group == 128) return launch_fused<kLmW_Q8, 4>(a, s);
+      if (a.group == 32) return launch_k<kLmW_Q8, 1>(a, s);
+      if (a.group == 64) return launch_k<kLmW_Q8, 2>(a, s);
+      if (a.group == 128) return launch_k<kLmW_Q8, 4>(a, s);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }

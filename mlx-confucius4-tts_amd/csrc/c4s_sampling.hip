@@ -146,6 +146,111 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
   if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, certain ? 0u : 1u, n_kept);
 }
 
+// The cut when the boundary entries X (more than one sort takes) all hold one
+// value z*: each has the mass e = exp(z* - m), and in the chain's order (value
+// descending, lower id first) X is ordered by id, which is thread order here,
+// so a member's rank is a prefix count. Member i is kept iff the mass at or
+// below it, M_i = S - (mass above X) - i e, exceeds thr S (sampling.cpp:60-65;
+// top_k rows: every member survives top_k, S = the survivors' mass); kept
+// members are ranks 0 .. k-1. A decision within the margin is taken again with
+// S and the mass above X summed in double. Sets ss.kthr; returns 1 decided, 3
+// decided with the double sums, 0 the multi-pass chain decides (X holds more
+// than one value, or the margin is not met even in double).
+template <int PT>
+__device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule& sr, int nX,
+                                    double thr, double S, double errS, double Ma, double eMa, uint32_t n_above,
+                                    StepSh& ss) {
+  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  const float ninf = neg_inf();
+  const bool topk = c.topk_on;
+  float zmax = ninf, zmin = -ninf;
+  uint32_t cnt = 0;
+  for (int j = 0; j < n; ++j) {
+    const float y = val[lo + j];
+    const float z = c.temp_on ? y / c.temp : y;
+    if (sr.side(z) == 0) {
+      zmax = fmaxf(zmax, z);
+      zmin = fminf(zmin, z);
+      ++cnt;
+    }
+  }
+  zmax = wave_max_dpp(zmax);
+  zmin = -wave_max_dpp(-zmin);
+  if (lane == 0) { ss.wmax[w] = zmax; ss.wmin[w] = zmin; }
+  const Scan2 rk = block_scan2((double)cnt, 0.0, 0u, ss.we, ss.wf, ss.ww);   // includes a barrier
+  float zs = ninf, zl = -ninf;
+#pragma unroll
+  for (int i = 0; i < kStepWaves; ++i) { zs = fmaxf(zs, ss.wmax[i]); zl = fminf(zl, ss.wmin[i]); }
+  if (!(zs == zl) || zs == ninf) return 0;   // not one value (or nothing finite)
+  const double e = exp((double)(zs - sr.m));
+  const double N = (double)nX;
+  const uint32_t mk = (uint32_t)max(0, c.min_keep);
+  double Sx = topk ? N * e : S, base = topk ? 0.0 : Ma, err = topk ? 0.0 : 2.0 * errS + eMa;
+  int k = 0, verdict = 1;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (thr <= 0.0) {   // p >= 1: only zero-mass positions can go
+      k = (thr < 0.0 || e > 0.0) ? nX : 0;
+      break;
+    }
+    const double A = thr * Sx;
+    // k = the members with M_i > A, M_i = Sx - base - i e decreasing in i
+    const double q = (Sx - base - A) / e;
+    k = q <= 0.0 ? 0 : (q >= N ? nX : (int)ceil(q));
+    while (k > 0 && !(Sx - base - (double)(k - 1) * e > A)) --k;
+    while (k < nX && Sx - base - (double)k * e > A) ++k;
+    const double mg = rel_eps(c.V) * Sx + err;
+    const bool sure = (k == 0 || fabs(Sx - base - (double)(k - 1) * e - A) > mg) &&
+                      (k == nX || fabs(Sx - base - (double)k * e - A) > mg);
+    if (sure) break;
+    if (pass == 1 || topk) return 0;
+    // decide again with S and the mass above X in double
+    double se = 0.0, sa = 0.0;
+    for (int j = 0; j < n; ++j) {
+      const float y = val[lo + j];
+      const float z = c.temp_on ? y / c.temp : y;
+      if (z != ninf) {
+        const double ed = exp((double)(z - sr.m));
+        se += ed;
+        if (sr.side(z) < 0) sa += ed;
+      }
+    }
+    se = wave_sum_dpp(se);
+    sa = wave_sum_dpp(sa);
+    if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; }
+    __syncthreads();
+    Sx = 0.0;
+    base = 0.0;
+#pragma unroll
+    for (int i = 0; i < kStepWaves; ++i) { Sx += ss.wc[i]; base += ss.wd[i]; }
+    err = 0.0;
+    verdict = 3;
+  }
+  // min_tokens_to_keep (sampling.cpp:67-68): the top min_keep positions stay
+  if (topk) {
+    if ((uint32_t)k < mk) k = (int)min(mk, (uint32_t)nX);
+  } else if (n_above + (uint32_t)k < mk) {
+    if (mk > n_above + (uint32_t)nX) return 0;
+    k = (int)(mk - n_above);
+  }
+  // the last kept member's key (rank k - 1), or with none kept, one above
+  // every member (the lowest id's key + 1)
+  const int want = k > 0 ? k - 1 : 0;
+  const int r0 = (int)rk.ex;
+  if (cnt > 0 && want >= r0 && want < r0 + (int)cnt) {
+    int rank = r0;
+    for (int j = 0; j < n; ++j) {
+      const float y = val[lo + j];
+      const float z = c.temp_on ? y / c.temp : y;
+      if (sr.side(z) == 0) {
+        if (rank == want) ss.kthr = key64(zs, lo + j) + (k > 0 ? 0ull : 1ull);
+        ++rank;
+      }
+    }
+  }
+  __syncthreads();
+  return verdict;
+}
+
 // The multi-pass chain (c4s_chain.hpp) on the penalised row staged in LDS
 // (`val`), for the rows the one pass leaves; kept out of line so that its
 // registers do not weigh on the one-pass path.
@@ -334,7 +439,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
           const int b = bucket_of(z[j], m);
           if (b < kNB - 1) {
             if (topk) atomicAdd(&hc[w * kNB + b], 1u);
-            else atomicAdd(&hm[w * kNB + b], (unsigned long long)(ej * 0x1p32f));
+            else atomicAdd(&hm[w * kNB + b], (unsigned long long)(ej * 0x1p32f) + kHistOne);
           }
         }
       }
@@ -371,74 +476,104 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         unsigned long long ms = 0ull;
 #pragma unroll
         for (int i = 0; i < kStepWaves; ++i) {
-          cn += hc[i * kNB + t];
-          ms += hm[i * kNB + t];
+          const unsigned long long h = hm[i * kNB + t];
+          cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
+          ms += h & (kHistOne - 1ull);
         }
         bcnt[t] = cn;
         bmass[t] = (double)ms * 0x1p-32;
       }
       __syncthreads();
+      const double B = S - thr * S;   // the mass the kept entries hold
+      const double Blo = B * (1.0 - 1e-3) - errS, Bhi = B * (1.0 + 1e-3) + errS;
       if (w == 0) {
-        uint32_t c4[4], lc = 0;
-        double m4[4], lmass = 0.0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          c4[q] = bcnt[4 * lane + q];
-          m4[q] = bmass[4 * lane + q];
-          lc += c4[q];
-          lmass += m4[q];
+        const Boundary bd = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, 0u, 0.0);
+        if (lane == 0) {
+          ss.bsel[0] = bd.lo;
+          ss.bsel[1] = bd.hi;
+          ss.bsel[2] = (int)bd.above;
+          ss.thru = bd.thru;
+          ss.mab = bd.mabove;
+          ss.nx = 0u;
         }
-        const uint32_t ci = wave_scan_u32(lc);
-        const double mi = wave_scan_f64(lmass);
-        uint32_t crun = ci - lc;
-        double mrun = mi - lmass;
-        int blo = -1, bhi = -1;
-        uint32_t above = 0;
-        const double B = S - thr * S;   // the mass the kept entries hold
-        const double Blo = B * (1.0 - 1e-3) - errS, Bhi = B * (1.0 + 1e-3) + errS;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int b = 4 * lane + q;
-          const double nx = mrun + m4[q];
-          if (topk) {
-            if (blo < 0 && crun + c4[q] >= (uint32_t)c.k) { blo = b; bhi = b; above = crun; }
-          } else {
-            if (blo < 0 && nx >= Blo) { blo = b; above = crun; }
-            if (bhi < 0 && nx >= Bhi) bhi = b;
-          }
-          mrun = nx;
-          crun += c4[q];
-        }
-        const uint64_t hl = __ballot(blo >= 0), hh = __ballot(bhi >= 0);
-        int rlo = -1, rhi = -1, rab = 0;
-        if (hl) {
-          const int f = __ffsll((unsigned long long)hl) - 1;
-          rlo = (int)readlane_u32((uint32_t)blo, f);
-          rab = (int)readlane_u32(above, f);
-        }
-        if (hh) rhi = (int)readlane_u32((uint32_t)bhi, __ffsll((unsigned long long)hh) - 1);
-        if (lane == 0) { ss.bsel[0] = rlo; ss.bsel[1] = rhi; ss.bsel[2] = rab; ss.nx = 0u; }
       }
       __syncthreads();
       C4S_PHASE(6);
       const int blo = ss.bsel[0], bhi = ss.bsel[1];
-      if (blo < 0 || bhi < 0) {
+      // the sub-window of the boundary buckets (all of them unless refined)
+      int slo = 0, shi = kNB - 1, lo2 = 0;
+      float sc2 = 0.0f;
+      bool refine = false;
+      if (blo >= 0 && bhi >= 0) {
+        // More boundary entries than one sort takes (flat rows): histogram the
+        // boundary buckets again, kNB sub-buckets over them (top_k: over the
+        // k-th entry's bucket), and keep the sub-buckets where the boundary
+        // falls. Not for the unbounded last bucket.
+        const uint32_t nest = topk ? ss.thru : ss.thru - (uint32_t)ss.bsel[2];
+        refine = nest > (uint32_t)kSortCap && bhi < kNB - 1;
+        if (refine) {
+          lo2 = topk ? bhi : blo;
+          sc2 = (float)kNB / (float)(bhi + 1 - lo2);
+          for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
+          __syncthreads();
+#pragma unroll
+          for (int j = 0; j < PT; ++j) {
+            if (j < n && z[j] != ninf) {
+              const int b = bucket_of(z[j], m);
+              if (b >= lo2 && b <= bhi) {
+                const int sb = sub_bucket_of(z[j], m, lo2, sc2);
+                if (topk) atomicAdd(&hc[w * kNB + sb], 1u);
+                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(mass32(z[j] - m) * 0x1p32f) + kHistOne);
+              }
+            }
+          }
+          __syncthreads();
+          if (t < kNB) {
+            uint32_t cn = 0;
+            unsigned long long ms = 0ull;
+#pragma unroll
+            for (int i = 0; i < kStepWaves; ++i) {
+              const unsigned long long h = hm[i * kNB + t];
+              cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
+              ms += h & (kHistOne - 1ull);
+            }
+            bcnt[t] = cn;
+            bmass[t] = (double)ms * 0x1p-32;
+          }
+          __syncthreads();
+          if (w == 0) {
+            const Boundary b2 = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, (uint32_t)ss.bsel[2],
+                                              ss.mab);
+            if (lane == 0) {
+              ss.sub[0] = topk ? 0 : b2.lo;   // top_k: every entry above the k-th stays in the sort
+              ss.sub[1] = b2.hi;
+            }
+          }
+          __syncthreads();
+          slo = ss.sub[0];
+          shi = ss.sub[1];
+        }
+      }
+      if (blo < 0 || bhi < 0 || slo < 0 || shi < 0) {
         one_pass = false;
       } else {
-        // X: the entries to sort. top_k: every bucket up to the k-th value (the
-        // survivors then are a prefix of X). top_p: the boundary buckets (every
-        // entry above them is kept, every entry below removed).
+        // X: the entries to sort. top_k: every entry up to the k-th value's
+        // (sub-)bucket (the survivors then are a prefix of X). top_p: the
+        // boundary (sub-)buckets; every entry above them is kept, every entry
+        // below removed. side(): -1 above X, 0 in X, 1 below (monotone in z).
         const int xlo = topk ? 0 : blo, xhi = bhi;
+        const SideRule sr{m, sc2, xlo, xhi, lo2, slo, shi, refine};
+        auto side = [&](float zj) { return sr.side(zj); };
         float ma32 = 0.0f;
-        uint32_t na = 0;   // entries above the boundary buckets
+        uint32_t na = 0;   // entries above X
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
           if (j < n) {
-            const int b = bucket_of(z[j], m);
-            if (b >= xlo && b <= xhi) {
+            const int sd = side(z[j]);
+            if (sd == 0) {
               const uint32_t slot = atomicAdd(&ss.nx, 1u);
               if (slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
-            } else if (b < xlo) {
+            } else if (sd < 0) {
               ma32 += mass32(z[j] - m);
               ++na;
             }
@@ -458,7 +593,11 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
 #pragma unroll
         for (int i = 0; i < kStepWaves; ++i) { Ma += ss.wc[i]; eMa += ss.wd[i]; n_above += ss.wv[i]; }
         if (nX > kSortCap) {
-          one_pass = false;
+          // more boundary entries than one sort takes: one_pass only if they
+          // all hold one value (ties), which needs no sort
+          verdict = tie_cut<PT>(c, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
+          tp_exact = verdict == 3;
+          if (verdict != 1 && verdict != 3) one_pass = false;
         } else {
           int P2 = 1;
           while (P2 < nX) P2 <<= 1;
@@ -488,7 +627,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
               if (j < n && z[j] != ninf) {
                 const double ed = exp((double)(z[j] - m));
                 se += ed;
-                if (bucket_of(z[j], m) < xlo) sa += ed;
+                if (side(z[j]) < 0) sa += ed;
               }
             }
             se = wave_sum_dpp(se);

@@ -52,6 +52,10 @@ constexpr int kSortCap = kStepThreads;   // boundary entries one sort handles (o
 // chain): per-wave bucket counters and masses (64-bit fixed point, 2^-32
 // units: integer LDS atomics), two sort exchange buffers, the boundary entries.
 constexpr size_t kHistBytes = (size_t)kStepWaves * kNB * 4;
+// top_p rows count entries in the same 64-bit atomic as their masses: a mass
+// is at most 2^32 units and a wave's bucket sum stays below 2^46 (at most
+// 64 x 65 entries), so bits 48.. hold the count.
+constexpr unsigned long long kHistOne = 1ull << 48;
 constexpr size_t kStepWorkBytes = 3 * kHistBytes + 3 * (size_t)kSortCap * 8;
 
 __host__ __device__ __forceinline__ size_t step_work_bytes(int V) {
@@ -101,6 +105,10 @@ struct StepSh {
   double wa[NW], wb[NW], wc[NW], wd[NW], we[NW], wf[NW];
   uint32_t wu[NW], wv[NW], ww[NW];
   int bsel[3];       // first boundary bucket, last boundary bucket, entries above the first
+  int sub[2];        // the same in the refined histogram over the boundary buckets
+  float wmin[NW];    // per-wave minimum (the boundary's tie test)
+  uint32_t thru;     // entries up to and including the last boundary bucket
+  double mab;        // mass of the entries above the first boundary bucket
   uint32_t nx;       // boundary entries (compaction counter)
   uint64_t kthr;     // kept iff key64 >= kthr
   int verdict;       // 1 decided, 2 decide again with every mass in double, 0 multi-pass chain
@@ -125,6 +133,91 @@ __device__ __forceinline__ double mass32_err(float e) { return (double)e * 0x1p-
 __device__ __forceinline__ int bucket_of(float z, float m) {
   const float q = (m - z) * kBucketScale;   // monotone in z; +inf for z = -inf
   return q < (float)(kNB - 1) ? (int)q : kNB - 1;
+}
+
+// The refined histogram: kNB sub-buckets over buckets lo2 .. lo2 + kNB / sc2 - 1
+// (an entry of those buckets; monotone in z like bucket_of).
+__device__ __forceinline__ int sub_bucket_of(float z, float m, int lo2, float sc2) {
+  const float v = ((m - z) * kBucketScale - (float)lo2) * sc2;
+  return v < (float)(kNB - 1) ? (int)fmaxf(v, 0.0f) : kNB - 1;
+}
+
+// Which side of the boundary entries X an entry of value z lies on: -1 above
+// (kept without sorting), 0 in X, 1 below (removed); monotone in z. X is the
+// buckets xlo .. xhi and, when refined, within buckets lo2 .. xhi only the
+// sub-buckets slo .. shi.
+struct SideRule {
+  float m, sc2;
+  int xlo, xhi, lo2, slo, shi;
+  bool refine;
+  __device__ __forceinline__ int side(float z) const {
+    const int b = bucket_of(z, m);
+    if (b < xlo) return -1;
+    if (b > xhi) return 1;
+    if (!refine || b < lo2) return 0;
+    const int sb = sub_bucket_of(z, m, lo2, sc2);
+    return sb < slo ? -1 : (sb > shi ? 1 : 0);
+  }
+};
+
+// Wave 0: where the kept set's boundary falls in a histogram of kNB buckets in
+// descending value order (cnt entries and mass ms each; c0 entries of mass m0
+// come before bucket 0). top_k: the bucket of the k-th entry (lo == hi);
+// top_p: the first bucket whose running mass reaches Blo, and the first that
+// reaches Bhi. Lane l takes buckets 4l .. 4l + 3. -1 where none does.
+struct Boundary {
+  int lo, hi;
+  uint32_t above;   // entries before bucket lo
+  double mabove;    // their mass
+  uint32_t thru;    // entries up to and including bucket hi
+};
+__device__ Boundary boundary_scan(const uint32_t* cnt, const double* ms, bool topk, uint32_t k, double Blo,
+                                  double Bhi, uint32_t c0, double m0) {
+  const int lane = lane_id();
+  uint32_t c4[4], lc = 0;
+  double m4[4], lmass = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    c4[q] = cnt[4 * lane + q];
+    m4[q] = ms[4 * lane + q];
+    lc += c4[q];
+    lmass += m4[q];
+  }
+  const uint32_t ci = wave_scan_u32(lc);
+  const double mi = wave_scan_f64(lmass);
+  uint32_t crun = c0 + ci - lc;
+  double mrun = m0 + (mi - lmass);
+  int blo = -1, bhi = -1;
+  uint32_t above = 0, thru = 0;
+  double mab = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int b = 4 * lane + q;
+    const double nx = mrun + m4[q];
+    const uint32_t cx = crun + c4[q];
+    if (topk) {
+      if (blo < 0 && cx >= k) { blo = b; bhi = b; above = crun; thru = cx; }
+    } else {
+      if (blo < 0 && nx >= Blo) { blo = b; above = crun; mab = mrun; }
+      if (bhi < 0 && nx >= Bhi) { bhi = b; thru = cx; }
+    }
+    mrun = nx;
+    crun = cx;
+  }
+  Boundary r{-1, -1, 0u, 0.0, 0u};
+  const uint64_t hl = __ballot(blo >= 0), hh = __ballot(bhi >= 0);
+  if (hl) {
+    const int f = __ffsll((unsigned long long)hl) - 1;
+    r.lo = (int)readlane_u32((uint32_t)blo, f);
+    r.above = readlane_u32(above, f);
+    r.mabove = readlane_f64(mab, f);
+  }
+  if (hh) {
+    const int f = __ffsll((unsigned long long)hh) - 1;
+    r.hi = (int)readlane_u32((uint32_t)bhi, f);
+    r.thru = readlane_u32(thru, f);
+  }
+  return r;
 }
 
 // Strict total order of the chain: value descending, then lower id first

@@ -16,8 +16,10 @@ from gpu_util import dev
 
 pytestmark = pytest.mark.gpu
 
-ATOL = 2e-3
-RTOL = 1e-3
+# Measured on MI355X: at most 1.5e-5 for rows of mean ~0 and 5.8e-5 for rows of
+# mean 4 (the folded LayerNorm's G - mu c cancellation), |logit| <= 4.
+ATOL = 2e-4
+RTOL = 0.0
 
 
 def _weights(kind, head, seed, group):

@@ -43,6 +43,25 @@ def test_batch64_general_rows(orc, gpu_ctx):
     compare_with_oracle(orc, gpu_ctx, b)
 
 
+@pytest.mark.parametrize("sigma", [0.3, 0.7, 1.5])
+def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma):
+    """Narrow logit ranges (an LM head's output): hundreds of entries share the
+    boundary bucket of the nucleus cut or of the k-th value, so the one-pass
+    step refines the boundary buckets in a second histogram."""
+    b = W.batch64(seed=40, rows=64)
+    g = np.random.default_rng(41)
+    b.logits[:] = (sigma * g.standard_normal(b.logits.shape)).astype(np.float32)
+    b.top_k[:] = np.resize(np.array([0, 0, 0, 50, 200, 0, 400, 0], np.int32), 64)
+    b.top_p[:] = np.resize(np.array([0.9, 0.8, 0.95, 1.0, 0.9, 0.5, 1.0, 0.99], np.float32), 64)
+    print(f"flat rows sigma={sigma}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    one_pass = (st[:, 0] & 16) != 0
+    print("rows decided in one pass", int(one_pass.sum()), "of", b.n_rows)
+    for i in np.flatnonzero(~one_pass):
+        print(f"  row {i}: top_k {b.top_k[i]} top_p {b.top_p[i]} temp {b.temp[i]:.3f} pen {b.pen[i]} stats {st[i]}")
+    assert one_pass.mean() > 0.9
+
+
 @pytest.mark.parametrize("sweep", ["greedy", "top_k1", "top_p"])
 def test_bf16_ties(orc, gpu_ctx, sweep):
     b = W.bf16_ties(seed=3, rows=1024, sweep=sweep)
