@@ -49,7 +49,9 @@ constexpr int kTileN = 32;
 // buffers), and wave w takes the chunk's steps w and w + 4. The first two
 // chunks' loads are issued before the weights (loads complete in issue order,
 // so the first chunk does not wait behind the weight window); each later
-// chunk's loads are issued one chunk ahead. Each wave keeps the weights of its
+// chunk's loads are issued one chunk ahead. gamma and beta of the chunk are
+// staged with it (a step that loaded them itself would wait, in issue order,
+// for the next chunk's rows). Each wave keeps the weights of its
 // next kSteps steps in flight (all of them for D = 1280). Reading x straight
 // from global memory in MFMA fragment order instead (16 rows, 64 bytes each,
 // per load) stalled the L1 on tag conflicts and cost three times as long. The
@@ -65,7 +67,8 @@ constexpr int kXPitch = kChunkK * 2 + 16;                         // bytes per s
 constexpr int kXLoads = kTileM * kChunkK * 2 / 16 / kLmThreads;   // 16-byte loads per thread per chunk
 constexpr int kRowPieces = kChunkK / 8;                           // 16-byte pieces per staged row
 constexpr size_t kXBytes = (size_t)kTileM * kXPitch;
-constexpr size_t kRedBytes = (size_t)kLmWaves * kTileM * (kTileN + 1) * 4;
+constexpr int kRedPitch = kTileM + 4;                             // floats per column of a partial tile (+4: conflict-free)
+constexpr size_t kRedBytes = (size_t)kLmWaves * kTileN * kRedPitch * 4;
 static_assert(kRedBytes <= 2 * kXBytes, "the partial sums fit over the staging buffers");
 
 // Two floats to two bf16, round to nearest even (v_cvt_pk_bf16_f32); the
@@ -98,6 +101,7 @@ template <int WK> struct WRaw;
 template <> struct WRaw<kLmW_BF16> {
   uint4 v;
   __device__ void load(const void* w, int64_t off) { v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w) + off); }
+  __device__ uint4 bf16() const { return v; }
   __device__ void get(float (&o)[8]) const {
     const uint32_t q[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -126,19 +130,34 @@ template <> struct WRaw<kLmW_Q8> {
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = (float)(((i < 4 ? v.x : v.y) >> (8 * (i & 3))) & 0xFFu);
   }
+  // the codes as bf16 (exact: integers below 256 have at most 8 significant bits)
+  __device__ uint4 bf16() const {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t q = (i < 2 ? v.x : v.y) >> (16 * (i & 1));
+      o[i] = pack_bf16((float)(q & 0xFFu), (float)((q >> 8) & 0xFFu));
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  }
 };
 
 // WK: weight kind; SPU: k-steps of 32 per scale group (1 unless 8-bit).
 template <int WK, int SPU>
 __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_lmhead(LmHeadArgs a) {
   constexpr bool kQ = WK == kLmW_Q8;
+  constexpr bool kCdMfma = WK != kLmW_F32;   // c and d on the matrix engine (the weights are bf16-exact)
   // chunks whose weights a wave keeps in flight (kWaveSteps steps each)
-  constexpr int kWin = WK == kLmW_F32 ? 2 : (WK == kLmW_Q8 && SPU > 1 ? 2 : 5);
+  constexpr int kWin = WK == kLmW_F32 ? 2 : (WK == kLmW_Q8 ? (SPU > 1 ? 2 : 3) : 5);
   __shared__ __align__(16) unsigned char xs[2 * kXBytes];
+  __shared__ __align__(16) float gbs[2][2][kChunkK];   // by buffer: gamma, beta of the chunk
+  // by buffer: gamma hi, gamma lo, beta hi, beta lo as bf16 (rows 0-3 of an MFMA
+  // block whose product with the raw weights gives c and d; bf16 / 8-bit only)
+  __shared__ __align__(16) uint16_t cda[kCdMfma ? 2 : 1][4][kChunkK];
   __shared__ float st1[kLmWaves][kTileM], st2[kLmWaves][kTileM];
   __shared__ float scd[kLmWaves][2][kTileN];
-  __shared__ double rmu[kTileM], rinv[kTileM], ccol[kTileN], dcol[kTileN];
-  float (*red)[kTileM][kTileN + 1] = reinterpret_cast<float (*)[kTileM][kTileN + 1]>(xs);
+  __shared__ float rmu[kTileM], rinv[kTileM], ccol[kTileN], dcol[kTileN];
+  float (*red)[kTileN][kRedPitch] = reinterpret_cast<float (*)[kTileN][kRedPitch]>(xs);   // [wave][column][row]
   const int n0 = blockIdx.x * kTileN;
   const int m0 = blockIdx.y * kTileM;
   const int D = a.D, V = a.V, M = a.M;
@@ -151,7 +170,8 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float cp[2] = {0.f, 0.f}, dp[2] = {0.f, 0.f};   // this lane's parts of c and d (its k, its columns)
+  float cp[2] = {0.f, 0.f}, dp[2] = {0.f, 0.f};   // fp32 weights: this lane's parts of c and d
+  f32x4 acd[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};   // the c / d block by column block
   const int col[2] = {min(n0 + r, V - 1), min(n0 + 16 + r, V - 1)};
   const int64_t woff[2] = {(int64_t)col[0] * D + 8 * g, (int64_t)col[1] * D + 8 * g};
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
@@ -170,19 +190,48 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   auto x_lds = [&](int buf, int j) {
     return reinterpret_cast<uint4*>(&xs[buf * kXBytes + (kRowsPerLoad * j + tr) * kXPitch + tc * 2]);
   };
+  // gamma (threads 0 .. 63) and beta (64 .. 127): four floats of the chunk each
+  constexpr int kGbPieces = kChunkK / 4;
+  const bool gb_t = t < 2 * kGbPieces;
+  const int gb_a = t / kGbPieces, gb_o = (t % kGbPieces) * 4;
+  auto gb_piece = [&](int ch) {
+    const int k = ch * kChunkK + gb_o;
+    return *reinterpret_cast<const float4*>((gb_a ? a.beta : a.gamma) + (k < D ? k : 0));
+  };
+  auto gb_store = [&](int buf, float4 v) {
+    *reinterpret_cast<float4*>(&gbs[buf][gb_a][gb_o]) = v;
+    if constexpr (kCdMfma) {
+      uint32_t h0, l0, h1, l1;
+      split2(v.x, v.y, h0, l0);
+      split2(v.z, v.w, h1, l1);
+      *reinterpret_cast<uint2*>(&cda[buf][2 * gb_a][gb_o]) = make_uint2(h0, h1);
+      *reinterpret_cast<uint2*>(&cda[buf][2 * gb_a + 1][gb_o]) = make_uint2(l0, l1);
+    }
+  };
   // the first two chunks' rows, then the weight window (slot i: the steps of chunk i)
   uint4 xv[kXLoads];
+  float4 gv = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < kXLoads; ++j) *x_lds(0, j) = x_piece(0, j);
+  if (gb_t) gb_store(0, gb_piece(0));
 #pragma unroll
   for (int j = 0; j < kXLoads; ++j) xv[j] = x_piece(min(1, nchunks - 1), j);
+  if (gb_t) gv = gb_piece(min(1, nchunks - 1));
   WRaw<WK> wr[kWin][kWaveSteps][2];
+  float qs[kQ ? kWin : 1][kWaveSteps][2], qb[kQ ? kWin : 1][kWaveSteps][2];   // 8-bit: scale and offset
   auto w_load = [&](int i, int ch) {
 #pragma unroll
     for (int h = 0; h < kWaveSteps; ++h) {
-      const int k0 = min(ch * kLmWaves * kWaveSteps + h * kLmWaves + w, nsteps - 1) * 32;   // past the end: unused
+      const int step = min(ch * kLmWaves * kWaveSteps + h * kLmWaves + w, nsteps - 1);   // past the end: unused
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) wr[i][h][nt].load(a.weight, woff[nt] + k0);
+      for (int nt = 0; nt < 2; ++nt) {
+        wr[i][h][nt].load(a.weight, woff[nt] + step * 32);
+        if constexpr (kQ) {
+          const int64_t q = (int64_t)col[nt] * (nsteps / SPU) + step / SPU;
+          qs[i][h][nt] = a.wscale[q];
+          qb[i][h][nt] = a.wbias[q];
+        }
+      }
     }
   };
 #pragma unroll
@@ -198,20 +247,23 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
         if (ch + 1 < nchunks) {
 #pragma unroll
           for (int j = 0; j < kXLoads; ++j) *x_lds((ch + 1) & 1, j) = xv[j];
+          if (gb_t) gb_store((ch + 1) & 1, gv);
         }
 #pragma unroll
         for (int j = 0; j < kXLoads; ++j) xv[j] = x_piece(min(ch + 2, nchunks - 1), j);
+        if (gb_t) gv = gb_piece(min(ch + 2, nchunks - 1));
 #pragma unroll
         for (int h = 0; h < kWaveSteps; ++h) {
           const int step = ch * kLmWaves * kWaveSteps + h * kLmWaves + w;
           if (step < nsteps) {
-            const int k0 = step * 32, kk = k0 + 8 * g;
-            const float4 ga = *reinterpret_cast<const float4*>(a.gamma + kk), gb = *reinterpret_cast<const float4*>(a.gamma + kk + 4);
-            const float4 ba = *reinterpret_cast<const float4*>(a.beta + kk), bb = *reinterpret_cast<const float4*>(a.beta + kk + 4);
+            const int kc = (h * kLmWaves + w) * 32 + 8 * g;   // this lane's k within the chunk
+            const float* gl_ = gbs[ch & 1][0] + kc;
+            const float* bl_ = gbs[ch & 1][1] + kc;
+            const float4 ga = *reinterpret_cast<const float4*>(gl_), gb = *reinterpret_cast<const float4*>(gl_ + 4);
+            const float4 ba = *reinterpret_cast<const float4*>(bl_), bb = *reinterpret_cast<const float4*>(bl_ + 4);
             const float gm[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
             const float bt[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
             uint4 bh[2], bl[2];
-            float cq[2], dq[2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
               float wv[8], wg[8];
@@ -220,31 +272,45 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
                 wg[e] = wv[e] * gm[e];
-                c1 += wg[e];
-                d1 = __builtin_fmaf(wv[e], bt[e], d1);
+                if constexpr (!kCdMfma) {
+                  c1 += wg[e];
+                  d1 = __builtin_fmaf(wv[e], bt[e], d1);
+                }
               }
               split8(wg, bh[nt], bl[nt]);
-              cq[nt] = c1;
-              dq[nt] = d1;
+              if constexpr (!kCdMfma) {
+                cp[nt] += c1;
+                dp[nt] += d1;
+              }
             }
             uint4 gh, gl;
-            float cg = 0.f, db = 0.f;
-            float qsc[2], qbi[2];
+            float qsc[2] = {0.f, 0.f}, qbi[2] = {0.f, 0.f};
             if constexpr (kQ) {
               split8(gm, gh, gl);
 #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                cg += gm[e];
-                db += bt[e];
-              }
-              const int grp = step / SPU, ng = nsteps / SPU;
-#pragma unroll
               for (int nt = 0; nt < 2; ++nt) {
-                qsc[nt] = a.wscale[(int64_t)col[nt] * ng + grp];
-                qbi[nt] = a.wbias[(int64_t)col[nt] * ng + grp];
+                qsc[nt] = qs[i][h][nt];
+                qbi[nt] = qb[i][h][nt];
               }
             }
-            const unsigned char* xb = &xs[(ch & 1) * kXBytes + ((h * kLmWaves + w) * 32 + 8 * g) * 2];
+            if constexpr (kCdMfma) {
+              // c and d: rows 0-3 (gamma hi, lo, beta hi, lo) against the raw weights
+              uint4 cdf = make_uint4(0u, 0u, 0u, 0u);
+              if (r < 4) cdf = *reinterpret_cast<const uint4*>(&cda[ch & 1][r][kc]);
+              if constexpr (kQ) {
+                f32x4 Q = mfma_bf16(cdf, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                  const f32x4 P = mfma_bf16(cdf, wr[i][h][nt].bf16(), f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) acd[nt][e] = __builtin_fmaf(qsc[nt], P[e], __builtin_fmaf(qbi[nt], Q[e], acd[nt][e]));
+                }
+              } else {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) acd[nt] = mfma_bf16(cdf, wr[i][h][nt].bf16(), acd[nt]);
+              }
+            }
+            const unsigned char* xb = &xs[(ch & 1) * kXBytes + kc * 2];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
               const uint4 xa = *reinterpret_cast<const uint4*>(xb + (mt * 16 + r) * kXPitch);
@@ -271,16 +337,6 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
               acc[mt][2] = mfma_bf16(xa, ones, acc[mt][2]);
               acc[mt][3] = mfma_bf16(xa, xa, acc[mt][3]);
             }
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              if constexpr (kQ) {
-                cp[nt] = __builtin_fmaf(qsc[nt], cq[nt], __builtin_fmaf(qbi[nt], cg, cp[nt]));
-                dp[nt] = __builtin_fmaf(qsc[nt], dq[nt], __builtin_fmaf(qbi[nt], db, dp[nt]));
-              } else {
-                cp[nt] += cq[nt];
-                dp[nt] += dq[nt];
-              }
-            }
           }
         }
         // refill this slot with the steps kWin chunks later
@@ -294,9 +350,8 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[w][mt * 16 + 4 * g + i][nt * 16 + r] = acc[mt][nt][i];
+    for (int nt = 0; nt < 2; ++nt)   // rows 4g .. 4g + 3 of column r: one 16-byte store
+      *reinterpret_cast<f32x4*>(&red[w][nt * 16 + r][mt * 16 + 4 * g]) = acc[mt][nt];
     if (r == 0)   // every column of the ones product holds the row sums
 #pragma unroll
       for (int i = 0; i < 4; ++i) st1[w][mt * 16 + 4 * g + i] = acc[mt][2][i];
@@ -306,14 +361,21 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
       st2[w][mt * 16 + r] = dg;
     }
   }
-  // c and d: the four lanes of a column (g = 0..3) hold its k sub-ranges
+  // c and d of this wave's steps
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    float cc = cp[nt], dd = dp[nt];
-    cc += __shfl_xor(cc, 16, kWave);
-    cc += __shfl_xor(cc, 32, kWave);
-    dd += __shfl_xor(dd, 16, kWave);
-    dd += __shfl_xor(dd, 32, kWave);
+    float cc, dd;
+    if constexpr (kCdMfma) {   // lanes 0-15 hold rows 0-3 (gamma hi, lo, beta hi, lo) at column r
+      cc = acd[nt][0] + acd[nt][1];
+      dd = acd[nt][2] + acd[nt][3];
+    } else {                   // the four lanes of a column (g = 0..3) hold its k sub-ranges
+      cc = cp[nt];
+      dd = dp[nt];
+      cc += __shfl_xor(cc, 16, kWave);
+      cc += __shfl_xor(cc, 32, kWave);
+      dd += __shfl_xor(dd, 16, kWave);
+      dd += __shfl_xor(dd, 32, kWave);
+    }
     if (g == 0) {
       scd[w][0][nt * 16 + r] = cc;
       scd[w][1][nt * 16 + r] = dd;
@@ -330,8 +392,8 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
     }
     const double invD = 1.0 / (double)D;
     const double mu = S1 * invD;
-    rmu[t] = mu;
-    rinv[t] = 1.0 / sqrt(fmax(S2 * invD - mu * mu, 0.0) + (double)a.eps);
+    rmu[t] = (float)mu;
+    rinv[t] = (float)(1.0 / sqrt(fmax(S2 * invD - mu * mu, 0.0) + (double)a.eps));
   } else if (t < kTileM + kTileN) {
     const int cl = t - kTileM;
     double cc = 0.0, dd = 0.0;
@@ -340,18 +402,18 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
       cc += (double)scd[i][0][cl];
       dd += (double)scd[i][1][cl];
     }
-    ccol[cl] = cc;
-    dcol[cl] = dd + (double)a.bias[min(n0 + cl, V - 1)];
+    ccol[cl] = (float)cc;
+    dcol[cl] = (float)(dd + (double)a.bias[min(n0 + cl, V - 1)]);
   }
   __syncthreads();
   for (int o = t; o < kTileM * kTileN; o += kLmThreads) {
     const int row = o / kTileN, cl = o % kTileN;
     const int n = n0 + cl, m = m0 + row;
     if (n < V && m < M) {
-      double G = 0.0;
+      float G = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kLmWaves; ++i) G += (double)red[i][row][cl];
-      a.logits[(int64_t)m * a.ld_out + n] = (float)(rinv[row] * (G - rmu[row] * ccol[cl]) + dcol[cl]);
+      for (int i = 0; i < kLmWaves; ++i) G += red[i][cl][row];
+      a.logits[(int64_t)m * a.ld_out + n] = __builtin_fmaf(rinv[row], __builtin_fmaf(-rmu[row], ccol[cl], G), dcol[cl]);
     }
   }
 }
