@@ -683,6 +683,253 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   chain_fallback(io, c, work, val, sh);
 }
 
+// ---- large vocabularies: top_k in two passes -----------------------------------------
+//
+// A sampled row with top_k in [1, kT2MaxK] (e.g. 256 rows x V = 151936, k = 50)
+// does not need the whole row after top_k: every entry below the k-th largest
+// value is -inf from there on (sampling.cpp:30-40), so top_p (sampling.cpp:
+// 42-71) and the draw (text2semantic.cpp:150-165) only see the survivors.
+// Pass 1 reads the row once (penalty, temperature) for its maximum and a
+// histogram of the top kT2Bits bits of the order-preserving value keys, which
+// locates the bucket b* of the k-th largest value; pass 2 reads it again and
+// collects every entry of b* and above (at most kT2Cap) with its id. Sorted,
+// their first k give the threshold (ties kept). Wave 0 then replays top_p and
+// the draw on the survivors sequentially in double, in the reference's order
+// (top_p ascending by value, equal values higher id first; the draw in id
+// order), so the sums are the reference's own: the -inf positions add 0.
+constexpr int kT2Bits = 11;
+constexpr int kT2Buckets = 1 << kT2Bits;
+constexpr int kT2Copies = 4;        // histogram copies (by wave) to spread the LDS atomics
+constexpr int kT2Cap = 2 * NT;      // candidates the sort takes
+constexpr int kT2MaxK = NT;
+constexpr int kT2MaxV = 1 << 19;    // above: the LDS holds the history bitmap only
+
+struct T2Sh {
+  uint32_t hist[kT2Copies][kT2Buckets];
+  uint64_t list[kT2Cap];
+  double e[kT2Cap];                 // the draw's masses in id order
+  uint32_t wsum[NW];
+  float wmax[NW];
+  uint32_t n;
+  int bstar;
+  uint32_t nge, nkeep;
+  int tok;
+};
+
+__host__ __device__ __forceinline__ size_t t2_offset(int V) { return ((size_t)4 * ((V + 31) / 32) + 15) & ~(size_t)15; }
+
+// In-buffer descending bitonic sort of P (a power of two) 64-bit keys by the
+// NT threads of the workgroup.
+__device__ void bitonic_desc_u64(uint64_t* buf, int P) {
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int t = threadIdx.x; t < (P >> 1); t += NT) {
+        const int i = (t / j) * 2 * j + (t % j);
+        const int pi = i + j;
+        const uint64_t x = buf[i], y = buf[pi];
+        const bool down = (i & k) == 0;
+        if ((x < y) == down) { buf[i] = y; buf[pi] = x; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// The row's value at id i after penalty and temperature (sampling.cpp:19-28,
+// 14-17), as the multi-pass chain computes it.
+struct T2Row {
+  const float* xf;
+  const uint16_t* xb;
+  const uint32_t* bitmap;
+  bool pen_on, temp_on;
+  float pen, temp;
+  __device__ __forceinline__ float z(int i, float x) const {
+    if (pen_on && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = (x < 0) ? x * pen : x / pen;
+    return temp_on ? x / temp : x;
+  }
+  // f(i, z) for every id, each by one thread: 16-byte loads over the aligned body
+  template <class F>
+  __device__ __forceinline__ void each(int V, F&& f) const {
+    const int t = threadIdx.x;
+    if (xf) {
+      const RowShape rs = row_shape(xf, V);
+      const float4* p4 = reinterpret_cast<const float4*>(xf + rs.head);
+      for (int q = t; q < rs.nq; q += NT) {
+        const float4 v = p4[q];
+        const int i = rs.head + 4 * q;
+        f(i, z(i, v.x));
+        f(i + 1, z(i + 1, v.y));
+        f(i + 2, z(i + 2, v.z));
+        f(i + 3, z(i + 3, v.w));
+      }
+      if (t < rs.head) f(t, z(t, xf[t]));
+      else if (t < rs.head + rs.tail) {
+        const int i = rs.head + 4 * rs.nq + (t - rs.head);
+        f(i, z(i, xf[i]));
+      }
+    } else {
+      for (int i = t; i < V; i += NT) f(i, z(i, __uint_as_float((uint32_t)xb[i] << 16)));
+    }
+  }
+};
+
+// Returns false (nothing written) when the survivors' bucket holds more than
+// the sort takes; the multi-pass chain decides the row then.
+__device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts) {
+  const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
+  const float ninf = neg_inf();
+  for (int i = t; i < kT2Copies * kT2Buckets; i += NT) (&ts.hist[0][0])[i] = 0u;
+  if (t == 0) ts.n = 0u;
+  __syncthreads();
+  // pass 1: maximum and histogram
+  uint32_t* hist = ts.hist[w % kT2Copies];
+  float lmax = ninf;
+  src.each(V, [&](int, float zi) {
+    lmax = fmaxf(lmax, zi);
+    atomicAdd(&hist[fkey(zi) >> (32 - kT2Bits)], 1u);
+  });
+  lmax = wave_max_f32(lmax);
+  if (lane == 0) ts.wmax[w] = lmax;
+  __syncthreads();
+  // b*: thread t takes buckets 2047 - 2t (higher) and 2046 - 2t; counts from the top
+  const int bh = kT2Buckets - 1 - 2 * t, bl = bh - 1;
+  uint32_t ch = 0, cl = 0;
+#pragma unroll
+  for (int q = 0; q < kT2Copies; ++q) { ch += ts.hist[q][bh]; cl += ts.hist[q][bl]; }
+  const uint32_t inc = wave_scan_u32(ch + cl);
+  if (lane == kWave - 1) ts.wsum[w] = inc;
+  __syncthreads();
+  uint32_t ex = inc - (ch + cl);
+  for (int i = 0; i < w; ++i) ex += ts.wsum[i];
+  const uint32_t k = (uint32_t)c.k;
+  if (ex < k && k <= ex + ch) { ts.bstar = bh; ts.nge = ex + ch; }
+  else if (ex + ch < k && k <= ex + ch + cl) { ts.bstar = bl; ts.nge = ex + ch + cl; }
+  __syncthreads();
+  const int bstar = ts.bstar;
+  const uint32_t nge = ts.nge;
+  if (nge > (uint32_t)kT2Cap) return false;   // uniform
+  // pass 2: the candidates (bucket >= b*)
+  src.each(V, [&](int i, float zi) {
+    const uint32_t key = fkey(zi);
+    if ((int)(key >> (32 - kT2Bits)) >= bstar) {
+      const uint32_t slot = atomicAdd(&ts.n, 1u);
+      ts.list[slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+    }
+  });
+  __syncthreads();
+  const int n = (int)ts.n;   // == nge
+  int P = 1;
+  while (P < n) P <<= 1;
+  for (int i = n + t; i < P; i += NT) ts.list[i] = 0ull;
+  __syncthreads();
+  bitonic_desc_u64(ts.list, P);
+  // top_k: every entry with the k-th largest value or above survives
+  const uint32_t kkey = (uint32_t)(ts.list[k - 1] >> 32);
+  if (w == 0) {
+    int ns = (int)k;
+    while (ns < n && (uint32_t)(ts.list[ns] >> 32) >= kkey) ++ns;
+    const float vmax = kfloat((uint32_t)(ts.list[0] >> 32));
+    int nkeep = ns;
+    if (c.topp_on) {
+      // sampling.cpp:52-65 in ascending order (list position ns - 1 - j)
+      double total = 0.0;
+      for (int base = 0; base < ns; base += kWave) {
+        const int j = base + lane;
+        const double e = j < ns ? exp((double)(kfloat((uint32_t)(ts.list[ns - 1 - j] >> 32)) - vmax)) : 0.0;
+        const int cnt = min(kWave, ns - base);
+        for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+      }
+      const double thr = 1.0 - (double)c.p;
+      double cum = 0.0;
+      int removed = 0;
+      bool stop = false;
+      for (int base = 0; base < ns && !stop; base += kWave) {
+        const int j = base + lane;
+        const double q = j < ns ? exp((double)(kfloat((uint32_t)(ts.list[ns - 1 - j] >> 32)) - vmax)) / total : 0.0;
+        const int cnt = min(kWave, ns - base);
+        for (int u = 0; u < cnt; ++u) {
+          cum += __shfl(q, u, kWave);
+          if (cum <= thr) removed = base + u + 1;
+          else { stop = true; break; }
+        }
+      }
+      nkeep = ns - removed;
+      const int mk = min(max(0, c.min_keep), ns);   // sampling.cpp:67-68
+      if (nkeep < mk) nkeep = mk;
+    }
+    if (lane == 0) ts.nkeep = (uint32_t)nkeep;
+  }
+  __syncthreads();
+  const int nkeep = (int)ts.nkeep;
+  // the state before the draw: kept values, -inf elsewhere
+  if (a.out_masked) {
+    float* mrow = a.out_masked + (int64_t)row * V;
+    for (int i = t; i < V; i += NT) mrow[i] = ninf;
+    __syncthreads();
+    for (int j = t; j < nkeep; j += NT) {   // the row's own value (the key folds -0 onto +0)
+      const int i = (int)~(uint32_t)ts.list[j];
+      mrow[i] = src.z(i, src.xf ? src.xf[i] : __uint_as_float((uint32_t)src.xb[i] << 16));
+    }
+  }
+  // the kept entries in id order: (~id) as the high half sorts descending by it
+  int Pk = 1;
+  while (Pk < nkeep) Pk <<= 1;
+  __syncthreads();
+  for (int j = t; j < Pk; j += NT) {
+    const uint64_t v = j < nkeep ? ts.list[j] : 0ull;
+    ts.list[j] = j < nkeep ? (((uint64_t)(uint32_t)v << 32) | (v >> 32)) : 0ull;
+  }
+  __syncthreads();
+  bitonic_desc_u64(ts.list, Pk);
+  if (w == 0) {
+    // text2semantic.cpp:150-165 over the kept entries in id order (the maximum
+    // starts from -1e30f; -inf positions add 0)
+    float m = -1e30f;
+    for (int j = lane; j < nkeep; j += kWave) m = fmaxf(m, kfloat((uint32_t)ts.list[j]));
+    m = wave_max_f32(m);
+    double total = 0.0;
+    for (int base = 0; base < nkeep; base += kWave) {
+      const int j = base + lane;
+      const float zj = j < nkeep ? kfloat((uint32_t)ts.list[j]) : ninf;
+      const double e = (j < nkeep && zj != ninf) ? exp((double)(zj - m)) : 0.0;
+      if (j < nkeep) ts.e[j] = e;
+      const int cnt = min(kWave, nkeep - base);
+      for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+    }
+    const uint64_t st2 = xorshift64(a.rng[row]);
+    const double r = unit_from_state(st2) * total;
+    int tok = V - 1;   // no id reached r (text2semantic.cpp:160)
+    double acc = 0.0;
+    bool done = false;
+    for (int base = 0; base < nkeep && !done; base += kWave) {
+      const int j = base + lane;
+      const double e = j < nkeep ? ts.e[j] : 0.0;
+      const int cnt = min(kWave, nkeep - base);
+      for (int q = 0; q < cnt; ++q) {
+        acc += __shfl(e, q, kWave);
+        if (r <= acc) {
+          tok = (int)~(uint32_t)(ts.list[base + q] >> 32);
+          done = true;
+          break;
+        }
+      }
+    }
+    if (lane == 0) {
+      a.out_tok[row] = tok;
+      a.rng[row] = st2;
+      join_history(a, row, tok);
+      if (a.stats) {
+        uint32_t* st = a.stats + 4 * (int64_t)row;
+        st[0] = 1u | 2u | 4u | 32u;
+        st[1] = 0u;
+        st[2] = 0u;
+        st[3] = (uint32_t)nkeep;
+      }
+    }
+  }
+  return true;
+}
+
 __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ Scratch sh;
@@ -713,6 +960,18 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
     __syncthreads();
   }
   const int64_t roff = (int64_t)row * a.ld;
+  if (c.draw && c.topk_on && c.k <= kT2MaxK && V <= kT2MaxV && a.rng) {
+    T2Row tr;
+    tr.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
+    tr.xb = a.dtype == 1 ? static_cast<const uint16_t*>(a.logits) + roff : nullptr;
+    tr.bitmap = bitmap;
+    tr.pen_on = c.pen_on;
+    tr.pen = c.pen;
+    tr.temp_on = c.temp_on;
+    tr.temp = c.temp;
+    if (topk_two_pass(a, row, c, tr, *reinterpret_cast<T2Sh*>(smem + t2_offset(V)))) return;
+    __syncthreads();
+  }
   GlobalRow src;
   src.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
   src.xb = a.dtype == 1 ? static_cast<const uint16_t*>(a.logits) + roff : nullptr;
@@ -837,7 +1096,9 @@ size_t rows_lds_bytes(int V) {
 
 size_t stream_lds_bytes(int V, int) { return rows_lds_bytes(V); }
 
-size_t rows_global_lds_bytes(int V) { return 4 * (size_t)((V + 31) / 32); }
+size_t rows_global_lds_bytes(int V) {
+  return V <= kT2MaxV ? t2_offset(V) + sizeof(T2Sh) : 4 * (size_t)((V + 31) / 32);
+}
 
 size_t rows_step_lds_bytes(int V) {
   return step_work_bytes(V) + 4 * ((size_t)vpad(V) + 4) + 4 * (size_t)bitmap_words(V);

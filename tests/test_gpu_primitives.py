@@ -142,3 +142,21 @@ def test_lane_draw_id_order_and_replay():
     o = out.cpu().numpy().reshape(n, 2)
     assert o[:, 0].tolist() == expect
     assert o[1::4, 1].sum() > 20      # boundary cases went through the sequential replay
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_hbm_probe(gpu_ctx, mode):
+    """The bandwidth probes: copy (mode 0) reproduces the source exactly over
+    256 MiB (a size that is not a multiple of the grid's spans); read (mode 1)
+    writes nothing for ordinary data. Their runs also calibrate the HBM
+    traffic counters (a copy of known size)."""
+    import torch
+    n = (256 << 20) // 4 + 12
+    src = torch.arange(n, dtype=torch.int32, device="cuda").view(torch.float32)
+    dst = torch.full((n,), -1, dtype=torch.int32, device="cuda").view(torch.float32)
+    gpu_ctx.hbm_probe(src, dst, n * 4, mode)
+    torch.cuda.synchronize()
+    if mode == 0:
+        assert torch.equal(dst.view(torch.int32), src.view(torch.int32))
+    else:
+        assert bool((dst.view(torch.int32) == -1).all())
