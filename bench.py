@@ -35,6 +35,7 @@ sys.path.insert(0, os.path.join(REPO, "mlx-confucius4-tts_amd"))
 
 METRIC = "sampled rows/sec + achieved HBM GB/s (% peak), V=8194 batch 64"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_FLOPS = 2.5e15   # dense bf16 MFMA
 
 
 def log(*a):
@@ -198,8 +199,8 @@ def bench_lmhead(torch, ctx, W, s, hist_ids, hist_off, temp, top_k, top_p, pen, 
     tok = torch.empty(M, dtype=torch.int32, device="cuda")
     rng = rng0.clone()
     flops = 2 * M * D * V
-    out = {"workload": f"{M} rows, D={D}, V={V}: LayerNorm + linear + bias (one kernel), then the chain "
-                       "of the batch-64 job; graph-replayed us per call",
+    out = {"workload": f"{M} rows, D={D}, V={V}: LayerNorm + linear + bias (one kernel, k_lmhead), then the "
+                       "chain of the batch-64 job; graph-replayed us per call",
            "flops_per_call": flops}
     for kind, (wt, quant, wbytes) in weights.items():
         nbytes = wbytes + 2 * M * D + 4 * V + 8 * D + 4 * M * V
@@ -207,6 +208,7 @@ def bench_lmhead(torch, ctx, W, s, hist_ids, hist_off, temp, top_k, top_p, pen, 
         r = _rate(M, nbytes, us)
         r["bytes_per_call"] = int(nbytes)
         r["achieved_TFLOPs"] = round(flops / (us * 1e-6) / 1e12, 2)
+        r["frac_of_mfma_peak"] = round(flops / (us * 1e-6) / PEAK_BF16_FLOPS, 4)   # algorithmic flops
         us2 = time_graph(torch, lambda: ctx.lmhead_sample(hidden, gamma, beta, wt, bias, hist_ids, hist_off, temp,
                                                           top_k, top_p, pen, rng, tok, logits=head_out,
                                                           do_sample=do_sample, quant=quant), 100, s)

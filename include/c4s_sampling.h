@@ -199,6 +199,37 @@ int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, 
  * that overlap on one GPU, from any context or stream, race. */
 int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream);
 
+/* The LM head's tensors read from the reference's weight store
+ * (src/core/weights.cpp:13-58: <root>.safetensors when that file exists, else
+ * <root>/<name>.npy per tensor; names of src/t2s/text2semantic.cpp:114-115:
+ * final_norm.weight, final_norm.bias, semantic_head.weight [V][D],
+ * semantic_head.bias), converted to the storage `wdtype` and copied to the
+ * calling thread's current HIP device. C4S_W_Q8 from float weights makes
+ * groups of `group` inputs (bias = the group's minimum, scale = its range / 255);
+ * a file that already holds an 8-bit head (u32 weight words of four codes,
+ * least significant byte first, plus semantic_head.scales and
+ * semantic_head.biases of [V][D / group]) is taken as it is. The pointers go
+ * into c4s_head (hidden, logits and M are the caller's). Errors: C4S_EINVAL or
+ * C4S_EHIP, text from c4s_weights_last_error() (this thread's last failure). */
+typedef struct c4s_head_weights {
+  float* gamma;                 /* [D] device */
+  float* beta;                  /* [D] device */
+  void* weight;                 /* [V][D] device, in wdtype */
+  float* bias;                  /* [V] device */
+  float* wscale;                /* C4S_W_Q8: [V][D / group] device */
+  float* wbias;                 /* C4S_W_Q8: [V][D / group] device */
+  int32_t D, V, wdtype, group;
+} c4s_head_weights;
+int c4s_head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_head_weights* out);
+int c4s_head_weights_free(c4s_head_weights* w);
+/* Host only (no device): one tensor of the store as fp32 (f16/bf16/f32/f64
+ * data), its shape in shape[0 .. *ndim) (up to 8 dimensions); out may be NULL
+ * to ask for the shape, else it must hold cap >= the element count. The
+ * reference's npy loader (include/c4tts/npy.h:47-137) / load_safetensors. */
+int c4s_tensor_read_f32(const char* root, const char* name, float* out, int64_t cap, int64_t* shape,
+                        int32_t* ndim);
+const char* c4s_weights_last_error(void);
+
 /* hist_bits[b] = the set of row b's CSR history ids in [0, vocab) (ids
  * outside are skipped, sampling.cpp:24); the starting state of
  * c4s_rows.hist_bits (text2semantic.cpp:196-372 keeps gen[b] across steps). */

@@ -55,6 +55,12 @@ class Head(C.Structure):
                 ("group", C.c_int32), ("wscale", _vp), ("wbias", _vp)]
 
 
+class HeadWeights(C.Structure):
+    """c4s_head_weights: the LM head's tensors on the device (c4s_head_weights_load)."""
+    _fields_ = [("gamma", _vp), ("beta", _vp), ("weight", _vp), ("bias", _vp), ("wscale", _vp),
+                ("wbias", _vp), ("D", C.c_int32), ("V", C.c_int32), ("wdtype", C.c_int32), ("group", C.c_int32)]
+
+
 def header_functions() -> list[str]:
     """Names of every function the public header declares."""
     txt = open(HEADER).read()
@@ -106,6 +112,10 @@ def lib() -> C.CDLL:
     L.c4s_host_argmax.argtypes = [_vp, _vp, C.c_int32, _vp]
     L.c4s_host_draw.argtypes = [_vp, _vp, C.c_int32, _vp, _vp]
     L.c4s_hbm_probe.argtypes = [_vp, _vp, _vp, C.c_int64, C.c_int32, _vp]
+    L.c4s_tensor_read_f32.argtypes = [C.c_char_p, C.c_char_p, _vp, C.c_int64, _vp, _vp]
+    L.c4s_head_weights_load.argtypes = [C.c_char_p, C.c_int32, C.c_int32, C.POINTER(HeadWeights)]
+    L.c4s_head_weights_free.argtypes = [C.POINTER(HeadWeights)]
+    L.c4s_weights_last_error.restype = C.c_char_p
     _lib = L
     return L
 
@@ -148,6 +158,37 @@ def _close_live_contexts() -> None:
             ctx.close()
         except Exception:
             pass
+
+
+def read_tensor(root: str, name: str):
+    """One tensor of the reference's weight store (<root>.safetensors, else
+    <root>/<name>.npy) as float32 numpy, read by the library on the host."""
+    import numpy as np
+    shape = np.zeros(8, np.int64)
+    nd = C.c_int32(0)
+    rc = lib().c4s_tensor_read_f32(root.encode(), name.encode(), None, 0, shape.ctypes.data, C.byref(nd))
+    if rc:
+        raise C4SError(f"tensor_read: code {rc}: {lib().c4s_weights_last_error().decode()}")
+    out = np.empty(tuple(shape[: nd.value]), np.float32)
+    rc = lib().c4s_tensor_read_f32(root.encode(), name.encode(), out.ctypes.data, out.size, shape.ctypes.data,
+                                   C.byref(nd))
+    if rc:
+        raise C4SError(f"tensor_read: code {rc}: {lib().c4s_weights_last_error().decode()}")
+    return out
+
+
+def load_head_weights(root: str, wdtype: int = W_BF16, group: int = 64) -> HeadWeights:
+    """final_norm.* and semantic_head.* of the store at `root` on the current
+    device, in storage `wdtype`; free with free_head_weights."""
+    hw = HeadWeights()
+    rc = lib().c4s_head_weights_load(root.encode(), wdtype, group, C.byref(hw))
+    if rc:
+        raise C4SError(f"head_weights_load: code {rc}: {lib().c4s_weights_last_error().decode()}")
+    return hw
+
+
+def free_head_weights(hw: HeadWeights) -> None:
+    lib().c4s_head_weights_free(C.byref(hw))
 
 
 class Context:
@@ -228,6 +269,16 @@ class Context:
                     bias=_p(bias), M=M, D=D, V=V, logits=_p(logits),
                     ld_out=(logits.shape[1] if logits is not None else V), wdtype=kind, group=group,
                     wscale=_p(ws), wbias=_p(wb))
+
+    def lmhead_loaded(self, hw: HeadWeights, hidden, logits, eps=1e-5, stream=None):
+        """c4s_lmhead with the tensors of load_head_weights."""
+        M, D = hidden.shape
+        if D != hw.D:
+            raise ValueError(f"hidden has D={D}, the head D={hw.D}")
+        h = Head(hidden=_p(hidden), gamma=hw.gamma, beta=hw.beta, eps=eps, weight=hw.weight, bias=hw.bias,
+                 M=M, D=D, V=hw.V, logits=_p(logits), ld_out=logits.shape[1], wdtype=hw.wdtype, group=hw.group,
+                 wscale=hw.wscale, wbias=hw.wbias)
+        self._check(lib().c4s_lmhead(self._h, C.byref(h), _stream_handle(stream)), "lmhead")
 
     def lmhead(self, hidden, gamma, beta, weight, bias, logits, eps=1e-5, stream=None, quant=None):
         h = self._head(hidden, gamma, beta, weight, bias, logits, eps, quant)

@@ -104,14 +104,17 @@ __device__ __forceinline__ void step_out(const StepIO& io, int V, int tok, uint6
 }
 
 // The draw of the one-pass step (text2semantic.cpp:150-165) once the kept set
-// is known: e[] are this thread's kept fp32 masses (0 elsewhere), ds the
-// workgroup scan of their sums with the error bound in tot2. The thread whose
-// interval holds r decides; inside the margin its wave recomputes the draw in
-// double (draw_replay).
+// is known: the kept fp32 masses of each thread and ds, the workgroup scan of
+// their sums with the error bound in tot2. The thread whose interval holds r
+// decides. When it cannot (r within the bound of one end of its entry: on a
+// flat row of thousands of kept entries a few percent of rows a call), every
+// thread recomputes its kept masses in double and the workgroup scans them
+// again (bound rel_eps, about 1e-11 relative); only if that still does not
+// decide does one wave replay the draw sequentially (draw_replay).
 template <int PT>
 __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, const KeptRule& kr, const float (&z)[PT],
                                             int lo, int n, float m, const Scan2& ds, uint32_t n_kept,
-                                            uint32_t st_path, uint32_t st_exact) {
+                                            uint32_t st_path, uint32_t st_exact, StepSh& ss) {
   const int t = threadIdx.x;
   const uint64_t st2 = xorshift64(*io.rng);
   const double u = unit_from_state(st2);
@@ -139,11 +142,42 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
     }
     certain = found >= 0 && (acc - r > margin) && (r - prev > margin);
   }
-  if (__ballot(owner && !certain)) {
-    const int tk = draw_replay(io, c, kr, m, u);
-    if (owner) { found = tk; }
+  if (!__syncthreads_or(owner && !certain)) {
+    if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, 0u, n_kept);
+    return;
   }
-  if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, certain ? 0u : 1u, n_kept);
+  // the kept masses in double, scanned by the workgroup
+  double dk = 0.0;
+#pragma unroll
+  for (int j = 0; j < PT; ++j)
+    if (j < n && z[j] != neg_inf() && kept_by(kr, z[j], m, lo + j)) dk += exp((double)(z[j] - m));
+  const Scan2 d2 = block_scan2(dk, 0.0, 0u, ss.wa, ss.wb, ss.wu);
+  const double r2 = u * d2.tot;
+  const double m2 = 2.0 * rel_eps(c.V) * d2.tot;
+  const bool own2 = (d2.ex < r2 && r2 <= d2.in) || (t == kStepThreads - 1 && r2 > d2.in);
+  found = -1;
+  certain = false;
+  if (own2 && r2 > 0.0) {
+    double acc = d2.ex, prev = d2.ex;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const double ej = (j < n && z[j] != neg_inf() && kept_by(kr, z[j], m, lo + j)) ? exp((double)(z[j] - m)) : 0.0;
+      if (found < 0 && ej > 0.0) {
+        const double na = acc + ej;
+        if (na >= r2) { found = lo + j; prev = acc; }
+        acc = na;
+      }
+    }
+    certain = found >= 0 && (acc - r2 > m2) && (r2 - prev > m2);
+  }
+  if (!__syncthreads_or(own2 && !certain)) {
+    if (own2) step_out(io, c.V, found, st2, true, st_path, st_exact, 1u, n_kept);
+    return;
+  }
+  if (wave_id() == 0) {   // the reference's sequential sums, one wave
+    const int tk = draw_replay(io, c, kr, m, u);
+    if (lane_id() == 0) step_out(io, c.V, tk, st2, true, st_path, st_exact, 2u, n_kept);
+  }
 }
 
 // The cut when the boundary entries X (more than one sort takes) all hold one
@@ -160,7 +194,7 @@ template <int PT>
 __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule& sr, int nX,
                                     double thr, double S, double errS, double Ma, double eMa, uint32_t n_above,
                                     StepSh& ss) {
-  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int lane = lane_id(), w = wave_id();
   const float ninf = neg_inf();
   const bool topk = c.topk_on;
   float zmax = ninf, zmin = -ninf;
@@ -462,7 +496,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         for (int j = 0; j < PT; ++j)
           if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
       C4S_PHASE(10);
-      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u);
+      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss);
       C4S_PHASE(15);
       return;
     } else {
@@ -673,7 +707,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
     C4S_PHASE(10);
     if ((ds.utot >> 16) == 0u) {
       draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
-                      tp_exact ? 1u : 0u);
+                      tp_exact ? 1u : 0u, ss);
       C4S_PHASE(15);
       return;
     }
