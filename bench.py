@@ -433,8 +433,9 @@ def main():
                                "one stream call per bench step",
                    "rows": R, "vocab": V, "ar_steps": T,
                    "launch": ("k_stream_lds" if args.sequential else
-                              "chunks of 64-256 steps (x6/5), three summary buffers, one call in flight: k_stream_scan of the next chunk on 22 of 32 CUs beside "
-                              "k_stream_list + k_stream_chain (4 of 32) | k_stream_rowp + k_stream_segfix (6 of 32)")},
+                              "chunks of 64-256 steps (x6/5), three summary buffers, one call in flight: k_stream_scan of the next chunk on 24 of 32 CUs beside "
+                              "k_stream_list + k_stream_chain (4 of 32) | k_stream_spec (4 of 32: per full-vocabulary row, 5 waves decide "
+                              "steps ahead, 1 checks them in order)")},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic,

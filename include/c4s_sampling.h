@@ -148,6 +148,11 @@ typedef struct c4s_stream {
 /* c4s_stream.flags: run every step of every row in one persistent kernel
  * instead of the two-phase path (scan of all steps, then the per-row chain). */
 #define C4S_STREAM_SEQUENTIAL 1u
+/* c4s_stream.flags: in the two-phase path, decide full-vocabulary rows one
+ * step after the other (the pipelined row chain) instead of several steps at
+ * once with each checked against the tokens drawn since (the default for
+ * calls of at most 1024 steps). Both give the same tokens. */
+#define C4S_STREAM_NO_SPECULATION 2u
 
 /* LM head: LayerNorm(hidden) -> bf16 -> hidden @ weight^T + bias -> f32 logits
  * (text2semantic.cpp:118-121; nn.cpp:73-83 eps/biased variance, nn.cpp:11-16

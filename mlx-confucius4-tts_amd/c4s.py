@@ -25,6 +25,7 @@ T_ARGMAX, T_DRAW = 16, 32
 MODE_CUSTOM = 256
 STAT_PATH, STAT_TOPP_EXACT, STAT_DRAW_EXACT, STAT_KEPT = 0, 1, 2, 3
 STREAM_SEQUENTIAL = 1
+STREAM_NO_SPECULATION = 2
 W_BF16, W_F32, W_Q8 = 0, 1, 2   # c4s_head.wdtype
 
 _vp = C.c_void_p
@@ -241,14 +242,15 @@ class Context:
                                              _stream_handle(stream)), "hist_bits_init")
 
     def sample_stream(self, logits, hist_ids, hist_off, temp, top_k, top_p, pen, rng, out_tokens,
-                      do_sample=None, stop_token=-1, out_stats=None, stream=None, sequential=False):
+                      do_sample=None, stop_token=-1, out_stats=None, stream=None, sequential=False,
+                      speculate=True):
         n_steps, n_rows, ld = logits.shape
         s = Stream(logits=_p(logits), ld=ld, step_stride=n_rows * ld, n_steps=n_steps,
                    n_rows=n_rows, vocab=ld, stop_token=stop_token, hist_ids=_p(hist_ids),
                    hist_offsets=_p(hist_off), temperature=_p(temp), top_k=_p(top_k),
                    top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample),
                    rng_state=_p(rng), out_tokens=_p(out_tokens), out_stats=_p(out_stats),
-                   flags=STREAM_SEQUENTIAL if sequential else 0)
+                   flags=(STREAM_SEQUENTIAL if sequential else 0) | (0 if speculate else STREAM_NO_SPECULATION))
         self._check(lib().c4s_sample_stream(self._h, C.byref(s), _stream_handle(stream)),
                     "sample_stream")
 

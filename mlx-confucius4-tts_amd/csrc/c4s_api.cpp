@@ -64,6 +64,7 @@ constexpr int kStreamVocabMax = c4s::kLdsVocabMax;
 constexpr size_t kLdsLimit = 160 * 1024;
 constexpr size_t kChainStaticLds = 38 * 1024;      // chain kernels' static LDS (upper bound)
 constexpr size_t kRowPStaticLds = 40 * 1024;       // pipelined row chain's static LDS (upper bound)
+constexpr size_t kSpecStaticLds = 12 * 1024;       // speculative row chain's static LDS (upper bound)
 constexpr size_t kSumBudget = (size_t)512 << 20;   // stream summaries per chunk of steps
 constexpr int kScanStepsPerGroup = 8;
 // Chunks of the overlapped stream: the first is short (its scan is not
@@ -80,7 +81,7 @@ constexpr int kOverlapStepsPerGroup = 1;   // one step a scan workgroup: the sho
 // Of every 32 CUs, the chains' shares in the overlapped stream: the
 // full-vocabulary chain (a workgroup holds a whole CU's LDS) and the list
 // chain (two workgroups a CU); the scans take the rest.
-constexpr int kRowCusPer32 = 6;
+constexpr int kRowCusPer32 = 4;
 constexpr int kListCusPer32 = 4;
 constexpr int kMaxSegments = 8;   // step segments per row without penalty
 
@@ -396,7 +397,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   a.rng = st->rng_state;
   a.out_tok = st->out_tokens;
   a.stats = st->out_stats;
-  if (st->flags & ~(uint32_t)C4S_STREAM_SEQUENTIAL) return fail(ctx, C4S_EINVAL, "stream: unknown flags");
+  if (st->flags & ~(uint32_t)(C4S_STREAM_SEQUENTIAL | C4S_STREAM_NO_SPECULATION))
+    return fail(ctx, C4S_EINVAL, "stream: unknown flags");
   if (c4s::stream_lds_bytes(a.vocab, 0) + 4096 > kLdsLimit)
     return fail(ctx, C4S_EINVAL, "stream: row state exceeds LDS");
   DeviceGuard g(ctx->device);
@@ -448,7 +450,13 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   rc = ensure(ctx, &ctx->segres, &ctx->segres_bytes, (size_t)a.n_rows * nseg * 4 * sizeof(uint64_t),
               "segment results", hs);
   if (rc) return rc;
+  // Full-vocabulary rows: the speculative chain (several steps decided at
+  // once, each checked in order) when a call's drawn ids fit its lists, else
+  // the pipelined chain with step segments for rows without penalty.
+  const bool spec = !(st->flags & C4S_STREAM_NO_SPECULATION) && a.n_steps <= c4s::stream_spec_max_steps() &&
+                    c4s::stream_spec_lds_bytes(a.vocab) + kSpecStaticLds <= kLdsLimit;
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
+    if (spec) return c4s::launch_stream_spec(a, w, on);
     hipError_t e = c4s::launch_stream_rowp(a, w, on);
     return e == hipSuccess ? c4s::launch_stream_segfix(a, w, on) : e;
   };

@@ -26,6 +26,12 @@
 #ifndef C4S_ROW_TIME
 #define C4S_ROW_TIME(n) ((void)0)
 #endif
+#ifndef C4S_SPEC_T
+#define C4S_SPEC_T(n) ((void)0)
+#define C4S_SPEC_DECL ((void)0)
+#define C4S_SPEC_END(w) ((void)0)
+#define C4S_SPEC_EV(step, ev) ((void)0)
+#endif
 
 namespace c4s {
 

@@ -802,15 +802,48 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   return true;
 }
 
+// Where a step reads raw values and the set of ids drawn during the stream.
+// RowAcc: the raw row and the drawn-id bitmap staged in LDS.
+//   hit(id)  id was drawn during the stream (it is then penalised again)
+//   hval(id) raw value of a drawn id
+//   raw(id)  raw value of any id (the dense draw's chunk)
+//   pen(id)  id is penalised (H0 or drawn)
+struct RowAcc {
+  const float* v;
+  const uint32_t* bmN;
+  const uint32_t* bmH0;
+  __device__ __forceinline__ bool hit(int id) const { return (bmN[id >> 5] >> (id & 31)) & 1u; }
+  __device__ __forceinline__ float hval(int id) const { return v[id]; }
+  __device__ __forceinline__ float raw(int id) const { return v[id]; }
+  __device__ __forceinline__ bool pen(int id) const { return ((bmH0[id >> 5] | bmN[id >> 5]) >> (id & 31)) & 1u; }
+};
+
+// What a decided step rests on, so that it can be checked later against ids
+// drawn after the set it was decided with: kind 1, a nucleus cut (the kept
+// ranks [0, q), the masses above ranks q - 1 and q, the cut value); kind 2,
+// the dense draw (the prefixes through and before the token, the uniform);
+// kind 0, nothing to check against (the step is redone).
+struct SpecInfo {
+  int kind;
+  int q;
+  int chk1;    // rank q - 1 is at or past min_keep (its margin is checked)
+  float zcut;  // z of rank q - 1
+  float mt;    // the maximum
+  double S, rho, err, eps, dmass, p;
+  double A1, A2;
+  double af, pf, u;
+};
+
 // Dense draw (top_p keeps every id of nonzero mass; zero masses never win),
 // text2semantic.cpp:150-165: r = u * S, the chunk prefixes (summary chunk
 // masses less the corrections, times rho) locate r, the chunk's masses are
 // recomputed exactly from the staged row. False when r is not inside its
 // chunk by the error margin.
-__device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int V, const float* val,
-                                           const uint32_t* bmN, const uint32_t* bmH0, const uint64_t* sum,
+template <class Acc>
+__device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int V, const Acc& acc,
+                                           const uint64_t* sum,
                                            const double* cdelta, double u, double S, double rho, double err,
-                                           float mt, StepOut& o) {
+                                           float mt, StepOut& o, SpecInfo* si) {
   const int lane = lane_id();
   const float ninf = neg_inf();
   const double eps = rel_eps(V);
@@ -857,15 +890,15 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   // the chunk's values and bitmap words read unconditionally (ids clamped into
   // the chunk), so that both reads of each id go out together
   const int ja = min(ia, hi - 1), jb = min(ib, hi - 1);
-  const float xa = val[ja], xb = val[jb];
-  const uint32_t ha = bmH0[ja >> 5] | bmN[ja >> 5], hb = bmH0[jb >> 5] | bmN[jb >> 5];
-  auto mass_of = [&](float x, uint32_t hw, int id) -> double {
-    const float y = (c.pen_on && ((hw >> (id & 31)) & 1u)) ? pen_exact(x, c.pen) : x;
+  const float xa = acc.raw(ja), xb = acc.raw(jb);
+  const bool ha = acc.pen(ja), hb = acc.pen(jb);
+  auto mass_of = [&](float x, bool pn) -> double {
+    const float y = (c.pen_on && pn) ? pen_exact(x, c.pen) : x;
     const float z = c.temp_on ? y / c.temp : y;
     return (z == ninf) ? 0.0 : exp((double)(z - mt));
   };
-  const double ea = ia < hi ? mass_of(xa, ha, ja) : 0.0;
-  const double eb = ib < hi ? mass_of(xb, hb, jb) : 0.0;
+  const double ea = ia < hi ? mass_of(xa, ha) : 0.0;
+  const double eb = ib < hi ? mass_of(xb, hb) : 0.0;
   C4S_PHASE(14);
   const double sa = wave_scan_f64(ea) + pstar;
   const double ta = readlane_f64(sa, kWave - 1);
@@ -892,6 +925,17 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
   o.tok = tok;
   o.kept = (uint32_t)V;
   o.dex = 0;
+  if (si) {
+    si->kind = 2;
+    si->mt = mt;
+    si->S = S;
+    si->rho = rho;
+    si->err = err;
+    si->eps = eps;
+    si->af = af;
+    si->pf = pf;
+    si->u = u;
+  }
   return true;
 }
 
@@ -900,10 +944,11 @@ __device__ __forceinline__ bool dense_draw(const SumHdr& h, const RowCfg& c, int
 // unhit entries move to lanes 0..nu-1 in rank order by one lane permute; the
 // cut is one prefix scan, the draw the lane draw. Same decisions and margins
 // as row_step; false, with rng and o unchanged, when the step needs row_step.
-__device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c, int V, const float* val,
-                                               const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
+template <class Acc>
+__device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c, int V, const Acc& acc,
+                                               double dsum, double derr,
                                                const uint64_t* sum, const double* cdelta, uint64_t& rng,
-                                               StepOut& o) {
+                                               StepOut& o, SpecInfo* si = nullptr) {
   const int lane = lane_id();
   if (h.flags & 1u) return false;
   const int n = h.n;
@@ -913,9 +958,9 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const uint64_t e = sum[lane];
   const float m32 = reinterpret_cast<const float*>(sum + kYW)[lane];
   const int id = v ? ent_id(e) : 0;
-  const uint32_t bw = bmN[id >> 5];
-  const float xr = val[id];
-  const bool hit = c.pen_on && v && ((bw >> (id & 31)) & 1u);
+  const bool drawn = acc.hit(id);
+  const float xr = acc.hval(id);
+  const bool hit = c.pen_on && v && drawn;
   // a drawn id is never in H0: its value is the raw one (the penalty and the
   // temperature are monotone, so the largest penalised hit comes from the largest raw one)
   const float hraw = hit ? xr : ninf;
@@ -955,7 +1000,7 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   const double u = unit_from_state(st);
   C4S_PHASE(6);
   if (!(thr > 0.0)) {
-    if (!dense_draw(h, c, V, val, bmN, bmH0, sum, cdelta, u, S, rho, err, mt, o)) return false;
+    if (!dense_draw(h, c, V, acc, sum, cdelta, u, S, rho, err, mt, o, si)) return false;
     rng = st;
     return true;
   }
@@ -978,6 +1023,21 @@ __device__ __forceinline__ bool row_step_lanes(const SumHdr& h, const RowCfg& c,
   if (q > nu) return false;
   const float zq1 = readlane_f32(z, q - 1);
   if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
+  if (si) {
+    si->kind = 1;
+    si->q = q;
+    si->chk1 = q - 1 >= c.min_keep;
+    si->zcut = zq1;
+    si->mt = mt;
+    si->S = S;
+    si->rho = rho;
+    si->err = err;
+    si->eps = eps;
+    si->dmass = dmass;
+    si->p = (double)c.p;
+    si->A1 = readlane_f64(above, q - 1);
+    si->A2 = readlane_f64(inc, q - 1);
+  }
   C4S_PHASE(7);
   // the draw on the kept ranks [0, q): first with the masses above, then exact
   const bool kept = lane < q;
@@ -1104,10 +1164,10 @@ __device__ __forceinline__ int inv_draw(CS& cs, uint32_t gen, int q, bool approx
 // ranks then go to LDS for the id-order draw (inv_draw). Same decisions and
 // margins as row_step; false, with rng and o unchanged, when the step needs
 // row_step (its generation counter may have moved, which is harmless).
-template <class CS>
-__device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c, int V, const float* val,
-                                                const uint32_t* bmN, double dsum, double derr, const uint64_t* sum,
-                                                uint64_t& rng, CS& cs, StepOut& o) {
+template <class CS, class Acc>
+__device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c, int V, const Acc& acc,
+                                                double dsum, double derr, const uint64_t* sum,
+                                                uint64_t& rng, CS& cs, StepOut& o, SpecInfo* si = nullptr) {
   constexpr int K = 4;
   const int lane = lane_id();
   if (h.flags & 1u) return false;
@@ -1127,7 +1187,7 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   // the four entries' reads go out together: entries, then bitmap words and
   // raw values. A drawn id is never in H0: its value is the raw one.
   int id[K];
-  uint32_t bw[K];
+  bool dr[K];
   float xr[K];
 #pragma unroll
   for (int i = 0; i < K; ++i) {
@@ -1138,13 +1198,13 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   for (int i = 0; i < K; ++i) id[i] = (p0 + i < n) ? ent_id(e[i]) : 0;
 #pragma unroll
   for (int i = 0; i < K; ++i) {
-    bw[i] = bmN[id[i] >> 5];
-    xr[i] = val[id[i]];
+    dr[i] = acc.hit(id[i]);
+    xr[i] = acc.hval(id[i]);
   }
 #pragma unroll
   for (int i = 0; i < K; ++i) {
     const bool v = p0 + i < n;
-    const bool hit = c.pen_on & v & (((bw[i] >> (id[i] & 31)) & 1u) != 0u);
+    const bool hit = c.pen_on & v & dr[i];
     hraw = hit ? fmaxf(hraw, xr[i]) : hraw;
     un[i] = v & !hit;
     z[i] = un[i] ? kfloat(ent_key(e[i])) : ninf;
@@ -1212,10 +1272,12 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
   for (int i = 0; i < K; ++i) ls += em[i];
   const double inc = wave_scan_f64(ls);
   double ab = inc - ls;
+  double abv[K];
   bool unsure = false, tiny = false;
   int qloc = 0x7fffffff;
 #pragma unroll
   for (int i = 0; i < K; ++i) {
+    abv[i] = ab;
     const double D = ab - pS;
     unsure |= un[i] && rk[i] >= c.min_keep && !(fabs(D) > marg + (eps + dmass) * ab);
     tiny |= un[i] && D < 0.0 && em[i] < 0x1p-1000;
@@ -1236,8 +1298,31 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
     zs = m ? z[i] : zs;
     has |= m;
   }
-  const float zq1 = readlane_f32(zs, __ffsll((unsigned long long)__ballot(has)) - 1);
+  const int lq = __ffsll((unsigned long long)__ballot(has)) - 1;
+  const float zq1 = readlane_f32(zs, lq);
   if (!(zo < zq1) || !(zend < zq1) || !(hm < zq1)) return false;
+  if (si) {
+    double a1 = 0.0, a2 = 0.0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const bool m = un[i] && rk[i] == q - 1;
+      a1 = m ? abv[i] : a1;
+      a2 = m ? abv[i] + em[i] : a2;
+    }
+    si->kind = 1;
+    si->q = q;
+    si->chk1 = q - 1 >= c.min_keep;
+    si->zcut = zq1;
+    si->mt = mt;
+    si->S = S;
+    si->rho = rho;
+    si->err = err;
+    si->eps = eps;
+    si->dmass = dmass;
+    si->p = (double)c.p;
+    si->A1 = readlane_f64(a1, lq);
+    si->A2 = readlane_f64(a2, lq);
+  }
   // Id-order draw (text2semantic.cpp:150-165) over the kept ranks: every entry
   // of the list's first np writes its stored mass, value and id (-1 unless
   // kept) at its id-order place among them (the scan's place bytes); four
@@ -1345,11 +1430,11 @@ __device__ __forceinline__ bool row_step_lanes4(const SumHdr& h, const RowCfg& c
 // its error derr; per chunk in `cdelta`) and the raw row in LDS (`val`). The
 // list is compacted lazily, 256 entries at a time, only as deep as the decision
 // needs; cs provides the compaction and slot arrays.
-template <class CS>
-__device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const float* val,
-                         const uint32_t* bmN, const uint32_t* bmH0, double dsum, double derr,
+template <class CS, class Acc>
+__device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V, const Acc& acc,
+                         double dsum, double derr,
                          const uint64_t* sum, const double* cdelta, uint64_t& rng, CS& cs,
-                         StepOut& o) {
+                         StepOut& o, SpecInfo* si = nullptr) {
   const int lane = lane_id();
   o.why = kWhySummary;
   if (h.flags & 1u) return false;
@@ -1381,7 +1466,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
     for (int i = 0; i < 4; ++i) {
       const bool v = p0 + i < n;
       // every lane reads its bitmap word (no branch around the load)
-      const bool drawn = bit_of(bmN, v ? ent_id(e[i]) : 0);
+      const bool drawn = acc.hit(v ? ent_id(e[i]) : 0);
       hit[i] = c.pen_on & v & drawn;
       un[i] = v & !hit[i];
       cu += un[i] ? 1u : 0u;
@@ -1400,7 +1485,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
         ++rk;
       }
       if (hit[i]) {   // sampling.cpp:26, then :16; a drawn id is never in H0, so its value is the raw one
-        const float y = pen_exact(val[id], c.pen);
+        const float y = pen_exact(acc.hval(id), c.pen);
         hm = fmaxf(hm, c.temp_on ? y / c.temp : y);
       }
     }
@@ -1519,6 +1604,24 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
     if (!(zo < zq1)) return false;
     o.why = kWhyHit;
     if (!(wave_max_dpp(hm) < zq1)) return false;
+    if (si) {   // the masses above ranks q - 1 and q, summed again over the kept ranks
+      double a1 = 0.0;
+      for (int r0 = 0; r0 < q - 1; r0 += kWave) a1 += (r0 + lane < q - 1) ? mass_of(r0 + lane, false) : 0.0;
+      a1 = wave_sum_dpp(a1);
+      si->kind = 1;
+      si->q = q;
+      si->chk1 = q - 1 >= c.min_keep;
+      si->zcut = zq1;
+      si->mt = mt;
+      si->S = S;
+      si->rho = rho;
+      si->err = err;
+      si->eps = eps;
+      si->dmass = dmass;
+      si->p = (double)c.p;
+      si->A1 = a1;
+      si->A2 = a1 + mass_of(q - 1, false);
+    }
     // The draw on the kept ranks [0, q): first with the masses above (a decision
     // inside their error is not replayed), then, if needed, with exact masses.
     if (q <= kWave) {   // kept ranks are the first chunk: lane = rank
@@ -1538,7 +1641,7 @@ __device__ __forceinline__ bool row_step(const SumHdr& h, const RowCfg& c, int V
     return true;
   }
 
-  if (!dense_draw(h, c, V, val, bmN, bmH0, sum, cdelta, u, S, rho, err, mt, o)) return false;
+  if (!dense_draw(h, c, V, acc, sum, cdelta, u, S, rho, err, mt, o, si)) return false;
   rng = st;
   return true;
 }
@@ -2128,9 +2231,10 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
         StepOut o{0, 0u, 0u, 0u};
         // the register path when the scan's cut hint leaves room for hits within 64 ranks
         const int hint = (int)(uint32_t)sw[kHdrW + 5];
-        const bool ok = ((dense || hint <= kLanesHint) && row_step_lanes(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, o)) ||
-                        (!dense && hint <= 4 * kWave && row_step_lanes4(h, c, V, val, bmN, ds, de, sw, rng, ps, o)) ||
-                        row_step(h, c, V, val, bmN, bmH0, ds, de, sw, cd, rng, ps, o);
+        const RowAcc rac{val, bmN, bmH0};
+        const bool ok = ((dense || hint <= kLanesHint) && row_step_lanes(h, c, V, rac, ds, de, sw, cd, rng, o)) ||
+                        (!dense && hint <= 4 * kWave && row_step_lanes4(h, c, V, rac, ds, de, sw, rng, ps, o)) ||
+                        row_step(h, c, V, rac, ds, de, sw, cd, rng, ps, o);
         const bool retry = attempt == 0 && !ok && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin);
         C4S_PHASE(2);
         if (attempt == 0 && dense)
@@ -2443,7 +2547,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
       if (wv == 0) {
         double ds = 0.0, de = 0.0;
         for (int i = 0; i < NW; ++i) { ds += cs.wd[i]; de += cs.we[i]; }
-        const bool ok = row_step(h, c, V, val, bmN, bmH0, ds, de, cs.sum, cs.cdelta, rng, cs, o);
+        const bool ok = row_step(h, c, V, RowAcc{val, bmN, bmH0}, ds, de, cs.sum, cs.cdelta, rng, cs, o);
         for (int i = lane; i < kMaxChunks; i += kWave) cs.cdelta[i] = 0.0;
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
@@ -2508,6 +2612,670 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
   for (int i = t; i < nwords; i += NT) stw[kStBits + i] = bmN[i];
 }
 
+
+// ---- speculative full-vocabulary chain --------------------------------------------
+//
+// One workgroup per row: wave kSpecVW validates, the others decide. A step
+// depends on earlier steps only through the ids drawn before it (the
+// penalty) and its RNG state, which is fixed. Decider k takes steps
+// s_first + k, + kSpecND, ... and decides each against the ids drawn before
+// the validated frontier when it starts (at most kSpecND - 1 steps behind).
+// Wave 0 takes the steps in order and accepts a decision when the ids drawn
+// since provably leave it as it is: none of them is kept by it (none reaches
+// the cut value, or the maximum of a dense row, and none is its token), and
+// the mass their penalty removes moves neither the nucleus cut (ranks q - 1
+// and q keep their sides with the error margins) nor, for the dense draw,
+// r = u * S out of the drawn id's prefix interval. Otherwise wave 0 decides
+// the step again with every drawn id. Only summaries are staged: a decider
+// gathers the drawn ids' raw values from the step's row in HBM, and wave 0
+// gathers, for each decided token, its raw values in the next 64 steps, so
+// that the check reads LDS only. A step no summary path settles stops every
+// wave for the exact chain on the row read into LDS.
+
+constexpr int kSpecND = 5;                 // decider waves
+constexpr int NTS = (kSpecND + 1) * kWave;
+constexpr int kSpecGv = 1024;              // ids a call can draw (its steps at most)
+constexpr int kRing = 16;                  // per-token value rows kept by wave 0
+constexpr int kSpinMax = 1 << 22;          // wave 0's wait for a decision (about 0.3 s)
+constexpr int kSpecVW = 3;                 // the checking wave: alone on its SIMD (waves go to SIMDs in turn)
+constexpr int kHist = 8;                   // steps of tokens the checking wave keeps in registers
+static_assert(kHist >= kSpecND, "history covers the steps a decision can lag");
+static_assert(kRing >= 2 * kSpecND, "ring covers the steps a check looks back");
+
+struct SpecCS {   // a decider's rank and slot arrays (what row_step needs)
+  uint32_t inv[kListLarge + 1];
+  uint32_t gen;
+  float lz[kListLarge + 1];
+  float lm[kListLarge + 1];
+  int lid[kListLarge + 1];
+  int lslot[kListLarge];
+};
+
+struct SpecRec {
+  int tag;   // step of this decision (written last), -1 none
+  int tok;
+  int nF;    // drawn ids the decision knew (a prefix of the drawn list)
+  int F;     // ... those drawn before step F
+  int fresh; // tok is none of them, nor in H0, nor the stop token
+  int ok;
+  int ring;  // the decider gathers tok's values of the next steps into ring row tag
+  uint32_t why, dex, kept;
+  double ds, de;
+  // The check, with DL the mass the ids drawn since remove (sum of m(x) -
+  // m(pen x)), Y its error bound plus |DL| 2^-50, Da the part of DL from ids
+  // below tok. kind 1 (nucleus): no new id reaches zlim (the cut value),
+  // w (DL + Y) < g1 (rank q - 1 stays kept) and w (DL - Y) > g2 (rank q stays
+  // out). kind 2 (dense): no new id reaches zlim (the maximum) nor is tok,
+  // w (u DL - ome Da - 2 Y) > g1 and w (Da - ome u DL - 2 Y) > g2 (r stays
+  // inside tok's prefix interval). Any other kind: decide again.
+  int kind;
+  float zlim;
+  double g1, g2, w, u, ome;
+  float ma, mb, mrel;   // mass coefficients of the step (mass_coef of its m0)
+  SpecInfo si;
+};
+
+struct SpecCtl {
+  int ringtag[kRing];   // step whose token's values ring row r holds (landed), else -1
+  int snap;   // (frontier << 16) | drawn ids before the frontier
+  int halt;   // step of an exact chain run by every wave, else -1
+  int done;
+  int err;
+  int qend;   // first step not decided
+  int stopped;
+  int tok;
+  uint64_t rng;
+  uint32_t acc[4];
+};
+
+// Drawn set of one decision: ids whose drawn index is below nF; raw values of
+// drawn ids by drawn index in gv, any other raw value from the row in HBM.
+struct SpecAcc {
+  const uint16_t* didx;
+  const float* gv;
+  const uint32_t* bmH0;
+  const float* grow;
+  int nF;
+  __device__ __forceinline__ bool hit(int id) const { return (int)didx[id] < nF; }
+  __device__ __forceinline__ float hval(int id) const { return gv[min((int)didx[id], kSpecGv - 1)]; }
+  __device__ __forceinline__ float raw(int id) const { return grow[id]; }
+  __device__ __forceinline__ bool pen(int id) const { return bit_of(bmH0, id) || hit(id); }
+};
+
+struct SpecLayout {
+  size_t didx, tok, tstep, ring, tout, dec, stride, o_gv, o_cd, o_cs, total;
+};
+__host__ __device__ inline size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
+__host__ __device__ inline SpecLayout spec_layout(int V) {
+  SpecLayout L;
+  L.didx = 0;
+  L.tok = al16(L.didx + 2 * (size_t)V);
+  L.tstep = al16(L.tok + 4 * (size_t)kSpecGv);
+  L.ring = al16(L.tstep + 2 * (size_t)kSpecGv);
+  L.tout = al16(L.ring + 4 * (size_t)kRing * kWave);
+  L.dec = al16(L.tout + 2 * (size_t)kSpecGv);
+  L.o_gv = al16(8 * (size_t)kSumWordsP);
+  L.o_cd = al16(L.o_gv + 4 * (size_t)kSpecGv);
+  L.o_cs = al16(L.o_cd + 8 * (size_t)kMaxChunks);
+  L.stride = al16(L.o_cs + sizeof(SpecCS));
+  size_t dec = (size_t)kSpecND * L.stride;
+  const size_t rowb = al16(4 * ((size_t)vpad(V) + 4));   // the exact chain's row over the deciders' areas
+  L.total = L.dec + (dec > rowb ? dec : rowb);
+  return L;
+}
+
+template <class CS, class Acc>
+__device__ __forceinline__ bool spec_decide(const SumHdr& h, const RowCfg& c, int V, const Acc& acc, double ds,
+                                            double de, const uint64_t* sw, double* cd, uint64_t& r, CS& cs,
+                                            StepOut& o, SpecInfo* si, bool dense) {
+  const int hint = (int)(uint32_t)sw[kHdrW + 5];
+  return ((dense || hint <= kLanesHint) && row_step_lanes(h, c, V, acc, ds, de, sw, cd, r, o, si)) ||
+         (!dense && hint <= 4 * kWave && row_step_lanes4(h, c, V, acc, ds, de, sw, r, cs, o, si)) ||
+         row_step(h, c, V, acc, ds, de, sw, cd, r, cs, o, si);
+}
+
+// Corrections of one step over drawn indices [0, n): the mass of the raw value
+// minus that of the penalised one (fp32 with the error bound el, or exact),
+// added per chunk into cd for dense rows (cd cleared by the caller).
+__device__ __forceinline__ double spec_corrections(const float* gv, const int* tokl, int n, const SumHdr& h,
+                                                   const RowCfg& c, double* cd, bool exact, double& el) {
+  const int lane = lane_id();
+  double dl = 0.0, ell = 0.0;
+  if (!(h.flags & 1u)) {
+    const MassCoef mk = mass_coef(c, h.m0);
+    const float rpen = 1.0f / c.pen;
+    for (int j0 = 0; j0 < n; j0 += 4 * kWave) {
+      float x[4];
+      int id[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {   // reads in bounds, issued together
+        const int j = min(j0 + i * kWave + lane, kSpecGv - 1);
+        x[i] = gv[j];
+        id[i] = cd ? tokl[j] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (j0 + i * kWave + lane >= n) continue;
+        double d;
+        if (exact) {
+          d = mass_exact(x[i], c, h.m0) - mass_exact(pen_exact(x[i], c.pen), c, h.m0);
+        } else {
+          float e0, e1;
+          const float m1 = mass_approx(x[i], mk, e0);
+          const float m2 = mass_approx(pen_approx(x[i], c.pen, rpen), mk, e1);
+          d = (double)m1 - (double)m2;
+          ell += (double)e0 + (double)e1;
+        }
+        if (cd) atomicAdd(&cd[chunk_of(id[i], h.head, h.nchunk)], d);
+        dl += d;
+      }
+    }
+  }
+  el = wave_sum_dpp(ell);
+  return wave_sum_dpp(dl);
+}
+
+// Volatile LDS accesses (p points into LDS). Through an LDS pointer: a
+// generic (flat) access would also wait for this wave's global loads.
+template <typename T>
+__device__ __forceinline__ T vload(const T* p) {
+  typedef const volatile __attribute__((address_space(3))) T LT;
+  return *(LT*)(const __attribute__((address_space(3))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ void vstore(T* p, T v) {
+  typedef volatile __attribute__((address_space(3))) T LT;
+  *(LT*)(__attribute__((address_space(3))) T*)p = v;
+}
+__device__ __forceinline__ void lgkm_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Waits until at most n of this wave's vector memory operations are in flight.
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n < 0 ? 0 : (n > 15 ? 15 : n)) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+    case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+    case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+  }
+}
+
+__global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ SpecRec recs[kSpecND];
+  __shared__ SpecCtl ctl;
+  __shared__ ScratchT<kSpecND + 1> xs;   // exact steps
+  __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (stream_mode(c, V) != kModeRow) return;
+  int s_first;
+  if (!fast_begin(a, w, row, NTS, s_first)) return;
+  const int s_end = w.s_end;
+  const uint64_t rng0 = a.rng[row];
+  const uint32_t* stw = w.state + (size_t)row * kStateWords;
+  const SpecLayout L = spec_layout(V);
+  uint16_t* didx = reinterpret_cast<uint16_t*>(smem + L.didx);
+  int* tokl = reinterpret_cast<int*>(smem + L.tok);
+  uint16_t* tstep = reinterpret_cast<uint16_t*>(smem + L.tstep);
+  float* ring = reinterpret_cast<float*>(smem + L.ring);
+  int16_t* tout = reinterpret_cast<int16_t*>(smem + L.tout);
+  auto dbase = [&](int k) { return smem + L.dec + (size_t)k * L.stride; };
+  auto dsum = [&](int k) { return reinterpret_cast<uint64_t*>(dbase(k)); };
+  auto dgv = [&](int k) { return reinterpret_cast<float*>(dbase(k) + L.o_gv); };
+  auto dcd = [&](int k) { return reinterpret_cast<double*>(dbase(k) + L.o_cd); };
+  auto dcs = [&](int k) -> SpecCS& { return *reinterpret_cast<SpecCS*>(dbase(k) + L.o_cs); };
+  const float* base = a.logits + (int64_t)row * a.ld;
+  auto rowp = [&](int s) { return base + (int64_t)s * a.step_stride; };
+  const bool dense = !(1.0 - (double)c.p > 0.0);
+  const int nwords = bitmap_words(V);
+  C4S_SPEC_DECL;
+
+  // Prologue: H0 and the ids drawn in earlier chunks, listed in id order.
+  fast_bitmaps(a, stw, row, V, NTS, bmH0, bmN, true);
+  for (int i = t; i < V; i += NTS) didx[i] = 0xFFFFu;
+  if (t < kSpecND) recs[t].tag = -1;
+  __syncthreads();
+  if (wv == 0) {
+    int n = 0;
+    for (int w0 = 0; w0 < nwords; w0 += kWave) {
+      const int wb = w0 + lane;
+      uint32_t bits = wb < nwords ? bmN[wb] : 0u;
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wave_scan_u32(cnt);
+      int p = n + (int)(incl - cnt);
+      while (bits) {
+        const int id = 32 * wb + __ffs(bits) - 1;
+        bits &= bits - 1;
+        if (p < kSpecGv && id < V) {
+          tokl[p] = id;
+          tstep[p] = 0;
+          didx[id] = (uint16_t)p;
+        }
+        ++p;
+      }
+      n += (int)readlane_u32(incl, kWave - 1);
+    }
+    if (lane == 0) {
+      ctl.snap = (s_first << 16) | min(n, kSpecGv);
+      ctl.halt = -1;
+      ctl.done = 0;
+      ctl.err = n > kSpecGv ? 1 : 0;
+      ctl.qend = s_first;
+      ctl.stopped = 0;
+      for (int i = 0; i < kRing; ++i) ctl.ringtag[i] = -1;
+      ctl.rng = rng0;
+      for (int i = 0; i < 4; ++i) ctl.acc[i] = stw[1 + i];
+    }
+  }
+  __syncthreads();
+
+  // Every wave runs the exact chain of step hq on the raw row read into LDS
+  // over the deciders' areas (text2semantic.cpp:142-166); ends at a barrier.
+  auto exact_all = [&](int hq) __attribute__((always_inline)) {
+    __syncthreads();
+    float* X = reinterpret_cast<float*>(smem + L.dec);
+    const float* src = rowp(hq);
+    for (int i = t; i < V; i += NTS) X[i] = src[i];
+    __syncthreads();
+    if (c.pen_on) {   // H0 and the stream's ids are disjoint: each id once
+      penalise_chunk<NTS>(X, bmH0, V, c.pen);
+      penalise_chunk<NTS>(X, bmN, V, c.pen);
+    }
+    __syncthreads();
+    uint64_t r = ctl.rng;
+    LdsRowNC srow{X, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    const int tok = run_chain(srow, xs, c, r, nullptr, xs.step_stats);
+    __syncthreads();
+    if (t == 0) {
+      ctl.tok = tok;
+      ctl.rng = r;
+    }
+    __syncthreads();
+  };
+
+  if (wv == kSpecVW) {
+    // ---- the checking wave: takes the decisions in step order ----
+    int q = s_first;
+    int n = ctl.snap & 0xFFFF;
+    uint64_t rng = rng0;
+    uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
+    bool stopped = false, bad = ctl.err != 0;
+    const float rpen = 1.0f / c.pen;
+    // the last kHist steps: lane (step % kHist) holds the step, its token and
+    // whether the token joined the drawn ids
+    int htok = -1, hstep = -1;
+    bool hfresh = false;
+    // the values of decided token tk in steps gs + 1 .. gs + 64, into ring row gs
+    auto issue_ring = [&](int gs, int tk) __attribute__((always_inline)) {
+      const int tc = (tk >= 0 && tk < V) ? tk : 0;
+      const int sidx = min(gs + 1 + lane, a.n_steps - 1);
+      __builtin_amdgcn_global_load_lds((glb_ptr_t)(rowp(sidx) + tc),
+                                       (lds_ptr_t)(ring + (gs & (kRing - 1)) * kWave), 4, 0, 0);
+    };
+    while (q < s_end && !bad) {
+      C4S_SPEC_T(0);
+      const int k = (q - s_first) % kSpecND;
+      SpecRec& rc = recs[k];
+      int spins = 0;
+      while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
+      if (spins > kSpinMax) {
+        bad = true;
+        break;
+      }
+      C4S_SPEC_T(1);
+      C4S_SPEC_EV(q, 2);
+      const int nFd = rc.nF, rtok = rc.tok, Fd = rc.F, rok = rc.ok, rfresh = rc.fresh, kind = rc.kind;
+      const float zlim = rc.zlim;
+      const MassCoef mk{rc.ma, rc.mb, rc.mrel};
+      // The ids drawn since the decision (steps [Fd, q)) are in the history
+      // lanes; their values at step q are in the ring rows of their steps.
+      const bool isnew = lane < kHist && hfresh && hstep >= Fd && hstep < q;
+      const uint64_t nm = __ballot(isnew);
+      const int nn = __popcll(nm);
+      const int rslot = hstep & (kRing - 1);
+      spins = 0;
+      while (__ballot(isnew && vload(&ctl.ringtag[rslot]) != hstep) && ++spins <= kSpinMax)
+        __builtin_amdgcn_s_sleep(1);
+      if (spins > kSpinMax) {
+        bad = true;
+        break;
+      }
+      C4S_SPEC_T(2);
+      const float x = ring[rslot * kWave + ((q - hstep - 1) & (kWave - 1))];
+      const float z = c.temp_on ? x / c.temp : x;
+      float e0, e1;
+      const float m1 = mass_approx(x, mk, e0);
+      const float m2 = mass_approx(pen_approx(x, c.pen, rpen), mk, e1);
+      const double d = isnew ? (double)m1 - (double)m2 : 0.0;
+      const double e = isnew ? (double)e0 + (double)e1 : 0.0;
+      // the history and the drawn list agree unless the decision is older than the history
+      bool accept = rok != 0 && nn == n - nFd && q - Fd <= kHist;
+      double DL = 0.0, EL = 0.0, Da = 0.0;
+      for (uint64_t b = nm; b; b &= b - 1) {
+        const int j = __ffsll((unsigned long long)b) - 1;
+        const double dj = readlane_f64(d, j);
+        DL += dj;
+        EL += readlane_f64(e, j);
+        Da += ((int)readlane_u32((uint32_t)htok, j) < rtok) ? dj : 0.0;
+      }
+      if (accept && nn > 0) {
+        const double Y = EL + fabs(DL) * 0x1p-50;
+        if (kind == 1) {
+          accept = !__ballot(isnew && !(z < zlim)) && rc.w * (DL + Y) < rc.g1 && rc.w * (DL - Y) > rc.g2;
+        } else if (kind == 2) {
+          accept = !__ballot(isnew && (!(z < zlim) || htok == rtok)) &&
+                   rc.w * (rc.u * DL - rc.ome * Da - 2.0 * Y) > rc.g1 &&
+                   rc.w * (Da - rc.ome * rc.u * DL - 2.0 * Y) > rc.g2;
+        } else {
+          accept = false;
+        }
+      }
+      int tokq = rtok;
+      uint32_t dex = rc.dex, kept = rc.kept;
+      bool exact = false;
+      C4S_SPEC_T(3);
+      if (!accept) {
+        // decide again with every drawn id: the ids drawn since the decision
+        // (drawn list [nFd, n)) join the decider's list with their values
+        const SumHdr h = hdr_from(dsum(k));
+        const int nl = n - nFd;
+        const bool hl = lane < nl;
+        const int idx = min(nFd + lane, kSpecGv - 1);
+        const int tl = tokl[idx];
+        const int ts = tstep[idx];
+        const float xl = ring[(ts & (kRing - 1)) * kWave + ((q - ts - 1) & (kWave - 1))];
+        float f0, f1;
+        const float l1 = mass_approx(xl, mk, f0);
+        const float l2 = mass_approx(pen_approx(xl, c.pen, rpen), mk, f1);
+        const double dl = hl ? (double)l1 - (double)l2 : 0.0;
+        const double el = hl ? (double)f0 + (double)f1 : 0.0;
+        float* gvk = dgv(k);
+        double* cd = dcd(k);
+        if (hl && nl <= kWave) gvk[idx] = xl;
+        if (dense && hl && nl <= kWave) atomicAdd(&cd[chunk_of(tl, h.head, h.nchunk)], dl);
+        wave_sync();
+        double ds = rc.ds + wave_sum_dpp(dl), de = rc.de + wave_sum_dpp(el);
+        StepOut o{0, 0u, 0u, 0u};
+        uint64_t r = rng;
+        const int nn = nl;
+        bool ok = nn <= kWave &&
+                  spec_decide(h, c, V, SpecAcc{didx, gvk, bmH0, rowp(q), n}, ds, de, dsum(k), cd, r, dcs(k), o,
+                              (SpecInfo*)nullptr, dense);
+        if (!ok && nn <= kWave && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin)) {
+          if (dense)
+            for (int i = lane; i < kMaxChunks; i += kWave) cd[i] = 0.0;
+          wave_sync();
+          double el;
+          ds = spec_corrections(gvk, tokl, n, h, c, dense ? cd : nullptr, true, el);
+          wave_sync();
+          r = rng;
+          ok = spec_decide(h, c, V, SpecAcc{didx, gvk, bmH0, rowp(q), n}, ds, 0.0, dsum(k), cd, r, dcs(k), o,
+                           (SpecInfo*)nullptr, dense);
+        }
+        if (ok) {
+          tokq = o.tok;
+          dex = o.dex;
+          kept = o.kept;
+        } else {
+          if (lane == 0) acc[0] |= 1u << (20 + o.why);
+          exact = true;
+        }
+      }
+      C4S_SPEC_T(4);
+      if (exact) {
+        // every wave stops (the deciders' areas hold the row), then resumes at q + 1
+        if (lane == 0) {
+          ctl.rng = rng;
+          lgkm_wait();
+          vstore(&ctl.halt, q);
+        }
+        exact_all(q);
+        tokq = ctl.tok;
+        if (lane == 0) {
+          const uint32_t* stp = xs.step_stats;
+          acc[0] |= stp[0];
+          acc[1] += 1u;
+          acc[2] += stp[2];
+          acc[3] += stp[3];
+          for (int i = 0; i < kSpecND; ++i) recs[i].tag = -1;
+        }
+        // ring rows of dropped decisions (steps after q) are stale
+        if (lane < kRing && ctl.ringtag[lane] > q) ctl.ringtag[lane] = -1;
+      }
+      if (!accept) {   // ring row q: the values of the token decided here
+        spins = 0;
+        while (!exact && rc.ring && vload(&ctl.ringtag[q & (kRing - 1)]) != q && ++spins <= kSpinMax)
+          __builtin_amdgcn_s_sleep(1);   // the decider's gather lands first
+        issue_ring(q, tokq);
+        wait_vm(0);
+        if (lane == 0) vstore(&ctl.ringtag[q & (kRing - 1)], q);
+      }
+      C4S_SPEC_T(5);
+      if (lane == 0) {
+        tout[q - s_first] = (int16_t)tokq;
+        if (!exact) {
+          acc[0] |= 64u | 1u;
+          acc[2] += dex;
+          acc[3] += kept;
+        }
+      }
+      rng = exact ? ctl.rng : xorshift64(rng);
+      if (tokq == a.stop_token) {
+        stopped = true;
+        ++q;
+        if (exact) {
+          lgkm_wait();
+          if (lane == 0) vstore(&ctl.halt, -1);
+          __syncthreads();
+        }
+        break;
+      }
+      // text2semantic.cpp:333-334: the token joins the drawn ids unless it is
+      // the stop token or already penalised (an accepted decision knows all
+      // but the ids drawn since it)
+      const bool fresh = accept ? (rfresh != 0 && !__ballot(isnew && htok == tokq))
+                                : (c.pen_on && tokq >= 0 && tokq < V && !bit_of(bmH0, tokq) &&
+                                   didx[tokq] == 0xFFFFu);
+      if (lane == (q & (kHist - 1))) {
+        htok = tokq;
+        hstep = q;
+        hfresh = fresh && n < kSpecGv;
+      }
+      if (fresh && n >= kSpecGv) bad = true;
+      if (fresh && n < kSpecGv) {
+        if (lane == 0) {
+          tokl[n] = tokq;
+          tstep[n] = (uint16_t)q;
+          didx[tokq] = (uint16_t)n;
+          bmN[tokq >> 5] |= 1u << (tokq & 31);
+        }
+        ++n;
+      }
+      ++q;
+      lgkm_wait();
+      if (lane == 0) vstore(&ctl.snap, (q << 16) | n);
+      C4S_SPEC_T(6);
+      C4S_SPEC_EV(q - 1, 3);
+      if (exact) {
+        lgkm_wait();
+        if (lane == 0) vstore(&ctl.halt, -1);
+        __syncthreads();   // the deciders resume from the new frontier
+      }
+    }
+    wait_vm(0);
+    if (lane == 0) {
+      ctl.qend = q;
+      ctl.stopped = stopped ? 1 : 0;
+      ctl.rng = rng;
+      if (bad) acc[0] |= 1u << 30;
+      for (int i = 0; i < 4; ++i) ctl.acc[i] = acc[i];
+      lgkm_wait();
+      vstore(&ctl.done, 1);
+    }
+  } else {
+    // ---- deciders ----
+    const int k = wv < kSpecVW ? wv : wv - 1;
+    auto start_at = [&](int from, int& q, uint64_t& rq) __attribute__((always_inline)) {
+      q = from + (((k - (from - s_first)) % kSpecND) + kSpecND) % kSpecND;
+      rq = rng0;
+      for (int i = s_first; i < q; ++i) rq = xorshift64(rq);
+    };
+    int q;
+    uint64_t rq;
+    start_at(s_first, q, rq);
+    SpecCS& cs = dcs(k);
+    uint64_t* sw = dsum(k);
+    float* gv = dgv(k);
+    double* cd = dcd(k);
+    if (lane == 0) cs.gen = 0u;
+    int pend = -1;   // step whose token's ring gather this wave has in flight
+    for (;;) {
+      int snap = 0;
+      bool halted = false, quit = false;
+      if (pend >= 0) {   // the gather has landed: its ring row is usable
+        wait_loads();
+        if (lane == 0) vstore(&ctl.ringtag[pend & (kRing - 1)], pend);
+        pend = -1;
+      }
+      C4S_SPEC_T(0);
+      for (;;) {
+        if (vload(&ctl.halt) >= 0) { halted = true; break; }
+        if (vload(&ctl.done)) { quit = true; break; }
+        snap = vload(&ctl.snap);
+        if (q < s_end && (snap >> 16) > q - kSpecND) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (quit) break;
+      if (halted) {
+        exact_all(vload(&ctl.halt));
+        __syncthreads();   // the checking wave has moved the frontier past the exact step
+        start_at(vload(&ctl.snap) >> 16, q, rq);
+        if (lane == 0) cs.gen = 0u;
+        continue;
+      }
+      C4S_SPEC_T(1);
+      C4S_SPEC_EV(q, 0);
+      const int nF = snap & 0xFFFF;
+      const float* grow = rowp(q);
+      // the step's summary into this wave's slot, the drawn ids' raw values into gv
+      const uint64_t* sg = sum_words(w, a.n_rows, q, row);
+      for (int q0 = 0; q0 < kSumQuads; q0 += kWave)
+        if (q0 + lane < kSumQuads)
+          __builtin_amdgcn_global_load_lds((glb_ptr_t)(sg + 2 * (q0 + lane)), (lds_ptr_t)(sw + 2 * q0), 16, 0, 0);
+      for (int j0 = 0; j0 < nF; j0 += 4 * kWave) {
+        int id[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) id[i] = tokl[min(j0 + i * kWave + lane, kSpecGv - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (j0 + i * kWave + lane < nF)
+            __builtin_amdgcn_global_load_lds((glb_ptr_t)(grow + id[i]), (lds_ptr_t)(gv + j0 + i * kWave), 4, 0,
+                                             0);
+      }
+      if (dense)
+        for (int i = lane; i < kMaxChunks; i += kWave) cd[i] = 0.0;
+      C4S_SPEC_T(2);
+      wait_loads();
+      wave_sync();
+      C4S_SPEC_T(3);
+      const SumHdr h = hdr_from(sw);
+      double de = 0.0, ds = 0.0;
+      if (c.pen_on) ds = spec_corrections(gv, tokl, nF, h, c, dense ? cd : nullptr, false, de);
+      wave_sync();
+      C4S_SPEC_T(4);
+      SpecRec& rc = recs[k];
+      SpecInfo* si = &rc.si;   // the decision writes what it rests on straight into its record
+      if (lane == 0) si->kind = 0;
+      StepOut o{0, 0u, 0u, 0u};
+      uint64_t r = rq;
+      bool ok = spec_decide(h, c, V, SpecAcc{didx, gv, bmH0, grow, nF}, ds, de, sw, cd, r, cs, o, si, dense);
+      if (!ok && c.pen_on && (o.why == kWhyDraw || o.why == kWhyMargin)) {
+        if (dense)
+          for (int i = lane; i < kMaxChunks; i += kWave) cd[i] = 0.0;
+        wave_sync();
+        ds = spec_corrections(gv, tokl, nF, h, c, dense ? cd : nullptr, true, de);
+        de = 0.0;
+        wave_sync();
+        if (lane == 0) si->kind = 0;
+        r = rq;
+        ok = spec_decide(h, c, V, SpecAcc{didx, gv, bmH0, grow, nF}, ds, de, sw, cd, r, cs, o, si, dense);
+      }
+      C4S_SPEC_T(5);
+      if (ok) {   // the token's values in the next 64 steps, for the checks of later steps
+        const int tc = (o.tok >= 0 && o.tok < V) ? o.tok : 0;
+        const int sidx = min(q + 1 + lane, a.n_steps - 1);
+        __builtin_amdgcn_global_load_lds((glb_ptr_t)(rowp(sidx) + tc),
+                                         (lds_ptr_t)(ring + (q & (kRing - 1)) * kWave), 4, 0, 0);
+        pend = q;
+      }
+      if (lane == 0) {
+        const int tk = o.tok;
+        rc.tok = tk;
+        rc.nF = nF;
+        rc.F = snap >> 16;
+        rc.fresh = (ok && c.pen_on && tk >= 0 && tk < V && tk != a.stop_token && !bit_of(bmH0, tk) &&
+                    (int)didx[tk] >= nF) ? 1 : 0;
+        rc.ok = ok ? 1 : 0;
+        rc.ring = ok ? 1 : 0;
+        const MassCoef mk = mass_coef(c, h.m0);
+        rc.ma = mk.a;
+        rc.mb = mk.b;
+        rc.mrel = mk.relc;
+        const int kd = ok ? si->kind : 0;
+        rc.kind = kd;
+        if (kd == 1) {
+          const double c1 = si->eps + si->dmass;
+          rc.w = si->p * si->rho;
+          rc.g1 = si->chk1 ? si->p * si->S - si->A1 - si->p * si->err - si->eps * si->S - c1 * si->A1
+                           : __builtin_inf();
+          rc.g2 = si->p * si->S - si->A2 + si->p * si->err + si->eps * si->S + c1 * si->A2;
+          rc.zlim = si->zcut;
+        } else if (kd == 2) {
+          rc.w = si->rho;
+          rc.u = si->u;
+          rc.ome = 1.0 - si->eps;
+          rc.g1 = si->u * si->S - si->af + 2.0 * si->err + si->eps * si->af;
+          rc.g2 = si->pf - si->u * si->S + 2.0 * si->err + si->eps * si->u * si->S;
+          rc.zlim = si->mt;
+        }
+        rc.why = o.why;
+        rc.dex = o.dex;
+        rc.kept = o.kept;
+        rc.ds = ds;
+        rc.de = de;
+        lgkm_wait();
+        vstore(&rc.tag, q);
+      }
+      C4S_SPEC_EV(q, 1);
+      q += kSpecND;
+      for (int i = 0; i < kSpecND; ++i) rq = xorshift64(rq);
+      C4S_SPEC_T(6);
+    }
+  }
+  C4S_SPEC_END(wv);
+  __syncthreads();
+  // Epilogue: tokens of the chunk (-1 after a stop), the row state.
+  const int qend = ctl.qend;
+  for (int s2 = s_first + t; s2 < s_end; s2 += NTS)
+    a.out_tok[(int64_t)s2 * a.n_rows + row] = s2 < qend ? (int)tout[s2 - s_first] : -1;
+  uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
+  fast_end(a, w, row, V, NTS, s_end, ctl.stopped != 0, ctl.rng, acc, bmN);
+}
+
 }  // namespace
 
 size_t stream_chain_lds_bytes(int V) {
@@ -2548,6 +3316,20 @@ hipError_t launch_stream_rowp(const StreamArgs& a, const StreamWs& w, hipStream_
   (void)hipGetLastError();
   hipLaunchKernelGGL(k_stream_rowp, dim3(a.n_rows, max(1, w.nseg)), dim3(NTC), stream_rowp_lds_bytes(a.vocab), s, a,
                      w);
+  return hipGetLastError();
+}
+
+size_t stream_spec_lds_bytes(int V) {
+  if (V > kLdsVocabMax) return 0;
+  return spec_layout(V).total;
+}
+
+int stream_spec_max_steps() { return kSpecGv; }
+
+hipError_t launch_stream_spec(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_spec, dim3(a.n_rows), dim3(NTS), stream_spec_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 

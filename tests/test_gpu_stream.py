@@ -9,7 +9,7 @@ from gpu_util import dev
 pytestmark = pytest.mark.gpu
 
 
-def run_stream(ctx, p, x, stop_token=-1, sequential=False):
+def run_stream(ctx, p, x, stop_token=-1, sequential=False, speculate=True):
     import torch
     steps, rows, V = x.shape
     out = torch.full((steps, rows), -9, dtype=torch.int32, device="cuda")
@@ -18,7 +18,7 @@ def run_stream(ctx, p, x, stop_token=-1, sequential=False):
     ctx.sample_stream(dev(x, torch), dev(p["hist_ids"], torch), dev(p["hist_off"], torch),
                       dev(p["temp"], torch), dev(p["top_k"], torch), dev(p["top_p"], torch),
                       dev(p["pen"], torch), rng, out, do_sample=dev(p["do_sample"], torch),
-                      stop_token=stop_token, out_stats=st, sequential=sequential)
+                      stop_token=stop_token, out_stats=st, sequential=sequential, speculate=speculate)
     torch.cuda.synchronize()
     return out.cpu().numpy(), rng.cpu().numpy().view(np.uint64), st.cpu().numpy()
 
@@ -167,11 +167,11 @@ def test_stream_overlapped_chunks(orc, gpu_ctx, V):
     assert np.array_equal(stoks, toks) and np.array_equal(srng, rng)
 
 
-@pytest.mark.parametrize("rows,steps", [(80, 260), (81, 260), (1, 300)])
+@pytest.mark.parametrize("rows,steps", [(64, 260), (65, 260), (80, 260), (1, 300)])
 def test_stream_row_counts(orc, gpu_ctx, rows, steps):
-    """Row counts around the overlapped stream's limit on a 256-CU device (80
-    rows: chains and scans on their CU sets; 81: one chunk on every CU) and a
-    single row, every row mode, against the oracle."""
+    """Row counts around the overlapped stream's limit on a 256-CU device (64
+    rows: chains and scans on their CU sets; 65 and more: one chunk on every
+    CU) and a single row, every row mode, against the oracle."""
     V = 8194
     p = _mixed_params(5151 + rows, rows, V)
     x = W.batch64_logits(5152 + rows, steps, rows, V)
@@ -227,3 +227,42 @@ def test_per_step_launches_match_stream(orc, gpu_ctx):
     otoks, _ = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"],
                                  p["top_p"], p["pen"], p["do_sample"], p["rng"], n_threads=16)
     assert np.array_equal(got, otoks)
+
+
+@pytest.mark.parametrize("kind", ["nucleus", "dense", "mixed"])
+def test_stream_speculative_chain(orc, gpu_ctx, kind):
+    """Full-vocabulary rows decided several steps ahead and checked in order
+    (the default two-phase path) against the oracle and against the pipelined
+    chain that decides one step after the other: penalised nucleus rows whose
+    cut often moves with the tokens drawn since (many steps decided again, and
+    exact-chain steps that stop every wave of the row), dense rows (p = 1 and
+    p > 1), rows without penalty, and stop tokens planted mid-stream."""
+    steps, rows, V = 300, 24, 8194
+    p = W.batch64_params(seed=777, rows=rows, V=V)
+    g = np.random.default_rng(778)
+    p["top_k"][:] = 0
+    if kind == "nucleus":
+        p["top_p"][:] = g.choice(np.array([0.5, 0.8, 0.9, 0.95], np.float32), rows)
+        p["pen"][:] = 10.0
+    elif kind == "dense":
+        p["top_p"][:] = g.choice(np.array([1.0, 1.2], np.float32), rows)
+        p["pen"][:] = g.choice(np.array([1.3, 10.0], np.float32), rows)
+    else:
+        p["top_p"][:] = g.choice(np.array([0.0, 0.3, 0.9, 1.0], np.float32), rows)
+        p["pen"][:] = g.choice(np.array([1.0, 1.2, 10.0], np.float32), rows)
+    x = W.batch64_logits(779, steps, rows, V)
+    stop = V - 1
+    for s, r in [(37, 2), (150, 5), (299, 7), (64, 11)]:
+        x[s, r, stop] = 80.0
+    print(f"speculative chain {kind}: gpu", flush=True)
+    toks, rng, st = run_stream(gpu_ctx, p, x, stop_token=stop)
+    ptoks, prng, pst = run_stream(gpu_ctx, p, x, stop_token=stop, speculate=False)
+    print(f"speculative chain {kind}: oracle", flush=True)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"], p["top_p"],
+                                    p["pen"], p["do_sample"], p["rng"], stop_token=stop, n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first (step, row) {bad[:5].tolist()}"
+    assert np.array_equal(rng, orng)
+    assert np.array_equal(ptoks, toks) and np.array_equal(prng, rng)
+    assert not (st[:, 0].astype(np.uint32) & (1 << 30)).any()   # no row gave up waiting
+    print("exact steps", int(st[:, 1].sum()), "per row", st[:, 1].tolist())
