@@ -455,6 +455,9 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // the pipelined chain with step segments for rows without penalty.
   const bool spec = !(st->flags & C4S_STREAM_NO_SPECULATION) && a.n_steps <= c4s::stream_spec_max_steps() &&
                     c4s::stream_spec_lds_bytes(a.vocab) + kSpecStaticLds <= kLdsLimit;
+  // Greedy and top-k rows likewise: the speculative list chain, else one wave a row.
+  const bool spec_list = !(st->flags & C4S_STREAM_NO_SPECULATION) && a.n_steps <= c4s::stream_spec_max_steps() &&
+                         c4s::stream_lspec_lds_bytes(a.vocab) + kSpecStaticLds <= kLdsLimit;
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
     if (spec) return c4s::launch_stream_spec(a, w, on);
     hipError_t e = c4s::launch_stream_rowp(a, w, on);
@@ -509,7 +512,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
         (e = launch_row_chain(w, side_on)) != hipSuccess ||
         (e = hipEventRecord(ctx->ev_side[buf], side_on)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream row-chain launch");
-    if ((e = c4s::launch_stream_list(a, w, chain_on)) != hipSuccess ||
+    if ((e = (spec_list ? c4s::launch_stream_lspec(a, w, chain_on) : c4s::launch_stream_list(a, w, chain_on))) !=
+            hipSuccess ||
         (e = c4s::launch_stream_chain(a, w, chain_on)) != hipSuccess ||
         (e = hipEventRecord(ctx->ev_chain[buf], chain_on)) != hipSuccess)
       return hip_fail(ctx, e, "sample_stream chain launch");

@@ -684,7 +684,8 @@ struct StepOut {
   int tok;
   uint32_t kept;
   uint32_t dex;
-  uint32_t why;   // reason of a fallback to the exact step (bit index, see kWhy*)
+  uint32_t why;     // reason of a fallback to the exact step (bit index, see kWhy*)
+  uint32_t nsurv;   // list_step: top-k survivors (their ids in cs.lid)
 };
 
 // Fallback reasons, reported as bit 20 + reason in the per-row path statistics.
@@ -703,8 +704,15 @@ enum : uint32_t {
 // Candidate-list step for greedy and top-k rows (one wave; two entries per
 // lane: keys e0, e1 and their values before the temperature yb0, yb1).
 // Returns false (nothing changed) when a decision needs the exact step.
-__device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, float yb1,
-                          const RowCfg& c, int V, const uint32_t* bmN, uint64_t& rng, ChainSh& cs,
+// Drawn-id set as a bitmap (hit test of list_step).
+struct BitsHit {
+  const uint32_t* bm;
+  __device__ __forceinline__ bool hit(int id) const { return bit_of(bm, id); }
+};
+
+template <class Hit, class CS>
+__device__ __forceinline__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, float yb1,
+                          const RowCfg& c, int V, const Hit& hs, uint64_t& rng, CS& cs,
                           StepOut& o) {
   const int lane = lane_id();
   o.why = kWhySummary;
@@ -713,8 +721,8 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   const float ninf = neg_inf();
   const bool v0 = lane < n, v1 = lane + kWave < n;
   const int id0 = ent_id(e0), id1 = ent_id(e1);
-  const bool h0 = c.pen_on && v0 && bit_of(bmN, id0);
-  const bool h1 = c.pen_on && v1 && bit_of(bmN, id1);
+  const bool h0 = c.pen_on && v0 && hs.hit(id0);
+  const bool h1 = c.pen_on && v1 && hs.hit(id1);
   // z of an unhit entry is its key; a hit is penalised (sampling.cpp:26) and divided again
   float z0 = v0 ? kfloat(ent_key(e0)) : ninf, z1 = v1 ? kfloat(ent_key(e1)) : ninf;
   if (h0) { const float y = pen_exact(yb0, c.pen); z0 = c.temp_on ? y / c.temp : y; }
@@ -759,6 +767,7 @@ __device__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, 
   const int nsurv = __popcll(__ballot(s0)) + __popcll(__ballot(s1));
   o.why = kWhyTies;
   if (nsurv > kWave) return false;
+  o.nsurv = (uint32_t)nsurv;
   // survivors are the unhit ranks [0, nsurv): one per lane in rank order
   if (s0) { cs.lz[r0] = z0; cs.lid[r0] = id0; cs.lslot[r0] = ent_rank(e0); }
   if (s1) { cs.lz[r1] = z1; cs.lid[r1] = id1; cs.lslot[r1] = ent_rank(e1); }
@@ -1807,7 +1816,7 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
     if (s + 4 < w.s_end) load(s + 4, r);
     C4S_LIST_PHASE(1);
     StepOut o{0, 0u, 0u, 0u};
-    const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, bmN, rng, cs, o);
+    const bool ok = list_step(h, e0, e1, yb0, yb1, c, V, BitsHit{bmN}, rng, cs, o);
     if (!ok && lane == 0) acc[0] |= 1u << (20 + o.why);
     const int tok = ok ? o.tok : exact(s);
     if (lane == 0) {
@@ -2500,7 +2509,7 @@ __global__ __launch_bounds__(NT) void k_stream_chain(StreamArgs a, StreamWs w) {
         const uint64_t e0 = (lane < h.n) ? lst[lane] : 0ull;
         const uint64_t e1 = (lane + kWave < h.n) ? lst[lane + kWave] : 0ull;
         const float* ly = reinterpret_cast<const float*>(cs.sum + kYW);
-        const bool ok = list_step(h, e0, e1, ly[lane], ly[lane + kWave], c, V, bmN, rng, cs, o);
+        const bool ok = list_step(h, e0, e1, ly[lane], ly[lane + kWave], c, V, BitsHit{bmN}, rng, cs, o);
         if (lane == 0) { cs.bi[0] = ok ? 1 : 0; cs.bi[1] = o.tok; cs.bi[2] = ok ? (int)o.kept : (int)o.why; cs.bi[3] = (int)o.dex; cs.rng = rng; }
       }
       pbits = 32u;
@@ -3276,6 +3285,396 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
   fast_end(a, w, row, V, NTS, s_end, ctl.stopped != 0, ctl.rng, acc, bmN);
 }
 
+
+// ---- speculative candidate-list chain -----------------------------------------------
+//
+// Greedy and top-k rows (k <= 64), one workgroup per row: wave kLND checks,
+// the others decide, as in the full-vocabulary chain. A greedy or top-k
+// decision depends on ids drawn before it only through its candidates: an id
+// drawn since that is neither the greedy token nor one of the top-k survivors
+// leaves the decision as it is (the penalty only lowers values, and top_p and
+// the draw read the survivors alone). So the checking wave accepts a decision
+// unless an id drawn since is one of its survivors; otherwise it decides the
+// step again from the decider's stored candidate list with every drawn id,
+// and a step the list cannot settle stops every wave for the exact chain on
+// the row read into LDS.
+
+constexpr int kLND = 4;                   // deciding waves
+constexpr int NTL = (kLND + 1) * kWave;
+constexpr int kLVW = kLND;                // the checking wave (the last)
+
+struct LSpecCS {   // list_step's survivor arrays
+  float lz[kWave + 1];
+  int lid[kWave + 1];
+  int lslot[kWave + 1];
+};
+
+struct LSpecRec {
+  int tag;     // step of this decision (written last), -1 none
+  int tok;
+  int nF;      // drawn ids the decision knew (a prefix of the drawn list)
+  int F;       // ... those drawn before step F
+  int fresh;   // tok is none of them, nor in H0, nor the stop token
+  int ok;
+  int nsurv;   // survivors in the decider's lid (greedy: the token)
+  uint32_t why, dex, kept;
+};
+
+struct LSpecCtl {
+  int snap;   // (frontier << 16) | drawn ids before the frontier
+  int halt;   // step of an exact chain run by every wave, else -1
+  int done;
+  int err;
+  int qend;
+  int stopped;
+  int tok;
+  uint64_t rng;
+  uint32_t acc[4];
+};
+
+struct LSpecLayout {
+  size_t didx, tok, tout, xrow, dec, stride, o_e1, o_hw, o_y0, o_y1, o_cs, total;
+};
+__host__ __device__ inline LSpecLayout lspec_layout(int V) {
+  LSpecLayout L;
+  L.didx = 0;
+  L.tok = al16(2 * (size_t)V);
+  L.tout = al16(L.tok + 4 * (size_t)kSpecGv);
+  L.xrow = al16(L.tout + 2 * (size_t)kSpecGv);
+  L.dec = al16(L.xrow + 4 * ((size_t)vpad(V) + 4));
+  L.o_e1 = 8 * (size_t)kWave;          // candidate list of a decision: e0, e1, hw, y0, y1 by lane
+  L.o_hw = L.o_e1 + 8 * (size_t)kWave;
+  L.o_y0 = L.o_hw + 8 * (size_t)kWave;
+  L.o_y1 = L.o_y0 + 4 * (size_t)kWave;
+  L.o_cs = al16(L.o_y1 + 4 * (size_t)kWave);
+  L.stride = al16(L.o_cs + sizeof(LSpecCS));
+  L.total = L.dec + (size_t)kLND * L.stride;
+  return L;
+}
+
+// Drawn set of one decision: ids whose drawn index is below nF.
+struct IdxHit {
+  const uint16_t* didx;
+  int nF;
+  __device__ __forceinline__ bool hit(int id) const { return (int)didx[id] < nF; }
+};
+
+// At most 128 VGPRs (four waves a SIMD): two workgroups of five waves share a CU.
+__global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k_stream_lspec(StreamArgs a,
+                                                                                          StreamWs w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ LSpecRec recs[kLND];
+  __shared__ LSpecCtl ctl;
+  __shared__ ScratchT<kLND + 1> xs;   // exact steps
+  __shared__ uint32_t bmH0[kStateWords], bmN[kStateWords];
+  const int row = blockIdx.x;
+  const int V = a.vocab;
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, nullptr, a.do_sample);
+  if (stream_mode(c, V) != kModeList) return;
+  int s_first;
+  if (!fast_begin(a, w, row, NTL, s_first)) return;
+  const int s_end = w.s_end;
+  const uint64_t rng0 = a.rng[row];
+  const uint32_t* stw = w.state + (size_t)row * kStateWords;
+  const LSpecLayout L = lspec_layout(V);
+  uint16_t* didx = reinterpret_cast<uint16_t*>(smem + L.didx);
+  int* tokl = reinterpret_cast<int*>(smem + L.tok);
+  int16_t* tout = reinterpret_cast<int16_t*>(smem + L.tout);
+  float* xrow = reinterpret_cast<float*>(smem + L.xrow);
+  auto dbase = [&](int k) { return smem + L.dec + (size_t)k * L.stride; };
+  auto dcs = [&](int k) -> LSpecCS& { return *reinterpret_cast<LSpecCS*>(dbase(k) + L.o_cs); };
+  const float* base = a.logits + (int64_t)row * a.ld;
+  auto rowp = [&](int s) { return base + (int64_t)s * a.step_stride; };
+  const int nwords = bitmap_words(V);
+
+  // Prologue: H0 and the ids drawn in earlier chunks, listed in id order.
+  fast_bitmaps(a, stw, row, V, NTL, bmH0, bmN, true);
+  for (int i = t; i < V; i += NTL) didx[i] = 0xFFFFu;
+  if (t < kLND) recs[t].tag = -1;
+  __syncthreads();
+  if (wv == kLVW) {
+    int n = 0;
+    for (int w0 = 0; w0 < nwords; w0 += kWave) {
+      const int wb = w0 + lane;
+      uint32_t bits = wb < nwords ? bmN[wb] : 0u;
+      const uint32_t cnt = (uint32_t)__popc(bits);
+      const uint32_t incl = wave_scan_u32(cnt);
+      int p = n + (int)(incl - cnt);
+      while (bits) {
+        const int id = 32 * wb + __ffs(bits) - 1;
+        bits &= bits - 1;
+        if (p < kSpecGv && id < V) {
+          tokl[p] = id;
+          didx[id] = (uint16_t)p;
+        }
+        ++p;
+      }
+      n += (int)readlane_u32(incl, kWave - 1);
+    }
+    if (lane == 0) {
+      ctl.snap = (s_first << 16) | min(n, kSpecGv);
+      ctl.halt = -1;
+      ctl.done = 0;
+      ctl.err = n > kSpecGv ? 1 : 0;
+      ctl.qend = s_first;
+      ctl.stopped = 0;
+      ctl.rng = rng0;
+      for (int i = 0; i < 4; ++i) ctl.acc[i] = stw[1 + i];
+    }
+  }
+  __syncthreads();
+
+  // Every wave runs the exact chain of step hq on the raw row read into LDS
+  // (text2semantic.cpp:142-166); ends at a barrier.
+  auto exact_all = [&](int hq) __attribute__((always_inline)) {
+    __syncthreads();
+    const float* src = rowp(hq);
+    for (int i = t; i < V; i += NTL) xrow[i] = src[i];
+    __syncthreads();
+    if (c.pen_on) {   // H0 and the stream's ids are disjoint: each id once
+      penalise_chunk<NTL>(xrow, bmH0, V, c.pen);
+      penalise_chunk<NTL>(xrow, bmN, V, c.pen);
+    }
+    __syncthreads();
+    uint64_t r = ctl.rng;
+    LdsRowNC srow{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    const int tok = run_chain(srow, xs, c, r, nullptr, xs.step_stats);
+    __syncthreads();
+    if (t == 0) {
+      ctl.tok = tok;
+      ctl.rng = r;
+    }
+    __syncthreads();
+  };
+
+  if (wv == kLVW) {
+    // ---- the checking wave: takes the decisions in step order ----
+    int q = s_first;
+    int n = ctl.snap & 0xFFFF;
+    uint64_t rng = rng0;
+    uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
+    bool stopped = false, bad = ctl.err != 0;
+    int htok = -1, hstep = -1;   // lane (step % kHist): a recent step, its token, whether it was drawn anew
+    bool hfresh = false;
+    while (q < s_end && !bad) {
+      const int k = (q - s_first) % kLND;
+      LSpecRec& rc = recs[k];
+      int spins = 0;
+      while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
+      if (spins > kSpinMax) {
+        bad = true;
+        break;
+      }
+      C4S_SPEC_EV(q, 2);
+      const int nFd = rc.nF, rtok = rc.tok, Fd = rc.F, rok = rc.ok, rfresh = rc.fresh, ns = rc.nsurv;
+      LSpecCS& cs = dcs(k);
+      // the ids drawn since the decision (steps [Fd, q)) against its survivors
+      const bool isnew = lane < kHist && hfresh && hstep >= Fd && hstep < q;
+      const uint64_t nm = __ballot(isnew);
+      const int nn = __popcll(nm);
+      bool accept = rok != 0 && nn == n - nFd && q - Fd <= kHist;
+      if (accept && nn > 0) {
+        const int sid = lane < ns ? cs.lid[lane] : -1;
+        for (uint64_t b = nm; b && accept; b &= b - 1) {
+          const int tj = (int)readlane_u32((uint32_t)htok, __ffsll((unsigned long long)b) - 1);
+          accept = !__ballot(sid == tj);
+        }
+      }
+      int tokq = rtok;
+      uint32_t dex = rc.dex, kept = rc.kept;
+      bool exact = false;
+      uint64_t rnext = c.greedy ? rng : xorshift64(rng);
+      if (!accept) {
+        // decide again from the decider's candidate list with every drawn id
+        unsigned char* db = dbase(k);
+        const uint64_t e0r = reinterpret_cast<const uint64_t*>(db)[lane];
+        const uint64_t e1r = reinterpret_cast<const uint64_t*>(db + L.o_e1)[lane];
+        const uint64_t hwr = reinterpret_cast<const uint64_t*>(db + L.o_hw)[lane];
+        const float y0 = reinterpret_cast<const float*>(db + L.o_y0)[lane];
+        const float y1 = reinterpret_cast<const float*>(db + L.o_y1)[lane];
+        const SumHdr h = hdr_lanes(hwr);
+        const uint64_t e0 = (lane < h.n) ? e0r : 0ull;
+        const uint64_t e1 = (lane + kWave < h.n) ? e1r : 0ull;
+        StepOut o{0, 0u, 0u, 0u};
+        uint64_t r = rng;
+        const bool ok = list_step(h, e0, e1, y0, y1, c, V, IdxHit{didx, n}, r, cs, o);
+        if (ok) {
+          tokq = o.tok;
+          dex = o.dex;
+          kept = o.kept;
+          rnext = r;
+        } else {
+          if (lane == 0) acc[0] |= 1u << (20 + o.why);
+          exact = true;
+        }
+      }
+      if (exact) {   // every wave stops, then resumes at q + 1
+        if (lane == 0) {
+          ctl.rng = rng;
+          lgkm_wait();
+          vstore(&ctl.halt, q);
+        }
+        exact_all(q);
+        tokq = ctl.tok;
+        rnext = ctl.rng;
+        if (lane == 0) {
+          const uint32_t* stp = xs.step_stats;
+          acc[0] |= stp[0];
+          acc[1] += 1u;
+          acc[2] += stp[2];
+          acc[3] += stp[3];
+          for (int i = 0; i < kLND; ++i) recs[i].tag = -1;
+        }
+      }
+      if (lane == 0) {
+        tout[q - s_first] = (int16_t)tokq;
+        if (!exact) {
+          acc[0] |= 32u | 1u;
+          acc[2] += dex;
+          acc[3] += kept;
+        }
+      }
+      rng = rnext;
+      if (tokq == a.stop_token) {
+        stopped = true;
+        ++q;
+        if (exact) {
+          lgkm_wait();
+          if (lane == 0) vstore(&ctl.halt, -1);
+          __syncthreads();
+        }
+        break;
+      }
+      // text2semantic.cpp:333-334: the token joins the drawn ids unless it is
+      // the stop token or already penalised
+      const bool fresh = accept ? (rfresh != 0 && !__ballot(isnew && htok == tokq))
+                                : (c.pen_on && tokq >= 0 && tokq < V && !bit_of(bmH0, tokq) &&
+                                   didx[tokq] == 0xFFFFu);
+      if (lane == (q & (kHist - 1))) {
+        htok = tokq;
+        hstep = q;
+        hfresh = fresh && n < kSpecGv;
+      }
+      if (fresh && n >= kSpecGv) bad = true;
+      if (fresh && n < kSpecGv) {
+        if (lane == 0) {
+          tokl[n] = tokq;
+          didx[tokq] = (uint16_t)n;
+          bmN[tokq >> 5] |= 1u << (tokq & 31);
+        }
+        ++n;
+      }
+      ++q;
+      lgkm_wait();
+      if (lane == 0) vstore(&ctl.snap, (q << 16) | n);
+      C4S_SPEC_EV(q - 1, 3);
+      if (exact) {
+        lgkm_wait();
+        if (lane == 0) vstore(&ctl.halt, -1);
+        __syncthreads();   // the deciders resume from the new frontier
+      }
+    }
+    if (lane == 0) {
+      ctl.qend = q;
+      ctl.stopped = stopped ? 1 : 0;
+      ctl.rng = rng;
+      if (bad) acc[0] |= 1u << 30;
+      for (int i = 0; i < 4; ++i) ctl.acc[i] = acc[i];
+      lgkm_wait();
+      vstore(&ctl.done, 1);
+    }
+  } else {
+    // ---- deciders ----
+    const int k = wv;
+    auto start_at = [&](int from, int& q, uint64_t& rq) __attribute__((always_inline)) {
+      q = from + (((k - (from - s_first)) % kLND) + kLND) % kLND;
+      rq = rng0;
+      if (!c.greedy)
+        for (int i = s_first; i < q; ++i) rq = xorshift64(rq);
+    };
+    auto load = [&](int s, ListRegs& r) __attribute__((always_inline)) {
+      const uint64_t* sw = sum_words(w, a.n_rows, min(s, s_end - 1), row);
+      r.e0 = sw[lane];
+      r.e1 = sw[lane + kWave];
+      r.hw = sw[kHdrW + (lane & 7)];
+      const float* sy = reinterpret_cast<const float*>(sw + kYW);
+      r.y0 = sy[lane];
+      r.y1 = sy[lane + kWave];
+    };
+    int q;
+    uint64_t rq;
+    start_at(s_first, q, rq);
+    LSpecCS& cs = dcs(k);
+    unsigned char* db = dbase(k);
+    LSpecRec& rc = recs[k];
+    ListRegs P{};
+    load(q, P);
+    for (;;) {
+      int snap = 0;
+      bool halted = false, quit = false;
+      for (;;) {
+        if (vload(&ctl.halt) >= 0) { halted = true; break; }
+        if (vload(&ctl.done)) { quit = true; break; }
+        snap = vload(&ctl.snap);
+        if (q < s_end && (snap >> 16) > q - kLND) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (quit) break;
+      if (halted) {
+        exact_all(vload(&ctl.halt));
+        __syncthreads();   // the checking wave has moved the frontier past the exact step
+        start_at(vload(&ctl.snap) >> 16, q, rq);
+        load(q, P);
+        continue;
+      }
+      C4S_SPEC_EV(q, 0);
+      const int nF = snap & 0xFFFF;
+      const ListRegs R = P;
+      if (q + kLND < s_end) load(q + kLND, P);   // the next decision's list, in flight meanwhile
+      const SumHdr h = hdr_lanes(R.hw);
+      const uint64_t e0 = (lane < h.n) ? R.e0 : 0ull;
+      const uint64_t e1 = (lane + kWave < h.n) ? R.e1 : 0ull;
+      StepOut o{0, 0u, 0u, 0u};
+      uint64_t r = rq;
+      const bool ok = list_step(h, e0, e1, R.y0, R.y1, c, V, IdxHit{didx, nF}, r, cs, o);
+      // the list, for the checking wave's second decision
+      reinterpret_cast<uint64_t*>(db)[lane] = R.e0;
+      reinterpret_cast<uint64_t*>(db + L.o_e1)[lane] = R.e1;
+      reinterpret_cast<uint64_t*>(db + L.o_hw)[lane] = R.hw;
+      reinterpret_cast<float*>(db + L.o_y0)[lane] = R.y0;
+      reinterpret_cast<float*>(db + L.o_y1)[lane] = R.y1;
+      if (lane == 0) {
+        const int tk = o.tok;
+        if (c.greedy) cs.lid[0] = tk;
+        rc.tok = tk;
+        rc.nF = nF;
+        rc.F = snap >> 16;
+        rc.fresh = (ok && c.pen_on && tk >= 0 && tk < V && tk != a.stop_token && !bit_of(bmH0, tk) &&
+                    (int)didx[tk] >= nF) ? 1 : 0;
+        rc.ok = ok ? 1 : 0;
+        rc.nsurv = c.greedy ? 1 : (int)o.nsurv;
+        rc.why = o.why;
+        rc.dex = o.dex;
+        rc.kept = o.kept;
+        lgkm_wait();
+        vstore(&rc.tag, q);
+      }
+      C4S_SPEC_EV(q, 1);
+      q += kLND;
+      if (!c.greedy)
+        for (int i = 0; i < kLND; ++i) rq = xorshift64(rq);
+    }
+  }
+  __syncthreads();
+  // Epilogue: tokens of the chunk (-1 after a stop), the row state.
+  const int qend = ctl.qend;
+  for (int s2 = s_first + t; s2 < s_end; s2 += NTL)
+    a.out_tok[(int64_t)s2 * a.n_rows + row] = s2 < qend ? (int)tout[s2 - s_first] : -1;
+  uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
+  fast_end(a, w, row, V, NTL, s_end, ctl.stopped != 0, ctl.rng, acc, bmN);
+}
+
 }  // namespace
 
 size_t stream_chain_lds_bytes(int V) {
@@ -3325,6 +3724,18 @@ size_t stream_spec_lds_bytes(int V) {
 }
 
 int stream_spec_max_steps() { return kSpecGv; }
+
+size_t stream_lspec_lds_bytes(int V) {
+  if (V > kLdsVocabMax) return 0;
+  return lspec_layout(V).total;
+}
+
+hipError_t launch_stream_lspec(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
+  if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(k_stream_lspec, dim3(a.n_rows), dim3(NTL), stream_lspec_lds_bytes(a.vocab), s, a, w);
+  return hipGetLastError();
+}
 
 hipError_t launch_stream_spec(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;

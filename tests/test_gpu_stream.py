@@ -229,14 +229,16 @@ def test_per_step_launches_match_stream(orc, gpu_ctx):
     assert np.array_equal(got, otoks)
 
 
-@pytest.mark.parametrize("kind", ["nucleus", "dense", "mixed"])
+@pytest.mark.parametrize("kind", ["nucleus", "dense", "mixed", "list"])
 def test_stream_speculative_chain(orc, gpu_ctx, kind):
-    """Full-vocabulary rows decided several steps ahead and checked in order
-    (the default two-phase path) against the oracle and against the pipelined
-    chain that decides one step after the other: penalised nucleus rows whose
-    cut often moves with the tokens drawn since (many steps decided again, and
+    """Rows decided several steps ahead and checked in order (the default
+    two-phase path) against the oracle and against the chains that decide one
+    step after the other: penalised full-vocabulary nucleus rows whose cut
+    often moves with the tokens drawn since (many steps decided again, and
     exact-chain steps that stop every wave of the row), dense rows (p = 1 and
-    p > 1), rows without penalty, and stop tokens planted mid-stream."""
+    p > 1), rows without penalty, greedy and top-k rows (decided again when a
+    token drawn since is one of their survivors), and stop tokens planted
+    mid-stream."""
     steps, rows, V = 300, 24, 8194
     p = W.batch64_params(seed=777, rows=rows, V=V)
     g = np.random.default_rng(778)
@@ -247,10 +249,17 @@ def test_stream_speculative_chain(orc, gpu_ctx, kind):
     elif kind == "dense":
         p["top_p"][:] = g.choice(np.array([1.0, 1.2], np.float32), rows)
         p["pen"][:] = g.choice(np.array([1.3, 10.0], np.float32), rows)
-    else:
+    elif kind == "mixed":
         p["top_p"][:] = g.choice(np.array([0.0, 0.3, 0.9, 1.0], np.float32), rows)
         p["pen"][:] = g.choice(np.array([1.0, 1.2, 10.0], np.float32), rows)
+    else:
+        p["top_k"][:] = g.choice(np.array([1, 2, 5, 20, 50, 64], np.int32), rows)
+        p["top_p"][:] = g.choice(np.array([0.5, 0.9, 1.0], np.float32), rows)
+        p["pen"][:] = g.choice(np.array([1.0, 1.5, 10.0], np.float32), rows)
+        p["do_sample"][::5] = 0   # greedy rows
     x = W.batch64_logits(779, steps, rows, V)
+    if kind == "list":   # narrow rows: the penalised ids often come back among the survivors
+        x[:, :, :256] += 6.0
     stop = V - 1
     for s, r in [(37, 2), (150, 5), (299, 7), (64, 11)]:
         x[s, r, stop] = 80.0
