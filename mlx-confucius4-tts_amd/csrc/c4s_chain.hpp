@@ -139,6 +139,7 @@ struct LdsRow {
     __syncthreads();
   }
   __device__ uint32_t* sort_buf() const { return reinterpret_cast<uint32_t*>(E); }
+  __device__ size_t sort_bytes() const { return 8 * (size_t)V; }
 };
 
 // Row staged in LDS without a mass cache (kernels whose LDS holds several rows):
@@ -150,6 +151,7 @@ struct LdsRowNC {
   uint32_t thr_key;
   bool topk_on;
   uint32_t* sortbuf;
+  uint32_t sortcap = 0;   // bytes of sortbuf (0: the keys only)
   static constexpr bool kCache = false;
 
   __device__ float zraw(int i) const { return val[i]; }
@@ -164,6 +166,7 @@ struct LdsRowNC {
     __syncthreads();
   }
   __device__ uint32_t* sort_buf() const { return sortbuf; }
+  __device__ size_t sort_bytes() const { return sortcap; }
 };
 
 // Row re-read from HBM on every pass.
@@ -179,6 +182,7 @@ struct GlobalRow {
   uint32_t thr_key;
   bool topk_on;
   uint32_t* sortbuf;       // global workspace for the exact top_p pass
+  uint32_t sortcap;        // its bytes
   static constexpr bool kCache = false;
 
   __device__ float y(int i) const {
@@ -198,6 +202,7 @@ struct GlobalRow {
   __device__ void cache(int, double) {}
   __device__ void apply_temperature(float t, int, int) { temp_on = true; temp = t; }
   __device__ uint32_t* sort_buf() const { return sortbuf; }
+  __device__ size_t sort_bytes() const { return sortcap; }
 };
 
 // Wave w owns ids [w*seg, min(V, (w+1)*seg)), visited in slices of 64.
@@ -421,14 +426,53 @@ __device__ long long exact_top_p(const Src& src, Seg sg, ScratchT<NWX>& sh, floa
   for (int i = n_fin + threadIdx.x; i < P; i += NTX) buf[i] = 0xFFFFFFFFu;
   __syncthreads();
   bitonic_sort_u32<NTX>(buf, P);
-  if (wave_id() == 0) {
+  C4S_SPEC_EV(0, 0);
+  // The masses in windows of the buffer's free space after the keys: every
+  // wave computes a window's exp (and quotients), wave 0 adds them one after
+  // the other; without room for a window, wave 0 computes them itself.
+  const size_t kb = ((size_t)n_fin * 4 + 15) & ~(size_t)15;
+  const size_t cap = src.sort_bytes();
+  int W = cap > kb ? (int)min((size_t)2048, (cap - kb) / 8) : 0;
+  W &= ~(kWave - 1);
+  if (W >= kWave) {
+    double* ew = reinterpret_cast<double*>(reinterpret_cast<unsigned char*>(buf) + kb);
+    double total = 0.0;
+    for (int w0 = 0; w0 < (int)n_fin; w0 += W) {
+      const int wn = min(W, (int)n_fin - w0);
+      for (int j = threadIdx.x; j < wn; j += NTX) ew[j] = exp((double)(kfloat(buf[w0 + j]) - maxv));
+      __syncthreads();
+      if (wave_id() == 0) total = seq_sum_mem(total, ew, wn);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) sh.bd[7] = total;
+    __syncthreads();
+    total = sh.bd[7];
+    C4S_SPEC_EV(0, 1);
+    double cum = 0.0;
+    uint32_t removed = 0;
+    for (int w0 = 0; w0 < (int)n_fin; w0 += W) {
+      const int wn = min(W, (int)n_fin - w0);
+      for (int j = threadIdx.x; j < wn; j += NTX) ew[j] = exp((double)(kfloat(buf[w0 + j]) - maxv)) / total;
+      __syncthreads();
+      if (wave_id() == 0) {
+        bool stop = false;
+        removed = w0 + seq_cut_mem(cum, ew, wn, thr, stop);
+        if (lane_id() == 0) {
+          sh.bu[4] = removed;
+          sh.bu[7] = stop ? 1u : 0u;
+        }
+      }
+      __syncthreads();
+      if (sh.bu[7]) break;
+    }
+    C4S_SPEC_EV(0, 2);
+  } else if (wave_id() == 0) {
     const int l = lane_id();
     double total = 0.0;
     for (int base = 0; base < (int)n_fin; base += kWave) {
       const int j = base + l;
       const double e = (j < (int)n_fin) ? exp((double)(kfloat(buf[j]) - maxv)) : 0.0;
-      const int cnt = min(kWave, (int)n_fin - base);
-      for (int t = 0; t < cnt; ++t) total += __shfl(e, t, kWave);
+      total = seq_sum_lanes(total, e, min(kWave, (int)n_fin - base));
     }
     double cum = 0.0;
     uint32_t removed = 0;
@@ -436,15 +480,11 @@ __device__ long long exact_top_p(const Src& src, Seg sg, ScratchT<NWX>& sh, floa
     for (int base = 0; base < (int)n_fin && !stop; base += kWave) {
       const int j = base + l;
       const double q = (j < (int)n_fin) ? exp((double)(kfloat(buf[j]) - maxv)) / total : 0.0;
-      const int cnt = min(kWave, (int)n_fin - base);
-      for (int t = 0; t < cnt; ++t) {
-        cum += __shfl(q, t, kWave);
-        if (cum <= thr) removed = base + t + 1;
-        else { stop = true; break; }
-      }
+      removed = base + seq_cut_lanes(cum, q, min(kWave, (int)n_fin - base), thr, stop);
     }
     if (l == 0) sh.bu[4] = removed;
   }
+  C4S_SPEC_EV(0, 3);
   __syncthreads();
   const uint32_t rfin = sh.bu[4];
   __syncthreads();
@@ -1078,14 +1118,11 @@ __device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowC
                 e = exp((double)(zi - maxv_d));
             }
             const int cnt = min(kWave, V - base);
-            for (int q = 0; q < cnt; ++q) {
-              const double eq = __shfl(e, q, kWave);
-              if (pass == 0) {
-                total += eq;
-              } else {
-                acc += eq;
-                if (rr <= acc) { t = base + q; done = true; break; }
-              }
+            if (pass == 0) {
+              total = seq_sum_lanes(total, e, cnt);
+            } else {
+              const int q = seq_find_lanes(acc, e, cnt, rr);
+              if (q >= 0) { t = base + q; done = true; }
             }
           }
           if (pass == 1 && lane == 0) sh.bi[2] = t;

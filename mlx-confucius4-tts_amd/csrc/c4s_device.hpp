@@ -243,6 +243,87 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
+// Sequential double sums over the lanes (the reference's loops add one term
+// after the other): lane indices are constants of an unrolled loop, so each
+// term costs two scalar reads and the dependent chain is the adds alone.
+// seq_sum_lanes: total + e[0] + e[1] + ... + e[n-1] in that order (n <= 64,
+// wave-uniform).
+__device__ __forceinline__ double seq_sum_lanes(double total, double e, int n) {
+#pragma unroll
+  for (int t = 0; t < kWave; ++t)
+    if (t < n) total += readlane_f64(e, t);
+  return total;
+}
+// seq_find_lanes: the same running sum continued from acc; returns the first
+// t < n after whose term r <= acc (acc then the sum through t), else -1 (acc
+// the sum of all n terms).
+__device__ __forceinline__ int seq_find_lanes(double& acc, double e, int n, double r) {
+#pragma unroll
+  for (int t = 0; t < kWave; ++t) {
+    if (t < n) {
+      acc += readlane_f64(e, t);
+      if (r <= acc) return t;
+    }
+  }
+  return -1;
+}
+// seq_sum_mem / seq_cut_mem: the same over n terms in memory (LDS or global),
+// every lane reading the same addresses and computing the same sum, 16 terms
+// loaded at a time, so the chain is plain FP64 adds on vector registers.
+__device__ __forceinline__ double seq_sum_mem(double total, const double* p, int n) {
+  for (int j = 0; j < n; j += 16) {
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = p[min(j + i, n - 1)];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) total += (j + i < n) ? v[i] : 0.0;   // + 0.0 leaves a sum >= 0 unchanged
+  }
+  return total;
+}
+// top_p's removal loop over n terms from cum: returns how many leading terms
+// leave cum <= thr; sets stop (and cum to the sum through the first term past
+// thr) when one takes it above.
+__device__ __forceinline__ int seq_cut_mem(double& cum, const double* p, int n, double thr, bool& stop) {
+  for (int j = 0; j < n; j += 16) {
+    double v[16], cs[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = p[min(j + i, n - 1)];
+    double x = cum;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x += (j + i < n) ? v[i] : 0.0;
+      cs[i] = x;
+    }
+    int first = 16;
+#pragma unroll
+    for (int i = 15; i >= 0; --i)
+      if (j + i < n && !(cs[i] <= thr)) first = i;
+    if (first < 16) {
+      stop = true;
+      cum = cs[first];
+      return j + first;
+    }
+    cum = x;
+  }
+  return n;
+}
+// seq_cut_lanes: top_p's removal loop (sampling.cpp:60-65) over n terms from
+// cum: the number of leading terms after which cum <= thr still holds; sets
+// stop when a term took cum above thr (cum only grows).
+__device__ __forceinline__ int seq_cut_lanes(double& cum, double q, int n, double thr, bool& stop) {
+#pragma unroll
+  for (int t = 0; t < kWave; ++t) {
+    if (t < n) {
+      cum += readlane_f64(q, t);
+      if (!(cum <= thr)) {
+        stop = true;
+        return t;
+      }
+    }
+  }
+  return n;
+}
+
 // ---- workgroup reductions ------------------------------------------------------
 // `red` is LDS scratch with room for one entry per wave (typed views of the same
 // bytes are fine). Every thread returns the result. Two barriers: the trailing

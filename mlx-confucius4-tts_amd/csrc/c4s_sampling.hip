@@ -870,8 +870,7 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
       for (int base = 0; base < ns; base += kWave) {
         const int j = base + lane;
         const double e = j < ns ? exp((double)(kfloat((uint32_t)(ts.list[ns - 1 - j] >> 32)) - vmax)) : 0.0;
-        const int cnt = min(kWave, ns - base);
-        for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+        total = seq_sum_lanes(total, e, min(kWave, ns - base));
       }
       const double thr = 1.0 - (double)c.p;
       double cum = 0.0;
@@ -880,12 +879,7 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
       for (int base = 0; base < ns && !stop; base += kWave) {
         const int j = base + lane;
         const double q = j < ns ? exp((double)(kfloat((uint32_t)(ts.list[ns - 1 - j] >> 32)) - vmax)) / total : 0.0;
-        const int cnt = min(kWave, ns - base);
-        for (int u = 0; u < cnt; ++u) {
-          cum += __shfl(q, u, kWave);
-          if (cum <= thr) removed = base + u + 1;
-          else { stop = true; break; }
-        }
+        removed = base + seq_cut_lanes(cum, q, min(kWave, ns - base), thr, stop);
       }
       nkeep = ns - removed;
       const int mk = min(max(0, c.min_keep), ns);   // sampling.cpp:67-68
@@ -927,8 +921,7 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
       const float zj = j < nkeep ? kfloat((uint32_t)ts.list[j]) : ninf;
       const double e = (j < nkeep && zj != ninf) ? exp((double)(zj - m)) : 0.0;
       if (j < nkeep) ts.e[j] = e;
-      const int cnt = min(kWave, nkeep - base);
-      for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+      total = seq_sum_lanes(total, e, min(kWave, nkeep - base));
     }
     const uint64_t st2 = xorshift64(a.rng[row]);
     const double r = unit_from_state(st2) * total;
@@ -938,14 +931,10 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
     for (int base = 0; base < nkeep && !done; base += kWave) {
       const int j = base + lane;
       const double e = j < nkeep ? ts.e[j] : 0.0;
-      const int cnt = min(kWave, nkeep - base);
-      for (int q = 0; q < cnt; ++q) {
-        acc += __shfl(e, q, kWave);
-        if (r <= acc) {
-          tok = (int)~(uint32_t)(ts.list[base + q] >> 32);
-          done = true;
-          break;
-        }
+      const int q = seq_find_lanes(acc, e, min(kWave, nkeep - base), r);
+      if (q >= 0) {
+        tok = (int)~(uint32_t)(ts.list[base + q] >> 32);
+        done = true;
       }
     }
     if (lane == 0) {
@@ -1018,6 +1007,7 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
   src.thr_key = 0u;
   src.topk_on = false;
   src.sortbuf = a.sort_ws + (int64_t)row * a.sort_ws_stride;
+  src.sortcap = (uint32_t)(a.sort_ws_stride * 4);
   uint64_t rng = a.rng ? a.rng[row] : 0ull;
   float* masked = a.out_masked ? a.out_masked + (int64_t)row * V : nullptr;
   uint32_t* st = a.stats ? a.stats + 4 * (int64_t)row : nullptr;

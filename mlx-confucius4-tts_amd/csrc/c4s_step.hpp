@@ -369,19 +369,15 @@ __device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const
   double total = 0.0;
   for (int base = 0; base < V; base += kWave) {
     const double e = mass_at(base + lane);
-    const int cnt = min(kWave, V - base);
-    for (int q = 0; q < cnt; ++q) total += __shfl(e, q, kWave);
+    total = seq_sum_lanes(total, e, min(kWave, V - base));
   }
   const double rr = u * total;
   if (!(rr > 0.0)) return 0;
   double acc = 0.0;
   for (int base = 0; base < V; base += kWave) {
     const double e = mass_at(base + lane);
-    const int cnt = min(kWave, V - base);
-    for (int q = 0; q < cnt; ++q) {
-      acc += __shfl(e, q, kWave);
-      if (rr <= acc) return base + q;
-    }
+    const int q = seq_find_lanes(acc, e, min(kWave, V - base), rr);
+    if (q >= 0) return base + q;
   }
   return V - 1;
 }

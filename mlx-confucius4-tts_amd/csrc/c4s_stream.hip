@@ -1795,7 +1795,7 @@ __global__ __launch_bounds__(kWave) void k_stream_list(StreamArgs a, StreamWs w)
       penalise_wave(xrow, bmN, V, c.pen);
     }
     __syncthreads();
-    LdsRowNC src{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    LdsRowNC src{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride, (uint32_t)(w.sort_stride * 4)};
     const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
     __syncthreads();
     if (lane == 0) {
@@ -2318,7 +2318,7 @@ __global__ __launch_bounds__(NTC) void k_stream_rowp(StreamArgs a, StreamWs w) {
         penalise_chunk<NTC>(val, bmN, V, c.pen);
       }
       __syncthreads();
-      LdsRowNC src{val, V, 0u, false, sortbuf};
+      LdsRowNC src{val, V, 0u, false, sortbuf, (uint32_t)(w.sort_stride * 4)};
       const int tok = run_chain(src, xs, c, rng, nullptr, xs.step_stats);
       if (t == 0) {
         const uint32_t* stp = xs.step_stats;
@@ -2906,7 +2906,7 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
     }
     __syncthreads();
     uint64_t r = ctl.rng;
-    LdsRowNC srow{X, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    LdsRowNC srow{X, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride, (uint32_t)(w.sort_stride * 4)};
     const int tok = run_chain(srow, xs, c, r, nullptr, xs.step_stats);
     __syncthreads();
     if (t == 0) {
@@ -3438,7 +3438,7 @@ __global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k
     }
     __syncthreads();
     uint64_t r = ctl.rng;
-    LdsRowNC srow{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride};
+    LdsRowNC srow{xrow, V, 0u, false, w.sortbuf + (int64_t)row * w.sort_stride, (uint32_t)(w.sort_stride * 4)};
     const int tok = run_chain(srow, xs, c, r, nullptr, xs.step_stats);
     __syncthreads();
     if (t == 0) {
