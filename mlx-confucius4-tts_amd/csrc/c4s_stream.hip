@@ -149,12 +149,14 @@ __device__ __forceinline__ bool bit_of(const uint32_t* bm, int id) {
 
 // ---- scan (all CUs) -----------------------------------------------------------------
 
+constexpr int kIdWords = (kLdsVocabMax / 32 + 1 + 3) & ~3;   // bitmap_words(kLdsVocabMax)
+static_assert(kIdWords <= 2 * NTA, "two id-bitmap words a thread");
+
 struct ScanSh {
   uint32_t hist[2048];
   uint64_t cand[kCandCap];
   float candy[kCandCap];   // value before the temperature, by candidate position
   uint32_t bm[kStateWords];
-  uint32_t wtot[16][NWA];
   uint32_t red[NWA];
   uint32_t redm[NWA];
   double redd[NWA];
@@ -162,10 +164,9 @@ struct ScanSh {
   double edge[8];
   uint32_t bu[4];
   double redh[NWA];                // per wave: mass of its list positions below NTA
-  uint32_t lmark[kCandCap / 32];   // candidate positions of the list entries
-  uint32_t lpre[kCandCap / 32];    // marks before each word
-  uint32_t fmark[kCandCap / 32];   // the same for the list's first NTA entries
-  uint32_t fpre[kCandCap / 32];
+  uint32_t lmark[kIdWords];        // ids of the list entries
+  uint32_t fmark[kIdWords];        // ids of the list's first NTA entries
+  uint32_t pre2[kIdWords];         // marks before each word: lmark's (low half), fmark's (high half)
   uint32_t place4[NTA / 4];        // their id-order places, a byte each, stored as words
 };
 
@@ -285,35 +286,55 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
     const float* p = a.logits + (int64_t)s * a.step_stride + (int64_t)row * a.ld;
     const RowShape rs = row_shape(p, V);
     const float4* p4 = reinterpret_cast<const float4*>(p + rs.head);
-    float4 xv[NQ];
+    // The thread's values as keys (0 past the row: below every key of a value).
+    uint32_t kq[NQ][4];
+    {
+      float4 xv[NQ];
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const int q = t + NTA * j;
-      xv[j] = (q < rs.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < NQ; ++j) {
+        const int q = t + NTA * j;
+        xv[j] = (q < rs.nq) ? p4[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const bool in = t + NTA * j < rs.nq;
+        kq[j][0] = in ? fkey(xv[j].x) : 0u;
+        kq[j][1] = in ? fkey(xv[j].y) : 0u;
+        kq[j][2] = in ? fkey(xv[j].z) : 0u;
+        kq[j][3] = in ? fkey(xv[j].w) : 0u;
+      }
     }
     const bool eh = t < rs.head;
     const bool et = !eh && t < rs.head + rs.tail;
     const int eid = eh ? t : rs.head + 4 * rs.nq + (t - rs.head);
-    const float xe = (eh || et) ? p[eid] : 0.f;
+    const uint32_t ke = (eh || et) ? fkey(p[eid]) : 0u;
 
     // Per-thread top-2 (top-4 for large lists) keys.
     uint32_t t1 = 0, t2 = 0, t3 = 0, t4 = 0;
-    auto ins = [&](uint32_t k) {
-      if (large) { t4 = max(t4, min(t3, k)); t3 = max(t3, min(t2, k)); }
-      t2 = max(t2, min(t1, k));
-      t1 = max(t1, k);
-    };
+    if (large) {
+      auto ins4 = [&](uint32_t k) {
+        t4 = max(t4, min(t3, k));
+        t3 = max(t3, min(t2, k));
+        t2 = max(t2, min(t1, k));
+        t1 = max(t1, k);
+      };
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      if (t + NTA * j < rs.nq) {
-        ins(fkey(xv[j].x)); ins(fkey(xv[j].y)); ins(fkey(xv[j].z)); ins(fkey(xv[j].w));
-      }
+      for (int j = 0; j < NQ; ++j) { ins4(kq[j][0]); ins4(kq[j][1]); ins4(kq[j][2]); ins4(kq[j][3]); }
+      ins4(ke);
+    } else {
+      auto ins2 = [&](uint32_t k) {
+        t2 = max(t2, min(t1, k));
+        t1 = max(t1, k);
+      };
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) { ins2(kq[j][0]); ins2(kq[j][1]); ins2(kq[j][2]); ins2(kq[j][3]); }
+      ins2(ke);
     }
-    if (eh || et) ins(fkey(xe));
     C4S_SCAN_PHASE(1);
 
     // L0: a key at or below the msel-th largest of those keys (two 11-bit passes).
     for (int i = t; i < 2048; i += NTA) sh.hist[i] = 0u;
+    for (int i = t; i < kIdWords; i += NTA) { sh.lmark[i] = 0u; sh.fmark[i] = 0u; }
     __syncthreads();
     if (t1) atomicAdd(&sh.hist[t1 >> 21], 1u);
     if (t2) atomicAdd(&sh.hist[t2 >> 21], 1u);
@@ -336,78 +357,45 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
         L0 = (b1 << 21) | (b2 << 10);
       }
     }
+    L0 = max(L0, 1u);   // the same set of values; excludes the zero keys past the row
     C4S_SCAN_PHASE(2);
 
-    // Candidates (key >= L0) compacted in id order: head, body quads by slot, tail.
-    uint32_t cnt[NQ + 2];
+    // Candidates (key >= L0) in thread order: one scan of the per-thread
+    // counts places them (their id order comes from id bitmaps below).
+    uint32_t cnt = 0;
     uint32_t below = 0;   // largest key under L0 (raw value: bounds the penalised one)
-    {
-      const uint32_t ke = fkey(xe);
-      cnt[0] = (eh && ke >= L0) ? 1u : 0u;
-      cnt[NQ + 1] = (et && ke >= L0) ? 1u : 0u;
-      if ((eh || et) && ke < L0) below = ke;
+    if (ke >= L0) ++cnt; else below = ke;
 #pragma unroll
-      for (int j = 0; j < NQ; ++j) {
-        uint32_t cj = 0;
-        if (t + NTA * j < rs.nq) {
-          const uint32_t k0 = fkey(xv[j].x), k1 = fkey(xv[j].y), k2 = fkey(xv[j].z), k3 = fkey(xv[j].w);
-          cj = (k0 >= L0) + (k1 >= L0) + (k2 >= L0) + (k3 >= L0);
-          below = max(below, max(max(k0 < L0 ? k0 : 0u, k1 < L0 ? k1 : 0u),
-                                 max(k2 < L0 ? k2 : 0u, k3 < L0 ? k3 : 0u)));
-        }
-        cnt[j + 1] = cj;
+    for (int j = 0; j < NQ; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t k = kq[j][i];
+        cnt += (k >= L0) ? 1u : 0u;
+        below = max(below, k < L0 ? k : 0u);
       }
-    }
-    uint32_t ex[NQ + 2];
-#pragma unroll
-    for (int sl = 0; sl < NQ + 2; ++sl) {
-      const uint32_t inc = wave_scan_u32(cnt[sl]);
-      ex[sl] = inc - cnt[sl];
-      if (lane == kWave - 1) sh.wtot[sl][wv] = inc;
-    }
     {
       const uint32_t bm = wave_max_u32(below);
       if (lane == 0) sh.redm[wv] = bm;
     }
-    __syncthreads();
-    uint32_t C = 0, tout = 0;
+    uint32_t C;
+    uint32_t pos = scan_excl_nta(cnt, sh.red, C);   // its barriers also publish redm
+    uint32_t tout = 0;
 #pragma unroll
     for (int ww = 0; ww < NWA; ++ww) tout = max(tout, sh.redm[ww]);
     // raw values bound the penalised ones; the quotient is monotone in them
     if (tout != 0u && c.temp_on) tout = fkey(kfloat(tout) / c.temp);
-#pragma unroll
-    for (int sl = 0; sl < NQ + 2; ++sl) {
-      uint32_t pre = 0, tot = 0;
-#pragma unroll
-      for (int ww = 0; ww < NWA; ++ww) {
-        const uint32_t x = sh.wtot[sl][ww];
-        pre += (ww < wv) ? x : 0u;
-        tot += x;
-      }
-      ex[sl] += C + pre;
-      C += tot;
-    }
     const bool overflow = C > (uint32_t)kCandCap;
     C4S_SCAN_PHASE(3);
-    if (!overflow) {
-      // raw value and id of each candidate at its id-order position
-      auto put = [&](uint32_t pos, float x, int id) {
-        sh.candy[pos] = x;
-        sh.cand[pos] = (uint64_t)(uint32_t)id;
-      };
-      if (eh && fkey(xe) >= L0) put(ex[0], xe, eid);
-      if (et && fkey(xe) >= L0) put(ex[NQ + 1], xe, eid);
+    if (!overflow && cnt) {
+      // key and id of each candidate
+      auto put = [&](uint32_t k, int id) { sh.cand[pos++] = ((uint64_t)k << 32) | (uint32_t)id; };
+      if (ke >= L0) put(ke, eid);
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
-        const int q = t + NTA * j;
-        if (q < rs.nq && cnt[j + 1]) {
-          uint32_t pos = ex[j + 1];
-          const int id = rs.head + 4 * q;
-          if (fkey(xv[j].x) >= L0) put(pos++, xv[j].x, id);
-          if (fkey(xv[j].y) >= L0) put(pos++, xv[j].y, id + 1);
-          if (fkey(xv[j].z) >= L0) put(pos++, xv[j].z, id + 2);
-          if (fkey(xv[j].w) >= L0) put(pos++, xv[j].w, id + 3);
-        }
+        const int id = rs.head + 4 * (t + NTA * j);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (kq[j][i] >= L0) put(kq[j][i], id + i);
       }
     }
     __syncthreads();
@@ -415,8 +403,9 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
     // temperature (:16), its entry.
     if (!overflow)
       for (int i = t; i < (int)C; i += NTA) {
-        const int id = (int)(uint32_t)sh.cand[i];
-        const float x = sh.candy[i];
+        const uint64_t cw = sh.cand[i];
+        const int id = (int)(uint32_t)cw;
+        const float x = kfloat((uint32_t)(cw >> 32));
         const float y = (c.pen_on && bit_of(sh.bm, id)) ? pen_exact(x, pen) : x;
         sh.cand[i] = make_entry(c.temp_on ? y / c.temp : y, id, i);
         sh.candy[i] = y;
@@ -444,13 +433,14 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       if (small) {
         const uint64_t mine = (t < (int)C) ? sh.cand[t] : ~0ull;
         uint32_t r = 0;
-        for (int j = 0; j < C8; j += 8) {
-          uint64_t o[8];
+        if (wv * kWave < (int)C)   // waves without an entry skip the count
+          for (int j = 0; j < C8; j += 8) {
+            uint64_t o[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = sh.cand[j + i];
+            for (int i = 0; i < 8; ++i) o[i] = sh.cand[j + i];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) r += (o[i] > mine) ? 1u : 0u;
-        }
+            for (int i = 0; i < 8; ++i) r += (o[i] > mine) ? 1u : 0u;
+          }
         if (t < (int)C) srt[r] = mine;
         __syncthreads();
       } else {
@@ -481,23 +471,26 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       // exp((double)fl(z - z_max)) as the reference computes it, in fp32.
       float* ly = reinterpret_cast<float*>(sw + kYW);
       const float zmax = kfloat(ent_key(srt[0]));
-      // The stored rank is the id-order rank among the list entries:
-      // candidates sit in id order, so it counts the list's candidate
-      // positions below the entry's own. Full-vocabulary rows also get each
-      // of the first NTA entries' id-order place among those NTA.
-      if (t < kCandCap / 32) { sh.lmark[t] = 0u; sh.fmark[t] = 0u; }
-      __syncthreads();
+      // The stored rank is the id-order rank among the list entries: the
+      // list's ids below the entry's own, counted in an id bitmap of the
+      // list. Full-vocabulary rows also get each of the first NTA entries'
+      // id-order place among those NTA (a bitmap of their ids).
       for (int i = t; i < n; i += NTA) {
-        const int ci = ent_rank(srt[i]);
-        atomicOr(&sh.lmark[ci >> 5], 1u << (ci & 31));
-        if (i < NTA) atomicOr(&sh.fmark[ci >> 5], 1u << (ci & 31));
+        const int id = ent_id(srt[i]);
+        atomicOr(&sh.lmark[id >> 5], 1u << (id & 31));
+        if (i < NTA) atomicOr(&sh.fmark[id >> 5], 1u << (id & 31));
       }
       __syncthreads();
-      if (wv < 2) {
-        const uint32_t* mk = wv ? sh.fmark : sh.lmark;
-        const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(mk[lane]) : 0u;
-        const uint32_t inc = wave_scan_u32(pc);
-        if (lane < kCandCap / 32) (wv ? sh.fpre : sh.lpre)[lane] = inc - pc;
+      {
+        // marks before each word, both bitmaps in one scan (16-bit halves: at
+        // most kListLarge marks); thread t takes words 2t and 2t + 1
+        const int wa = 2 * t, wb = 2 * t + 1;
+        const uint32_t pa = wa < kIdWords ? (uint32_t)__popc(sh.lmark[wa]) | ((uint32_t)__popc(sh.fmark[wa]) << 16) : 0u;
+        const uint32_t pb = wb < kIdWords ? (uint32_t)__popc(sh.lmark[wb]) | ((uint32_t)__popc(sh.fmark[wb]) << 16) : 0u;
+        uint32_t tot;
+        const uint32_t ex = scan_excl_nta(pa + pb, sh.red, tot);
+        if (wa < kIdWords) sh.pre2[wa] = ex;
+        if (wb < kIdWords) sh.pre2[wb] = ex + pa;
       }
       __syncthreads();
       // Entries t and t + NTA (n <= 2 NTA): every LDS read first, at clamped
@@ -505,11 +498,12 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       static_assert(kListLarge <= 2 * NTA, "two list entries a thread");
       const bool v0 = t < n, v1 = t + NTA < n;
       const uint64_t e0 = srt[v0 ? t : 0], e1 = srt[v1 ? t + NTA : 0];
-      const int c0 = ent_rank(e0), c1 = ent_rank(e1);
-      const uint32_t below0 = (1u << (c0 & 31)) - 1u, below1 = (1u << (c1 & 31)) - 1u;
-      const uint32_t lp0 = sh.lpre[c0 >> 5], lk0 = sh.lmark[c0 >> 5];
-      const uint32_t lp1 = sh.lpre[c1 >> 5], lk1 = sh.lmark[c1 >> 5];
-      const uint32_t fp0 = sh.fpre[c0 >> 5], fk0 = sh.fmark[c0 >> 5];
+      const int c0 = ent_rank(e0), c1 = ent_rank(e1);   // candidate positions
+      const int i0 = ent_id(e0), i1 = ent_id(e1);
+      const uint32_t below0 = (1u << (i0 & 31)) - 1u, below1 = (1u << (i1 & 31)) - 1u;
+      const uint32_t pr0 = sh.pre2[i0 >> 5], lk0 = sh.lmark[i0 >> 5], fk0 = sh.fmark[i0 >> 5];
+      const uint32_t pr1 = sh.pre2[i1 >> 5], lk1 = sh.lmark[i1 >> 5];
+      const uint32_t lp0 = pr0 & 0xFFFFu, lp1 = pr1 & 0xFFFFu, fp0 = pr0 >> 16;
       const float y0 = sh.candy[c0], y1 = sh.candy[c1];
       if (masses && v0)   // the place among the first NTA, to the summary as words below
         reinterpret_cast<uint8_t*>(sh.place4)[t] = (uint8_t)(fp0 + (uint32_t)__popc(fk0 & below0));
@@ -560,10 +554,11 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
         if (q < rs.nq) {
           const uint32_t hb = hq[j];
           const bool pon = c.pen_on;
-          qd = mass_exact((pon && (hb & 1u)) ? pen_exact(xv[j].x, pen) : xv[j].x, c, m0) +
-               mass_exact((pon && (hb & 2u)) ? pen_exact(xv[j].y, pen) : xv[j].y, c, m0) +
-               mass_exact((pon && (hb & 4u)) ? pen_exact(xv[j].z, pen) : xv[j].z, c, m0) +
-               mass_exact((pon && (hb & 8u)) ? pen_exact(xv[j].w, pen) : xv[j].w, c, m0);
+          const float x0 = kfloat(kq[j][0]), x1 = kfloat(kq[j][1]), x2 = kfloat(kq[j][2]), x3 = kfloat(kq[j][3]);
+          qd = mass_exact((pon && (hb & 1u)) ? pen_exact(x0, pen) : x0, c, m0) +
+               mass_exact((pon && (hb & 2u)) ? pen_exact(x1, pen) : x1, c, m0) +
+               mass_exact((pon && (hb & 4u)) ? pen_exact(x2, pen) : x2, c, m0) +
+               mass_exact((pon && (hb & 8u)) ? pen_exact(x3, pen) : x3, c, m0);
         }
         // 16 consecutive lanes hold the 16 quads of one chunk
         double d = qd;
@@ -578,6 +573,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       __syncthreads();
       if (eh || et) {
         const bool pb = c.pen_on && bit_of(sh.bm, eid);
+        const float xe = kfloat(ke);
         sh.edge[t] = mass_exact(pb ? pen_exact(xe, pen) : xe, c, m0);   // t < 6
       }
       if (t == 0) {
