@@ -24,6 +24,7 @@
 // bitmap, temperature re-applied on the fly).
 
 
+#include "c4s_list.hpp"
 #include "c4s_step.hpp"
 
 namespace c4s {
@@ -300,6 +301,219 @@ __device__ __noinline__ void chain_fallback(const StepIO& io, const RowCfg& c, u
   }
 }
 
+// ---- top-k rows on a candidate list --------------------------------------------------
+//
+// A sampled row with top_k in [1, 64] is decided by its largest values alone
+// (sampling.cpp:30-40 keeps the k largest and their ties; top_p and the draw,
+// :42-71 and text2semantic.cpp:150-165, then read the kept entries only). So
+// the step takes a candidate list as the AR stream's scan makes it, from the
+// penalised values y each thread holds (ids [lo, lo + n), thread order is id
+// order): a key L0 at or below the 112th largest of the threads' top-2 keys
+// (two 11-bit histogram passes), every value with key(y) >= L0 in id order
+// (one workgroup scan), the temperature on those alone (fl(y / T) is monotone
+// in y), their sort by (z desc, id asc), and a bound on every value outside.
+// One wave then decides the step on the first 128 entries (list_step). When
+// the list cannot settle it (a boundary tie group past the list, a cut inside
+// the error bound, ...), nothing has been written but the work area, and the
+// row takes the one-pass step.
+constexpr int kFastList = kListSmall;           // list entries the decision sees
+constexpr int kFastSel = kListSmall - 16;       // thread-top keys at or above L0
+static_assert(kStepThreads * 4 == 2048, "four histogram bins a thread");
+
+struct NoHit {   // no id drawn since the list was made
+  __device__ __forceinline__ bool hit(int) const { return false; }
+};
+
+struct FastSh {
+  uint32_t hist[2048];         // histogram, then the sorted candidates (uint64)
+  uint64_t cand[kCandCap];     // candidates: key(y) | id, then their entries
+  float candy[kCandCap];       // y by candidate position
+  uint64_t lst[kFastList];     // the list: entries with their id-order rank among the list
+  float ly[kFastList];
+  uint32_t lmark[kCandCap / 32], lpre[kCandCap / 32];
+  uint32_t red[kStepWaves], redm[kStepWaves];
+  uint32_t bu[4];
+  LSpecCS cs;
+};
+static_assert(sizeof(FastSh) <= 3 * kHistBytes, "the list step's area lies in the histograms");
+
+// Exclusive scan of v over the workgroup (thread order); total in `tot`.
+__device__ __forceinline__ uint32_t fast_scan(uint32_t v, uint32_t* red, uint32_t& tot) {
+  const uint32_t inc = wave_scan_u32(v);
+  if (lane_id() == kWave - 1) red[wave_id()] = inc;
+  __syncthreads();
+  uint32_t pre = 0;
+  tot = 0;
+#pragma unroll
+  for (int w = 0; w < kStepWaves; ++w) {
+    const uint32_t x = red[w];
+    pre += (w < wave_id()) ? x : 0u;
+    tot += x;
+  }
+  __syncthreads();
+  return pre + inc - v;
+}
+
+// Bin of the 2048 (scanned from the top) holding the m-th largest counted key,
+// and the count above it; false when fewer than m keys were counted.
+__device__ __forceinline__ bool fast_pick(FastSh& fs, uint32_t m, uint32_t& bin, uint32_t& above) {
+  const int t = threadIdx.x;
+  uint32_t cb[4], loc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { cb[i] = fs.hist[2047 - 4 * t - i]; loc += cb[i]; }
+  uint32_t total;
+  const uint32_t ex = fast_scan(loc, fs.red, total);
+  if (total < m) return false;
+  if (ex < m && ex + loc >= m) {
+    uint32_t run = ex;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (run < m && run + cb[i] >= m) { fs.bu[0] = 2047 - 4 * t - i; fs.bu[1] = run; }
+      run += cb[i];
+    }
+  }
+  __syncthreads();
+  bin = fs.bu[0];
+  above = fs.bu[1];
+  __syncthreads();
+  return true;
+}
+
+template <int PT>
+__device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int V, const float (&y)[PT], int lo,
+                                          int n, FastSh& fs) {
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  uint32_t ky[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) ky[j] = (j < n) ? fkey(y[j]) : 0u;   // 0: below every key of a value
+  uint32_t t1 = 0, t2 = 0;
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    t2 = max(t2, min(t1, ky[j]));
+    t1 = max(t1, ky[j]);
+  }
+  // L0: two 11-bit passes over the threads' top-2 keys
+  for (int i = t; i < 2048; i += kStepThreads) fs.hist[i] = 0u;
+  if (t < kCandCap / 32) fs.lmark[t] = 0u;
+  __syncthreads();
+  if (t1) atomicAdd(&fs.hist[t1 >> 21], 1u);
+  if (t2) atomicAdd(&fs.hist[t2 >> 21], 1u);
+  __syncthreads();
+  uint32_t L0 = 0;
+  {
+    uint32_t b1, ab1;
+    if (fast_pick(fs, kFastSel, b1, ab1)) {
+      for (int i = t; i < 2048; i += kStepThreads) fs.hist[i] = 0u;
+      __syncthreads();
+      if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[(t1 >> 10) & 2047u], 1u);
+      if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[(t2 >> 10) & 2047u], 1u);
+      __syncthreads();
+      uint32_t b2, ab2;
+      fast_pick(fs, kFastSel - ab1, b2, ab2);
+      L0 = (b1 << 21) | (b2 << 10);
+    }
+  }
+  L0 = max(L0, 1u);   // the same values; excludes the zero keys past the row
+  // candidates in id order; the largest key under L0 bounds everything else
+  uint32_t cnt = 0, below = 0;
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    cnt += (ky[j] >= L0) ? 1u : 0u;
+    below = max(below, ky[j] < L0 ? ky[j] : 0u);
+  }
+  {
+    const uint32_t bm = wave_max_u32(below);
+    if (lane == 0) fs.redm[wv] = bm;
+  }
+  uint32_t C;
+  uint32_t pos = fast_scan(cnt, fs.red, C);   // its barriers also publish redm
+  uint32_t tout = 0;
+#pragma unroll
+  for (int w = 0; w < kStepWaves; ++w) tout = max(tout, fs.redm[w]);
+  if (tout != 0u && c.temp_on) tout = fkey(kfloat(tout) / c.temp);   // the quotient is monotone in y
+  if (C > (uint32_t)kCandCap || C == 0u) return false;   // uniform
+#pragma unroll
+  for (int j = 0; j < PT; ++j)
+    if (ky[j] >= L0) fs.cand[pos++] = ((uint64_t)ky[j] << 32) | (uint32_t)(lo + j);
+  __syncthreads();
+  // entries: z = fl(y / T) (sampling.cpp:16) with the candidate's position
+  for (int i = t; i < (int)C; i += kStepThreads) {
+    const uint64_t cw = fs.cand[i];
+    const float yv = kfloat((uint32_t)(cw >> 32));
+    fs.cand[i] = make_entry(c.temp_on ? yv / c.temp : yv, (int)(uint32_t)cw, i);
+    fs.candy[i] = yv;
+  }
+  const int C8 = ((int)C + 7) & ~7;
+  if (t < C8 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
+  __syncthreads();
+  // sort by rank counting (entries are distinct: their ids are)
+  uint64_t* srt = reinterpret_cast<uint64_t*>(fs.hist);
+  static_assert(sizeof(FastSh::hist) >= (kFastList + 1) * sizeof(uint64_t), "the sorted head fits");
+  for (int base = 0; base < (int)C; base += kStepThreads) {
+    const int i = base + t;
+    const uint64_t mine = (i < (int)C) ? fs.cand[i] : ~0ull;
+    uint32_t r = 0;
+    if (base + wv * kWave < (int)C)   // waves without an entry skip the count
+      for (int j = 0; j < C8; j += 8) {
+        uint64_t o[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] = fs.cand[j + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) r += (o[q] > mine) ? 1u : 0u;
+      }
+    if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;   // the list and the entry after it
+  }
+  __syncthreads();
+  // the list: the leading entries above the bound, at most kFastList
+  const int nl = min((int)C, kFastList + 1);
+  uint32_t nab = 0;
+  for (int i = t; i < nl; i += kStepThreads) nab += (ent_key(srt[i]) > tout) ? 1u : 0u;
+  uint32_t n_all;
+  (void)fast_scan(nab, fs.red, n_all);
+  const int nlist = min((int)n_all, kFastList);
+  if ((int)n_all > kFastList) tout = max(tout, ent_key(srt[kFastList]));
+  // the draw starts its maximum at -1e30 (text2semantic.cpp:150): below it the one-pass step decides
+  if (nlist == 0 || !(kfloat(ent_key(srt[0])) >= -1e30f)) return false;
+  // id-order rank among the list: candidates sit in id order, so it counts
+  // the list's candidate positions below the entry's own
+  for (int i = t; i < nlist; i += kStepThreads) {
+    const int ci = ent_rank(srt[i]);
+    atomicOr(&fs.lmark[ci >> 5], 1u << (ci & 31));
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(fs.lmark[lane]) : 0u;
+    const uint32_t inc = wave_scan_u32(pc);
+    if (lane < kCandCap / 32) fs.lpre[lane] = inc - pc;
+  }
+  __syncthreads();
+  if (t < nlist) {
+    const uint64_t e = srt[t];
+    const int ci = ent_rank(e);
+    fs.lst[t] = (e & ~1023ull) | (fs.lpre[ci >> 5] + (uint32_t)__popc(fs.lmark[ci >> 5] & ((1u << (ci & 31)) - 1u)));
+    fs.ly[t] = fs.candy[ci];
+  }
+  __syncthreads();
+  if (wv == 0) {
+    SumHdr h{};
+    h.n = nlist;
+    h.tout = tout;
+    h.flags = 0u;
+    const bool a0 = lane < nlist, a1 = lane + kWave < nlist;
+    const uint64_t e0 = a0 ? fs.lst[lane] : 0ull, e1 = a1 ? fs.lst[lane + kWave] : 0ull;
+    const float y0 = a0 ? fs.ly[lane] : 0.0f, y1 = a1 ? fs.ly[lane + kWave] : 0.0f;
+    uint64_t r = io.rng ? *io.rng : 0ull;
+    StepOut o{0, 0u, 0u, 0u, 0u};
+    const bool ok = list_step(h, e0, e1, y0, y1, c, V, NoHit{}, r, fs.cs, o);
+    if (lane == 0) {
+      fs.bu[2] = ok ? 1u : 0u;
+      if (ok) step_out(io, V, o.tok, r, true, 1u | 2u | 4u | 16u | 32u, 0u, o.dex, o.kept);
+    }
+  }
+  __syncthreads();
+  return fs.bu[2] != 0u;
+}
+
 // One AR step of the reference chain (C4S_MODE_CHAIN) for one row per
 // workgroup, in one pass where it can (c4s_step.hpp), else the multi-pass
 // chain on the row staged in LDS. PT >= the ids a thread owns.
@@ -421,6 +635,13 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         if (j < n) io.masked[lo + j] = y[j];
     if (t == 0) step_out(io, V, bi, 0ull, false, 8u | 16u, 0u, 0u, (uint32_t)V);
     return;
+  }
+
+  // top-k rows with k <= 64: on a candidate list when it settles the step
+  if (c.draw && c.topk_on && c.k <= kWave && c.p > 0.0f && !io.masked) {
+    if (list_fast<PT>(io, c, V, y, lo, n, *reinterpret_cast<FastSh*>(work))) return;
+    for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
+    __syncthreads();
   }
 
   // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----

@@ -23,11 +23,12 @@ def test_single_row_sampled_and_greedy(orc, gpu_ctx):
                                                        greedy.hist_ids, 10.0))
 
 
+@pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("seed", [2, 21, 22])
-def test_batch64_one_step(orc, gpu_ctx, seed):
+def test_batch64_one_step(orc, gpu_ctx, seed, masked):
     b = W.batch64(seed=seed, rows=64)
-    print(f"batch64 seed={seed}", flush=True)
-    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    print(f"batch64 seed={seed} masked={masked}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=masked)
     print("exact top_p passes", int(st[:, 1].sum()), "exact draws", int(st[:, 2].sum()))
     one_pass = (st[:, 0] & 16) != 0
     print("rows decided in one pass", int(one_pass.sum()), "of", b.n_rows)
@@ -43,8 +44,9 @@ def test_batch64_general_rows(orc, gpu_ctx):
     compare_with_oracle(orc, gpu_ctx, b)
 
 
+@pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("sigma", [0.3, 0.7, 1.5])
-def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma):
+def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma, masked):
     """Narrow logit ranges (an LM head's output): hundreds of entries share the
     boundary bucket of the nucleus cut or of the k-th value, so the one-pass
     step refines the boundary buckets in a second histogram."""
@@ -53,8 +55,8 @@ def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma):
     b.logits[:] = (sigma * g.standard_normal(b.logits.shape)).astype(np.float32)
     b.top_k[:] = np.resize(np.array([0, 0, 0, 50, 200, 0, 400, 0], np.int32), 64)
     b.top_p[:] = np.resize(np.array([0.9, 0.8, 0.95, 1.0, 0.9, 0.5, 1.0, 0.99], np.float32), 64)
-    print(f"flat rows sigma={sigma}", flush=True)
-    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    print(f"flat rows sigma={sigma} masked={masked}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=masked)
     one_pass = (st[:, 0] & 16) != 0
     print("rows decided in one pass", int(one_pass.sum()), "of", b.n_rows)
     for i in np.flatnonzero(~one_pass):
@@ -62,15 +64,57 @@ def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma):
     assert one_pass.mean() > 0.9
 
 
+@pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("sweep", ["greedy", "top_k1", "top_p"])
-def test_bf16_ties(orc, gpu_ctx, sweep):
+def test_bf16_ties(orc, gpu_ctx, sweep, masked):
     b = W.bf16_ties(seed=3, rows=1024, sweep=sweep)
-    print(f"bf16_ties {sweep}", flush=True)
-    tok, st = compare_with_oracle(orc, gpu_ctx, b)
+    print(f"bf16_ties {sweep} masked={masked}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=masked)
     if sweep == "top_k1":
         assert (st[:, 3] > 1).all()      # the tied maxima all survive top_k=1
     if sweep == "top_p":
         assert st[:, 1].sum() > 0        # rows whose nucleus cut falls in a tie take the exact sort
+
+
+def _list_decided(st):
+    """Rows the candidate-list step decided (statistics word 0, bit 5)."""
+    return (st[:, 0] & 32) != 0
+
+
+@pytest.mark.parametrize("seed", [2, 21])
+def test_candidate_list_rows(orc, gpu_ctx, seed):
+    """Sampled top-k rows with k <= 64 and no masked-row output are decided on
+    a candidate list (every other row takes the one-pass step)."""
+    b = W.batch64(seed=seed, rows=64)
+    b.top_k[::7] = 64
+    b.top_k[3::7] = 1
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=False)
+    tk = (b.top_k >= 1) & (b.top_k <= 64) & (b.do_sample != 0)
+    used = _list_decided(st)
+    print("list rows", int(used.sum()), "of", int(tk.sum()), "top-k rows")
+    assert not used[~tk].any()
+    assert used[tk].mean() > 0.9
+
+
+def test_candidate_list_production_defaults(orc, gpu_ctx):
+    """The pipeline defaults on every row (pipeline.h:31-35: temperature 0.8,
+    top_k 30, top_p 0.8, penalty 10) over ten AR steps, each step's token
+    joining the history."""
+    b = W.batch64(seed=9, rows=64)
+    b.temp[:] = 0.8
+    b.top_k[:] = 30
+    b.top_p[:] = 0.8
+    b.pen[:] = 10.0
+    x = W.batch64_logits(77, 10, rows=64)
+    hist = [list(b.hist_ids[b.hist_off[r]:b.hist_off[r + 1]]) for r in range(64)]
+    for s in range(10):
+        b.logits = x[s]
+        b.hist_ids, b.hist_off = W.csr([np.asarray(h, np.int32) for h in hist])
+        tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=False)
+        assert _list_decided(st).mean() > 0.9
+        b.rng = gpu_rows(gpu_ctx, b, masked=False)[1]
+        for r in range(64):
+            hist[r].append(int(tok[r]))
 
 
 def test_large_vocab(orc, gpu_ctx):
@@ -103,8 +147,9 @@ def _rows_from(rows, temp, top_k, top_p, pen, hist, do_sample=None, seed=1234):
                    rng=W.seed_batch(seed, n))
 
 
+@pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("V", [1, 2, 3, 63, 64, 65, 1000, 9216, 12288, 12289, 40000])
-def test_vocab_sizes(orc, gpu_ctx, V):
+def test_vocab_sizes(orc, gpu_ctx, V, masked):
     g = np.random.default_rng(V)
     n = 24
     x = (g.standard_normal((n, V)) * 2).astype(np.float32)
@@ -117,10 +162,11 @@ def test_vocab_sizes(orc, gpu_ctx, V):
                 pen=g.choice(np.array([1.0, 1.3, 10.0, 0.5], np.float32), n),
                 do_sample=(g.random(n) > 0.2).astype(np.uint8), rng=W.seed_batch(V, n))
     mk = g.choice(np.array([1, 1, 1, 0, 2, 7, V + 4], np.int32), n)
-    compare_with_oracle(orc, gpu_ctx, b, min_keep=mk)
+    compare_with_oracle(orc, gpu_ctx, b, min_keep=mk, masked=masked)
 
 
-def test_edge_rows(orc, gpu_ctx):
+@pytest.mark.parametrize("masked", [True, False])
+def test_edge_rows(orc, gpu_ctx, masked):
     ninf = -np.inf
     rows = [
         [ninf] * 16,                                        # all -inf
@@ -134,19 +180,21 @@ def test_edge_rows(orc, gpu_ctx):
         [-800.0, 0.0, -745.0, -746.0, -744.0] + [-9000.0] * 11,
     ]
     n = len(rows)
-    for temp, k, p in [(1.0, 0, 1.0), (0.8, 2, 0.5), (1.0, 1, 0.0), (2.0, 0, 0.3), (0.5, 3, 1.0)]:
+    for temp, k, p in [(1.0, 0, 1.0), (0.8, 2, 0.5), (1.0, 1, 0.0), (2.0, 0, 0.3), (0.5, 3, 1.0), (0.8, 16, 0.8),
+                       (1.0, 15, 1e-6)]:
         b = _rows_from(rows, [temp] * n, [k] * n, [p] * n, [1.0] * n, [[]] * n)
-        compare_with_oracle(orc, gpu_ctx, b)
+        compare_with_oracle(orc, gpu_ctx, b, masked=masked)
         for mk in (0, 2, 17):
-            compare_with_oracle(orc, gpu_ctx, b, min_keep=np.full(n, mk, np.int32))
+            compare_with_oracle(orc, gpu_ctx, b, min_keep=np.full(n, mk, np.int32), masked=masked)
 
 
-def test_row_active_and_mixed_greedy(orc, gpu_ctx):
+@pytest.mark.parametrize("masked", [True, False])
+def test_row_active_and_mixed_greedy(orc, gpu_ctx, masked):
     b = W.batch64(seed=5, rows=64)
     b.do_sample[::3] = 0
     active = np.ones(64, np.uint8)
     active[::5] = 0
-    tok, st = compare_with_oracle(orc, gpu_ctx, b, row_active=active)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, row_active=active, masked=masked)
     assert (tok[active == 0] == -1).all()
 
 
