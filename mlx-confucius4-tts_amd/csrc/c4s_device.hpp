@@ -244,26 +244,26 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 }
 
 // Sequential double sums over the lanes (the reference's loops add one term
-// after the other): lane indices are constants of an unrolled loop, so each
-// term costs two scalar reads and the dependent chain is the adds alone.
+// after the other): the lane index is a scalar loop counter, so each term
+// costs two scalar reads and the dependent chain is the adds alone. The loops
+// stay rolled: unrolled over 64 lanes they raised the scalar register pressure
+// of the kernels that inline them into spills (a 1024-thread kernel into
+// scratch, 2.7x its time).
 // seq_sum_lanes: total + e[0] + e[1] + ... + e[n-1] in that order (n <= 64,
 // wave-uniform).
 __device__ __forceinline__ double seq_sum_lanes(double total, double e, int n) {
-#pragma unroll
-  for (int t = 0; t < kWave; ++t)
-    if (t < n) total += readlane_f64(e, t);
+#pragma unroll 1
+  for (int t = 0; t < n; ++t) total += readlane_f64(e, t);
   return total;
 }
 // seq_find_lanes: the same running sum continued from acc; returns the first
 // t < n after whose term r <= acc (acc then the sum through t), else -1 (acc
 // the sum of all n terms).
 __device__ __forceinline__ int seq_find_lanes(double& acc, double e, int n, double r) {
-#pragma unroll
-  for (int t = 0; t < kWave; ++t) {
-    if (t < n) {
-      acc += readlane_f64(e, t);
-      if (r <= acc) return t;
-    }
+#pragma unroll 1
+  for (int t = 0; t < n; ++t) {
+    acc += readlane_f64(e, t);
+    if (r <= acc) return t;
   }
   return -1;
 }
@@ -311,14 +311,12 @@ __device__ __forceinline__ int seq_cut_mem(double& cum, const double* p, int n, 
 // cum: the number of leading terms after which cum <= thr still holds; sets
 // stop when a term took cum above thr (cum only grows).
 __device__ __forceinline__ int seq_cut_lanes(double& cum, double q, int n, double thr, bool& stop) {
-#pragma unroll
-  for (int t = 0; t < kWave; ++t) {
-    if (t < n) {
-      cum += readlane_f64(q, t);
-      if (!(cum <= thr)) {
-        stop = true;
-        return t;
-      }
+#pragma unroll 1
+  for (int t = 0; t < n; ++t) {
+    cum += readlane_f64(q, t);
+    if (!(cum <= thr)) {
+      stop = true;
+      return t;
     }
   }
   return n;

@@ -414,6 +414,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     }
   }
   L0 = max(L0, 1u);   // the same values; excludes the zero keys past the row
+  C4S_PHASE(11);
   // candidates in id order; the largest key under L0 bounds everything else
   uint32_t cnt = 0, below = 0;
 #pragma unroll
@@ -446,6 +447,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   const int C8 = ((int)C + 7) & ~7;
   if (t < C8 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
   __syncthreads();
+  C4S_PHASE(12);
   // sort by rank counting (entries are distinct: their ids are)
   uint64_t* srt = reinterpret_cast<uint64_t*>(fs.hist);
   static_assert(sizeof(FastSh::hist) >= (kFastList + 1) * sizeof(uint64_t), "the sorted head fits");
@@ -464,6 +466,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;   // the list and the entry after it
   }
   __syncthreads();
+  C4S_PHASE(13);
   // the list: the leading entries above the bound, at most kFastList
   const int nl = min((int)C, kFastList + 1);
   uint32_t nab = 0;
@@ -494,6 +497,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     fs.ly[t] = fs.candy[ci];
   }
   __syncthreads();
+  C4S_PHASE(14);
   if (wv == 0) {
     SumHdr h{};
     h.n = nlist;
@@ -511,6 +515,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     }
   }
   __syncthreads();
+  C4S_PHASE(15);
   return fs.bu[2] != 0u;
 }
 
