@@ -15,7 +15,8 @@ that call; --sequential times the single-kernel stream instead.
 
 Also reported: the same chain as one launch per AR step (per_call, eager and
 graph-replayed; with the history as CSR ids, and kept on the device as a set
-that each call extends); the other workloads (one row; 1024 bf16 rows with ties;
+that each call extends; and with the pipeline's default parameters on every
+row, the AR loop's usual case); the other workloads (one row; 1024 bf16 rows with ties;
 256 rows at V=151936; the LM head for bf16 / fp32 / 8-bit weights alone and
 with the chain); HBM copy and read probes; bit-exact parity of the first AR
 steps against the CPU oracle, and the oracle timed on host cores (1 thread and
@@ -341,10 +342,23 @@ def main():
                         do_sample=do_sample, hist_bits=bits, stop_token=V - 1)
         step_t[0] += 1
 
+    # the pipeline's defaults on every row (pipeline.h:31-35: temperature 0.8,
+    # top_k 30, top_p 0.8, penalty 10), as generate_batch passes them
+    d_temp, d_topk = torch.full_like(temp, 0.8), torch.full_like(top_k, 30)
+    d_topp, d_pen = torch.full_like(top_p, 0.8), torch.full_like(pen, 10.0)
+    rng3 = rng0.clone()
+
+    def defaults_call():
+        ctx.sample_rows(logits[step_t[0] % T], hist_ids, hist_off, d_temp, d_topk, d_topp, d_pen, rng3, tok1,
+                        do_sample=do_sample)
+        step_t[0] += 1
+
     call_bytes = R * (4 * V + 4) + 4 * h0.sum()
     bits_bytes = R * (4 * V + 4 + 4 * ((V + 31) // 32) + 4)
     call_us, call_graph_us = time_eager(torch, csr_call, n_calls, s2), time_graph(torch, csr_call, n_calls, s2)
     bits_us, bits_graph_us = time_eager(torch, bits_call, n_calls, s2), time_graph(torch, bits_call, n_calls, s2)
+    def_us, def_graph_us = (time_eager(torch, defaults_call, n_calls, s2),
+                            time_graph(torch, defaults_call, n_calls, s2))
     per_call = {"mode": "one launch per AR step, 64 rows, logits of that step only (the AR loop's own pattern)",
                 "us_per_call": round(call_us, 3), "graph_us_per_call": round(call_graph_us, 3),
                 "rows_per_s": round(R / (call_us * 1e-6), 1),
@@ -352,9 +366,13 @@ def main():
                 "graph_achieved_GBps": round(call_bytes / (call_graph_us * 1e-6) / 1e9, 1),
                 "hist_bits_us_per_call": round(bits_us, 3),
                 "hist_bits_graph_us_per_call": round(bits_graph_us, 3),
-                "hist_bits_graph_achieved_GBps": round(bits_bytes / (bits_graph_us * 1e-6) / 1e9, 1)}
+                "hist_bits_graph_achieved_GBps": round(bits_bytes / (bits_graph_us * 1e-6) / 1e9, 1),
+                "pipeline_defaults": "every row temperature 0.8, top_k 30, top_p 0.8, penalty 10 (pipeline.h:31-35)",
+                "defaults_us_per_call": round(def_us, 3), "defaults_graph_us_per_call": round(def_graph_us, 3),
+                "defaults_graph_rows_per_s": round(R / (def_graph_us * 1e-6), 1)}
     log(f"per-call: {call_us:.2f} us eager, {call_graph_us:.2f} us graph-replayed per 64-row step "
-        f"(history as a set: {bits_us:.2f} / {bits_graph_us:.2f} us)")
+        f"(history as a set: {bits_us:.2f} / {bits_graph_us:.2f} us; pipeline defaults on every row: "
+        f"{def_us:.2f} / {def_graph_us:.2f} us)")
 
     configs = {}
     configs["single_row"] = bench_single_row(torch, ctx, W, s2)
