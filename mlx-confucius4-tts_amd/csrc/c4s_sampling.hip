@@ -325,19 +325,19 @@ struct NoHit {   // no id drawn since the list was made
 };
 
 struct FastSh {
-  uint32_t hist[2048];         // histogram, then the sorted candidates (uint64)
+  uint32_t hist[2][2048];      // the two histogram passes; the first then holds the sorted head (uint64)
   uint64_t cand[kCandCap];     // candidates: key(y) | id, then their entries
   float candy[kCandCap];       // y by candidate position
-  uint64_t lst[kFastList];     // the list: entries with their id-order rank among the list
-  float ly[kFastList];
-  uint32_t lmark[kCandCap / 32], lpre[kCandCap / 32];
-  uint32_t red[kStepWaves], redm[kStepWaves];
-  uint32_t bu[4];
+  uint32_t lmark[kCandCap / 32];
+  uint32_t red[4][kStepWaves];   // one set per workgroup scan (no barrier between reuses)
+  uint32_t redm[kStepWaves];
+  uint32_t bu[8];
   LSpecCS cs;
 };
-static_assert(sizeof(FastSh) <= 3 * kHistBytes, "the list step's area lies in the histograms");
+static_assert(sizeof(FastSh) <= kStepWorkBytes, "the list step's area lies in the one pass's work area");
 
-// Exclusive scan of v over the workgroup (thread order); total in `tot`.
+// Exclusive scan of v over the workgroup (thread order); total in `tot`. One
+// barrier: each call uses its own `red`.
 __device__ __forceinline__ uint32_t fast_scan(uint32_t v, uint32_t* red, uint32_t& tot) {
   const uint32_t inc = wave_scan_u32(v);
   if (lane_id() == kWave - 1) red[wave_id()] = inc;
@@ -350,32 +350,32 @@ __device__ __forceinline__ uint32_t fast_scan(uint32_t v, uint32_t* red, uint32_
     pre += (w < wave_id()) ? x : 0u;
     tot += x;
   }
-  __syncthreads();
   return pre + inc - v;
 }
 
-// Bin of the 2048 (scanned from the top) holding the m-th largest counted key,
-// and the count above it; false when fewer than m keys were counted.
-__device__ __forceinline__ bool fast_pick(FastSh& fs, uint32_t m, uint32_t& bin, uint32_t& above) {
+// Bin of hist (2048 bins, scanned from the top) holding the m-th largest
+// counted key, and the count above it, through bu[0..1] of this pick; false
+// when fewer than m keys were counted.
+__device__ __forceinline__ bool fast_pick(const uint32_t* hist, uint32_t* red, uint32_t* bu, uint32_t m,
+                                          uint32_t& bin, uint32_t& above) {
   const int t = threadIdx.x;
   uint32_t cb[4], loc = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { cb[i] = fs.hist[2047 - 4 * t - i]; loc += cb[i]; }
+  for (int i = 0; i < 4; ++i) { cb[i] = hist[2047 - 4 * t - i]; loc += cb[i]; }
   uint32_t total;
-  const uint32_t ex = fast_scan(loc, fs.red, total);
-  if (total < m) return false;
+  const uint32_t ex = fast_scan(loc, red, total);
+  if (total < m) return false;   // uniform
   if (ex < m && ex + loc >= m) {
     uint32_t run = ex;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (run < m && run + cb[i] >= m) { fs.bu[0] = 2047 - 4 * t - i; fs.bu[1] = run; }
+      if (run < m && run + cb[i] >= m) { bu[0] = 2047 - 4 * t - i; bu[1] = run; }
       run += cb[i];
     }
   }
   __syncthreads();
-  bin = fs.bu[0];
-  above = fs.bu[1];
-  __syncthreads();
+  bin = bu[0];
+  above = bu[1];
   return true;
 }
 
@@ -393,23 +393,20 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     t1 = max(t1, ky[j]);
   }
   // L0: two 11-bit passes over the threads' top-2 keys
-  for (int i = t; i < 2048; i += kStepThreads) fs.hist[i] = 0u;
-  if (t < kCandCap / 32) fs.lmark[t] = 0u;
+  for (int i = t; i < 2 * 2048; i += kStepThreads) (&fs.hist[0][0])[i] = 0u;
   __syncthreads();
-  if (t1) atomicAdd(&fs.hist[t1 >> 21], 1u);
-  if (t2) atomicAdd(&fs.hist[t2 >> 21], 1u);
+  if (t1) atomicAdd(&fs.hist[0][t1 >> 21], 1u);
+  if (t2) atomicAdd(&fs.hist[0][t2 >> 21], 1u);
   __syncthreads();
   uint32_t L0 = 0;
   {
     uint32_t b1, ab1;
-    if (fast_pick(fs, kFastSel, b1, ab1)) {
-      for (int i = t; i < 2048; i += kStepThreads) fs.hist[i] = 0u;
-      __syncthreads();
-      if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[(t1 >> 10) & 2047u], 1u);
-      if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[(t2 >> 10) & 2047u], 1u);
+    if (fast_pick(fs.hist[0], fs.red[0], fs.bu, kFastSel, b1, ab1)) {
+      if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[1][(t1 >> 10) & 2047u], 1u);
+      if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[1][(t2 >> 10) & 2047u], 1u);
       __syncthreads();
       uint32_t b2, ab2;
-      fast_pick(fs, kFastSel - ab1, b2, ab2);
+      fast_pick(fs.hist[1], fs.red[1], fs.bu + 2, kFastSel - ab1, b2, ab2);
       L0 = (b1 << 21) | (b2 << 10);
     }
   }
@@ -427,7 +424,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     if (lane == 0) fs.redm[wv] = bm;
   }
   uint32_t C;
-  uint32_t pos = fast_scan(cnt, fs.red, C);   // its barriers also publish redm
+  uint32_t pos = fast_scan(cnt, fs.red[2], C);   // its barrier also publishes redm
   uint32_t tout = 0;
 #pragma unroll
   for (int w = 0; w < kStepWaves; ++w) tout = max(tout, fs.redm[w]);
@@ -448,9 +445,10 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   if (t < C8 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
   __syncthreads();
   C4S_PHASE(12);
-  // sort by rank counting (entries are distinct: their ids are)
-  uint64_t* srt = reinterpret_cast<uint64_t*>(fs.hist);
-  static_assert(sizeof(FastSh::hist) >= (kFastList + 1) * sizeof(uint64_t), "the sorted head fits");
+  // sort by rank counting (entries are distinct: their ids are); the first
+  // kFastList + 1 places are kept
+  uint64_t* srt = reinterpret_cast<uint64_t*>(fs.hist[0]);
+  static_assert(sizeof(FastSh::hist[0]) >= (kFastList + 1) * sizeof(uint64_t), "the sorted head fits");
   for (int base = 0; base < (int)C; base += kStepThreads) {
     const int i = base + t;
     const uint64_t mine = (i < (int)C) ? fs.cand[i] : ~0ull;
@@ -463,60 +461,55 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
 #pragma unroll
         for (int q = 0; q < 8; ++q) r += (o[q] > mine) ? 1u : 0u;
       }
-    if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;   // the list and the entry after it
+    if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;
   }
   __syncthreads();
   C4S_PHASE(13);
-  // the list: the leading entries above the bound, at most kFastList
-  const int nl = min((int)C, kFastList + 1);
-  uint32_t nab = 0;
-  for (int i = t; i < nl; i += kStepThreads) nab += (ent_key(srt[i]) > tout) ? 1u : 0u;
-  uint32_t n_all;
-  (void)fast_scan(nab, fs.red, n_all);
-  const int nlist = min((int)n_all, kFastList);
-  if ((int)n_all > kFastList) tout = max(tout, ent_key(srt[kFastList]));
-  // the draw starts its maximum at -1e30 (text2semantic.cpp:150): below it the one-pass step decides
-  if (nlist == 0 || !(kfloat(ent_key(srt[0])) >= -1e30f)) return false;
-  // id-order rank among the list: candidates sit in id order, so it counts
-  // the list's candidate positions below the entry's own
-  for (int i = t; i < nlist; i += kStepThreads) {
-    const int ci = ent_rank(srt[i]);
-    atomicOr(&fs.lmark[ci >> 5], 1u << (ci & 31));
-  }
-  __syncthreads();
   if (wv == 0) {
-    const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(fs.lmark[lane]) : 0u;
-    const uint32_t inc = wave_scan_u32(pc);
-    if (lane < kCandCap / 32) fs.lpre[lane] = inc - pc;
-  }
-  __syncthreads();
-  if (t < nlist) {
-    const uint64_t e = srt[t];
-    const int ci = ent_rank(e);
-    fs.lst[t] = (e & ~1023ull) | (fs.lpre[ci >> 5] + (uint32_t)__popc(fs.lmark[ci >> 5] & ((1u << (ci & 31)) - 1u)));
-    fs.ly[t] = fs.candy[ci];
-  }
-  __syncthreads();
-  C4S_PHASE(14);
-  if (wv == 0) {
-    SumHdr h{};
-    h.n = nlist;
-    h.tout = tout;
-    h.flags = 0u;
-    const bool a0 = lane < nlist, a1 = lane + kWave < nlist;
-    const uint64_t e0 = a0 ? fs.lst[lane] : 0ull, e1 = a1 ? fs.lst[lane + kWave] : 0ull;
-    const float y0 = a0 ? fs.ly[lane] : 0.0f, y1 = a1 ? fs.ly[lane + kWave] : 0.0f;
-    uint64_t r = io.rng ? *io.rng : 0ull;
-    StepOut o{0, 0u, 0u, 0u, 0u};
-    const bool ok = list_step(h, e0, e1, y0, y1, c, V, NoHit{}, r, fs.cs, o);
-    if (lane == 0) {
-      fs.bu[2] = ok ? 1u : 0u;
-      if (ok) step_out(io, V, o.tok, r, true, 1u | 2u | 4u | 16u | 32u, 0u, o.dex, o.kept);
+    // the list: the leading entries above the bound (a prefix), at most kFastList
+    const int nl = min((int)C, kFastList + 1);
+    const bool a0 = lane < nl, a1 = lane + kWave < nl;
+    uint64_t e0 = srt[a0 ? lane : 0], e1 = srt[a1 ? lane + kWave : 0];
+    const uint64_t e2 = srt[nl > 2 * kWave ? 2 * kWave : 0];
+    const int n_all = __popcll(__ballot(a0 && ent_key(e0) > tout)) + __popcll(__ballot(a1 && ent_key(e1) > tout)) +
+                      ((nl > 2 * kWave && ent_key(e2) > tout) ? 1 : 0);
+    const int nlist = min(n_all, kFastList);
+    if (n_all > kFastList) tout = max(tout, ent_key(e2));
+    const float ztop = kfloat(ent_key(srt[0]));   // C >= 1
+    // the draw starts its maximum at -1e30 (text2semantic.cpp:150): below it the one pass decides
+    bool ok = nlist > 0 && ztop >= -1e30f;
+    if (ok) {
+      // id-order rank among the list: candidates sit in id order, so it counts
+      // the list's candidate positions below the entry's own
+      const bool v0 = lane < nlist, v1 = lane + kWave < nlist;
+      const int c0 = ent_rank(e0), c1 = ent_rank(e1);
+      if (lane < kCandCap / 32) fs.lmark[lane] = 0u;
+      wave_sync();
+      if (v0) atomicOr(&fs.lmark[c0 >> 5], 1u << (c0 & 31));
+      if (v1) atomicOr(&fs.lmark[c1 >> 5], 1u << (c1 & 31));
+      wave_sync();
+      const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(fs.lmark[lane]) : 0u;
+      const uint32_t pre = wave_scan_u32(pc) - pc;   // lane w: marks before word w
+      const uint32_t p0 = (uint32_t)__builtin_amdgcn_ds_bpermute((c0 >> 5) << 2, (int)pre);
+      const uint32_t p1 = (uint32_t)__builtin_amdgcn_ds_bpermute((c1 >> 5) << 2, (int)pre);
+      const uint32_t m0 = fs.lmark[c0 >> 5], m1 = fs.lmark[c1 >> 5];
+      const float y0 = fs.candy[c0], y1 = fs.candy[c1];
+      e0 = v0 ? (e0 & ~1023ull) | (p0 + (uint32_t)__popc(m0 & ((1u << (c0 & 31)) - 1u))) : 0ull;
+      e1 = v1 ? (e1 & ~1023ull) | (p1 + (uint32_t)__popc(m1 & ((1u << (c1 & 31)) - 1u))) : 0ull;
+      SumHdr h{};
+      h.n = nlist;
+      h.tout = tout;
+      h.flags = 0u;
+      uint64_t r = io.rng ? *io.rng : 0ull;
+      StepOut o{0, 0u, 0u, 0u, 0u};
+      ok = list_step(h, e0, e1, v0 ? y0 : 0.0f, v1 ? y1 : 0.0f, c, V, NoHit{}, r, fs.cs, o);
+      if (ok && lane == 0) step_out(io, V, o.tok, r, true, 1u | 2u | 4u | 16u | 32u, 0u, o.dex, o.kept);
     }
+    if (lane == 0) fs.bu[4] = ok ? 1u : 0u;
   }
   __syncthreads();
   C4S_PHASE(15);
-  return fs.bu[2] != 0u;
+  return fs.bu[4] != 0u;
 }
 
 // One AR step of the reference chain (C4S_MODE_CHAIN) for one row per
