@@ -207,9 +207,10 @@ __device__ void bitonic_desc_u64(uint64_t* v, int P) {
 }
 
 
-// One workgroup scans steps [s0, s1) of one row. Thread t holds the float4
-// quads t + 256 j of the 16-byte aligned body and one head or tail id.
-template <int NQ>
+// One workgroup scans steps [s0, s1) of one row (ONE: exactly one step, so
+// that nothing is hoisted out of a loop that runs once). Thread t holds the
+// float4 quads t + 256 j of the 16-byte aligned body and one head or tail id.
+template <int NQ, bool ONE>
 __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w) {
   __shared__ ScanSh sh;
   const int row = blockIdx.y;
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
   const int mode = stream_mode(c, V);
   if (mode == kModeExact) return;
   const int s0 = w.s_begin + (int)blockIdx.x * w.steps_per_group;
-  const int s1 = min(w.s_end, s0 + w.steps_per_group);
+  const int s1 = ONE ? s0 + 1 : min(w.s_end, s0 + w.steps_per_group);
   if (s0 >= s1) return;
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
   const int cap = list_cap(c);
@@ -502,19 +503,14 @@ __global__ __launch_bounds__(NTA, 3) void k_stream_scan(StreamArgs a, StreamWs w
       // margins of a few ulp, and the masses carry no error term (err = 0).
       m0 = kfloat(ent_key(srt[0]));
       nchunk = max(1, (rs.nq + 15) >> 4);
-      // the quads' H0 bits first, all reads at once (quad index clamped into the row)
-      uint32_t hq[NQ];
-#pragma unroll
-      for (int j = 0; j < NQ; ++j) {
-        const int id = rs.head + 4 * max(0, min(t + NTA * j, rs.nq - 1));
-        hq[j] = (uint32_t)(((uint64_t)sh.bm[id >> 5] | ((uint64_t)sh.bm[(id >> 5) + 1] << 32)) >> (id & 31)) & 15u;
-      }
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
         const int q = t + NTA * j;
         double qd = 0.0;
         if (q < rs.nq) {
-          const uint32_t hb = hq[j];
+          const int qid = rs.head + 4 * q;   // the quad's H0 bits
+          const uint32_t hb =
+              (uint32_t)(((uint64_t)sh.bm[qid >> 5] | ((uint64_t)sh.bm[(qid >> 5) + 1] << 32)) >> (qid & 31)) & 15u;
           const bool pon = c.pen_on;
           const float x0 = kfloat(kq[j][0]), x1 = kfloat(kq[j][1]), x2 = kfloat(kq[j][2]), x3 = kfloat(kq[j][3]);
           qd = mass_exact((pon && (hb & 1u)) ? pen_exact(x0, pen) : x0, c, m0) +
@@ -3509,12 +3505,17 @@ hipError_t launch_stream_scan(const StreamArgs& a, const StreamWs& w, hipStream_
   const int steps = w.s_end - w.s_begin;
   const dim3 grid((unsigned)((steps + w.steps_per_group - 1) / w.steps_per_group), (unsigned)a.n_rows);
   const int nq_max = a.vocab >> 2;
-  if (nq_max <= 2 * NTA)
-    hipLaunchKernelGGL(k_stream_scan<2>, grid, dim3(NTA), 0, s, a, w);
-  else if (nq_max <= 8 * NTA)
-    hipLaunchKernelGGL(k_stream_scan<8>, grid, dim3(NTA), 0, s, a, w);
-  else
-    hipLaunchKernelGGL(k_stream_scan<12>, grid, dim3(NTA), 0, s, a, w);
+  const bool one = w.steps_per_group == 1;
+  if (nq_max <= 2 * NTA) {
+    if (one) hipLaunchKernelGGL((k_stream_scan<2, true>), grid, dim3(NTA), 0, s, a, w);
+    else hipLaunchKernelGGL((k_stream_scan<2, false>), grid, dim3(NTA), 0, s, a, w);
+  } else if (nq_max <= 8 * NTA) {
+    if (one) hipLaunchKernelGGL((k_stream_scan<8, true>), grid, dim3(NTA), 0, s, a, w);
+    else hipLaunchKernelGGL((k_stream_scan<8, false>), grid, dim3(NTA), 0, s, a, w);
+  } else {
+    if (one) hipLaunchKernelGGL((k_stream_scan<12, true>), grid, dim3(NTA), 0, s, a, w);
+    else hipLaunchKernelGGL((k_stream_scan<12, false>), grid, dim3(NTA), 0, s, a, w);
+  }
   return hipGetLastError();
 }
 
