@@ -2619,6 +2619,40 @@ __device__ __forceinline__ void vstore(T* p, T v) {
   typedef volatile __attribute__((address_space(3))) T LT;
   *(LT*)(__attribute__((address_space(3))) T*)p = v;
 }
+// One LDS word or-ed in place (ds_or_b32: no read back).
+__device__ __forceinline__ void lds_or(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_or((__attribute__((address_space(3))) uint32_t*)p, v, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// The fields of a record the check reads, read after its tag (see the checking wave).
+struct RecView {
+  int tag, nF, tok, F, ok, fresh, kind;
+  float zlim, ma, mb, mrel;
+  double g1, g2, w, u, ome;
+  uint32_t dex, kept;
+};
+__device__ __forceinline__ RecView rec_view(const SpecRec& rc) {
+  RecView v;
+  v.tag = vload(&rc.tag);
+  v.nF = vload(&rc.nF);
+  v.tok = vload(&rc.tok);
+  v.F = vload(&rc.F);
+  v.ok = vload(&rc.ok);
+  v.fresh = vload(&rc.fresh);
+  v.kind = vload(&rc.kind);
+  v.zlim = vload(&rc.zlim);
+  v.ma = vload(&rc.ma);
+  v.mb = vload(&rc.mb);
+  v.mrel = vload(&rc.mrel);
+  v.g1 = vload(&rc.g1);
+  v.g2 = vload(&rc.g2);
+  v.w = vload(&rc.w);
+  v.u = vload(&rc.u);
+  v.ome = vload(&rc.ome);
+  v.dex = vload(&rc.dex);
+  v.kept = vload(&rc.kept);
+  return v;
+}
 __device__ __forceinline__ void lgkm_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Waits until at most n of this wave's vector memory operations are in flight.
@@ -2762,32 +2796,46 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       C4S_SPEC_T(0);
       const int k = (q - s_first) % kSpecND;
       SpecRec& rc = recs[k];
-      int spins = 0;
-      while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
-      if (spins > kSpinMax) {
-        bad = true;
-        break;
+      // The tag, then the fields of the check, in one batch of LDS reads kept
+      // in order (volatile): the decider stores the fields before the tag, so
+      // when the tag read gives q the reads behind it see the decision.
+      RecView rv = rec_view(rc);
+      if (rv.tag != q) {
+        int spins = 0;
+        while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
+        if (spins > kSpinMax) {
+          bad = true;
+          break;
+        }
+        rv = rec_view(rc);
       }
+      int spins = 0;
       C4S_SPEC_T(1);
       C4S_SPEC_EV(q, 2);
-      const int nFd = rc.nF, rtok = rc.tok, Fd = rc.F, rok = rc.ok, rfresh = rc.fresh, kind = rc.kind;
-      const float zlim = rc.zlim;
-      const MassCoef mk{rc.ma, rc.mb, rc.mrel};
+      const int nFd = rv.nF, rtok = rv.tok, Fd = rv.F, rok = rv.ok, rfresh = rv.fresh, kind = rv.kind;
+      const float zlim = rv.zlim;
+      const MassCoef mk{rv.ma, rv.mb, rv.mrel};
       // The ids drawn since the decision (steps [Fd, q)) are in the history
       // lanes; their values at step q are in the ring rows of their steps.
       const bool isnew = lane < kHist && hfresh && hstep >= Fd && hstep < q;
       const uint64_t nm = __ballot(isnew);
       const int nn = __popcll(nm);
       const int rslot = hstep & (kRing - 1);
+      const int ridx = rslot * kWave + ((q - hstep - 1) & (kWave - 1));
+      // the ring row's tag, then its value, read together (valid when the tag is hstep)
+      int rtag = vload(&ctl.ringtag[rslot]);
+      float x = vload(&ring[ridx]);
       spins = 0;
-      while (__ballot(isnew && vload(&ctl.ringtag[rslot]) != hstep) && ++spins <= kSpinMax)
+      while (__ballot(isnew && rtag != hstep) && ++spins <= kSpinMax) {
         __builtin_amdgcn_s_sleep(1);
+        rtag = vload(&ctl.ringtag[rslot]);
+        x = vload(&ring[ridx]);
+      }
       if (spins > kSpinMax) {
         bad = true;
         break;
       }
       C4S_SPEC_T(2);
-      const float x = ring[rslot * kWave + ((q - hstep - 1) & (kWave - 1))];
       const float z = c.temp_on ? x / c.temp : x;
       float e0, e1;
       const float m1 = mass_approx(x, mk, e0);
@@ -2807,17 +2855,17 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       if (accept && nn > 0) {
         const double Y = EL + fabs(DL) * 0x1p-50;
         if (kind == 1) {
-          accept = !__ballot(isnew && !(z < zlim)) && rc.w * (DL + Y) < rc.g1 && rc.w * (DL - Y) > rc.g2;
+          accept = !__ballot(isnew && !(z < zlim)) && rv.w * (DL + Y) < rv.g1 && rv.w * (DL - Y) > rv.g2;
         } else if (kind == 2) {
           accept = !__ballot(isnew && (!(z < zlim) || htok == rtok)) &&
-                   rc.w * (rc.u * DL - rc.ome * Da - 2.0 * Y) > rc.g1 &&
-                   rc.w * (Da - rc.ome * rc.u * DL - 2.0 * Y) > rc.g2;
+                   rv.w * (rv.u * DL - rv.ome * Da - 2.0 * Y) > rv.g1 &&
+                   rv.w * (Da - rv.ome * rv.u * DL - 2.0 * Y) > rv.g2;
         } else {
           accept = false;
         }
       }
       int tokq = rtok;
-      uint32_t dex = rc.dex, kept = rc.kept;
+      uint32_t dex = rv.dex, kept = rv.kept;
       bool exact = false;
       C4S_SPEC_T(3);
       if (!accept) {
@@ -2933,7 +2981,7 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
           tokl[n] = tokq;
           tstep[n] = (uint16_t)q;
           didx[tokq] = (uint16_t)n;
-          bmN[tokq >> 5] |= 1u << (tokq & 31);
+          lds_or(&bmN[tokq >> 5], 1u << (tokq & 31));
         }
         ++n;
       }
