@@ -173,6 +173,7 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
   float cp[2] = {0.f, 0.f}, dp[2] = {0.f, 0.f};   // fp32 weights: this lane's parts of c and d
   f32x4 acd[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};   // the c / d block by column block
   const int col[2] = {min(n0 + r, V - 1), min(n0 + 16 + r, V - 1)};
+  const bool live1 = n0 + 16 < V;   // the second column block holds a column (uniform)
   const int64_t woff[2] = {(int64_t)col[0] * D + 8 * g, (int64_t)col[1] * D + 8 * g};
   const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
   // staging: piece j of this thread is row (kLmThreads / kRowPieces) j + t / kRowPieces,
@@ -225,6 +226,7 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
       const int step = min(ch * kLmWaves * kWaveSteps + h * kLmWaves + w, nsteps - 1);   // past the end: unused
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
+        if (nt == 1 && !live1) continue;
         wr[i][h][nt].load(a.weight, woff[nt] + step * 32);
         if constexpr (kQ) {
           const int64_t q = (int64_t)col[nt] * (nsteps / SPU) + step / SPU;
@@ -266,6 +268,7 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
             uint4 bh[2], bl[2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
+              if (nt == 1 && !live1) continue;
               float wv[8], wg[8];
               wr[i][h][nt].get(wv);
               float c1 = 0.f, d1 = 0.f;
@@ -307,7 +310,8 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
                 }
               } else {
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) acd[nt] = mfma_bf16(cdf, wr[i][h][nt].bf16(), acd[nt]);
+                for (int nt = 0; nt < 2; ++nt)
+                  if (nt == 0 || live1) acd[nt] = mfma_bf16(cdf, wr[i][h][nt].bf16(), acd[nt]);
               }
             }
             const unsigned char* xb = &xs[(ch & 1) * kXBytes + kc * 2];
@@ -330,6 +334,7 @@ __global__ __launch_bounds__(kLmThreads) __attribute__((amdgpu_waves_per_eu(2)))
               } else {
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
+                  if (nt == 1 && !live1) continue;
                   acc[mt][nt] = mfma_bf16(xa, bh[nt], acc[mt][nt]);
                   acc[mt][nt] = mfma_bf16(xa, bl[nt], acc[mt][nt]);
                 }

@@ -40,7 +40,11 @@ CASES = [("bf16", 64, 1280, 8194, 64, 0.0), ("bf16", 5, 64, 100, 64, 0.0), ("bf1
          ("bf16", 3, 2080, 300, 64, 0.0), ("bf16", 9, 4096, 130, 64, 0.0), ("bf16", 16, 1280, 1000, 64, 4.0),
          ("f32", 64, 1280, 8194, 64, 0.0), ("f32", 70, 96, 517, 64, 0.0), ("f32", 16, 1280, 1000, 64, 4.0),
          ("q8", 64, 1280, 8194, 64, 0.0), ("q8", 5, 64, 100, 32, 0.0), ("q8", 70, 256, 1000, 128, 0.0),
-         ("q8", 33, 1280, 777, 32, 4.0)]
+         ("q8", 33, 1280, 777, 32, 4.0),
+         # column tiles of 64 with the last one wider: 2 and 4 blocks past the fourth, and V below one tile;
+         # fp32 weights over two staged K blocks
+         ("bf16", 7, 128, 90, 64, 0.0), ("f32", 5, 96, 127, 64, 0.0), ("q8", 9, 256, 37, 32, 0.0),
+         ("f32", 3, 2080, 300, 64, 0.0)]
 
 
 @pytest.mark.parametrize("kind,M,D,V,group,shift", CASES)
