@@ -85,18 +85,17 @@ struct RowCfg {
   int min_keep;
 };
 
-__device__ __forceinline__ RowCfg make_cfg(const uint32_t mode, int V, int row, const float* temp,
-                           const int32_t* top_k, const float* top_p, const float* pen,
-                           const int32_t* min_keep, const uint8_t* do_sample) {
+// The processor configuration from one row's parameter values.
+__device__ __forceinline__ RowCfg make_cfg_vals(const uint32_t mode, int V, float pen, float temp, int32_t k, float p,
+                                                int32_t min_keep, bool sample) {
   RowCfg c;
   c.V = V;
-  c.pen = pen ? pen[row] : 1.0f;
-  c.temp = temp ? temp[row] : 1.0f;
-  c.k = top_k ? top_k[row] : 0;
-  c.p = top_p ? top_p[row] : 1.0f;
-  c.min_keep = min_keep ? min_keep[row] : 1;
+  c.pen = pen;
+  c.temp = temp;
+  c.k = k;
+  c.p = p;
+  c.min_keep = min_keep;
   if (!(mode & kCustom)) {
-    const bool sample = do_sample ? (do_sample[row] != 0) : true;
     c.pen_on = c.pen != 1.0f;                      // sampling.cpp:21
     c.greedy = !sample;                            // text2semantic.cpp:144-145
     c.draw = sample;
@@ -112,6 +111,14 @@ __device__ __forceinline__ RowCfg make_cfg(const uint32_t mode, int V, int row, 
     c.topp_on = !c.greedy && (mode & kTopP);
   }
   return c;
+}
+
+__device__ __forceinline__ RowCfg make_cfg(const uint32_t mode, int V, int row, const float* temp,
+                           const int32_t* top_k, const float* top_p, const float* pen,
+                           const int32_t* min_keep, const uint8_t* do_sample) {
+  return make_cfg_vals(mode, V, pen ? pen[row] : 1.0f, temp ? temp[row] : 1.0f, top_k ? top_k[row] : 0,
+                       top_p ? top_p[row] : 1.0f, min_keep ? min_keep[row] : 1,
+                       (mode & kCustom) || (do_sample ? (do_sample[row] != 0) : true));
 }
 
 // ---- element sources ---------------------------------------------------------

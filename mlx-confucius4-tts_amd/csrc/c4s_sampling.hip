@@ -515,6 +515,17 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
 // One AR step of the reference chain (C4S_MODE_CHAIN) for one row per
 // workgroup, in one pass where it can (c4s_step.hpp), else the multi-pass
 // chain on the row staged in LDS. PT >= the ids a thread owns.
+// Byte i of a per-row flag array, nonzero or not, read through the aligned
+// dword that holds it: a scalar load (the flags are the same for the whole
+// workgroup), where a byte load would go through the vector memory path and be
+// waited for at once. The dword never leaves the allocation's 256-byte granule.
+__device__ __forceinline__ bool flag_byte(const uint8_t* __restrict__ p, int i) {
+  const uint8_t* b = p + i;
+  const int sh = (int)(reinterpret_cast<uintptr_t>(b) & 3);
+  const uint32_t wd = *reinterpret_cast<const uint32_t*>(b - sh);
+  return ((wd >> (8 * sh)) & 0xFFu) != 0u;
+}
+
 template <int PT>
 __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -523,11 +534,31 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   const int row = blockIdx.x;
   const int V = a.vocab;
   const int t = threadIdx.x, lane = lane_id(), w = wave_id();
-  if (a.row_active && !a.row_active[row]) {
+  // Every read that depends on no other goes out first: the row's flags and
+  // parameters, its history offsets, then the row itself (fp32 rows into
+  // registers here, stored to LDS below); nothing waits on them before the
+  // row's loads are in flight, so the step pays one memory round trip up front
+  // instead of one per dependent read.
+  const int64_t roff = (int64_t)row * a.ld;
+  const float* xf_row = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
+  StepFetch f;
+  if (xf_row) step_fetch(xf_row, V, f);
+  const bool act = a.row_active ? flag_byte(a.row_active, row) : true;
+  const bool sample = a.do_sample ? flag_byte(a.do_sample, row) : true;
+  const float pv = a.pen ? a.pen[row] : 1.0f, tv = a.temp ? a.temp[row] : 1.0f;
+  const int32_t kv = a.top_k ? a.top_k[row] : 0, mv = a.min_keep ? a.min_keep[row] : 1;
+  const float ppv = a.top_p ? a.top_p[row] : 1.0f;
+  const bool csr_arg = a.hist_off && !a.hist_bits;
+  int64_t h0 = 0, h1 = 0;
+  if (csr_arg) {
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
+  }
+  if (!act) {
     if (t == 0) a.out_tok[row] = -1;
     return;
   }
-  const RowCfg c = make_cfg(0u, V, row, a.temp, a.top_k, a.top_p, a.pen, a.min_keep, a.do_sample);
+  const RowCfg c = make_cfg_vals(0u, V, pv, tv, kv, ppv, mv, sample);
   C4S_PHASE(0);
   unsigned char* work = smem;
   float* vbuf = reinterpret_cast<float*>(smem + step_work_bytes(V));
@@ -538,10 +569,9 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   uint64_t* list = sbuf + 2 * kSortCap;
   const int P = odd_chunk<kStepThreads>(V);
   const int lo = min(V, t * P), n = min(V, lo + P) - lo;
-  const int64_t roff = (int64_t)row * a.ld;
   const bool csr = c.pen_on && !a.hist_bits;
   StepIO io;
-  io.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;
+  io.xf = xf_row;
   io.xb = a.dtype == 1 ? static_cast<const uint16_t*>(a.logits) + roff : nullptr;
   io.bitmap = csr ? bitmap : nullptr;
   io.hbits = (c.pen_on && a.hist_bits) ? a.hist_bits + (int64_t)row * hist_words(V) : nullptr;
@@ -553,17 +583,10 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   io.stop_token = a.stop_token;
   const float ninf = neg_inf();
 
-  // history offsets first (the ids depend on them), then the row into LDS
-  // with coalesced 16-byte loads, then the first history ids
-  int64_t h0 = 0, h1 = 0;
-  if (csr) {
-    h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
-  }
+  // the row into LDS (fp32: its loads went out above), then the first history ids
+  if (!csr) h0 = h1 = 0;
   float* val;
   if (io.xf) {
-    StepFetch f;
-    step_fetch(io.xf, V, f);
     val = step_store(io.xf, V, f, vbuf);
   } else {
     val = stage_row_bf16(io.xb, V, vbuf);
