@@ -583,23 +583,30 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   io.stop_token = a.stop_token;
   const float ninf = neg_inf();
 
-  // the row into LDS (fp32: its loads went out above), then the first history ids
+  // The history's first two ids of this thread (or this thread's words of the
+  // history set) go out behind the row's loads, before anything waits for the
+  // row: storing the row to LDS waits for the row alone.
   if (!csr) h0 = h1 = 0;
+  const int hid = (csr && h0 + t < h1) ? a.hist_ids[h0 + t] : -1;
+  const int hid2 = (csr && h0 + t + kStepThreads < h1) ? a.hist_ids[h0 + t + kStepThreads] : -1;
+  // penalty bits of this thread's ids: words lo/32 .. lo/32 + 2 (up to 65 ids
+  // from bit lo % 32 span at most three words)
+  static_assert(PT <= 65, "a thread's ids span at most three bitmap words");
+  uint32_t pw[3] = {0u, 0u, 0u};
+  if (io.hbits) {
+    // every load unconditional (index clamped), so nothing waits for them here:
+    // the penalty below keeps only the bits of ids lo .. lo + n - 1, and a
+    // clamped word past the set would stand for ids at or above V
+    const int w0 = lo >> 5, hwn = hist_words(V);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) pw[q] = io.hbits[min(w0 + q, hwn - 1)];
+  }
+  // the row into LDS (fp32: its loads went out above)
   float* val;
   if (io.xf) {
     val = step_store(io.xf, V, f, vbuf);
   } else {
     val = stage_row_bf16(io.xb, V, vbuf);
-  }
-  const int hid = (csr && h0 + t < h1) ? a.hist_ids[h0 + t] : -1;
-  // penalty bits of this thread's ids: words lo/32 .. lo/32 + 2 (up to 65 ids
-  // from bit lo % 32 span at most three words)
-  static_assert(PT <= 65, "a thread's ids span at most three bitmap words");
-  uint32_t pw[3] = {0u, 0u, 0u};
-  if (io.hbits && n > 0) {
-    const int w0 = lo >> 5, hwn = hist_words(V);
-#pragma unroll
-    for (int q = 0; q < 3; ++q) pw[q] = (w0 + q < hwn) ? io.hbits[w0 + q] : 0u;
   }
   // LDS: the history bitmap and the histograms start at zero
   const int nw = bitmap_words(V);
@@ -610,7 +617,8 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   __syncthreads();
   if (csr) {
     if (hid >= 0 && hid < V) atomicOr(&bitmap[hid >> 5], 1u << (hid & 31));   // sampling.cpp:24
-    for (int64_t j = h0 + t + kStepThreads; j < h1; j += kStepThreads) {
+    if (hid2 >= 0 && hid2 < V) atomicOr(&bitmap[hid2 >> 5], 1u << (hid2 & 31));
+    for (int64_t j = h0 + t + 2 * kStepThreads; j < h1; j += kStepThreads) {
       const int id = a.hist_ids[j];
       if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
     }
