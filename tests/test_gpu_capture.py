@@ -1,6 +1,8 @@
 """Graph capture: c4s_sample_rows (no workspace at vocab <= 12288) captured
 into a HIP graph gives, on every replay, the tokens and RNG states of the same
-call made eagerly; c4s_sample_stream refuses capture with C4S_EINVAL."""
+call made eagerly; a call whose workspace would grow is refused under capture
+and captures once an eager call has sized it; c4s_sample_stream refuses
+capture with C4S_EINVAL."""
 import numpy as np
 import pytest
 
@@ -70,3 +72,54 @@ def test_sample_stream_refuses_capture(gpu_ctx):
         except c4s.C4SError as e:
             err = str(e)
     assert err is not None and "code 1" in err and "captured" in err
+
+
+def test_large_vocab_workspace_is_sized_outside_capture():
+    """A vocabulary above 12288 needs the context's key workspace: the first
+    such call under capture is refused (no allocation inside a capture) and
+    queues nothing; once an eager call of that shape has sized the workspace,
+    the same call captures, and its replays give the eager call's tokens."""
+    import torch
+    ctx = c4s.Context(0)   # a fresh context: no workspace yet
+    try:
+        b = W.batch64(seed=91, rows=4, V=20000)
+        a = _args(torch, b)
+        s = torch.cuda.Stream()
+        tok = torch.full((4,), -5, dtype=torch.int32, device="cuda")
+        rng = dev(b.rng, torch)
+        torch.cuda.synchronize()
+
+        def call():
+            ctx.sample_rows(a["logits"], a["hist_ids"], a["hist_off"], a["temp"], a["top_k"], a["top_p"],
+                            a["pen"], rng, tok, do_sample=a["do_sample"], stream=s)
+
+        g0 = torch.cuda.CUDAGraph()
+        err = None
+        with torch.cuda.graph(g0, stream=s):
+            try:
+                call()
+            except c4s.C4SError as e:
+                err = str(e)
+        assert err is not None and "code 1" in err and "graph capture" in err
+        assert bool((tok == -5).all()), "the refused call queued work"
+        # eager: sizes the workspace and gives the reference tokens
+        with torch.cuda.stream(s):
+            call()
+        s.synchronize()
+        want_tok, want_rng = tok.cpu().numpy().copy(), rng.cpu().numpy().copy()
+        rng.copy_(dev(b.rng, torch))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            call()
+        for k in range(3):
+            rng.copy_(dev(b.rng, torch))
+            tok.fill_(-5)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            _ = (a["logits"] * 2).sum().item()   # eager work between replays
+            assert np.array_equal(tok.cpu().numpy(), want_tok), k
+            assert np.array_equal(rng.cpu().numpy(), want_rng), k
+    finally:
+        ctx.close()
