@@ -44,7 +44,9 @@ CASES = [("bf16", 64, 1280, 8194, 64, 0.0), ("bf16", 5, 64, 100, 64, 0.0), ("bf1
          # column tiles of 64 with the last one wider: 2 and 4 blocks past the fourth, and V below one tile;
          # fp32 weights over two staged K blocks
          ("bf16", 7, 128, 90, 64, 0.0), ("f32", 5, 96, 127, 64, 0.0), ("q8", 9, 256, 37, 32, 0.0),
-         ("f32", 3, 2080, 300, 64, 0.0)]
+         ("f32", 3, 2080, 300, 64, 0.0),
+         # a last partial tile of exactly 16 columns (its second block skipped) and of 17 (it is not)
+         ("bf16", 6, 96, 48, 64, 0.0), ("q8", 6, 128, 49, 32, 0.0)]
 
 
 @pytest.mark.parametrize("kind,M,D,V,group,shift", CASES)
