@@ -35,6 +35,18 @@ def test_batch64_one_step(orc, gpu_ctx, seed, masked):
     assert one_pass.mean() > 0.9
 
 
+@pytest.mark.parametrize("masked", [True, False])
+def test_long_histories(orc, gpu_ctx, masked):
+    """Histories of 1500-3000 ids (more than two per thread of the step's 512):
+    every id past the first 1024 of a row joins the penalty set in the
+    step's loop after the first two per thread."""
+    p = W.batch64_params(seed=61, rows=16, h_lo=1500, h_hi=3000)
+    b = W.Batch(logits=W.batch64_logits(1061, 1, 16)[0], **p)
+    assert int(np.diff(b.hist_off).min()) > 1024
+    print(f"long histories masked={masked}", flush=True)
+    compare_with_oracle(orc, gpu_ctx, b, masked=masked)
+
+
 def test_batch64_general_rows(orc, gpu_ctx):
     """top_k = 0 rows (full-vocabulary nucleus) with assorted p and temperatures."""
     b = W.batch64(seed=31, rows=64)
