@@ -112,10 +112,19 @@ __device__ __forceinline__ void step_out(const StepIO& io, int V, int tok, uint6
 // thread recomputes its kept masses in double and the workgroup scans them
 // again (bound rel_eps, about 1e-11 relative); only if that still does not
 // decide does one wave replay the draw sequentially (draw_replay).
+// The row's configuration and I/O as one LDS copy for the workgroup: the
+// out-of-line helpers take them by reference, and a reference to a copy in
+// registers would make the compiler keep that copy in per-lane scratch memory
+// for the whole kernel (about 120 bytes a lane written at entry).
+struct StepRowSh {
+  RowCfg cfg;
+  StepIO io;
+};
+
 template <int PT>
 __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, const KeptRule& kr, const float (&z)[PT],
                                             int lo, int n, float m, const Scan2& ds, uint32_t n_kept,
-                                            uint32_t st_path, uint32_t st_exact, StepSh& ss) {
+                                            uint32_t st_path, uint32_t st_exact, StepSh& ss, const StepRowSh& rs) {
   const int t = threadIdx.x;
   const uint64_t st2 = xorshift64(*io.rng);
   const double u = unit_from_state(st2);
@@ -176,7 +185,7 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
     return;
   }
   if (wave_id() == 0) {   // the reference's sequential sums, one wave
-    const int tk = draw_replay(io, c, kr, m, u);
+    const int tk = draw_replay(rs.io, rs.cfg, kr, m, u);
     if (lane_id() == 0) step_out(io, c.V, tk, st2, true, st_path, st_exact, 2u, n_kept);
   }
 }
@@ -192,7 +201,7 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
 // decided with the double sums, 0 the multi-pass chain decides (X holds more
 // than one value, or the margin is not met even in double).
 template <int PT>
-__device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule& sr, int nX,
+__device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule sr, int nX,
                                     double thr, double S, double errS, double Ma, double eMa, uint32_t n_above,
                                     StepSh& ss) {
   const int lane = lane_id(), w = wave_id();
@@ -531,6 +540,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ StepScratch sh;
   __shared__ StepSh ss;
+  __shared__ StepRowSh rs;
   const int row = blockIdx.x;
   const int V = a.vocab;
   const int t = threadIdx.x, lane = lane_id(), w = wave_id();
@@ -581,6 +591,10 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   io.stats = a.stats ? a.stats + 4 * (int64_t)row : nullptr;
   io.join = a.hist_bits ? a.hist_bits + (int64_t)row * hist_words(V) : nullptr;
   io.stop_token = a.stop_token;
+  if (t == 0) {   // read only after the barrier below
+    rs.cfg = c;
+    rs.io = io;
+  }
   const float ninf = neg_inf();
 
   // The history's first two ids of this thread (or this thread's words of the
@@ -746,7 +760,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         for (int j = 0; j < PT; ++j)
           if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
       C4S_PHASE(10);
-      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss);
+      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs);
       C4S_PHASE(15);
       return;
     } else {
@@ -879,7 +893,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         if (nX > kSortCap) {
           // more boundary entries than one sort takes: one_pass only if they
           // all hold one value (ties), which needs no sort
-          verdict = tie_cut<PT>(c, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
+          verdict = tie_cut<PT>(rs.cfg, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
           tp_exact = verdict == 3;
           if (verdict != 1 && verdict != 3) one_pass = false;
         } else {
@@ -893,12 +907,12 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
             if (t < nX) list[t] = v;
             __syncthreads();
             C4S_PHASE(8);
-            decide_cut<true>(c, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+            decide_cut<true>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           } else if (w == 0) {
             v = lane < nX ? list[lane] : 0ull;
             v = sort_desc(v, P2, sbuf);
             C4S_PHASE(8);
-            decide_cut<false>(c, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+            decide_cut<false>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           }
           __syncthreads();
           verdict = ss.verdict;
@@ -921,8 +935,8 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
             double Se = 0.0, Mae = 0.0;
 #pragma unroll
             for (int i = 0; i < kStepWaves; ++i) { Se += ss.wc[i]; Mae += ss.wd[i]; }
-            if (block) decide_cut<true>(c, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
-            else if (w == 0) decide_cut<false>(c, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            if (block) decide_cut<true>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            else if (w == 0) decide_cut<false>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
             __syncthreads();
             verdict = ss.verdict;
           }
@@ -957,14 +971,14 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
     C4S_PHASE(10);
     if ((ds.utot >> 16) == 0u) {
       draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
-                      tp_exact ? 1u : 0u, ss);
+                      tp_exact ? 1u : 0u, ss, rs);
       C4S_PHASE(15);
       return;
     }
   }
   // ---- the multi-pass chain on the row staged in LDS (c4s_chain.hpp) ----
   __syncthreads();   // every thread is done with the work area
-  chain_fallback(io, c, work, val, sh);
+  chain_fallback(rs.io, rs.cfg, work, val, sh);
 }
 
 // ---- large vocabularies: top_k in two passes -----------------------------------------

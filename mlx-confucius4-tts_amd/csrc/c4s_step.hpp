@@ -338,7 +338,7 @@ __device__ __forceinline__ float kept_mass32(const KeptRule& kr, float z, float 
 // first id whose prefix reaches r = u * sum taken when both ends of its
 // interval are farther than rel_eps from r; otherwise the reference's
 // sequential sums in id order.
-__device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const KeptRule& kr, float m, double u) {
+__device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const KeptRule kr, float m, double u) {
   const int lane = lane_id();
   const int V = c.V;
   auto mass_at = [&](int i) -> double {
