@@ -521,6 +521,329 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   return fs.bu[4] != 0u;
 }
 
+// The one pass of a sampled row, specialised by the row's kind (top_k on; top_p
+// with p < 1; p >= 1, a dense draw) so that the per-value loops carry no tests
+// of the kind. Returns true when the row is finished; false leaves the row to
+// the multi-pass chain (nothing written but the work area).
+constexpr int kKindTopK = 0, kKindTopP = 1, kKindDense = 2;
+
+template <int PT, int kKind>
+__device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, const float (&y)[PT], int lo, int n,
+                                             float* val, uint32_t* hc, unsigned long long* hm, uint64_t* sbuf,
+                                             uint64_t* list, StepSh& ss, const StepRowSh& rs) {
+  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  const float ninf = neg_inf();
+  // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----
+  float z[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? y[j] / c.temp : y[j];
+  {
+    float lm = ninf;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) lm = fmaxf(lm, z[j]);
+    lm = wave_max_dpp(lm);
+    if (lane == 0) ss.wmax[w] = lm;
+  }
+  C4S_PHASE(2);
+  __syncthreads();
+  C4S_PHASE(3);
+  float m = ninf;
+#pragma unroll
+  for (int i = 0; i < kStepWaves; ++i) m = fmaxf(m, ss.wmax[i]);
+  const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 removes while cum <= 1 - p
+  constexpr bool topk = kKind == kKindTopK;
+  constexpr bool dense = kKind == kKindDense;
+  // The draw's maximum starts from -1e30f (text2semantic.cpp:150): below it, or
+  // for an all -inf row, or with p <= 0, the multi-pass chain decides.
+  bool one_pass = !(m < -1e30f) && thr < 1.0;
+  int verdict = 0;
+  bool tp_exact = false;
+  if (one_pass) {
+    // fp32 masses; the dense rows' kept set; the histogram (counts for top_k,
+    // masses for top_p). Sums per thread in fp32: bound (2^-20 + PT 2^-24)
+    // relative (terms and summation) + 2^-125 a term (underflow).
+    // Every value goes through the same instructions (no branch a value): z is
+    // -inf past the thread's ids, and an entry of the unbounded last bucket
+    // adds zero to it.
+    float s32 = 0.0f;
+    uint32_t flags = 0, kc = 0, nf = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      const bool fin = z[j] != ninf;
+      const float tt = z[j] - m;
+      nf += fin ? 1u : 0u;
+      if (topk) {
+        const int b = bucket_of(z[j], m);   // the last bucket for -inf
+        atomicAdd(&hc[w * kNB + b], b < kNB - 1 ? 1u : 0u);
+      } else {
+        float ej = fin ? mass32(tt) : 0.0f;
+        if (dense) {
+          // p == 1 removes the zero-mass positions: exp((double)tt) == 0 below
+          // about -745.13; near that, and for subnormal kept masses, the chain decides
+          const bool kp = fin && (thr < 0.0 || tt > -745.0f);
+          if (fin && ((thr == 0.0 && tt <= -745.0f && tt >= -745.25f) || (kp && tt < -690.0f))) flags = 1u;
+          ej = kp ? ej : 0.0f;
+          kc += kp ? 1u : 0u;
+        } else {
+          // 2^-32 fixed point, truncated (ej <= 1; 1 itself saturates 256 units low)
+          const int b = bucket_of(z[j], m);
+          const uint32_t q = (uint32_t)fminf(ej * 0x1p32f, 4294967040.0f);
+          atomicAdd(&hm[w * kNB + b], b < kNB - 1 ? (unsigned long long)q + kHistOne : 0ull);
+        }
+        s32 += ej;
+      }
+    }
+    const double s = (double)s32;
+    const double er = s * (0x1p-20 + PT * 0x1p-24) + (double)nf * 0x1p-125;
+    C4S_PHASE(4);
+    const Scan2 sc = block_scan2(s, er, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
+    C4S_PHASE(5);
+    const uint32_t n_pos = sc.utot & 0xFFFFu;   // dense rows: kept ids with a finite value
+    // p == 1 with min_keep above the positive-mass count keeps zero-mass values
+    // unmasked (sampling.cpp:67-68): the multi-pass chain handles that
+    if ((sc.utot >> 16) || (dense && thr == 0.0 && n_pos < (uint32_t)max(0, c.min_keep))) {
+      one_pass = false;
+    } else if (dense) {
+      // nothing to cut: the draw over the fp32 masses scanned above
+      const KeptRule kr{true, thr < 0.0, 0ull};
+      if (io.masked)
+#pragma unroll
+        for (int j = 0; j < PT; ++j)
+          if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
+      C4S_PHASE(10);
+      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs);
+      C4S_PHASE(15);
+      return true;
+    } else {
+      const double S = sc.tot, errS = sc.tot2;
+      // boundary buckets: threads 0..255 merge one bucket each over the waves,
+      // then wave 0 scans them (lane l holds buckets 4l .. 4l+3)
+      uint32_t* bcnt = reinterpret_cast<uint32_t*>(sbuf);           // sort buffers are free here
+      double* bmass = reinterpret_cast<double*>(sbuf) + kNB;
+      if (t < kNB) {
+        uint32_t cn = 0;
+        unsigned long long ms = 0ull;
+#pragma unroll
+        for (int i = 0; i < kStepWaves; ++i) {
+          const unsigned long long h = hm[i * kNB + t];
+          cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
+          ms += h & (kHistOne - 1ull);
+        }
+        bcnt[t] = cn;
+        bmass[t] = (double)ms * 0x1p-32;
+      }
+      __syncthreads();
+      const double B = S - thr * S;   // the mass the kept entries hold
+      const double Blo = B * (1.0 - 1e-3) - errS, Bhi = B * (1.0 + 1e-3) + errS;
+      if (w == 0) {
+        const Boundary bd = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, 0u, 0.0);
+        if (lane == 0) {
+          ss.bsel[0] = bd.lo;
+          ss.bsel[1] = bd.hi;
+          ss.bsel[2] = (int)bd.above;
+          ss.thru = bd.thru;
+          ss.mab = bd.mabove;
+          ss.nx = 0u;
+        }
+      }
+      __syncthreads();
+      C4S_PHASE(6);
+      const int blo = ss.bsel[0], bhi = ss.bsel[1];
+      // the sub-window of the boundary buckets (all of them unless refined)
+      int slo = 0, shi = kNB - 1, lo2 = 0;
+      float sc2 = 0.0f;
+      bool refine = false;
+      if (blo >= 0 && bhi >= 0) {
+        // More boundary entries than one sort takes (flat rows): histogram the
+        // boundary buckets again, kNB sub-buckets over them (top_k: over the
+        // k-th entry's bucket), and keep the sub-buckets where the boundary
+        // falls. Not for the unbounded last bucket.
+        const uint32_t nest = topk ? ss.thru : ss.thru - (uint32_t)ss.bsel[2];
+        refine = nest > (uint32_t)kSortCap && bhi < kNB - 1;
+        if (refine) {
+          lo2 = topk ? bhi : blo;
+          sc2 = (float)kNB / (float)(bhi + 1 - lo2);
+          for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
+          __syncthreads();
+#pragma unroll
+          for (int j = 0; j < PT; ++j) {
+            if (j < n && z[j] != ninf) {
+              const int b = bucket_of(z[j], m);
+              if (b >= lo2 && b <= bhi) {
+                const int sb = sub_bucket_of(z[j], m, lo2, sc2);
+                if (topk) atomicAdd(&hc[w * kNB + sb], 1u);
+                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(mass32(z[j] - m) * 0x1p32f) + kHistOne);
+              }
+            }
+          }
+          __syncthreads();
+          if (t < kNB) {
+            uint32_t cn = 0;
+            unsigned long long ms = 0ull;
+#pragma unroll
+            for (int i = 0; i < kStepWaves; ++i) {
+              const unsigned long long h = hm[i * kNB + t];
+              cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
+              ms += h & (kHistOne - 1ull);
+            }
+            bcnt[t] = cn;
+            bmass[t] = (double)ms * 0x1p-32;
+          }
+          __syncthreads();
+          if (w == 0) {
+            const Boundary b2 = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, (uint32_t)ss.bsel[2],
+                                              ss.mab);
+            if (lane == 0) {
+              ss.sub[0] = topk ? 0 : b2.lo;   // top_k: every entry above the k-th stays in the sort
+              ss.sub[1] = b2.hi;
+            }
+          }
+          __syncthreads();
+          slo = ss.sub[0];
+          shi = ss.sub[1];
+        }
+      }
+      if (blo < 0 || bhi < 0 || slo < 0 || shi < 0) {
+        one_pass = false;
+      } else {
+        // X: the entries to sort. top_k: every entry up to the k-th value's
+        // (sub-)bucket (the survivors then are a prefix of X). top_p: the
+        // boundary (sub-)buckets; every entry above them is kept, every entry
+        // below removed. side(): -1 above X, 0 in X, 1 below (monotone in z).
+        const int xlo = topk ? 0 : blo, xhi = bhi;
+        const SideRule sr{m, sc2, xlo, xhi, lo2, slo, shi, refine};
+        auto side = [&](float zj) { return sr.side(zj); };
+        // X's entries go to `list`, each wave taking one block of slots with
+        // one atomic (slot order is arbitrary: the sort orders them)
+        float ma32 = 0.0f;
+        uint32_t na = 0, xm = 0, cx = 0;   // entries above X; this thread's X entries
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+          const int sd = side(z[j]);
+          const bool inx = j < n && sd == 0, abv = j < n && sd < 0;
+          xm |= inx ? 1u << j : 0u;
+          cx += inx ? 1u : 0u;
+          ma32 += abv ? mass32(z[j] - m) : 0.0f;
+          na += abv ? 1u : 0u;
+        }
+        {
+          const uint32_t inc = wave_scan_u32(cx);
+          uint32_t wb = 0;
+          if (lane == kWave - 1 && inc > 0u) wb = atomicAdd(&ss.nx, inc);
+          uint32_t slot = readlane_u32(wb, kWave - 1) + inc - cx;
+#pragma unroll
+          for (int j = 0; j < PT; ++j) {
+            if ((xm >> j) & 1u) {
+              if (slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
+              ++slot;
+            }
+          }
+        }
+        double ma = (double)ma32;
+        double ema = ma * (0x1p-20 + PT * 0x1p-24) + (double)na * 0x1p-125;
+        ma = wave_sum_dpp(ma);
+        ema = wave_sum_dpp(ema);
+        na = wave_sum_u32(na);
+        if (lane == 0) { ss.wc[w] = ma; ss.wd[w] = ema; ss.wv[w] = na; }
+        __syncthreads();
+        C4S_PHASE(7);
+        const int nX = (int)ss.nx;
+        double Ma = 0.0, eMa = 0.0;
+        uint32_t n_above = 0;
+#pragma unroll
+        for (int i = 0; i < kStepWaves; ++i) { Ma += ss.wc[i]; eMa += ss.wd[i]; n_above += ss.wv[i]; }
+        if (nX > kSortCap) {
+          // more boundary entries than one sort takes: one_pass only if they
+          // all hold one value (ties), which needs no sort
+          verdict = tie_cut<PT>(rs.cfg, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
+          tp_exact = verdict == 3;
+          if (verdict != 1 && verdict != 3) one_pass = false;
+        } else {
+          int P2 = 1;
+          while (P2 < nX) P2 <<= 1;
+          const bool block = P2 > kWave;
+          uint64_t v = 0ull;
+          if (block) {
+            v = t < nX ? list[t] : 0ull;
+            v = sort_desc(v, P2, sbuf);
+            if (t < nX) list[t] = v;
+            __syncthreads();
+            C4S_PHASE(8);
+            decide_cut<true>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+          } else if (w == 0) {
+            v = lane < nX ? list[lane] : 0ull;
+            v = sort_desc(v, P2, sbuf);
+            C4S_PHASE(8);
+            decide_cut<false>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
+          }
+          __syncthreads();
+          verdict = ss.verdict;
+          if (verdict == 2) {
+            // decide again with every mass in double (S and the mass above the boundary)
+            tp_exact = true;
+            double se = 0.0, sa = 0.0;
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+              if (j < n && z[j] != ninf) {
+                const double ed = exp((double)(z[j] - m));
+                se += ed;
+                if (side(z[j]) < 0) sa += ed;
+              }
+            }
+            se = wave_sum_dpp(se);
+            sa = wave_sum_dpp(sa);
+            if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; }
+            __syncthreads();
+            double Se = 0.0, Mae = 0.0;
+#pragma unroll
+            for (int i = 0; i < kStepWaves; ++i) { Se += ss.wc[i]; Mae += ss.wd[i]; }
+            if (block) decide_cut<true>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            else if (w == 0) decide_cut<false>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
+            __syncthreads();
+            verdict = ss.verdict;
+          }
+          C4S_PHASE(9);
+          if (verdict != 1) one_pass = false;
+        }
+      }
+    }
+  }
+  if (one_pass) {
+    // the draw over the kept set: key >= the last kept key
+    const uint64_t kthr = ss.kthr;
+    const KeptRule kr{false, false, kthr};
+    float ks32 = 0.0f;
+    uint32_t kc = 0, flags = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {   // z is -inf past the thread's ids: never kept with a mass
+      bool kp;
+      const float ej = kept_mass32(kr, z[j], m, lo + j, kp);
+      const bool kf = kp && z[j] != ninf;
+      flags |= (kf && z[j] - m < -690.0f) ? 1u : 0u;   // subnormal kept masses: libm implementations may disagree
+      kc += kf ? 1u : 0u;
+      ks32 += ej;
+    }
+    if (io.masked)
+#pragma unroll
+      for (int j = 0; j < PT; ++j) {
+        bool kp;
+        kept_mass32(kr, z[j], m, lo + j, kp);
+        if (j < n) io.masked[lo + j] = kp ? z[j] : ninf;
+      }
+    const double ks = (double)ks32;
+    const double ek = ks * (0x1p-20 + PT * 0x1p-24) + (double)kc * 0x1p-125;
+    const Scan2 ds = block_scan2(ks, ek, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
+    C4S_PHASE(10);
+    if ((ds.utot >> 16) == 0u) {
+      draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
+                      tp_exact ? 1u : 0u, ss, rs);
+      C4S_PHASE(15);
+      return true;
+    }
+  }
+  return false;
+}
+
 // One AR step of the reference chain (C4S_MODE_CHAIN) for one row per
 // workgroup, in one pass where it can (c4s_step.hpp), else the multi-pass
 // chain on the row staged in LDS. PT >= the ids a thread owns.
@@ -543,7 +866,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   __shared__ StepRowSh rs;
   const int row = blockIdx.x;
   const int V = a.vocab;
-  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int t = threadIdx.x;
   // Every read that depends on no other goes out first: the row's flags and
   // parameters, its history offsets, then the row itself (fp32 rows into
   // registers here, stored to LDS below); nothing waits on them before the
@@ -687,295 +1010,11 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
     __syncthreads();
   }
 
-  // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----
-  float z[PT];
-#pragma unroll
-  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? y[j] / c.temp : y[j];
-  {
-    float lm = ninf;
-#pragma unroll
-    for (int j = 0; j < PT; ++j) lm = fmaxf(lm, z[j]);
-    lm = wave_max_dpp(lm);
-    if (lane == 0) ss.wmax[w] = lm;
-  }
-  C4S_PHASE(2);
-  __syncthreads();
-  C4S_PHASE(3);
-  float m = ninf;
-#pragma unroll
-  for (int i = 0; i < kStepWaves; ++i) m = fmaxf(m, ss.wmax[i]);
-  const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 removes while cum <= 1 - p
-  const bool topk = c.topk_on;
-  const bool dense = !topk && thr <= 0.0;
-  // The draw's maximum starts from -1e30f (text2semantic.cpp:150): below it, or
-  // for an all -inf row, or with p <= 0, the multi-pass chain decides.
-  bool one_pass = !(m < -1e30f) && thr < 1.0;
-  int verdict = 0;
-  bool tp_exact = false;
-  if (one_pass) {
-    // fp32 masses; the dense rows' kept set; the histogram (counts for top_k,
-    // masses for top_p). Sums per thread in fp32: bound (2^-20 + PT 2^-24)
-    // relative (terms and summation) + 2^-125 a term (underflow).
-    float s32 = 0.0f;
-    uint32_t flags = 0, kc = 0, nf = 0;
-#pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      if (j < n && z[j] != ninf) {
-        const float tt = z[j] - m;
-        float ej = topk ? 0.0f : mass32(tt);
-        if (dense) {
-          // p == 1 removes the zero-mass positions: exp((double)tt) == 0 below
-          // about -745.13; near that, and for subnormal kept masses, the chain decides
-          const bool kp = thr < 0.0 || tt > -745.0f;
-          if ((thr == 0.0 && tt <= -745.0f && tt >= -745.25f) || (kp && tt < -690.0f)) flags = 1u;
-          if (!kp) ej = 0.0f;
-          kc += kp ? 1u : 0u;
-        }
-        s32 += ej;
-        ++nf;
-        if (!dense) {
-          const int b = bucket_of(z[j], m);
-          if (b < kNB - 1) {
-            if (topk) atomicAdd(&hc[w * kNB + b], 1u);
-            else atomicAdd(&hm[w * kNB + b], (unsigned long long)(ej * 0x1p32f) + kHistOne);
-          }
-        }
-      }
-    }
-    const double s = (double)s32;
-    const double er = s * (0x1p-20 + PT * 0x1p-24) + (double)nf * 0x1p-125;
-    C4S_PHASE(4);
-    const Scan2 sc = block_scan2(s, er, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
-    C4S_PHASE(5);
-    const uint32_t n_pos = sc.utot & 0xFFFFu;   // dense rows: kept ids with a finite value
-    // p == 1 with min_keep above the positive-mass count keeps zero-mass values
-    // unmasked (sampling.cpp:67-68): the multi-pass chain handles that
-    if ((sc.utot >> 16) || (dense && thr == 0.0 && n_pos < (uint32_t)max(0, c.min_keep))) {
-      one_pass = false;
-    } else if (dense) {
-      // nothing to cut: the draw over the fp32 masses scanned above
-      const KeptRule kr{true, thr < 0.0, 0ull};
-      if (io.masked)
-#pragma unroll
-        for (int j = 0; j < PT; ++j)
-          if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
-      C4S_PHASE(10);
-      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs);
-      C4S_PHASE(15);
-      return;
-    } else {
-      const double S = sc.tot, errS = sc.tot2;
-      // boundary buckets: threads 0..255 merge one bucket each over the waves,
-      // then wave 0 scans them (lane l holds buckets 4l .. 4l+3)
-      uint32_t* bcnt = reinterpret_cast<uint32_t*>(sbuf);           // sort buffers are free here
-      double* bmass = reinterpret_cast<double*>(sbuf) + kNB;
-      if (t < kNB) {
-        uint32_t cn = 0;
-        unsigned long long ms = 0ull;
-#pragma unroll
-        for (int i = 0; i < kStepWaves; ++i) {
-          const unsigned long long h = hm[i * kNB + t];
-          cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
-          ms += h & (kHistOne - 1ull);
-        }
-        bcnt[t] = cn;
-        bmass[t] = (double)ms * 0x1p-32;
-      }
-      __syncthreads();
-      const double B = S - thr * S;   // the mass the kept entries hold
-      const double Blo = B * (1.0 - 1e-3) - errS, Bhi = B * (1.0 + 1e-3) + errS;
-      if (w == 0) {
-        const Boundary bd = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, 0u, 0.0);
-        if (lane == 0) {
-          ss.bsel[0] = bd.lo;
-          ss.bsel[1] = bd.hi;
-          ss.bsel[2] = (int)bd.above;
-          ss.thru = bd.thru;
-          ss.mab = bd.mabove;
-          ss.nx = 0u;
-        }
-      }
-      __syncthreads();
-      C4S_PHASE(6);
-      const int blo = ss.bsel[0], bhi = ss.bsel[1];
-      // the sub-window of the boundary buckets (all of them unless refined)
-      int slo = 0, shi = kNB - 1, lo2 = 0;
-      float sc2 = 0.0f;
-      bool refine = false;
-      if (blo >= 0 && bhi >= 0) {
-        // More boundary entries than one sort takes (flat rows): histogram the
-        // boundary buckets again, kNB sub-buckets over them (top_k: over the
-        // k-th entry's bucket), and keep the sub-buckets where the boundary
-        // falls. Not for the unbounded last bucket.
-        const uint32_t nest = topk ? ss.thru : ss.thru - (uint32_t)ss.bsel[2];
-        refine = nest > (uint32_t)kSortCap && bhi < kNB - 1;
-        if (refine) {
-          lo2 = topk ? bhi : blo;
-          sc2 = (float)kNB / (float)(bhi + 1 - lo2);
-          for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
-          __syncthreads();
-#pragma unroll
-          for (int j = 0; j < PT; ++j) {
-            if (j < n && z[j] != ninf) {
-              const int b = bucket_of(z[j], m);
-              if (b >= lo2 && b <= bhi) {
-                const int sb = sub_bucket_of(z[j], m, lo2, sc2);
-                if (topk) atomicAdd(&hc[w * kNB + sb], 1u);
-                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(mass32(z[j] - m) * 0x1p32f) + kHistOne);
-              }
-            }
-          }
-          __syncthreads();
-          if (t < kNB) {
-            uint32_t cn = 0;
-            unsigned long long ms = 0ull;
-#pragma unroll
-            for (int i = 0; i < kStepWaves; ++i) {
-              const unsigned long long h = hm[i * kNB + t];
-              cn += hc[i * kNB + t] + (uint32_t)(h >> 48);
-              ms += h & (kHistOne - 1ull);
-            }
-            bcnt[t] = cn;
-            bmass[t] = (double)ms * 0x1p-32;
-          }
-          __syncthreads();
-          if (w == 0) {
-            const Boundary b2 = boundary_scan(bcnt, bmass, topk, (uint32_t)c.k, Blo, Bhi, (uint32_t)ss.bsel[2],
-                                              ss.mab);
-            if (lane == 0) {
-              ss.sub[0] = topk ? 0 : b2.lo;   // top_k: every entry above the k-th stays in the sort
-              ss.sub[1] = b2.hi;
-            }
-          }
-          __syncthreads();
-          slo = ss.sub[0];
-          shi = ss.sub[1];
-        }
-      }
-      if (blo < 0 || bhi < 0 || slo < 0 || shi < 0) {
-        one_pass = false;
-      } else {
-        // X: the entries to sort. top_k: every entry up to the k-th value's
-        // (sub-)bucket (the survivors then are a prefix of X). top_p: the
-        // boundary (sub-)buckets; every entry above them is kept, every entry
-        // below removed. side(): -1 above X, 0 in X, 1 below (monotone in z).
-        const int xlo = topk ? 0 : blo, xhi = bhi;
-        const SideRule sr{m, sc2, xlo, xhi, lo2, slo, shi, refine};
-        auto side = [&](float zj) { return sr.side(zj); };
-        float ma32 = 0.0f;
-        uint32_t na = 0;   // entries above X
-#pragma unroll
-        for (int j = 0; j < PT; ++j) {
-          if (j < n) {
-            const int sd = side(z[j]);
-            if (sd == 0) {
-              const uint32_t slot = atomicAdd(&ss.nx, 1u);
-              if (slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
-            } else if (sd < 0) {
-              ma32 += mass32(z[j] - m);
-              ++na;
-            }
-          }
-        }
-        double ma = (double)ma32;
-        double ema = ma * (0x1p-20 + PT * 0x1p-24) + (double)na * 0x1p-125;
-        ma = wave_sum_dpp(ma);
-        ema = wave_sum_dpp(ema);
-        na = wave_sum_u32(na);
-        if (lane == 0) { ss.wc[w] = ma; ss.wd[w] = ema; ss.wv[w] = na; }
-        __syncthreads();
-        C4S_PHASE(7);
-        const int nX = (int)ss.nx;
-        double Ma = 0.0, eMa = 0.0;
-        uint32_t n_above = 0;
-#pragma unroll
-        for (int i = 0; i < kStepWaves; ++i) { Ma += ss.wc[i]; eMa += ss.wd[i]; n_above += ss.wv[i]; }
-        if (nX > kSortCap) {
-          // more boundary entries than one sort takes: one_pass only if they
-          // all hold one value (ties), which needs no sort
-          verdict = tie_cut<PT>(rs.cfg, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
-          tp_exact = verdict == 3;
-          if (verdict != 1 && verdict != 3) one_pass = false;
-        } else {
-          int P2 = 1;
-          while (P2 < nX) P2 <<= 1;
-          const bool block = P2 > kWave;
-          uint64_t v = 0ull;
-          if (block) {
-            v = t < nX ? list[t] : 0ull;
-            v = sort_desc(v, P2, sbuf);
-            if (t < nX) list[t] = v;
-            __syncthreads();
-            C4S_PHASE(8);
-            decide_cut<true>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
-          } else if (w == 0) {
-            v = lane < nX ? list[lane] : 0ull;
-            v = sort_desc(v, P2, sbuf);
-            C4S_PHASE(8);
-            decide_cut<false>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
-          }
-          __syncthreads();
-          verdict = ss.verdict;
-          if (verdict == 2) {
-            // decide again with every mass in double (S and the mass above the boundary)
-            tp_exact = true;
-            double se = 0.0, sa = 0.0;
-#pragma unroll
-            for (int j = 0; j < PT; ++j) {
-              if (j < n && z[j] != ninf) {
-                const double ed = exp((double)(z[j] - m));
-                se += ed;
-                if (side(z[j]) < 0) sa += ed;
-              }
-            }
-            se = wave_sum_dpp(se);
-            sa = wave_sum_dpp(sa);
-            if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; }
-            __syncthreads();
-            double Se = 0.0, Mae = 0.0;
-#pragma unroll
-            for (int i = 0; i < kStepWaves; ++i) { Se += ss.wc[i]; Mae += ss.wd[i]; }
-            if (block) decide_cut<true>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
-            else if (w == 0) decide_cut<false>(rs.cfg, v, nX, m, thr, Se, 0.0, Mae, 0.0, n_above, list, ss);
-            __syncthreads();
-            verdict = ss.verdict;
-          }
-          C4S_PHASE(9);
-          if (verdict != 1) one_pass = false;
-        }
-      }
-    }
-  }
-  if (one_pass) {
-    // the draw over the kept set: key >= the last kept key
-    const uint64_t kthr = ss.kthr;
-    const KeptRule kr{false, false, kthr};
-    float ks32 = 0.0f;
-    uint32_t kc = 0, flags = 0;
-#pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      if (j < n) {
-        bool kp;
-        const float ej = kept_mass32(kr, z[j], m, lo + j, kp);
-        if (kp && z[j] != ninf) {
-          if (z[j] - m < -690.0f) flags = 1u;   // subnormal kept masses: libm implementations may disagree
-          ++kc;
-        }
-        ks32 += ej;
-        if (io.masked) io.masked[lo + j] = kp ? z[j] : ninf;
-      }
-    }
-    const double ks = (double)ks32;
-    const double ek = ks * (0x1p-20 + PT * 0x1p-24) + (double)kc * 0x1p-125;
-    const Scan2 ds = block_scan2(ks, ek, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
-    C4S_PHASE(10);
-    if ((ds.utot >> 16) == 0u) {
-      draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
-                      tp_exact ? 1u : 0u, ss, rs);
-      C4S_PHASE(15);
-      return;
-    }
-  }
+  bool done;
+  if (c.topk_on) done = sampled_step<PT, kKindTopK>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
+  else if (c.p >= 1.0f) done = sampled_step<PT, kKindDense>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
+  else done = sampled_step<PT, kKindTopP>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
+  if (done) return;
   // ---- the multi-pass chain on the row staged in LDS (c4s_chain.hpp) ----
   __syncthreads();   // every thread is done with the work area
   chain_fallback(rs.io, rs.cfg, work, val, sh);
