@@ -156,11 +156,14 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
     if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, 0u, n_kept);
     return;
   }
-  // the kept masses in double, scanned by the workgroup
+  // the kept masses in double, scanned by the workgroup. The kept test is the
+  // one pass's (kept_in): a dense row reaches this draw only without values
+  // whose double mass lies near underflow, so `z - m > -745` there is
+  // exactly `exp((double)(z - m)) > 0`.
   double dk = 0.0;
 #pragma unroll
   for (int j = 0; j < PT; ++j)
-    if (j < n && z[j] != neg_inf() && kept_by(kr, z[j], m, lo + j)) dk += exp((double)(z[j] - m));
+    if (j < n && z[j] != neg_inf() && kept_in(kr, z[j], m, lo + j)) dk += exp((double)(z[j] - m));
   const Scan2 d2 = block_scan2(dk, 0.0, 0u, ss.wa, ss.wb, ss.wu);
   const double r2 = u * d2.tot;
   const double m2 = 2.0 * rel_eps(c.V) * d2.tot;
@@ -171,7 +174,7 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
     double acc = d2.ex, prev = d2.ex;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      const double ej = (j < n && z[j] != neg_inf() && kept_by(kr, z[j], m, lo + j)) ? exp((double)(z[j] - m)) : 0.0;
+      const double ej = (j < n && z[j] != neg_inf() && kept_in(kr, z[j], m, lo + j)) ? exp((double)(z[j] - m)) : 0.0;
       if (found < 0 && ej > 0.0) {
         const double na = acc + ej;
         if (na >= r2) { found = lo + j; prev = acc; }
@@ -723,8 +726,10 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           const bool inx = j < n && sd == 0, abv = j < n && sd < 0;
           xm |= inx ? 1u << j : 0u;
           cx += inx ? 1u : 0u;
-          ma32 += abv ? mass32(z[j] - m) : 0.0f;
-          na += abv ? 1u : 0u;
+          if (abv) {   // few entries lie above X: a branch skips whole waves
+            ma32 += mass32(z[j] - m);
+            ++na;
+          }
         }
         {
           const uint32_t inc = wave_scan_u32(cx);

@@ -327,10 +327,12 @@ __device__ __forceinline__ bool kept_by(const KeptRule& kr, float z, float m, in
 }
 // The same test in the one pass (dense rows whose t = fl(z - m) lies within
 // [-745.25, -745] leave it, so `t > -745` decides there), and the fp32 mass.
+__device__ __forceinline__ bool kept_in(const KeptRule& kr, float z, float m, int id) {
+  return kr.dense ? (kr.all || (z != neg_inf() && z - m > -745.0f)) : key64(z, id) >= kr.kthr;
+}
 __device__ __forceinline__ float kept_mass32(const KeptRule& kr, float z, float m, int id, bool& kept) {
-  const bool fin = z != neg_inf();
-  kept = kr.dense ? (kr.all || (fin && z - m > -745.0f)) : key64(z, id) >= kr.kthr;
-  return (kept && fin) ? mass32(z - m) : 0.0f;
+  kept = kept_in(kr, z, m, id);
+  return (kept && z != neg_inf()) ? mass32(z - m) : 0.0f;
 }
 
 // The draw recomputed in double by one wave from the row (text2semantic.cpp:
