@@ -47,7 +47,8 @@ enum {
   C4S_OK = 0,
   C4S_EINVAL = 1, /* null pointer, bad size/dtype/mode, unsupported shape */
   C4S_EHIP = 2,   /* a HIP call failed; see c4s_last_error */
-  C4S_ENOMEM = 3
+  C4S_ENOMEM = 3,
+  C4S_ETIMEOUT = 4 /* a c4s_sample_stream call of this context gave up a row (see c4s_stream_status) */
 };
 
 enum { C4S_DTYPE_F32 = 0, C4S_DTYPE_BF16 = 1 };
@@ -78,7 +79,9 @@ enum {
 /* Per-row statistics (c4s_rows.out_stats, 4 words per row). */
 enum {
   C4S_STAT_PATH = 0,       /* bit0 drawn, bit1 top-k applied, bit2 top-p applied, bit3 greedy,
-                              bit4 decided without the multi-pass chain */
+                              bit4 decided without the multi-pass chain, bit5 decided on a candidate
+                              list; c4s_stream.out_stats: or-ed over the steps, and bit30 when the row's
+                              speculative chain gave up (see c4s_stream_status) */
   C4S_STAT_TOPP_EXACT = 1, /* nucleus cut fell inside the error bound -> exact pass ran */
   C4S_STAT_DRAW_EXACT = 2, /* draw fell inside the error bound -> exact pass ran */
   C4S_STAT_KEPT = 3        /* ids left with nonzero weight before the draw */
@@ -187,6 +190,20 @@ int c4s_sample_rows(c4s_ctx* ctx, const c4s_rows* rows, void* stream);
  * on the GPU: one call in flight per context. Not capturable: returns
  * C4S_EINVAL while `stream` is being captured into a graph. */
 int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream);
+/* The speculative chains of c4s_sample_stream (no counterpart in the
+ * reference, which decides each step on the host) wait on each other with
+ * bounded waits. A wait that expires (about 0.3 s by default; it does not
+ * happen on a working device) stops that row: its tokens from that step of
+ * the call are -1 and its RNG state stays at the step where it stopped. The
+ * context records it, and the next c4s_sample_stream call returns
+ * C4S_ETIMEOUT without queuing anything once the failing call has ended (the
+ * overlapped schedule waits for it; otherwise a call reports what has ended
+ * by then). c4s_stream_status synchronizes `stream` and returns C4S_ETIMEOUT
+ * or C4S_OK; either report clears the record. */
+int c4s_stream_status(c4s_ctx* ctx, void* stream);
+/* Polls of those bounded waits before they give up (<= 0: the default,
+ * 4194304). For tests of the C4S_ETIMEOUT path. */
+int c4s_set_wait_limit(c4s_ctx* ctx, int32_t polls);
 /* text2semantic.cpp:118-121 / :283-286 (head(cur)). */
 int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream);
 /* head(cur) then the chain on its logits (text2semantic.cpp:297-337 in one

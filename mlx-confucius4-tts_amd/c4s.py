@@ -17,7 +17,7 @@ REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "lib", "libc4s_sampling.so")
 HEADER = os.path.join(REPO, "include", "c4s_sampling.h")
 
-OK, EINVAL, EHIP, ENOMEM = 0, 1, 2, 3
+OK, EINVAL, EHIP, ENOMEM, ETIMEOUT = 0, 1, 2, 3, 4
 F32, BF16 = 0, 1
 MODE_CHAIN = 0
 P_PENALTY, P_TEMPERATURE, P_TOP_K, P_TOP_P = 1, 2, 4, 8
@@ -99,6 +99,8 @@ def lib() -> C.CDLL:
     L.c4s_version.restype = C.c_char_p
     L.c4s_sample_rows.argtypes = [_vp, C.POINTER(Rows), _vp]
     L.c4s_sample_stream.argtypes = [_vp, C.POINTER(Stream), _vp]
+    L.c4s_stream_status.argtypes = [_vp, _vp]
+    L.c4s_set_wait_limit.argtypes = [_vp, C.c_int32]
     L.c4s_hist_bits_init.argtypes = [_vp, _vp, _vp, C.c_int32, C.c_int32, _vp, _vp]
     L.c4s_lmhead.argtypes = [_vp, C.POINTER(Head), _vp]
     L.c4s_lmhead_sample.argtypes = [_vp, C.POINTER(Head), C.POINTER(Rows), _vp]
@@ -253,6 +255,15 @@ class Context:
                    flags=(STREAM_SEQUENTIAL if sequential else 0) | (0 if speculate else STREAM_NO_SPECULATION))
         self._check(lib().c4s_sample_stream(self._h, C.byref(s), _stream_handle(stream)),
                     "sample_stream")
+
+    def stream_status(self, stream=None):
+        """C4S_OK, or C4S_ETIMEOUT when a sample_stream call gave up a row (the
+        record is cleared); synchronizes `stream` first."""
+        return lib().c4s_stream_status(self._h, _stream_handle(stream))
+
+    def set_wait_limit(self, polls):
+        """Polls of the speculative chains' bounded waits before they give up (<= 0: default)."""
+        self._check(lib().c4s_set_wait_limit(self._h, int(polls)), "set_wait_limit")
 
     @staticmethod
     def _head(hidden, gamma, beta, weight, bias, logits, eps, quant=None):

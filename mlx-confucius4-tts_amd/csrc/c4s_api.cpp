@@ -56,6 +56,12 @@ struct c4s_ctx {
   // this device's address of the no-allocation entry point's static scratch
   // (null when the runtime could not give it)
   void* noalloc = nullptr;
+  // The speculative chains' give-up report: a word of pinned host memory that
+  // the kernels write through its device address, and the polls a bounded
+  // wait makes before it gives up.
+  volatile uint32_t* status_host = nullptr;
+  uint32_t* status_dev = nullptr;
+  int spin_max = c4s::kSpinMaxDefault;
 };
 
 namespace {
@@ -249,6 +255,18 @@ int c4s_create(int device, c4s_ctx** out) {
     delete ctx;
     return C4S_EINVAL;
   }
+  // The stream's status word (C4S_ETIMEOUT reports), host memory the device writes.
+  void* sh = nullptr;
+  if (hipHostMalloc(&sh, 64, hipHostMallocMapped) != hipSuccess) { delete ctx; return C4S_ENOMEM; }
+  ctx->status_host = static_cast<volatile uint32_t*>(sh);
+  *ctx->status_host = 0u;
+  void* sd = nullptr;
+  if (hipHostGetDevicePointer(&sd, sh, 0) != hipSuccess) {
+    (void)hipHostFree(sh);
+    delete ctx;
+    return C4S_EHIP;
+  }
+  ctx->status_dev = static_cast<uint32_t*>(sd);
   // The static scratch of c4s_lmhead_sample_noalloc: its address on this
   // device, asked for once, with the device current.
   if (c4s::noalloc_scratch(&ctx->noalloc) != hipSuccess) {
@@ -295,7 +313,39 @@ int c4s_destroy(c4s_ctx* ctx) {
                         ctx->ev_chain[0], ctx->ev_chain[1], ctx->ev_chain[2], ctx->ev_done, ctx->ev_side[0],
                         ctx->ev_side[1], ctx->ev_side[2]})
     if (ev) (void)hipEventDestroy(ev);
+  if (ctx->status_host) (void)hipHostFree(const_cast<uint32_t*>(ctx->status_host));
   delete ctx;
+  return C4S_OK;
+}
+
+namespace {
+// The status word of the stream calls that have ended, cleared: C4S_OK, or
+// C4S_ETIMEOUT with the reason in the context's error text.
+int take_status(c4s_ctx* ctx) {
+  const uint32_t s = *ctx->status_host;
+  if (!s) return C4S_OK;
+  *ctx->status_host = 0u;
+  return fail(ctx, C4S_ETIMEOUT,
+              (s & c4s::kStatusWaitExpired)
+                  ? "sample_stream: a speculative chain's bounded wait gave up; that call's tokens are -1 from the "
+                    "step where it stopped and its RNG states stop there"
+                  : "sample_stream: a speculative chain kept more drawn ids than it holds; that call's tokens are -1 "
+                    "from the step where it stopped");
+}
+}  // namespace
+
+int c4s_stream_status(c4s_ctx* ctx, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(ctx, e, "stream_status synchronize");
+  return take_status(ctx);
+}
+
+int c4s_set_wait_limit(c4s_ctx* ctx, int32_t polls) {
+  if (!ctx) return C4S_EINVAL;
+  ctx->spin_max = polls > 0 ? polls : c4s::kSpinMaxDefault;
   return C4S_OK;
 }
 
@@ -397,6 +447,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   a.rng = st->rng_state;
   a.out_tok = st->out_tokens;
   a.stats = st->out_stats;
+  a.spin_max = ctx->spin_max;
+  a.status = ctx->status_dev;
   if (st->flags & ~(uint32_t)(C4S_STREAM_SEQUENTIAL | C4S_STREAM_NO_SPECULATION))
     return fail(ctx, C4S_EINVAL, "stream: unknown flags");
   if (c4s::stream_lds_bytes(a.vocab, 0) + 4096 > kLdsLimit)
@@ -408,6 +460,8 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // workspaces, so it is not capturable: a graph would also keep pointers to
   // summary buffers that the next eager call reuses.
   if (is_capturing(hs)) return fail(ctx, C4S_EINVAL, "sample_stream: not allowed while the stream is captured");
+  // A call of this context that has ended gave up: report it before queuing.
+  if (const int rs = take_status(ctx)) return rs;
   // The two-phase stream needs the pipelined full-vocabulary chain (three
   // rows and summaries in LDS, V <= 8232); larger vocabularies, and callers
   // that ask for it, take the single-kernel stream.
@@ -474,6 +528,7 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   if (overlap) {
     const hipError_t ew = hipEventSynchronize(ctx->ev_done);
     if (ew != hipSuccess) return hip_fail(ctx, ew, "sample_stream previous call");
+    if (const int rs = take_status(ctx)) return rs;   // the previous call has ended now
   }
   hipError_t e0 = hipEventRecord(ctx->ev_start, hs);   // inputs and the previous call's chain
   if (e0 == hipSuccess) e0 = hipStreamWaitEvent(ctx->scan_s, ctx->ev_start, 0);

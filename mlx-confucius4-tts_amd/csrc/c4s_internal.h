@@ -75,7 +75,15 @@ struct StreamArgs {
   uint64_t* rng;
   int32_t* out_tok;      // [n_steps][n_rows]
   uint32_t* stats;       // optional [n_rows][4], accumulated over steps
+  // The speculative chains' bounded waits: polls before a wait gives up, and
+  // the word (host-visible) a chain that gave up sets to a nonzero value.
+  int spin_max;
+  uint32_t* status;
 };
+// Values of StreamArgs::status (bits).
+constexpr uint32_t kStatusWaitExpired = 1u;   // a checking wave's bounded wait gave up
+constexpr uint32_t kStatusDrawnOverflow = 2u; // more drawn ids than the speculative chain keeps
+constexpr int kSpinMaxDefault = 1 << 22;      // about 0.3 s of polls
 
 // Two-phase stream (scan, then chain). The scan writes one summary per
 // (step, row); its layout is fixed here so that host code can size the

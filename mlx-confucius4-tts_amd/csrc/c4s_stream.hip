@@ -2468,7 +2468,6 @@ constexpr int kSpecND = 5;                 // decider waves
 constexpr int NTS = (kSpecND + 1) * kWave;
 constexpr int kSpecGv = 1024;              // ids a call can draw (its steps at most)
 constexpr int kRing = 16;                  // per-token value rows kept by wave 0
-constexpr int kSpinMax = 1 << 22;          // wave 0's wait for a decision (about 0.3 s)
 constexpr int kSpecVW = 3;                 // the checking wave: alone on its SIMD (waves go to SIMDs in turn)
 constexpr int kHist = 8;                   // steps of tokens the checking wave keeps in registers
 static_assert(kHist >= kSpecND, "history covers the steps a decision can lag");
@@ -2779,7 +2778,7 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
     int n = ctl.snap & 0xFFFF;
     uint64_t rng = rng0;
     uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
-    bool stopped = false, bad = ctl.err != 0;
+    bool stopped = false, bad = ctl.err != 0, expired = false;
     const float rpen = 1.0f / c.pen;
     // the last kHist steps: lane (step % kHist) holds the step, its token and
     // whether the token joined the drawn ids
@@ -2802,9 +2801,10 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       RecView rv = rec_view(rc);
       if (rv.tag != q) {
         int spins = 0;
-        while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
-        if (spins > kSpinMax) {
+        while (vload(&rc.tag) != q && ++spins <= a.spin_max) __builtin_amdgcn_s_sleep(1);
+        if (spins > a.spin_max) {
           bad = true;
+          expired = true;
           break;
         }
         rv = rec_view(rc);
@@ -2826,13 +2826,14 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       int rtag = vload(&ctl.ringtag[rslot]);
       float x = vload(&ring[ridx]);
       spins = 0;
-      while (__ballot(isnew && rtag != hstep) && ++spins <= kSpinMax) {
+      while (__ballot(isnew && rtag != hstep) && ++spins <= a.spin_max) {
         __builtin_amdgcn_s_sleep(1);
         rtag = vload(&ctl.ringtag[rslot]);
         x = vload(&ring[ridx]);
       }
-      if (spins > kSpinMax) {
+      if (spins > a.spin_max) {
         bad = true;
+        expired = true;
         break;
       }
       C4S_SPEC_T(2);
@@ -2938,8 +2939,13 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       }
       if (!accept) {   // ring row q: the values of the token decided here
         spins = 0;
-        while (!exact && rc.ring && vload(&ctl.ringtag[q & (kRing - 1)]) != q && ++spins <= kSpinMax)
+        while (!exact && rc.ring && vload(&ctl.ringtag[q & (kRing - 1)]) != q && ++spins <= a.spin_max)
           __builtin_amdgcn_s_sleep(1);   // the decider's gather lands first
+        if (spins > a.spin_max) {   // its late gather could overwrite this ring row
+          bad = true;
+          expired = true;
+          break;
+        }
         issue_ring(q, tokq);
         wait_vm(0);
         if (lane == 0) vstore(&ctl.ringtag[q & (kRing - 1)], q);
@@ -2999,9 +3005,11 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
     wait_vm(0);
     if (lane == 0) {
       ctl.qend = q;
-      ctl.stopped = stopped ? 1 : 0;
+      ctl.stopped = (stopped || bad) ? 1 : 0;   // a row that gave up stops as at a stop token
       ctl.rng = rng;
       if (bad) acc[0] |= 1u << 30;
+      // a row that gave up stops here: the call reports it (the status word)
+      if (bad && a.status) *a.status = expired ? kStatusWaitExpired : kStatusDrawnOverflow;
       for (int i = 0; i < 4; ++i) ctl.acc[i] = acc[i];
       lgkm_wait();
       vstore(&ctl.done, 1);
@@ -3320,16 +3328,17 @@ __global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k
     int n = ctl.snap & 0xFFFF;
     uint64_t rng = rng0;
     uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
-    bool stopped = false, bad = ctl.err != 0;
+    bool stopped = false, bad = ctl.err != 0, expired = false;
     int htok = -1, hstep = -1;   // lane (step % kHist): a recent step, its token, whether it was drawn anew
     bool hfresh = false;
     while (q < s_end && !bad) {
       const int k = (q - s_first) % kLND;
       LSpecRec& rc = recs[k];
       int spins = 0;
-      while (vload(&rc.tag) != q && ++spins <= kSpinMax) __builtin_amdgcn_s_sleep(1);
-      if (spins > kSpinMax) {
+      while (vload(&rc.tag) != q && ++spins <= a.spin_max) __builtin_amdgcn_s_sleep(1);
+      if (spins > a.spin_max) {
         bad = true;
+        expired = true;
         break;
       }
       C4S_SPEC_EV(q, 2);
@@ -3443,9 +3452,11 @@ __global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k
     }
     if (lane == 0) {
       ctl.qend = q;
-      ctl.stopped = stopped ? 1 : 0;
+      ctl.stopped = (stopped || bad) ? 1 : 0;   // a row that gave up stops as at a stop token
       ctl.rng = rng;
       if (bad) acc[0] |= 1u << 30;
+      // a row that gave up stops here: the call reports it (the status word)
+      if (bad && a.status) *a.status = expired ? kStatusWaitExpired : kStatusDrawnOverflow;
       for (int i = 0; i < 4; ++i) ctl.acc[i] = acc[i];
       lgkm_wait();
       vstore(&ctl.done, 1);

@@ -275,3 +275,76 @@ def test_stream_speculative_chain(orc, gpu_ctx, kind):
     assert np.array_equal(ptoks, toks) and np.array_equal(prng, rng)
     assert not (st[:, 0].astype(np.uint32) & (1 << 30)).any()   # no row gave up waiting
     print("exact steps", int(st[:, 1].sum()), "per row", st[:, 1].tolist())
+
+
+@pytest.mark.parametrize("steps", [1024, 1025])
+def test_stream_speculation_limit(orc, gpu_ctx, steps):
+    """The speculative chains' step limit: 1024 steps is the longest call they
+    take (the drawn list and the 16-bit step fields at their largest), 1025 takes
+    the one-step-at-a-time chains on the overlapped schedule. Penalised rows of
+    every mode against the oracle, no row giving up."""
+    rows, V = 8, 8194
+    p = W.batch64_params(seed=4242, rows=rows, V=V)
+    g = np.random.default_rng(4243)
+    p["top_k"][:] = g.choice(np.array([0, 0, 20, 50], np.int32), rows)
+    p["top_p"][:] = g.choice(np.array([0.8, 0.9, 1.0], np.float32), rows)
+    p["pen"][:] = g.choice(np.array([1.0, 10.0], np.float32), rows)
+    p["do_sample"][3] = 0
+    x = W.batch64_logits(4244, steps, rows, V)
+    print(f"speculation limit {steps}: gpu", flush=True)
+    toks, rng, st = run_stream(gpu_ctx, p, x)
+    print(f"speculation limit {steps}: oracle", flush=True)
+    otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"], p["top_p"],
+                                    p["pen"], p["do_sample"], p["rng"], n_threads=16)
+    bad = np.argwhere(toks != otoks)
+    assert bad.size == 0, f"{len(bad)} mismatches, first (step, row) {bad[:5].tolist()}"
+    assert np.array_equal(rng, orng)
+    assert not (st[:, 0].astype(np.uint32) & (1 << 30)).any()
+    assert gpu_ctx.stream_status() == 0
+
+
+@pytest.mark.parametrize("steps", [128, 256])
+def test_stream_wait_expired_is_an_error(orc, steps):
+    """A speculative chain whose bounded wait gives up stops its row; the call
+    that follows reports it. The give-up is forced from the host (one poll a
+    wait: every checking wave gives up at its first wait and every kernel ends
+    normally). 128 steps run on the non-overlapped schedule, 256 on the
+    overlapped one. After the report the same context decides bit-exactly again."""
+    import torch
+
+    import c4s
+    rows, V = 8, 8194
+    p = W.batch64_params(seed=2, rows=rows, V=V)
+    p["top_k"][::2] = 0          # full-vocabulary rows (k_stream_spec) and top-k rows (k_stream_lspec)
+    x = W.batch64_logits(1003, steps, rows, V)
+    ctx = c4s.Context(0)
+    try:
+        ctx.set_wait_limit(1)
+        print(f"wait expired {steps}: forced give-up", flush=True)
+        toks, rng, st = run_stream(ctx, p, x)
+        gave_up = (st[:, 0].astype(np.uint32) >> 30) & 1
+        assert gave_up.all(), st[:, 0].tolist()
+        assert (toks[-1] == -1).all()              # stopped rows write -1 to the end of the call
+        assert ctx.stream_status() == c4s.ETIMEOUT
+        assert ctx.stream_status() == c4s.OK       # the report clears the record
+        # reported by the next call, which queues nothing
+        run_stream(ctx, p, x)
+        torch.cuda.synchronize()
+        out = torch.full((steps, rows), -9, dtype=torch.int32, device="cuda")
+        with pytest.raises(c4s.C4SError, match="code 4"):
+            ctx.sample_stream(dev(x, torch), dev(p["hist_ids"], torch), dev(p["hist_off"], torch),
+                              dev(p["temp"], torch), dev(p["top_k"], torch), dev(p["top_p"], torch),
+                              dev(p["pen"], torch), dev(p["rng"], torch), out,
+                              do_sample=dev(p["do_sample"], torch))
+        torch.cuda.synchronize()
+        assert (out.cpu().numpy() == -9).all()
+        # the default limit again: bit-exact, nothing to report
+        ctx.set_wait_limit(0)
+        print(f"wait expired {steps}: default limit", flush=True)
+        toks, rng, st = run_stream(ctx, p, x)
+        otoks, orng = orc.sample_stream(x, p["hist_ids"], p["hist_off"], p["temp"], p["top_k"], p["top_p"],
+                                        p["pen"], p["do_sample"], p["rng"], n_threads=16)
+        assert np.array_equal(toks, otoks) and np.array_equal(rng, orng)
+        assert ctx.stream_status() == c4s.OK
+    finally:
+        ctx.close()
