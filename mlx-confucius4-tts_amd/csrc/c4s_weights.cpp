@@ -19,6 +19,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <exception>
+#include <new>
 #include <string>
 #include <sys/stat.h>
 #include <vector>
@@ -27,17 +29,63 @@
 
 namespace {
 
+// Largest dimension, and largest element count, a tensor of the store may have
+// (far above an LM head's; the checks keep products and offsets from overflowing).
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+constexpr int64_t kMaxCount = (int64_t)1 << 36;
+
 struct Tensor {
   std::vector<float> f;        // values as fp32 (float data)
   std::vector<uint32_t> u;     // u32 data (packed 8-bit codes)
   std::vector<int64_t> shape;
   bool is_u32 = false;
-  int64_t count() const {
+  int64_t count() const {      // valid once shape_ok() held
     int64_t n = 1;
     for (int64_t d : shape) n *= d;
     return n;
   }
+  // every dimension in [1, kMaxDim] and at most kMaxCount elements
+  bool shape_ok() const {
+    int64_t n = 1;
+    for (int64_t d : shape) {
+      if (d < 1 || d > kMaxDim) return false;
+      n *= d;
+      if (n > kMaxCount) return false;
+    }
+    return true;
+  }
 };
+
+// Decimal digits as a non-negative integer; false past `limit` (no overflow).
+bool parse_count(const std::string& digits, int64_t limit, int64_t& out) {
+  out = 0;
+  if (digits.empty()) return false;
+  for (char ch : digits) {
+    if (ch < '0' || ch > '9') return false;
+    if (out > (limit - (ch - '0')) / 10) return false;
+    out = 10 * out + (ch - '0');
+  }
+  return true;
+}
+
+// Every decimal number of `list` in order (a shape tuple or a JSON list);
+// false when one exceeds `limit`.
+bool parse_ints(const std::string& list, int64_t limit, std::vector<int64_t>& v) {
+  v.clear();
+  std::string num;
+  for (size_t i = 0; i <= list.size(); ++i) {
+    const char ch = i < list.size() ? list[i] : ' ';
+    if (ch >= '0' && ch <= '9') {
+      num += ch;
+    } else if (!num.empty()) {
+      int64_t x;
+      if (!parse_count(num, limit, x)) return false;
+      v.push_back(x);
+      num.clear();
+    }
+  }
+  return true;
+}
 
 bool read_file(const std::string& path, std::vector<char>& buf) {
   std::FILE* fp = std::fopen(path.c_str(), "rb");
@@ -83,6 +131,10 @@ float bf16_to_float(uint16_t b) {
 enum Kind { kF16, kBF16, kF32, kF64, kU32, kBad };
 
 bool convert(const char* data, size_t bytes, Kind kind, Tensor& t, std::string& err) {
+  if (!t.shape_ok()) {
+    err = "a dimension is zero or too large";
+    return false;
+  }
   const int64_t n = t.count();
   const size_t es = kind == kF64 ? 8 : (kind == kF32 || kind == kU32) ? 4 : 2;
   if ((size_t)n * es != bytes) {
@@ -155,13 +207,7 @@ bool parse_npy(const std::vector<char>& f, Tensor& t, std::string& err) {
   else if (descr.find("<f2") != std::string::npos) kind = kF16;
   else if (descr.find("<u4") != std::string::npos) kind = kU32;
   if (kind == kBad) { err = "unsupported .npy dtype " + descr; return false; }
-  const std::string sh = dict_field(h, "shape");
-  t.shape.clear();
-  std::string num;
-  for (char ch : sh) {
-    if (ch >= '0' && ch <= '9') num += ch;
-    else if (!num.empty()) { t.shape.push_back(std::stoll(num)); num.clear(); }
-  }
+  if (!parse_ints(dict_field(h, "shape"), kMaxDim, t.shape)) { err = "bad .npy shape"; return false; }
   const size_t off = pre + hlen;
   return convert(f.data() + off, f.size() - off, kind, t, err);
 }
@@ -182,21 +228,11 @@ std::string json_field(const std::string& obj, const std::string& key) {
   return "";
 }
 
-std::vector<int64_t> json_ints(const std::string& list) {
-  std::vector<int64_t> v;
-  std::string num;
-  for (char ch : list) {
-    if (ch >= '0' && ch <= '9') num += ch;
-    else if (!num.empty()) { v.push_back(std::stoll(num)); num.clear(); }
-  }
-  return v;
-}
-
 bool parse_safetensors(const std::vector<char>& f, const std::string& name, Tensor& t, std::string& err) {
   if (f.size() < 8) { err = "not a .safetensors file"; return false; }
   uint64_t n = 0;
   for (int i = 0; i < 8; ++i) n |= (uint64_t)(unsigned char)f[i] << (8 * i);
-  if (8 + n > f.size()) { err = "truncated .safetensors header"; return false; }
+  if (n > f.size() - 8) { err = "truncated .safetensors header"; return false; }
   const std::string h(f.data() + 8, n);
   // the tensor's key: the quoted name followed (after blanks) by a colon
   size_t k = 0;
@@ -215,9 +251,10 @@ bool parse_safetensors(const std::vector<char>& f, const std::string& name, Tens
   Kind kind = dt == "F32" ? kF32 : dt == "F16" ? kF16 : dt == "BF16" ? kBF16 : dt == "F64" ? kF64 :
               dt == "U32" ? kU32 : kBad;
   if (kind == kBad) { err = "unsupported .safetensors dtype " + dt; return false; }
-  t.shape = json_ints(json_field(obj, "shape"));
-  const std::vector<int64_t> off = json_ints(json_field(obj, "data_offsets"));
-  if (off.size() != 2 || off[1] < off[0] || 8 + n + (uint64_t)off[1] > f.size()) {
+  std::vector<int64_t> off;
+  if (!parse_ints(json_field(obj, "shape"), kMaxDim, t.shape) ||
+      !parse_ints(json_field(obj, "data_offsets"), (int64_t)f.size(), off) || off.size() != 2 || off[1] < off[0] ||
+      (uint64_t)off[1] > f.size() - 8 - n) {
     err = "bad data_offsets for " + name;
     return false;
   }
@@ -270,8 +307,8 @@ extern "C" {
 
 const char* c4s_weights_last_error(void) { return g_err.c_str(); }
 
-int c4s_tensor_read_f32(const char* root, const char* name, float* out, int64_t cap, int64_t* shape,
-                        int32_t* ndim) {
+namespace {
+int tensor_read_f32(const char* root, const char* name, float* out, int64_t cap, int64_t* shape, int32_t* ndim) {
   if (!root || !name || !ndim) return fail("tensor_read: NULL argument");
   Tensor t;
   std::string err;
@@ -288,7 +325,7 @@ int c4s_tensor_read_f32(const char* root, const char* name, float* out, int64_t 
   return C4S_OK;
 }
 
-int c4s_head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_head_weights* out) {
+int head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_head_weights* out) {
   if (!root || !out) return fail("head_weights_load: NULL argument");
   std::memset(out, 0, sizeof(*out));
   if (wdtype != C4S_W_BF16 && wdtype != C4S_W_F32 && wdtype != C4S_W_Q8)
@@ -313,7 +350,7 @@ int c4s_head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_h
     Tensor s, o;
     if (!load_tensor(root, "semantic_head.scales", s, err) || !load_tensor(root, "semantic_head.biases", o, err))
       return fail(err);
-    if (s.shape.size() != 2 || s.shape[0] != V || o.shape != s.shape || D % s.shape[1] != 0)
+    if (s.shape.size() != 2 || s.shape[0] != V || o.shape != s.shape || s.shape[1] < 1 || D % s.shape[1] != 0)
       return fail("head_weights_load: scales / biases are not [V][D/group]");
     group = (int32_t)(D / s.shape[1]);
     q.resize((size_t)V * D);
@@ -370,6 +407,35 @@ int c4s_head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_h
     return fail("head_weights_load: device allocation or copy failed");
   }
   return C4S_OK;
+}
+
+}  // namespace
+
+// No exception leaves the C ABI: a malformed file that gets past the checks
+// above (or an allocation that fails) is reported as C4S_EINVAL / C4S_ENOMEM.
+int c4s_tensor_read_f32(const char* root, const char* name, float* out, int64_t cap, int64_t* shape,
+                        int32_t* ndim) {
+  try {
+    return tensor_read_f32(root, name, out, cap, shape, ndim);
+  } catch (const std::bad_alloc&) {
+    g_err = "tensor_read: out of host memory";
+    return C4S_ENOMEM;
+  } catch (const std::exception& e) {
+    return fail(std::string("tensor_read: ") + e.what());
+  }
+}
+
+int c4s_head_weights_load(const char* root, int32_t wdtype, int32_t group, c4s_head_weights* out) {
+  try {
+    return head_weights_load(root, wdtype, group, out);
+  } catch (const std::bad_alloc&) {
+    if (out) c4s_head_weights_free(out);
+    g_err = "head_weights_load: out of host memory";
+    return C4S_ENOMEM;
+  } catch (const std::exception& e) {
+    if (out) c4s_head_weights_free(out);
+    return fail(std::string("head_weights_load: ") + e.what());
+  }
 }
 
 int c4s_head_weights_free(c4s_head_weights* w) {

@@ -94,6 +94,65 @@ def test_store_errors(tmp_path):
         c4s.read_tensor(str(tmp_path / "nowhere"), "final_norm.weight")
 
 
+def _raw_safetensors(path, header_bytes, data=b"", length=None):
+    import struct
+    n = len(header_bytes) if length is None else length
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", n) + header_bytes + data)
+
+
+def test_corrupt_files_are_errors(tmp_path):
+    """Malformed stores come back as C4S_EINVAL with a message, in this process:
+    nothing throws through the C ABI and nothing reads past the file."""
+    import json
+    # a header length whose sum with the 8-byte prefix wraps around 2^64
+    _raw_safetensors(tmp_path / "wrap.safetensors", b"{}", length=(1 << 64) - 4)
+    with pytest.raises(c4s.C4SError, match="code 1.*truncated .safetensors header"):
+        c4s.read_tensor(str(tmp_path / "wrap"), "x")
+    # a data offset of 40 digits
+    hb = b'{"x": {"dtype": "F32", "shape": [2], "data_offsets": [0, 1' + b"0" * 40 + b']}}'
+    _raw_safetensors(tmp_path / "big.safetensors", hb, b"\0" * 8)
+    with pytest.raises(c4s.C4SError, match="code 1.*data_offsets"):
+        c4s.read_tensor(str(tmp_path / "big"), "x")
+    # a shape of 30 digits, and a shape with a zero dimension
+    for nm, shape in (("huge", [2, 10 ** 30]), ("zero", [4, 0])):
+        hb = json.dumps({"x": {"dtype": "F32", "shape": shape, "data_offsets": [0, 0]}}).encode()
+        _raw_safetensors(tmp_path / f"{nm}.safetensors", hb)
+        with pytest.raises(c4s.C4SError, match="code 1"):
+            c4s.read_tensor(str(tmp_path / nm), "x")
+    # .npy: a header longer than the file, a shape past the limit, a zero dimension
+    root = tmp_path / "npy"
+    root.mkdir()
+    np.save(root / "ok.npy", np.ones((3, 4), np.float32))
+    raw = (root / "ok.npy").read_bytes()
+    (root / "trunc.npy").write_bytes(raw[:9])
+    with pytest.raises(c4s.C4SError, match="code 1"):
+        c4s.read_tensor(str(root), "trunc")
+    (root / "longhdr.npy").write_bytes(raw[:8] + b"\xff\xff" + raw[10:40])
+    with pytest.raises(c4s.C4SError, match="truncated .npy header"):
+        c4s.read_tensor(str(root), "longhdr")
+    hdr = raw[10:10 + (raw[8] | raw[9] << 8)]
+    for nm, sh in (("npyhuge", b"(3, 99999999999999999999999)"), ("npyzero", b"(0, 4)")):
+        h2 = hdr.replace(b"(3, 4)", sh)
+        h2 = h2.rstrip(b" \n")
+        h2 += b" " * ((64 - (10 + len(h2) + 1) % 64) % 64) + b"\n"
+        (root / f"{nm}.npy").write_bytes(raw[:8] + len(h2).to_bytes(2, "little") + h2 + raw[10 + len(hdr):])
+        with pytest.raises(c4s.C4SError, match="code 1"):
+            c4s.read_tensor(str(root), nm)
+
+
+def test_packed_head_with_empty_scales_is_an_error(tmp_path):
+    """An 8-bit packed head whose scale tensors have zero columns: rejected before
+    any division by the group count (and before any device work)."""
+    arrs = _head_arrays(D=128, V=10)
+    root = _npy_store(tmp_path, {k: v for k, v in arrs.items() if k != "semantic_head.weight"})
+    np.save(os.path.join(root, "semantic_head.weight.npy"), np.zeros((10, 32), np.uint32))
+    np.save(os.path.join(root, "semantic_head.scales.npy"), np.zeros((10, 0), np.float32))
+    np.save(os.path.join(root, "semantic_head.biases.npy"), np.zeros((10, 0), np.float32))
+    with pytest.raises(c4s.C4SError, match="code 1"):
+        c4s.load_head_weights(root, c4s.W_Q8)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("kind", ["f32", "bf16", "q8", "q8_packed"])
 def test_head_from_store(tmp_path, orc, gpu_ctx, kind):
