@@ -159,7 +159,9 @@ size_t pow2_at_least(size_t n) {
   return p;
 }
 
-int validate_rows(c4s_ctx* ctx, const c4s_rows* r) {
+// logits_given: false when the logits are a buffer the call provides later
+// (the LM head entry points without a caller's logits buffer).
+int validate_rows(c4s_ctx* ctx, const c4s_rows* r, bool logits_given = true) {
   if (!r) return fail(ctx, C4S_EINVAL, "rows descriptor is NULL");
   if (r->n_rows < 0) return fail(ctx, C4S_EINVAL, "n_rows < 0");
   if (r->n_rows == 0) return C4S_OK;
@@ -167,7 +169,7 @@ int validate_rows(c4s_ctx* ctx, const c4s_rows* r) {
   if (r->ld < r->vocab) return fail(ctx, C4S_EINVAL, "ld < vocab");
   if (r->dtype != C4S_DTYPE_F32 && r->dtype != C4S_DTYPE_BF16)
     return fail(ctx, C4S_EINVAL, "unknown dtype");
-  if (!r->logits || !r->out_token) return fail(ctx, C4S_EINVAL, "logits/out_token is NULL");
+  if ((logits_given && !r->logits) || !r->out_token) return fail(ctx, C4S_EINVAL, "logits/out_token is NULL");
   const uint32_t m = r->mode;
   const bool custom = (m & C4S_MODE_CUSTOM) != 0;
   const uint32_t known = C4S_P_PENALTY | C4S_P_TEMPERATURE | C4S_P_TOP_K | C4S_P_TOP_P |
@@ -217,11 +219,18 @@ c4s::RowsArgs to_args(const c4s_rows* r) {
   return a;
 }
 
+// The sort workspace of vocabularies the step cannot stage in LDS.
+int rows_workspace(c4s_ctx* ctx, const c4s_rows* r, hipStream_t s) {
+  if (r->vocab <= c4s::kLdsVocabMax) return C4S_OK;
+  const size_t per_row = pow2_at_least((size_t)r->vocab) * sizeof(uint32_t);
+  return ensure(ctx, &ctx->ws, &ctx->ws_bytes, per_row * (size_t)r->n_rows, "sort workspace", s);
+}
+
 int launch_rows_checked(c4s_ctx* ctx, const c4s_rows* r, hipStream_t s) {
   c4s::RowsArgs a = to_args(r);
   if (r->vocab > c4s::kLdsVocabMax) {
     const size_t per_row = pow2_at_least((size_t)r->vocab) * sizeof(uint32_t);
-    int rc = ensure(ctx, &ctx->ws, &ctx->ws_bytes, per_row * (size_t)r->n_rows, "sort workspace", s);
+    int rc = rows_workspace(ctx, r, s);
     if (rc) return rc;
     a.sort_ws = static_cast<uint32_t*>(ctx->ws);
     a.sort_ws_stride = (int64_t)(per_row / sizeof(uint32_t));
@@ -507,11 +516,13 @@ int c4s_sample_stream(c4s_ctx* ctx, const c4s_stream* st, void* stream) {
   // Full-vocabulary rows: the speculative chain (several steps decided at
   // once, each checked in order) when a call's drawn ids fit its lists, else
   // the pipelined chain with step segments for rows without penalty.
+  // (a layout size of 0: the vocabulary has no layout, nothing fits)
+  const size_t spec_lds = c4s::stream_spec_lds_bytes(a.vocab), lspec_lds = c4s::stream_lspec_lds_bytes(a.vocab);
   const bool spec = !(st->flags & C4S_STREAM_NO_SPECULATION) && a.n_steps <= c4s::stream_spec_max_steps() &&
-                    c4s::stream_spec_lds_bytes(a.vocab) + kSpecStaticLds <= kLdsLimit;
+                    spec_lds > 0 && spec_lds + kSpecStaticLds <= kLdsLimit;
   // Greedy and top-k rows likewise: the speculative list chain, else one wave a row.
   const bool spec_list = !(st->flags & C4S_STREAM_NO_SPECULATION) && a.n_steps <= c4s::stream_spec_max_steps() &&
-                         c4s::stream_lspec_lds_bytes(a.vocab) + kSpecStaticLds <= kLdsLimit;
+                         lspec_lds > 0 && lspec_lds + kSpecStaticLds <= kLdsLimit;
   auto launch_row_chain = [&](const c4s::StreamWs& w, hipStream_t on) {
     if (spec) return c4s::launch_stream_spec(a, w, on);
     hipError_t e = c4s::launch_stream_rowp(a, w, on);
@@ -645,31 +656,44 @@ int c4s_lmhead(c4s_ctx* ctx, const c4s_head* head, void* stream) {
   return lmhead_impl(ctx, head, head->logits, head->ld_out, static_cast<hipStream_t>(stream));
 }
 
-int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream) {
-  if (!ctx) return C4S_EINVAL;
-  if (!head || !rows) return fail(ctx, C4S_EINVAL, "descriptor is NULL");
-  DeviceGuard g(ctx->device);
-  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
-  float* logits = head->logits;
-  int64_t ld = head->ld_out;
-  if (!logits) {
-    int rc = ensure(ctx, &ctx->logits_ws, &ctx->logits_bytes,
-                    (size_t)std::max(head->M, 1) * (size_t)std::max(head->V, 1) * 4, "logits workspace",
-                    static_cast<hipStream_t>(stream));
-    if (rc) return rc;
-    logits = static_cast<float*>(ctx->logits_ws);
-    ld = head->V;
-  }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = lmhead_impl(ctx, head, logits, ld, s);
-  if (rc) return rc;
-  c4s_rows r = *rows;
+namespace {
+// The rows of the sampler behind the LM head: logits, stride, dtype, row count
+// and vocabulary come from the head.
+c4s_rows head_rows(const c4s_rows& rows, const c4s_head* head, float* logits, int64_t ld) {
+  c4s_rows r = rows;
   r.logits = logits;
   r.ld = ld;
   r.dtype = C4S_DTYPE_F32;
   r.n_rows = head->M;
   r.vocab = head->V;
-  rc = validate_rows(ctx, &r);
+  return r;
+}
+}  // namespace
+
+// Both descriptors are checked, and every workspace sized, before anything is
+// queued: a call that fails queues nothing.
+int c4s_lmhead_sample(c4s_ctx* ctx, const c4s_head* head, const c4s_rows* rows, void* stream) {
+  if (!ctx) return C4S_EINVAL;
+  if (!head || !rows) return fail(ctx, C4S_EINVAL, "descriptor is NULL");
+  int rc = lmhead_check(ctx, head);
+  if (rc) return rc;
+  c4s_rows r = head_rows(*rows, head, head->logits, head->logits ? head->ld_out : head->V);
+  rc = validate_rows(ctx, &r, head->logits != nullptr);
+  if (rc) return rc;
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* logits = head->logits;
+  if (!logits) {
+    rc = ensure(ctx, &ctx->logits_ws, &ctx->logits_bytes,
+                (size_t)std::max(head->M, 1) * (size_t)std::max(head->V, 1) * 4, "logits workspace", s);
+    if (rc) return rc;
+    logits = static_cast<float*>(ctx->logits_ws);
+    r.logits = logits;
+  }
+  rc = rows_workspace(ctx, &r, s);
+  if (rc) return rc;
+  rc = lmhead_launch(ctx, head, logits, r.ld, s);
   if (rc) return rc;
   return launch_rows_checked(ctx, &r, s);
 }
@@ -688,21 +712,16 @@ int c4s_lmhead_sample_noalloc(c4s_ctx* ctx, const c4s_head* head, const c4s_rows
   if (lbytes > c4s::kNoAllocBytes)
     return fail(ctx, C4S_EINVAL, "lmhead_sample_noalloc: M x V x 4 logits (no logits buffer given) exceed the "
                                  "8 MiB static scratch");
-  DeviceGuard g(ctx->device);
-  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   unsigned char* base = static_cast<unsigned char*>(ctx->noalloc);
   float* logits = head->logits ? head->logits : reinterpret_cast<float*>(base);
   const int64_t ld = head->logits ? head->ld_out : head->V;
+  c4s_rows r = head_rows(*rows, head, logits, ld);
+  rc = validate_rows(ctx, &r);   // before anything writes the caller's logits or the shared scratch
+  if (rc) return rc;
+  DeviceGuard g(ctx->device);
+  if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
   rc = lmhead_launch(ctx, head, logits, ld, s);
-  if (rc) return rc;
-  c4s_rows r = *rows;
-  r.logits = logits;
-  r.ld = ld;
-  r.dtype = C4S_DTYPE_F32;
-  r.n_rows = head->M;
-  r.vocab = head->V;
-  rc = validate_rows(ctx, &r);
   if (rc) return rc;
   return launch_rows_checked(ctx, &r, s);
 }

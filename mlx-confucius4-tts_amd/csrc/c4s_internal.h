@@ -153,8 +153,8 @@ hipError_t launch_stream_lspec(const StreamArgs& a, const StreamWs& w, hipStream
 hipError_t launch_stream_chain(const StreamArgs& a, const StreamWs& w, hipStream_t s);
 size_t stream_chain_lds_bytes(int vocab);
 size_t stream_rowp_lds_bytes(int vocab);  // 0 when the pipelined row chain does not fit
-size_t stream_spec_lds_bytes(int vocab);  // dynamic LDS of the speculative row chain
-size_t stream_lspec_lds_bytes(int vocab); // dynamic LDS of the speculative list chain
+size_t stream_spec_lds_bytes(int vocab);  // dynamic LDS of the speculative row chain (0: no layout for vocab)
+size_t stream_lspec_lds_bytes(int vocab); // dynamic LDS of the speculative list chain (0: no layout for vocab)
 int stream_spec_max_steps();             // steps a call may have for it
 hipError_t launch_lmhead(const LmHeadArgs& a, hipStream_t s);
 hipError_t launch_hbm_probe(const void* src, void* dst, int64_t bytes, int mode, hipStream_t s);

@@ -104,3 +104,23 @@ def test_lmhead_rejects_bad_descriptors(gpu_ctx):
         gpu_ctx.lmhead(h, g, b, q, bias, out, quant=(sc, sc, 48))      # group not 32/64/128
     with pytest.raises(c4s.C4SError, match="code 1"):
         gpu_ctx.lmhead(h, g, b, q, bias, out, quant=(sc, sc, 128))     # group does not divide D
+
+
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_lmhead_sample_bad_rows_queue_nothing(gpu_ctx, noalloc):
+    """A rows descriptor that fails validation (no RNG state for sampled rows)
+    is reported before anything is queued: the caller's logits keep their
+    contents, and so do the token output and the RNG states."""
+    import torch
+    head, p = W.lmhead(seed=7, M=4, D=64, V=100)
+    h, g, b, bias, w = (dev(x, torch) for x in (head.hidden, head.gamma, head.beta, head.bias, head.weight))
+    logits = torch.full((4, 100), 7.0, dtype=torch.float32, device="cuda")
+    tok = torch.full((4,), -5, dtype=torch.int32, device="cuda")
+    fn = gpu_ctx.lmhead_sample_noalloc if noalloc else gpu_ctx.lmhead_sample
+    with pytest.raises(c4s.C4SError, match="code 1.*rng_state"):
+        fn(h, g, b, w, bias, dev(p["hist_ids"][:0], torch), dev(np.zeros(5, np.int64), torch),
+           dev(p["temp"][:4], torch), dev(p["top_k"][:4], torch), dev(p["top_p"][:4], torch),
+           dev(p["pen"][:4], torch), None, tok, logits=logits)
+    torch.cuda.synchronize()
+    assert (logits.cpu().numpy() == 7.0).all()
+    assert (tok.cpu().numpy() == -5).all()
