@@ -80,7 +80,8 @@ enum {
 enum {
   C4S_STAT_PATH = 0,       /* bit0 drawn, bit1 top-k applied, bit2 top-p applied, bit3 greedy,
                               bit4 decided without the multi-pass chain, bit5 decided on a candidate
-                              list; c4s_stream.out_stats: or-ed over the steps, and bit30 when the row's
+                              list, bit6 (vocab above 12288) the row read once; c4s_stream.out_stats:
+                              or-ed over the steps, and bit30 when the row's
                               speculative chain gave up (see c4s_stream_status) */
   C4S_STAT_TOPP_EXACT = 1, /* nucleus cut fell inside the error bound -> exact pass ran */
   C4S_STAT_DRAW_EXACT = 2, /* draw fell inside the error bound -> exact pass ran */

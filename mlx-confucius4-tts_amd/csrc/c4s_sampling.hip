@@ -1052,13 +1052,32 @@ struct T2Sh {
   double e[kT2Cap];                 // the draw's masses in id order
   uint32_t wsum[NW];
   float wmax[NW];
+  uint32_t wm4[NW];                 // one read: per-wave largest candidate key
   uint32_t n;
   int bstar;
   uint32_t nge, nkeep;
   int tok;
+  uint32_t pick[2];                 // one read: the picked candidate's bin and the candidates above it
+  uint32_t nq;                      // one read: gathered entries whose penalised key reaches the bound
 };
 
 __host__ __device__ __forceinline__ size_t t2_offset(int V) { return ((size_t)4 * ((V + 31) / 32) + 15) & ~(size_t)15; }
+
+// Descending sort of n <= NT distinct 64-bit keys by rank counting (each key's
+// place is the count of keys above it), through tmp; two barriers.
+__device__ __forceinline__ void rank_sort_desc_u64(uint64_t* buf, uint64_t* tmp, int n) {
+  const int t = threadIdx.x;
+  if (t < n) {
+    const uint64_t mine = buf[t];
+    int r = 0;
+    for (int j = 0; j < n; ++j) r += (buf[j] > mine) ? 1 : 0;
+    tmp[r] = mine;
+  }
+  __syncthreads();
+  if (t < n) buf[t] = tmp[t];
+  __syncthreads();
+}
+constexpr int kRankSortMax = 256;   // above: the bitonic network
 
 // In-buffer descending bitonic sort of P (a power of two) 64-bit keys by the
 // NT threads of the workgroup.
@@ -1115,56 +1134,223 @@ struct T2Row {
   }
 };
 
-// Returns false (nothing written) when the survivors' bucket holds more than
-// the sort takes; the multi-pass chain decides the row then.
-__device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts) {
-  const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
-  const float ninf = neg_inf();
-  for (int i = t; i < kT2Copies * kT2Buckets; i += NT) (&ts.hist[0][0])[i] = 0u;
-  if (t == 0) ts.n = 0u;
-  __syncthreads();
-  // pass 1: maximum and histogram
-  uint32_t* hist = ts.hist[w % kT2Copies];
-  float lmax = ninf;
-  src.each(V, [&](int, float zi) {
-    lmax = fmaxf(lmax, zi);
-    atomicAdd(&hist[fkey(zi) >> (32 - kT2Bits)], 1u);
-  });
-  lmax = wave_max_f32(lmax);
-  if (lane == 0) ts.wmax[w] = lmax;
-  __syncthreads();
-  // b*: thread t takes buckets 2047 - 2t (higher) and 2046 - 2t; counts from the top
-  const int bh = kT2Buckets - 1 - 2 * t, bl = bh - 1;
-  uint32_t ch = 0, cl = 0;
+// ---- one read of the row (fp32 rows, penalty >= 1) ----
+//
+// Each thread streams its ids once (16-byte loads, U of them in flight) and
+// keeps its four largest entries as packed keys: the top 23 bits of the
+// order-preserving key of the raw value x, then a 9-bit index of the entry
+// in the thread's stream (3 v_med3 and 1 v_max a value, no LDS atomics). The
+// penalty only lowers a value (penalty >= 1, sampling.cpp:26) and fl(y / T) is
+// monotone in y, so the raw keys bound the penalised and divided ones from
+// above. One pick over the 4 NT candidates, binned by their distance below
+// the largest, gives Q, the 23-bit prefix of the lowest key in the bin of the
+// (k + kOneSlack)-th largest candidate (the slack leaves room for entries the
+// penalty takes below Q). Every entry whose raw prefix reaches Q is gathered:
+// from the four of a thread whose fourth lies below Q, else from its stream
+// read again by its wave; each is read again (a few cache lines), penalised
+// and divided exactly, and goes to ts.list. The rest of the row stays out of
+// the top k when at least k gathered entries still reach Q after their
+// penalty (then the k-th largest value is at or above Q's smallest key, and
+// every entry at or above it was gathered; otherwise the pick is taken again
+// deeper down) and no value below Q can tie the k-th quotient (checked once
+// the list is sorted). Returns false, with nothing but the work area written,
+// when a check fails: the two passes over the row decide then.
+constexpr int kOneIdxBits = 9;
+constexpr uint32_t kOneEdge = (1u << kOneIdxBits) - 1;   // index of the thread's unaligned head / tail entry
+constexpr int kOneUnroll = 8;
+constexpr uint32_t kOneSlack = 16;
+constexpr int kOneBinShift = 15;   // candidate bins of 2^15 packed keys: 1/256 of a binade
+// 16-byte loads a thread; the unrolled loop rounds them up to kOneUnroll, and
+// every index it makes (padding past the row included) stays below kOneEdge
+constexpr int kOneMaxIters = 120;
+static_assert(kOneMaxIters % kOneUnroll == 0 && 4 * kOneMaxIters - 1 < (int)kOneEdge, "indices below the edge's");
+constexpr int kOneMaxV = 4 * NT * kOneMaxIters;
+
+__device__ __forceinline__ uint32_t one_pack(float x, uint32_t idx) {
+  return (fkey(x) & ~kOneEdge) | idx;
+}
+// The median of three (v_med3_u32): max(lo, min(hi, e)) when lo <= hi, which
+// the compiler cannot know here.
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t r;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// t0 >= t1 >= t2 >= t3 keeps the four largest (the order holds from the start, all zero)
+__device__ __forceinline__ void one_insert(uint32_t& t0, uint32_t& t1, uint32_t& t2, uint32_t& t3, uint32_t e) {
+  t3 = med3_u32(t3, t2, e);
+  t2 = med3_u32(t2, t1, e);
+  t1 = med3_u32(t1, t0, e);
+  t0 = max(t0, e);
+}
+
+// Bin of `hist` (nb bins scanned from the top, nb / NT a thread) holding the
+// m-th largest counted key, and the count above it, into ts.pick; false when
+// fewer than m keys were counted. Two barriers.
+template <int NB>
+__device__ __forceinline__ bool one_pick(const uint32_t* hist, uint32_t m, T2Sh& ts) {
+  constexpr int PB = NB / NT;
+  const int t = threadIdx.x, lane = lane_id(), w = wave_id();
+  uint32_t cb[PB], loc = 0;
 #pragma unroll
-  for (int q = 0; q < kT2Copies; ++q) { ch += ts.hist[q][bh]; cl += ts.hist[q][bl]; }
-  const uint32_t inc = wave_scan_u32(ch + cl);
+  for (int i = 0; i < PB; ++i) { cb[i] = hist[NB - 1 - PB * t - i]; loc += cb[i]; }
+  const uint32_t inc = wave_scan_u32(loc);
   if (lane == kWave - 1) ts.wsum[w] = inc;
   __syncthreads();
-  uint32_t ex = inc - (ch + cl);
-  for (int i = 0; i < w; ++i) ex += ts.wsum[i];
-  const uint32_t k = (uint32_t)c.k;
-  if (ex < k && k <= ex + ch) { ts.bstar = bh; ts.nge = ex + ch; }
-  else if (ex + ch < k && k <= ex + ch + cl) { ts.bstar = bl; ts.nge = ex + ch + cl; }
-  __syncthreads();
-  const int bstar = ts.bstar;
-  const uint32_t nge = ts.nge;
-  if (nge > (uint32_t)kT2Cap) return false;   // uniform
-  // pass 2: the candidates (bucket >= b*)
-  src.each(V, [&](int i, float zi) {
-    const uint32_t key = fkey(zi);
-    if ((int)(key >> (32 - kT2Bits)) >= bstar) {
-      const uint32_t slot = atomicAdd(&ts.n, 1u);
-      ts.list[slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+  uint32_t ex = inc - loc, total = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const uint32_t x = ts.wsum[i];
+    ex += (i < w) ? x : 0u;
+    total += x;
+  }
+  if (total < m) return false;   // uniform
+  if (ex < m && ex + loc >= m) {
+    uint32_t run = ex;
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      if (run < m && run + cb[i] >= m) { ts.pick[0] = (uint32_t)(NB - 1 - PB * t - i); ts.pick[1] = run; }
+      run += cb[i];
     }
-  });
+  }
   __syncthreads();
-  const int n = (int)ts.n;   // == nge
-  int P = 1;
-  while (P < n) P <<= 1;
-  for (int i = n + t; i < P; i += NT) ts.list[i] = 0ull;
+  return true;
+}
+
+__device__ __forceinline__ bool topk_one_read(const RowsArgs& a, const RowCfg& c, const float* xf, const uint32_t* bitmap,
+                              T2Sh& ts, uint32_t& qkey) {
+  const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
+  const RowShape rs = row_shape(xf, V);
+  const float4* p4 = reinterpret_cast<const float4*>(xf + rs.head);
+  const float ninf = neg_inf();
+  uint32_t t0 = 0u, t1 = 0u, t2 = 0u, t3 = 0u;   // 0: below every packed key
+  const int iters = (rs.nq + NT - 1) / NT;
+  for (int j0 = 0; j0 < iters; j0 += kOneUnroll) {
+    float4 v[kOneUnroll];
+#pragma unroll
+    for (int u = 0; u < kOneUnroll; ++u) {
+      const int q = t + NT * (j0 + u);
+      v[u] = (q < rs.nq) ? p4[q] : make_float4(ninf, ninf, ninf, ninf);
+    }
+#pragma unroll
+    for (int u = 0; u < kOneUnroll; ++u) {
+      const uint32_t i0 = 4u * (uint32_t)(j0 + u);
+      one_insert(t0, t1, t2, t3, one_pack(v[u].x, i0));
+      one_insert(t0, t1, t2, t3, one_pack(v[u].y, i0 + 1u));
+      one_insert(t0, t1, t2, t3, one_pack(v[u].z, i0 + 2u));
+      one_insert(t0, t1, t2, t3, one_pack(v[u].w, i0 + 3u));
+    }
+  }
+  const int edge = (t < rs.head) ? t : ((t < rs.head + rs.tail) ? rs.head + 4 * rs.nq + (t - rs.head) : -1);
+  if (edge >= 0) one_insert(t0, t1, t2, t3, one_pack(xf[edge], kOneEdge));
+  C4S_PHASE(8);
+  auto id_of = [&](uint32_t e) -> int {
+    const uint32_t ix = e & kOneEdge;
+    if (ix == kOneEdge) return edge;
+    return rs.head + 4 * (t + NT * (int)(ix >> 2)) + (int)(ix & 3u);
+  };
+  auto valid = [&](uint32_t e) {   // a real entry of the row (not padding past it)
+    const uint32_t ix = e & kOneEdge;
+    return e != 0u && (ix == kOneEdge ? edge >= 0 : t + NT * (int)(ix >> 2) < rs.nq);
+  };
+  // The candidates by their distance below the largest, M: bin b (from the
+  // top) holds the packed keys in (M - (b + 1) 2^S, M - b 2^S], 1/256 of a
+  // binade, the last bin everything farther down (the LDS atomics spread over
+  // many bins where a histogram of the keys' top bits had a few).
+  for (int i = t; i < kT2Buckets; i += NT) ts.hist[0][i] = 0u;
+  {
+    const uint32_t m0 = wave_max_u32(t0);
+    if (lane == 0) ts.wm4[w] = m0;
+    if (t == 0) { ts.n = 0u; ts.nq = 0u; }
+  }
   __syncthreads();
-  bitonic_desc_u64(ts.list, P);
+  uint32_t M = 0u;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) M = max(M, ts.wm4[i]);
+  const uint32_t tk[4] = {t0, t1, t2, t3};
+  uint32_t* h1 = ts.hist[0];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)   // one_pick scans from the highest bin: the bins nearest M
+    if (tk[i]) atomicAdd(&h1[(kT2Buckets - 1) - min((uint32_t)(kT2Buckets - 1), (M - tk[i]) >> kOneBinShift)], 1u);
+  __syncthreads();
+  C4S_PHASE(1);
+  const uint32_t k = (uint32_t)c.k;
+  uint32_t kb = k + kOneSlack;
+  for (int attempt = 0;; ++attempt) {
+    if (!one_pick<kT2Buckets>(h1, kb, ts)) return false;   // fewer candidates than that (uniform)
+    const uint32_t bfar = (kT2Buckets - 1) - ts.pick[0];   // bins below M
+    const int64_t lo = (int64_t)M - ((int64_t)(bfar + 1) << kOneBinShift) + 1;
+    // the bound: the prefix of the lowest key of that bin, above -inf's
+    if (bfar >= (uint32_t)(kT2Buckets - 1) || lo <= (int64_t)kKeyNegInf) return false;
+    const uint32_t Q = (uint32_t)lo >> kOneIdxBits;
+    const uint32_t kq = Q << kOneIdxBits;   // smallest key with prefix Q
+    C4S_PHASE(2);
+    // every entry whose raw prefix reaches Q, with its penalised
+    // (sampling.cpp:26) and divided (:16) value
+    uint32_t reach = 0u;
+    auto push = [&](int id, float x) {
+      float y = x;
+      if (c.pen_on && ((bitmap[id >> 5] >> (id & 31)) & 1u)) y = (y < 0) ? y * c.pen : y / c.pen;
+      reach += fkey(y) >= kq ? 1u : 0u;
+      const float z = c.temp_on ? y / c.temp : y;
+      const uint32_t slot = atomicAdd(&ts.n, 1u);
+      if (slot < (uint32_t)kT2Cap) ts.list[slot] = ((uint64_t)fkey(z) << 32) | (uint32_t)~(uint32_t)id;
+    };
+    // A thread whose fourth candidate lies below Q holds every such entry of
+    // its stream among its four; another may hold more: its wave reads that
+    // thread's stream again (16-byte loads, one a lane).
+    const bool redo = (t3 >> kOneIdxBits) >= Q;
+    if (!redo) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (valid(tk[i]) && (tk[i] >> kOneIdxBits) >= Q) {
+          const int id = id_of(tk[i]);
+          push(id, xf[id]);
+        }
+    }
+    for (uint64_t rm = __ballot(redo); rm; rm &= rm - 1) {
+      const int tf = w * kWave + (__ffsll((unsigned long long)rm) - 1);
+      for (int j = lane; j < iters; j += kWave) {
+        const int q = tf + NT * j;
+        if (q < rs.nq) {
+          const float4 v = p4[q];
+          const int i0 = rs.head + 4 * q;
+          if ((fkey(v.x) >> kOneIdxBits) >= Q) push(i0, v.x);
+          if ((fkey(v.y) >> kOneIdxBits) >= Q) push(i0 + 1, v.y);
+          if ((fkey(v.z) >> kOneIdxBits) >= Q) push(i0 + 2, v.z);
+          if ((fkey(v.w) >> kOneIdxBits) >= Q) push(i0 + 3, v.w);
+        }
+      }
+      const int ef = (tf < rs.head) ? tf : ((tf < rs.head + rs.tail) ? rs.head + 4 * rs.nq + (tf - rs.head) : -1);
+      if (lane == 0 && ef >= 0 && (fkey(xf[ef]) >> kOneIdxBits) >= Q) push(ef, xf[ef]);
+    }
+    reach = wave_sum_u32(reach);
+    if (lane == 0 && reach) atomicAdd(&ts.nq, reach);
+    __syncthreads();
+    C4S_PHASE(3);
+    const uint32_t n = ts.n, nq = ts.nq;
+    if (n > (uint32_t)kT2Cap) return false;   // uniform
+    if (nq >= k) {
+      qkey = kq;
+      return true;
+    }
+    // fewer than k reach Q after their penalty: a bound further down
+    if (attempt == 2) return false;
+    __syncthreads();   // every thread has read ts.n and ts.nq
+    if (t == 0) { ts.n = 0u; ts.nq = 0u; }
+    __syncthreads();
+    kb *= 4u;
+  }
+}
+
+// top_k, top_p and the draw on the sorted candidates ts.list[0, ts.n) (every
+// entry at or above the k-th largest value among them); returns true.
+__device__ __forceinline__ bool topk_finish(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts,
+                            uint32_t stat_bits) {
+  const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
+  const float ninf = neg_inf();
+  const uint32_t k = (uint32_t)c.k;
+  const int n = (int)ts.n;
   // top_k: every entry with the k-th largest value or above survives
   const uint32_t kkey = (uint32_t)(ts.list[k - 1] >> 32);
   if (w == 0) {
@@ -1197,6 +1383,7 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
   }
   __syncthreads();
   const int nkeep = (int)ts.nkeep;
+  C4S_PHASE(5);
   // the state before the draw: kept values, -inf elsewhere
   if (a.out_masked) {
     float* mrow = a.out_masked + (int64_t)row * V;
@@ -1211,12 +1398,15 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
   int Pk = 1;
   while (Pk < nkeep) Pk <<= 1;
   __syncthreads();
-  for (int j = t; j < Pk; j += NT) {
+  const int Ps = nkeep <= kRankSortMax ? nkeep : Pk;
+  for (int j = t; j < Ps; j += NT) {
     const uint64_t v = j < nkeep ? ts.list[j] : 0ull;
     ts.list[j] = j < nkeep ? (((uint64_t)(uint32_t)v << 32) | (v >> 32)) : 0ull;
   }
   __syncthreads();
-  bitonic_desc_u64(ts.list, Pk);
+  if (nkeep <= kRankSortMax) rank_sort_desc_u64(ts.list, reinterpret_cast<uint64_t*>(ts.e), nkeep);
+  else bitonic_desc_u64(ts.list, Pk);
+  C4S_PHASE(6);
   if (w == 0) {
     // text2semantic.cpp:150-165 over the kept entries in id order (the maximum
     // starts from -1e30f; -inf positions add 0)
@@ -1251,17 +1441,93 @@ __device__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const
       join_history(a, row, tok);
       if (a.stats) {
         uint32_t* st = a.stats + 4 * (int64_t)row;
-        st[0] = 1u | 2u | 4u | 32u;
+        st[0] = 1u | 2u | 4u | 32u | stat_bits;
         st[1] = 0u;
         st[2] = 0u;
         st[3] = (uint32_t)nkeep;
       }
     }
   }
+  C4S_PHASE(7);
   return true;
 }
 
+// Returns false (nothing written) when the survivors' bucket holds more than
+// the sort takes; the multi-pass chain decides the row then.
+__device__ __forceinline__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts) {
+  const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
+  const float ninf = neg_inf();
+  const uint32_t k = (uint32_t)c.k;
+  // one read of the row when its checks pass
+  uint32_t qkey = 0u;
+  bool one = src.xf && V <= kOneMaxV && (!c.pen_on || c.pen >= 1.0f) &&
+             topk_one_read(a, c, src.xf, src.bitmap, ts, qkey);
+  if (one) {
+    const int n = (int)ts.n;
+    if (n <= kRankSortMax) {
+      rank_sort_desc_u64(ts.list, reinterpret_cast<uint64_t*>(ts.e), n);   // the draw's masses come later
+    } else {
+      int P = 1;
+      while (P < n) P <<= 1;
+      for (int i = n + t; i < P; i += NT) ts.list[i] = 0ull;
+      __syncthreads();
+      bitonic_desc_u64(ts.list, P);
+    }
+    C4S_PHASE(4);
+    // no value below the bound ties the k-th quotient (the largest of them, divided)
+    if (c.temp_on && !(fkey(kfloat(qkey - 1u) / c.temp) < (uint32_t)(ts.list[k - 1] >> 32))) one = false;
+  }
+  if (one) return topk_finish(a, row, c, src, ts, 64u);
+  __syncthreads();   // the work area is free again
+  for (int i = t; i < kT2Copies * kT2Buckets; i += NT) (&ts.hist[0][0])[i] = 0u;
+  if (t == 0) ts.n = 0u;
+  __syncthreads();
+  // pass 1: maximum and histogram
+  uint32_t* hist = ts.hist[w % kT2Copies];
+  float lmax = ninf;
+  src.each(V, [&](int, float zi) {
+    lmax = fmaxf(lmax, zi);
+    atomicAdd(&hist[fkey(zi) >> (32 - kT2Bits)], 1u);
+  });
+  lmax = wave_max_f32(lmax);
+  if (lane == 0) ts.wmax[w] = lmax;
+  __syncthreads();
+  // b*: thread t takes buckets 2047 - 2t (higher) and 2046 - 2t; counts from the top
+  const int bh = kT2Buckets - 1 - 2 * t, bl = bh - 1;
+  uint32_t ch = 0, cl = 0;
+#pragma unroll
+  for (int q = 0; q < kT2Copies; ++q) { ch += ts.hist[q][bh]; cl += ts.hist[q][bl]; }
+  const uint32_t inc = wave_scan_u32(ch + cl);
+  if (lane == kWave - 1) ts.wsum[w] = inc;
+  __syncthreads();
+  uint32_t ex = inc - (ch + cl);
+  for (int i = 0; i < w; ++i) ex += ts.wsum[i];
+  if (ex < k && k <= ex + ch) { ts.bstar = bh; ts.nge = ex + ch; }
+  else if (ex + ch < k && k <= ex + ch + cl) { ts.bstar = bl; ts.nge = ex + ch + cl; }
+  __syncthreads();
+  const int bstar = ts.bstar;
+  const uint32_t nge = ts.nge;
+  if (nge > (uint32_t)kT2Cap) return false;   // uniform
+  // pass 2: the candidates (bucket >= b*)
+  src.each(V, [&](int i, float zi) {
+    const uint32_t key = fkey(zi);
+    if ((int)(key >> (32 - kT2Bits)) >= bstar) {
+      const uint32_t slot = atomicAdd(&ts.n, 1u);
+      ts.list[slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+    }
+  });
+  __syncthreads();
+  const int n = (int)ts.n;   // == nge
+  int P = 1;
+  while (P < n) P <<= 1;
+  for (int i = n + t; i < P; i += NT) ts.list[i] = 0ull;
+  __syncthreads();
+  bitonic_desc_u64(ts.list, P);
+  return topk_finish(a, row, c, src, ts, 0u);
+}
+
 __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
+  C4S_PHASE(14);
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ Scratch sh;
   const int row = blockIdx.x;
@@ -1291,6 +1557,7 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
     __syncthreads();
   }
   const int64_t roff = (int64_t)row * a.ld;
+  C4S_PHASE(0);
   if (c.draw && c.topk_on && c.k <= kT2MaxK && V <= kT2MaxV && a.rng) {
     T2Row tr;
     tr.xf = a.dtype == 0 ? static_cast<const float*>(a.logits) + roff : nullptr;

@@ -249,3 +249,54 @@ def test_host_helpers_match_oracle(orc, gpu_ctx):
         y = orc.top_p(orc.top_k(x, 30), 0.8)
         assert gpu_ctx.host_draw(y, 1234) == orc.draw(y, 1234)
     assert gpu_ctx.host_argmax(np.zeros(0, np.float32)) == 0
+
+
+def test_large_vocab_one_read_and_its_checks(orc, gpu_ctx):
+    """Large-vocabulary top-k rows read once (statistics bit 6), all bit for bit
+    against the oracle with the masked rows: six of the largest values in one
+    thread's stream (its fourth candidate reaches the bound: its wave reads its
+    stream again); the 60 largest values penalised below the bound (the bound
+    is taken again further down); a value just under a key prefix whose
+    quotient by the temperature ties the k-th largest one (0x3fc00200 and the
+    float before it, divided by 0.75, both round to 2.0000813); ties at the
+    k-th value kept; and a row whose largest values span more binades than the
+    candidate bins, which the two passes over the row decide (bit 6 clear).
+    V is odd, so the rows start at every 16-byte alignment (the head and tail
+    entries a thread holds apart)."""
+    rows, V = 6, 100003
+    b = W.large_vocab(seed=43, rows=rows, V=V, hist_len=400)
+    b.top_p[:] = np.array([0.95, 0.95, 0.9, 1.0, 1.0, 0.8], np.float32)
+    head = [((16 - (r * V * 4) % 16) % 16) // 4 for r in range(rows)]
+    nt = 1024
+
+    def stream_ids(r, t, n):   # the first n ids of thread t's stream in row r
+        return [head[r] + 4 * (t + nt * j) + e for j in range((n + 3) // 4) for e in range(4)][:n]
+    # row 1: six of the top values in thread 5's stream
+    for i, idx in enumerate(stream_ids(1, 5, 6)):
+        b.logits[1, idx] = 30.0 + i
+    # row 2: its 60 largest values are in the history, penalty 10
+    top = np.argsort(b.logits[2])[::-1][:60]
+    hist = [b.hist_ids[b.hist_off[r]:b.hist_off[r + 1]] for r in range(rows)]
+    hist[2] = np.concatenate([hist[2], top.astype(np.int32)])
+    b.pen[2] = 10.0
+    # row 3: 49 large values, then 17 copies of y_k (the smallest value of its
+    # key prefix: ranks k to k + 16 at the bound's prefix) and the float below
+    # it, whose quotients by T = 0.75 are equal
+    g = np.random.default_rng(7)
+    b.logits[3] = (0.1 * g.standard_normal(V) - 5.0).astype(np.float32)
+    ids3 = g.permutation(V)[:67]
+    b.logits[3, ids3[:49]] = (10.0 + 0.25 * np.arange(49)).astype(np.float32)
+    b.logits[3, ids3[49:66]] = np.array([0x3FC00200], np.uint32).view(np.float32)[0]
+    b.logits[3, ids3[66]] = np.array([0x3FC001FF], np.uint32).view(np.float32)[0]
+    b.temp[3], b.pen[3] = 0.75, 1.0
+    # row 4: k = 1 with three equal maxima
+    b.logits[4, [17, 50001, 99999]] = 40.0
+    b.top_k[4], b.pen[4] = 1, 1.0
+    # row 5: its 80 largest values from 2^60 down by factors of two
+    b.logits[5, g.permutation(V)[:80]] = np.ldexp(1.0, 60 - np.arange(80)).astype(np.float32)
+    b.hist_ids, b.hist_off = W.csr(hist)
+    print("large vocab one read: checks", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=True)
+    one = ((st[:, 0] >> 6) & 1).tolist()
+    assert one[:3] == [1, 1, 1] and one[4:] == [1, 0], st[:, 0].tolist()
+    assert st[4, 3] == 3 and st[3, 3] == 67     # ties kept: three maxima; every tied quotient survives
