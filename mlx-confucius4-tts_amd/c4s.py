@@ -293,6 +293,23 @@ class Context:
                  wscale=hw.wscale, wbias=hw.wbias)
         self._check(lib().c4s_lmhead(self._h, C.byref(h), _stream_handle(stream)), "lmhead")
 
+    def lmhead_sample_loaded(self, hw: HeadWeights, hidden, temp, top_k, top_p, pen, rng, out_token, logits=None,
+                             hist_ids=None, hist_off=None, hist_bits=None, do_sample=None, stop_token=-1, eps=1e-5,
+                             stream=None):
+        """c4s_lmhead_sample with the tensors of load_head_weights: one AR step
+        from the hidden rows to the tokens (text2semantic.cpp:297-337)."""
+        M, D = hidden.shape
+        if D != hw.D:
+            raise ValueError(f"hidden has D={D}, the head D={hw.D}")
+        h = Head(hidden=_p(hidden), gamma=hw.gamma, beta=hw.beta, eps=eps, weight=hw.weight, bias=hw.bias,
+                 M=M, D=D, V=hw.V, logits=_p(logits), ld_out=hw.V if logits is None else logits.shape[1],
+                 wdtype=hw.wdtype, group=hw.group, wscale=hw.wscale, wbias=hw.wbias)
+        r = Rows(hist_ids=_p(hist_ids), hist_offsets=_p(hist_off), temperature=_p(temp), top_k=_p(top_k),
+                 top_p=_p(top_p), rep_penalty=_p(pen), do_sample=_p(do_sample), rng_state=_p(rng),
+                 out_token=_p(out_token), mode=MODE_CHAIN, hist_bits=_p(hist_bits), stop_token=stop_token)
+        self._check(lib().c4s_lmhead_sample(self._h, C.byref(h), C.byref(r), _stream_handle(stream)),
+                    "lmhead_sample")
+
     def lmhead(self, hidden, gamma, beta, weight, bias, logits, eps=1e-5, stream=None, quant=None):
         h = self._head(hidden, gamma, beta, weight, bias, logits, eps, quant)
         self._check(lib().c4s_lmhead(self._h, C.byref(h), _stream_handle(stream)), "lmhead")

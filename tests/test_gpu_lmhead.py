@@ -124,3 +124,31 @@ def test_lmhead_sample_bad_rows_queue_nothing(gpu_ctx, noalloc):
     torch.cuda.synchronize()
     assert (logits.cpu().numpy() == 7.0).all()
     assert (tok.cpu().numpy() == -5).all()
+
+
+@pytest.mark.parametrize("kind", ["bf16", "f32", "q8"])
+def test_lmhead_outlier_channels(orc, gpu_ctx, kind):
+    """GPT-2-like hidden rows: a few channels with magnitudes of 100-300 in every
+    row (the rest N(0, 1)), so that the row's mean and variance are set by
+    them. The folded LayerNorm (x - mu) / sigma * gamma . W = (x . gamma W - mu
+    gamma . W) / sigma keeps the logits within the same tolerance of the
+    float64 LayerNorm + linear."""
+    import torch
+    M, D, V = 64, 1280, 8194
+    head, _ = W.lmhead(seed=17, M=M, D=D, V=V)
+    g = np.random.default_rng(18)
+    x = g.standard_normal((M, D)).astype(np.float32)
+    chans = np.array([37, 138, 447, 1003])
+    x[:, chans] = (np.array([150.0, -300.0, 100.0, 220.0]) * (1 + 0.1 * g.standard_normal((M, 4)))).astype(np.float32)
+    head.hidden = W.f32_to_bf16_bits(x)
+    wdev, quant, worc, kw = _weights(kind, head, 19, 64)
+    logits = torch.zeros((M, V), dtype=torch.float32, device="cuda")
+    print(f"lmhead outliers {kind}", flush=True)
+    gpu_ctx.lmhead(dev(head.hidden, torch), dev(head.gamma, torch), dev(head.beta, torch), wdev,
+                   dev(head.bias, torch), logits, quant=quant)
+    torch.cuda.synchronize()
+    got = logits.cpu().numpy()
+    want = orc.ln_lmhead(head.hidden, head.gamma, head.beta, worc, head.bias, n_threads=16, **kw)
+    err = np.abs(got.astype(np.float64) - want)
+    print(f"  max abs err {err.max():.3e}  max |logit| {np.abs(want).max():.3f}", flush=True)
+    assert np.all(err <= ATOL + RTOL * np.abs(want))
