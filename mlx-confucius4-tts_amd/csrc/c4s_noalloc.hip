@@ -1,6 +1,7 @@
 // Static device scratch of the no-allocation entry point
-// (c4s_lmhead_sample_noalloc): the LM head's normalised rows and, when the
-// caller passes no logits buffer, the logits handed to the sampler.
+// (c4s_lmhead_sample_noalloc): when the caller passes no logits buffer, the
+// LM head's logits handed to the sampler (the head folds its LayerNorm into
+// the GEMM and keeps nothing else in memory).
 //
 // The array lives in the library's code object: each GPU the library runs on
 // holds its own copy until the process ends. Host code never uses the array's
