@@ -16,7 +16,10 @@ that call; --sequential times the single-kernel stream instead.
 Also reported: the same chain as one launch per AR step (per_call, eager and
 graph-replayed; with the history as CSR ids, and kept on the device as a set
 that each call extends; and with the pipeline's default parameters on every
-row, the AR loop's usual case); the other workloads (one row; 1024 bf16 rows with ties;
+row, the AR loop's usual case); the level-1 drop-in at B = 1 (the reference's
+five sampling functions and the draw through c4tts/t2s_sampling.h, host vector
+in and out, microseconds per AR step; lib/bench_dropin run as a child process
+before this process touches the GPU); the other workloads (one row; 1024 bf16 rows with ties;
 256 rows at V=151936; the LM head for bf16 / fp32 / 8-bit weights alone and
 with the chain); HBM copy and read probes; bit-exact parity of the first AR
 steps against the CPU oracle, and the oracle timed on host cores (1 thread and
@@ -172,10 +175,49 @@ def bench_large_vocab(torch, ctx, W, s):
     nbytes = rows * (4 * V + 4 * 2048 + 24)
     fn = _rows_fn(torch, ctx, b, tok)
     out = {"workload": f"{rows} rows x V={V} fp32, top_k 50 / top_p 0.95 / temperature 0.7 / penalty 1.2, "
-                       "history 2048 ids; one sample_rows call", "bytes_per_call": int(nbytes)}
-    out.update(_rate(rows, nbytes, time_eager(torch, fn, 10, s)))
-    log(f"large vocab 256: {out['us_per_call']:.1f} us, {out['achieved_GBps']:.0f} GB/s")
+                       "history 2048 ids; one sample_rows call (graph-replayed; eager_us beside it)",
+           "bytes_per_call": int(nbytes)}
+    eager = time_eager(torch, fn, 10, s)
+    out.update(_rate(rows, nbytes, time_graph(torch, fn, 20, s)))
+    out["eager_us"] = round(eager, 3)
+    log(f"large vocab 256: {out['us_per_call']:.1f} us graph-replayed ({eager:.1f} eager), "
+        f"{out['achieved_GBps']:.0f} GB/s")
     return out
+
+
+def bench_dropin(steps=1000):
+    """lib/bench_dropin: the reference's AR loop body at B = 1 through the C++
+    drop-in (text2semantic.cpp:136-166 with c4tts/t2s_sampling.h), us per step.
+    Run as a child process before this process starts the GPU."""
+    import subprocess
+    exe = os.path.join(REPO, "mlx-confucius4-tts_amd", "lib", "bench_dropin")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} is not built"}
+    r = subprocess.run([exe, str(steps)], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": f"bench_dropin exited {r.returncode}: {r.stderr[-300:]}"}
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["workload"] = ("B = 1, V = 8194: copy the step's logits into a std::vector, then repetition_penalty, "
+                       "temperature, top_k, top_p and draw (sampled) or repetition_penalty and argmax (greedy), "
+                       "each a synchronous call on a host vector (c4tts/t2s_sampling.h); penalty 10, "
+                       "temperature 0.8, top_k 30, top_p 0.8; history from 200 ids")
+    out["reference_us_per_step"] = 19.0
+    out["reference_source"] = ("docs/OPTIONAL.md:88-89: host sampling 0.019 ms/step at B = 1 on an Apple "
+                               "M-series CPU (copy + processors + draw; greedy or sampled not stated)")
+    return out
+
+
+def host_cpu():
+    """The host's CPUs as the bench sees them."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
 
 
 def bench_lmhead(torch, ctx, W, s, hist_ids, hist_off, temp, top_k, top_p, pen, do_sample, rng0):
@@ -241,6 +283,11 @@ def main():
                "run with --gpus 1")
         print(msg, file=sys.stderr)
         sys.exit(2)
+
+    # the drop-in's own process uses the GPU before this one does
+    log("drop-in at B = 1 (child process)")
+    dropin = bench_dropin()
+    log(f"drop-in: {dropin}")
 
     import numpy as np
     import torch
@@ -400,6 +447,7 @@ def main():
         import oracle
         S = args.cpu_steps
         xs = logits[:S].cpu().numpy()
+        # the box allots 16 CPUs to a GPU: a worker pool stays within that share
         all_cores = min(len(os.sched_getaffinity(0)), 16)
 
         def run_cpu(nt):
@@ -426,7 +474,9 @@ def main():
                          f"on the first {S} AR steps x {R} rows of this job ({otoks.size} row-steps, about "
                          f"{med[1]:.1f} s per run on 1 thread), serial row loop as text2semantic.cpp:303",
                "all_cores": {"value": round(otoks.size / med[all_cores], 1), "cores": all_cores,
-                             "note": "rows of a step split over host threads (min(affinity, 16))"}}
+                             "note": "rows of a step split over host threads: min(affinity, 16), the "
+                                     "box's CPU share for one GPU"},
+               "host": host_cpu()}
         log(f"cpu: {cpu['value']:.0f} rows/s on 1 thread, {cpu['all_cores']['value']:.0f} on {all_cores}; "
             f"parity mismatches {mism}")
 
@@ -462,6 +512,7 @@ def main():
         "cpu_baseline": cpu,
         "parity": parity,
         "per_call": per_call,
+        "dropin_b1": dropin,
         "configs": configs,
         "hbm_probe": probe,
         "wall_s_timed": round(wall, 4),

@@ -2676,7 +2676,15 @@ __device__ __forceinline__ void wait_vm(int n) {
   }
 }
 
+// kForcedLimit: the bounded waits poll a.spin_max times (a test's limit);
+// otherwise the compile-time default, so that the production instance's
+// checking loop is built with a constant bound. (The checking wave's loop is
+// sensitive to its control flow: an extra exit in the middle of it made the
+// 1000-step call about 7% slower, so a wait that gives up only marks the row
+// and the loop's own test ends it.)
+template <bool kForcedLimit>
 __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
+  const int spin_max = kForcedLimit ? a.spin_max : kSpinMaxDefault;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ SpecRec recs[kSpecND];
   __shared__ SpecCtl ctl;
@@ -2801,8 +2809,8 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       RecView rv = rec_view(rc);
       if (rv.tag != q) {
         int spins = 0;
-        while (vload(&rc.tag) != q && ++spins <= a.spin_max) __builtin_amdgcn_s_sleep(1);
-        if (spins > a.spin_max) {
+        while (vload(&rc.tag) != q && ++spins <= spin_max) __builtin_amdgcn_s_sleep(1);
+        if (spins > spin_max) {
           bad = true;
           expired = true;
           break;
@@ -2826,12 +2834,12 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       int rtag = vload(&ctl.ringtag[rslot]);
       float x = vload(&ring[ridx]);
       spins = 0;
-      while (__ballot(isnew && rtag != hstep) && ++spins <= a.spin_max) {
+      while (__ballot(isnew && rtag != hstep) && ++spins <= spin_max) {
         __builtin_amdgcn_s_sleep(1);
         rtag = vload(&ctl.ringtag[rslot]);
         x = vload(&ring[ridx]);
       }
-      if (spins > a.spin_max) {
+      if (spins > spin_max) {
         bad = true;
         expired = true;
         break;
@@ -2939,13 +2947,11 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       }
       if (!accept) {   // ring row q: the values of the token decided here
         spins = 0;
-        while (!exact && rc.ring && vload(&ctl.ringtag[q & (kRing - 1)]) != q && ++spins <= a.spin_max)
+        while (!exact && rc.ring && vload(&ctl.ringtag[q & (kRing - 1)]) != q && ++spins <= spin_max)
           __builtin_amdgcn_s_sleep(1);   // the decider's gather lands first
-        if (spins > a.spin_max) {   // its late gather could overwrite this ring row
-          bad = true;
-          expired = true;
-          break;
-        }
+        // A late gather could still overwrite this ring row: the row stops
+        // after this step (its decision stands), at the loop's test.
+        if (spins > spin_max) bad = expired = true;
         issue_ring(q, tokq);
         wait_vm(0);
         if (lane == 0) vstore(&ctl.ringtag[q & (kRing - 1)], q);
@@ -3234,8 +3240,10 @@ struct IdxHit {
 };
 
 // At most 128 VGPRs (four waves a SIMD): two workgroups of five waves share a CU.
+template <bool kForcedLimit>
 __global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k_stream_lspec(StreamArgs a,
                                                                                           StreamWs w) {
+  const int spin_max = kForcedLimit ? a.spin_max : kSpinMaxDefault;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ LSpecRec recs[kLND];
   __shared__ LSpecCtl ctl;
@@ -3335,8 +3343,8 @@ __global__ __launch_bounds__(NTL) __attribute__((amdgpu_waves_per_eu(4))) void k
       const int k = (q - s_first) % kLND;
       LSpecRec& rc = recs[k];
       int spins = 0;
-      while (vload(&rc.tag) != q && ++spins <= a.spin_max) __builtin_amdgcn_s_sleep(1);
-      if (spins > a.spin_max) {
+      while (vload(&rc.tag) != q && ++spins <= spin_max) __builtin_amdgcn_s_sleep(1);
+      if (spins > spin_max) {
         bad = true;
         expired = true;
         break;
@@ -3615,14 +3623,20 @@ size_t stream_lspec_lds_bytes(int V) {
 hipError_t launch_stream_lspec(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_lspec, dim3(a.n_rows), dim3(NTL), stream_lspec_lds_bytes(a.vocab), s, a, w);
+  if (a.spin_max == kSpinMaxDefault)
+    hipLaunchKernelGGL(k_stream_lspec<false>, dim3(a.n_rows), dim3(NTL), stream_lspec_lds_bytes(a.vocab), s, a, w);
+  else
+    hipLaunchKernelGGL(k_stream_lspec<true>, dim3(a.n_rows), dim3(NTL), stream_lspec_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 
 hipError_t launch_stream_spec(const StreamArgs& a, const StreamWs& w, hipStream_t s) {
   if (a.n_rows <= 0 || w.s_end <= w.s_begin) return hipSuccess;
   (void)hipGetLastError();
-  hipLaunchKernelGGL(k_stream_spec, dim3(a.n_rows), dim3(NTS), stream_spec_lds_bytes(a.vocab), s, a, w);
+  if (a.spin_max == kSpinMaxDefault)
+    hipLaunchKernelGGL(k_stream_spec<false>, dim3(a.n_rows), dim3(NTS), stream_spec_lds_bytes(a.vocab), s, a, w);
+  else
+    hipLaunchKernelGGL(k_stream_spec<true>, dim3(a.n_rows), dim3(NTS), stream_spec_lds_bytes(a.vocab), s, a, w);
   return hipGetLastError();
 }
 
