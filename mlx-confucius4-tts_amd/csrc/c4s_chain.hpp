@@ -409,10 +409,228 @@ __device__ void bitonic_sort_u32(uint32_t* buf, int P) {
   }
 }
 
+// Ascending sort of n keys, stable LSD radix in 6-bit digits (buf -> tmp ->
+// buf ...): wave w owns the keys [w * seg, (w + 1) * seg); a digit's keys go
+// out in (digit, wave, position) order through a scan of per-wave counts
+// (hist: 64 * NWX words, column w written by wave w alone), and a lane's rank
+// among the lanes of its digit comes from six ballots. Digits in which no two
+// keys differ (`varying`: the OR of the keys XOR their AND) take no pass; the
+// keys end in buf. tot: NWX words for the scan's per-wave totals.
+template <int NWX>
+__device__ void radix_sort_asc_u32(uint32_t* buf, uint32_t* tmp, int n, uint32_t varying, uint32_t* hist,
+                                   uint32_t* tot) {
+  constexpr int NTX = NWX * kWave, kBits = 6, kNB = 1 << kBits;
+  constexpr int kPer = kNB * NWX / NTX;   // histogram words a thread scans
+  static_assert(kPer * NTX == kNB * NWX, "the scan covers the histogram");
+  const int t = threadIdx.x, w = wave_id(), lane = lane_id();
+  const int seg = (n + NWX - 1) / NWX;
+  const int lo = min(n, w * seg), hi = min(n, lo + seg);
+  const uint64_t below = lanemask_lt();
+  uint32_t* src = buf;
+  uint32_t* dst = tmp;
+  for (int shift = 0; shift < 32; shift += kBits) {
+    if (((varying >> shift) & (kNB - 1)) == 0u) continue;
+    for (int i = t; i < kNB * NWX; i += NTX) hist[i] = 0u;
+    __syncthreads();
+    // per-wave digit counts: the lowest lane of each digit adds its lanes
+    for (int b0 = lo; b0 < hi; b0 += kWave) {
+      const int b = b0 + lane;
+      const bool live = b < hi;
+      const uint32_t d = live ? (src[b] >> shift) & (kNB - 1) : 0u;
+      uint64_t same = __ballot(live);
+#pragma unroll
+      for (int bit = 0; bit < kBits; ++bit) {
+        const uint64_t on = __ballot(live && ((d >> bit) & 1u));
+        same &= ((d >> bit) & 1u) ? on : ~on;
+      }
+      if (live && (same & below) == 0ull) hist[d * NWX + w] += (uint32_t)__popcll(same);
+    }
+    __syncthreads();
+    // exclusive scan of the counts in (digit, wave) order
+    uint32_t v[kPer], loc = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) { v[i] = hist[t * kPer + i]; loc += v[i]; }
+    const uint32_t inc = wave_scan_u32(loc);
+    if (lane == kWave - 1) tot[w] = inc;
+    __syncthreads();
+    uint32_t ex = inc - loc;
+    for (int i = 0; i < w; ++i) ex += tot[i];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) { hist[t * kPer + i] = ex; ex += v[i]; }
+    __syncthreads();
+    // scatter in each wave's order: hist[d][w] is the next place of (d, w)
+    for (int b0 = lo; b0 < hi; b0 += kWave) {
+      const int b = b0 + lane;
+      const bool live = b < hi;
+      const uint32_t key = live ? src[b] : 0u;
+      const uint32_t d = (key >> shift) & (kNB - 1);
+      uint64_t same = __ballot(live);
+#pragma unroll
+      for (int bit = 0; bit < kBits; ++bit) {
+        const uint64_t on = __ballot(live && ((d >> bit) & 1u));
+        same &= ((d >> bit) & 1u) ? on : ~on;
+      }
+      uint32_t* place = &hist[d * NWX + w];
+      const uint32_t base = *place;
+      if (live) dst[base + __popcll(same & below)] = key;
+      __builtin_amdgcn_wave_barrier();   // every lane has read its place before one lane a digit moves it
+      if (live && (same & below) == 0ull) *place = base + (uint32_t)__popcll(same);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    __syncthreads();
+    uint32_t* x = src;
+    src = dst;
+    dst = x;
+  }
+  if (src != buf) {   // an odd number of passes
+    for (int i = t; i < n; i += NTX) buf[i] = src[i];
+    __syncthreads();
+  }
+}
+
+// exact_top_p (below) in the form for a workgroup of eight waves whose row and work area
+// are in LDS and whose registers are its own (the one-AR-step kernel's
+// fallback): one slot claim per wave and 64 keys; the radix sort when the work
+// area holds the keys twice (else the bitonic network); the masses in two
+// alternating windows, waves 1.. computing the next while wave 0 adds the
+// current one in unguarded 16-term blocks.
+template <int NWX, class Src>
+__device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh, float maxv, double thr, int V,
+                                      uint32_t* buf) {
+  constexpr int NTX = NWX * kWave;
+  const int lane = lane_id(), w = wave_id();
+  if (threadIdx.x == 0) sh.counter = 0;
+  __syncthreads();
+  // the finite keys; their OR and AND tell the radix sort which digits vary
+  uint32_t kor = 0u, kand = ~0u;
+  for (int b0 = sg.lo; b0 < sg.hi; b0 += kWave) {
+    const int i = b0 + lane;
+    const float zi = i < sg.hi ? src.z(i) : neg_inf();
+    const bool fin = zi != neg_inf();
+    const uint64_t m = __ballot(fin);
+    uint32_t slot = 0u;
+    if (lane == 0 && m != 0ull) slot = atomicAdd(&sh.counter, (uint32_t)__popcll(m));
+    slot = (uint32_t)__shfl((int)slot, 0, kWave);
+    if (fin) {
+      const uint32_t k = fkey(zi);
+      buf[slot + __popcll(m & lanemask_lt())] = k;
+      kor |= k;
+      kand &= k;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    kor |= (uint32_t)__shfl_xor((int)kor, o, kWave);
+    kand &= (uint32_t)__shfl_xor((int)kand, o, kWave);
+  }
+  if (lane == 0) {
+    sh.redu[w] = kor;
+    sh.wcnt[w] = kand;
+  }
+  __syncthreads();
+  const int nf = (int)sh.counter;
+  kor = 0u;
+  kand = ~0u;
+#pragma unroll
+  for (int i = 0; i < NWX; ++i) {
+    kor |= sh.redu[i];
+    kand &= sh.wcnt[i];
+  }
+  C4S_PHASE(11);
+  const size_t cap = src.sort_bytes();
+  if (cap >= 8 * (size_t)nf) {
+    // the second half of the work area and the selection histograms (free here)
+    radix_sort_asc_u32<NWX>(buf, buf + nf, nf, kor ^ kand, reinterpret_cast<uint32_t*>(sh.hmass), sh.hcnt);
+  } else {
+    int P = 1;
+    while (P < nf) P <<= 1;
+    for (int i = nf + threadIdx.x; i < P; i += NTX) buf[i] = 0xFFFFFFFFu;
+    __syncthreads();
+    bitonic_sort_u32<NTX>(buf, P);
+  }
+  C4S_PHASE(12);
+  const size_t kb = ((size_t)nf * 4 + 15) & ~(size_t)15;
+  const int W2 = cap > kb ? (int)min((size_t)2048, (cap - kb) / 16) & ~(kWave - 1) : 0;
+  if (W2 >= kWave) {
+    // window k of the masses (divided by div unless it is 0) and zeros up to
+    // its last 16-term block, by threads t0, t0 + nt, ...
+    auto fill = [&](double* dst, int k, double div, int t0, int nt) {
+      const int w0 = k * W2, wn = min(W2, nf - w0), wn16 = (wn + 15) & ~15;
+      for (int j = t0; j < wn16; j += nt) {
+        double e = 0.0;
+        if (j < wn) {
+          e = exp((double)(kfloat(buf[w0 + j]) - maxv));
+          if (div != 0.0) e = e / div;
+        }
+        dst[j] = e;
+      }
+    };
+    const int nwin = (nf + W2 - 1) / W2;
+    double* const ew = reinterpret_cast<double*>(reinterpret_cast<unsigned char*>(buf) + kb);
+    double* const win[2] = {ew, ew + W2};
+    fill(win[0], 0, 0.0, threadIdx.x, NTX);
+    __syncthreads();
+    double total = 0.0;
+    for (int k = 0; k < nwin; ++k) {
+      if (w == 0) total = seq_sum_blk(total, win[k & 1], min(W2, nf - k * W2));
+      else if (k + 1 < nwin) fill(win[(k + 1) & 1], k + 1, 0.0, threadIdx.x - kWave, NTX - kWave);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) sh.bd[7] = total;
+    __syncthreads();
+    total = sh.bd[7];
+    C4S_PHASE(13);
+    fill(win[0], 0, total, threadIdx.x, NTX);
+    __syncthreads();
+    double cum = 0.0;
+    for (int k = 0; k < nwin; ++k) {
+      // the stop flag alternates between bu[6] and bu[7]: wave 0 sets the next
+      // one while the other waves may still read this one
+      if (w == 0) {
+        bool stop = false;
+        const uint32_t removed = k * W2 + seq_cut_blk(cum, win[k & 1], min(W2, nf - k * W2), thr, stop);
+        if (lane == 0) {
+          sh.bu[4] = removed;
+          sh.bu[6 + (k & 1)] = stop ? 1u : 0u;
+        }
+      } else if (k + 1 < nwin) {
+        fill(win[(k + 1) & 1], k + 1, total, threadIdx.x - kWave, NTX - kWave);
+      }
+      __syncthreads();
+      if (sh.bu[6 + (k & 1)]) break;
+    }
+  } else if (w == 0) {
+    double total = 0.0;
+    for (int base = 0; base < nf; base += kWave) {
+      const int j = base + lane;
+      const double e = (j < nf) ? exp((double)(kfloat(buf[j]) - maxv)) : 0.0;
+      total = seq_sum_lanes(total, e, min(kWave, nf - base));
+    }
+    double cum = 0.0;
+    uint32_t removed = 0;
+    bool stop = false;
+    for (int base = 0; base < nf && !stop; base += kWave) {
+      const int j = base + lane;
+      const double q = (j < nf) ? exp((double)(kfloat(buf[j]) - maxv)) / total : 0.0;
+      removed = base + seq_cut_lanes(cum, q, min(kWave, nf - base), thr, stop);
+    }
+    if (lane == 0) sh.bu[4] = removed;
+  }
+  __syncthreads();
+  C4S_PHASE(15);
+  const uint32_t rfin = sh.bu[4];
+  __syncthreads();
+  return (long long)(V - nf) + rfin;
+}
+
 // Exact top_p removal count: sorts the finite keys ascending, then wave 0 runs
 // sampling.cpp:52-65 literally (sequential double sum, then sequential
 // cum += prob/sum against 1 - p). Returns R over all V positions (the -inf
-// positions come first in ascending order with probability 0).
+// positions come first in ascending order with probability 0). The form
+// for kernels that inline the chain beside live registers of their own: a
+// claim per key, the bitonic network, one window at a time.
 template <int NWX, class Src>
 __device__ long long exact_top_p(const Src& src, Seg sg, ScratchT<NWX>& sh, float maxv, double thr,
                                  int V, uint32_t* buf, uint32_t& n_fin_out) {
@@ -880,9 +1098,9 @@ __device__ __forceinline__ bool fast_topk_any(const float* val, int V, const Row
 }
 
 // ---- the chain ------------------------------------------------------------------
-template <int NWX, class Src>
+template <int NWX, class Src, bool kFastExact = false>
 __device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowCfg& c, uint64_t& rng,
-                                         float* masked, uint32_t* stats) {
+                                         float* masked, uint32_t* stats, bool tp_exact_first = false) {
   constexpr int NTX = NWX * kWave;
   const int V = c.V;
   const Seg sg = my_seg<NWX>(V);
@@ -923,17 +1141,22 @@ __device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowC
   bool any_kept = true;
   if (c.topp_on && maxv != neg_inf()) {
     st_path |= 4u;
+    // tp_exact_first: the caller's own mass test missed its margin with double
+    // sums, so the one below would too; the exact emulation decides at once
+    // (p < 1 is 1 - p > 0)
+    const bool direct = tp_exact_first && c.p < 1.0f;
     double sl = 0.0;
     uint32_t zl = 0;
-    for (int i = sg.lo + lane; i < sg.hi; i += kWave) {
-      const float zi = src.z(i);
-      const double e = (zi == neg_inf()) ? 0.0 : exp((double)(zi - maxv));
-      if (Src::kCache) src.cache(i, e);
-      sl += e;
-      zl += (e == 0.0) ? 1u : 0u;
-    }
-    const double S = block_sum_f64<NTX>(sl, sh.redd);
-    cache_ok = Src::kCache;
+    if (!direct)
+      for (int i = sg.lo + lane; i < sg.hi; i += kWave) {
+        const float zi = src.z(i);
+        const double e = (zi == neg_inf()) ? 0.0 : exp((double)(zi - maxv));
+        if (Src::kCache) src.cache(i, e);
+        sl += e;
+        zl += (e == 0.0) ? 1u : 0u;
+      }
+    const double S = direct ? 0.0 : block_sum_f64<NTX>(sl, sh.redd);
+    cache_ok = Src::kCache && !direct;
     const double thr = 1.0 - (double)c.p;   // sampling.cpp:64 compares cum <= (1.0 - p)
     long long R = 0;
     bool have_cross = false;
@@ -944,11 +1167,15 @@ __device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowC
       R = block_sum_u32<NTX>(zl, sh.redu);  // only zero-probability positions have cum == 0
     } else {
       const double eps = rel_eps(V);
-      if (cut_by_mass(src, sg, sh, maxv, thr * S, eps, V, R, cwkey, ceq, cnkeep)) {
+      if (!direct && cut_by_mass(src, sg, sh, maxv, thr * S, eps, V, R, cwkey, ceq, cnkeep)) {
         have_cross = (R < V);
       } else {
-        uint32_t nfin;
-        R = exact_top_p(src, sg, sh, maxv, thr, V, src.sort_buf(), nfin);
+        if constexpr (kFastExact) {
+          R = exact_top_p_fast<NWX>(src, sg, sh, maxv, thr, V, src.sort_buf());
+        } else {
+          uint32_t nfin;
+          R = exact_top_p(src, sg, sh, maxv, thr, V, src.sort_buf(), nfin);
+        }
         cache_ok = false;
         st_tp_exact = 1;
       }

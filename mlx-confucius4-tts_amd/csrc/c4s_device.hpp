@@ -307,6 +307,46 @@ __device__ __forceinline__ int seq_cut_mem(double& cum, const double* p, int n, 
   }
   return n;
 }
+// seq_sum_blk / seq_cut_blk: seq_sum_mem / seq_cut_mem over terms padded with
+// +0.0 to a multiple of 16 (read up to there), so that the blocks need no
+// bounds: the chain is loads and dependent FP64 adds only. An added +0.0
+// leaves a sum >= 0 unchanged and never takes cum above thr. The terms are
+// >= 0, so cum only grows: a block whose last sum is <= thr has every sum
+// <= thr, and only the block that ends above thr is added again, term by
+// term, to find the first.
+__device__ __forceinline__ double seq_sum_blk(double total, const double* p, int n) {
+#pragma unroll 1
+  for (int j = 0; j < n; j += 16) {
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = p[j + i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) total += v[i];
+  }
+  return total;
+}
+__device__ __forceinline__ int seq_cut_blk(double& cum, const double* p, int n, double thr, bool& stop) {
+#pragma unroll 1
+  for (int j = 0; j < n; j += 16) {
+    double v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = p[j + i];
+    double x = cum;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x += v[i];
+    if (!(x <= thr)) {
+      int i = 0;
+      x = cum + p[j];
+#pragma unroll 1
+      while (i < 15 && x <= thr) x += p[j + ++i];
+      stop = true;
+      cum = x;
+      return j + i;
+    }
+    cum = x;
+  }
+  return n;
+}
 // seq_cut_lanes: top_p's removal loop (sampling.cpp:60-65) over n terms from
 // cum: the number of leading terms after which cum <= thr still holds; sets
 // stop when a term took cum above thr (cum only grows).

@@ -119,6 +119,7 @@ __device__ __forceinline__ void step_out(const StepIO& io, int V, int tok, uint6
 struct StepRowSh {
   RowCfg cfg;
   StepIO io;
+  uint32_t tp_exact_first;   // 1: the one pass's top_p test missed its margin in double
 };
 
 template <int PT>
@@ -201,8 +202,9 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
 // top_k rows: every member survives top_k, S = the survivors' mass); kept
 // members are ranks 0 .. k-1. A decision within the margin is taken again with
 // S and the mass above X summed in double. Sets ss.kthr; returns 1 decided, 3
-// decided with the double sums, 0 the multi-pass chain decides (X holds more
-// than one value, or the margin is not met even in double).
+// decided with the double sums, 4 the margin is not met even in double (the
+// multi-pass chain decides, by the exact emulation), 0 the multi-pass chain
+// decides (X holds more than one value; top-k rows; min_tokens_to_keep).
 template <int PT>
 __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule sr, int nX,
                                     double thr, double S, double errS, double Ma, double eMa, uint32_t n_above,
@@ -249,7 +251,8 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
     const bool sure = (k == 0 || fabs(Sx - base - (double)(k - 1) * e - A) > mg) &&
                       (k == nX || fabs(Sx - base - (double)k * e - A) > mg);
     if (sure) break;
-    if (pass == 1 || topk) return 0;
+    if (topk) return 0;
+    if (pass == 1) return 4;
     // decide again with S and the mass above X in double
     double se = 0.0, sa = 0.0;
     for (int j = 0; j < n; ++j) {
@@ -302,11 +305,11 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
 // (`val`), for the rows the one pass leaves; kept out of line so that its
 // registers do not weigh on the one-pass path.
 __device__ __noinline__ void chain_fallback(const StepIO& io, const RowCfg& c, unsigned char* work, float* val,
-                                            StepScratch& sh) {
+                                            StepScratch& sh, bool tp_exact_first) {
   const int V = c.V, t = threadIdx.x;
   uint64_t rng = *io.rng;
   LdsRow src{val, reinterpret_cast<double*>(work), V, 0u, false};
-  const int tok = run_chain(src, sh, c, rng, io.masked, sh.step_stats);
+  const int tok = run_chain<kStepWaves, LdsRow, true>(src, sh, c, rng, io.masked, sh.step_stats, tp_exact_first);
   if (t == 0) {
     const uint32_t* sp = sh.step_stats;
     step_out(io, V, tok, rng, true, sp[0], sp[1], sp[2], sp[3]);
@@ -533,7 +536,7 @@ constexpr int kKindTopK = 0, kKindTopP = 1, kKindDense = 2;
 template <int PT, int kKind>
 __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, const float (&y)[PT], int lo, int n,
                                              float* val, uint32_t* hc, unsigned long long* hm, uint64_t* sbuf,
-                                             uint64_t* list, StepSh& ss, const StepRowSh& rs) {
+                                             uint64_t* list, StepSh& ss, StepRowSh& rs) {
   const int t = threadIdx.x, lane = lane_id(), w = wave_id();
   const float ninf = neg_inf();
   // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----
@@ -763,6 +766,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           verdict = tie_cut<PT>(rs.cfg, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
           tp_exact = verdict == 3;
           if (verdict != 1 && verdict != 3) one_pass = false;
+          if (verdict == 4 && t == 0) rs.tp_exact_first = 1u;
         } else {
           int P2 = 1;
           while (P2 < nX) P2 <<= 1;
@@ -809,6 +813,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           }
           C4S_PHASE(9);
           if (verdict != 1) one_pass = false;
+          if (verdict == 4 && t == 0) rs.tp_exact_first = 1u;
         }
       }
     }
@@ -922,6 +927,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   if (t == 0) {   // read only after the barrier below
     rs.cfg = c;
     rs.io = io;
+    rs.tp_exact_first = 0u;
   }
   const float ninf = neg_inf();
 
@@ -1022,7 +1028,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   if (done) return;
   // ---- the multi-pass chain on the row staged in LDS (c4s_chain.hpp) ----
   __syncthreads();   // every thread is done with the work area
-  chain_fallback(rs.io, rs.cfg, work, val, sh);
+  chain_fallback(rs.io, rs.cfg, work, val, sh, rs.tp_exact_first != 0u);
 }
 
 // ---- large vocabularies: top_k in two passes -----------------------------------------

@@ -389,7 +389,8 @@ __device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const
 // sorted entry (valid below nX). S, errS: the sum of all masses and its error
 // bound (rows without top-k); Ma, errMa: the mass above the boundary buckets
 // and its bound. Writes sh.kthr and sh.verdict (1; 2 when a decision falls
-// inside the margin while fp32 errors remain; 0).
+// inside the margin while fp32 errors remain; 4 when it does with none, on a
+// row without top-k; 0).
 template <bool kBlock>
 __device__ __noinline__ void decide_cut(const RowCfg& c, uint64_t v, int nX, float m, double thr, double S, double errS,
                            double Ma, double errMa, uint32_t n_above, const uint64_t* list, StepSh& sh) {
@@ -445,7 +446,7 @@ __device__ __noinline__ void decide_cut(const RowCfg& c, uint64_t v, int nX, flo
   const uint32_t mk = (uint32_t)max(0, c.min_keep);
   int verdict = 1;
   if (nuns) {
-    verdict = err > 0.0 ? 2 : 0;
+    verdict = err > 0.0 ? 2 : (topk ? 0 : 4);
   } else if (topk) {
     if (nk < mk) nk = min(mk, ns);
   } else if (n_above + nk < mk) {
