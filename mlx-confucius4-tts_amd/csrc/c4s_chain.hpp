@@ -409,93 +409,99 @@ __device__ void bitonic_sort_u32(uint32_t* buf, int P) {
   }
 }
 
-// Ascending sort of n keys, stable LSD radix in 6-bit digits (buf -> tmp ->
-// buf ...): wave w owns the keys [w * seg, (w + 1) * seg); a digit's keys go
-// out in (digit, wave, position) order through a scan of per-wave counts
-// (hist: 64 * NWX words, column w written by wave w alone), and a lane's rank
-// among the lanes of its digit comes from six ballots. Digits in which no two
-// keys differ (`varying`: the OR of the keys XOR their AND) take no pass; the
-// keys end in buf. tot: NWX words for the scan's per-wave totals.
+// Ascending sort of n <= 31 * NTX keys, buf -> buf + tmp_off -> buf ...: every
+// thread owns one chunk of K keys (K odd, so that lanes K words apart hit
+// distinct LDS banks): its run, sorted in registers by a 32-wide bitonic
+// network, then merge-path rounds that double the run length, a thread
+// writing the K outputs of its chunk's place in a pair of runs: a binary
+// search over the pair's diagonal gives where they start in each run, then a
+// sequential merge (equal keys from the first run first, in the search and
+// the merge alike). Ends in buf.
 template <int NWX>
-__device__ void radix_sort_asc_u32(uint32_t* buf, uint32_t* tmp, int n, uint32_t varying, uint32_t* hist,
-                                   uint32_t* tot) {
-  constexpr int NTX = NWX * kWave, kBits = 6, kNB = 1 << kBits;
-  constexpr int kPer = kNB * NWX / NTX;   // histogram words a thread scans
-  static_assert(kPer * NTX == kNB * NWX, "the scan covers the histogram");
-  const int t = threadIdx.x, w = wave_id(), lane = lane_id();
-  const int seg = (n + NWX - 1) / NWX;
-  const int lo = min(n, w * seg), hi = min(n, lo + seg);
-  const uint64_t below = lanemask_lt();
-  uint32_t* src = buf;
-  uint32_t* dst = tmp;
-  for (int shift = 0; shift < 32; shift += kBits) {
-    if (((varying >> shift) & (kNB - 1)) == 0u) continue;
-    for (int i = t; i < kNB * NWX; i += NTX) hist[i] = 0u;
-    __syncthreads();
-    // per-wave digit counts: the lowest lane of each digit adds its lanes
-    for (int b0 = lo; b0 < hi; b0 += kWave) {
-      const int b = b0 + lane;
-      const bool live = b < hi;
-      const uint32_t d = live ? (src[b] >> shift) & (kNB - 1) : 0u;
-      uint64_t same = __ballot(live);
+__device__ void merge_sort_asc_u32(uint32_t* buf, int tmp_off, int n) {
+  constexpr int NTX = NWX * kWave, R = 32;
+  const int t = threadIdx.x;
+  const int K = max(15, ((n + NTX - 1) / NTX) | 1);
+  {
+    const int b = t * K;
+    const int cnt = max(0, min(K, n - b));
+    uint32_t r[R];
 #pragma unroll
-      for (int bit = 0; bit < kBits; ++bit) {
-        const uint64_t on = __ballot(live && ((d >> bit) & 1u));
-        same &= ((d >> bit) & 1u) ? on : ~on;
-      }
-      if (live && (same & below) == 0ull) hist[d * NWX + w] += (uint32_t)__popcll(same);
-    }
-    __syncthreads();
-    // exclusive scan of the counts in (digit, wave) order
-    uint32_t v[kPer], loc = 0;
+    for (int i = 0; i < R; ++i) r[i] = i < cnt ? buf[b + i] : 0xFFFFFFFFu;   // the fill sorts last
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) { v[i] = hist[t * kPer + i]; loc += v[i]; }
-    const uint32_t inc = wave_scan_u32(loc);
-    if (lane == kWave - 1) tot[w] = inc;
-    __syncthreads();
-    uint32_t ex = inc - loc;
-    for (int i = 0; i < w; ++i) ex += tot[i];
+    for (int k = 2; k <= R; k <<= 1)
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) { hist[t * kPer + i] = ex; ex += v[i]; }
-    __syncthreads();
-    // scatter in each wave's order: hist[d][w] is the next place of (d, w)
-    for (int b0 = lo; b0 < hi; b0 += kWave) {
-      const int b = b0 + lane;
-      const bool live = b < hi;
-      const uint32_t key = live ? src[b] : 0u;
-      const uint32_t d = (key >> shift) & (kNB - 1);
-      uint64_t same = __ballot(live);
+      for (int j = k >> 1; j > 0; j >>= 1)
 #pragma unroll
-      for (int bit = 0; bit < kBits; ++bit) {
-        const uint64_t on = __ballot(live && ((d >> bit) & 1u));
-        same &= ((d >> bit) & 1u) ? on : ~on;
-      }
-      uint32_t* place = &hist[d * NWX + w];
-      const uint32_t base = *place;
-      if (live) dst[base + __popcll(same & below)] = key;
-      __builtin_amdgcn_wave_barrier();   // every lane has read its place before one lane a digit moves it
-      if (live && (same & below) == 0ull) *place = base + (uint32_t)__popcll(same);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
-    __syncthreads();
-    uint32_t* x = src;
-    src = dst;
-    dst = x;
+        for (int i = 0; i < R; ++i) {
+          const int l = i ^ j;
+          if (l > i) {
+            const uint32_t lo = min(r[i], r[l]), hi = max(r[i], r[l]);
+            r[i] = (i & k) ? hi : lo;
+            r[l] = (i & k) ? lo : hi;
+          }
+        }
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (i < cnt) buf[b + i] = r[i];
   }
-  if (src != buf) {   // an odd number of passes
-    for (int i = t; i < n; i += NTX) buf[i] = src[i];
+  __syncthreads();
+  C4S_PHASE(9);
+  // the source and destination as offsets from buf (a select between two
+  // pointers would hide from the compiler that they are LDS addresses)
+  int so = 0, dso = tmp_off;
+  for (int L = K; L < n; L <<= 1) {
+    const uint32_t* src = buf + so;
+    uint32_t* dst = buf + dso;
+    const int o = t * K;
+    if (o < n) {
+      const int base = o / (2 * L) * (2 * L);
+      const int na = min(L, n - base), nb = min(L, n - base - na);   // na >= 1
+      const uint32_t* A = src + base;
+      const uint32_t* B = A + na;
+      const int d = o - base;
+      int lo = max(0, d - nb), hi = min(d, na);
+      while (lo < hi) {   // the first i whose A[i] comes after B[d - i - 1]
+        const int mid = (lo + hi) >> 1;
+        if (A[mid] <= B[d - mid - 1]) lo = mid + 1;
+        else hi = mid;
+      }
+      int i = lo, j = d - lo;
+      const int cnt = min(K, n - o);
+      // the heads of both runs in registers; past a run's end its last key is
+      // read again and never taken
+      uint32_t av = A[min(i, na - 1)], bv = nb > 0 ? B[min(j, nb - 1)] : 0u;
+#pragma unroll
+      for (int q = 0; q < R; ++q) {
+        if (q < cnt) {
+          const bool ta = j >= nb || (i < na && av <= bv);
+          dst[o + q] = ta ? av : bv;
+          i += ta ? 1 : 0;
+          j += ta ? 0 : 1;
+          const uint32_t nv = ta ? A[min(i, na - 1)] : B[min(j, nb - 1)];
+          av = ta ? nv : av;
+          bv = ta ? bv : nv;
+        }
+      }
+    }
+    __syncthreads();
+    if (L == 512) C4S_PHASE(10);
+    const int x = so;
+    so = dso;
+    dso = x;
+  }
+  if (so != 0) {
+    for (int i = t; i < n; i += NTX) buf[i] = buf[so + i];
     __syncthreads();
   }
 }
 
 // exact_top_p (below) in the form for a workgroup of eight waves whose row and work area
 // are in LDS and whose registers are its own (the one-AR-step kernel's
-// fallback): one slot claim per wave and 64 keys; the radix sort when the work
-// area holds the keys twice (else the bitonic network); the masses in two
+// fallback): one slot claim per wave and 64 keys; the merge sort when the
+// work area holds the keys twice (else the bitonic network); the masses in two
 // alternating windows, waves 1.. computing the next while wave 0 adds the
-// current one in unguarded 16-term blocks.
+// current one in unguarded blocks.
 template <int NWX, class Src>
 __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh, float maxv, double thr, int V,
                                       uint32_t* buf) {
@@ -503,8 +509,7 @@ __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh,
   const int lane = lane_id(), w = wave_id();
   if (threadIdx.x == 0) sh.counter = 0;
   __syncthreads();
-  // the finite keys; their OR and AND tell the radix sort which digits vary
-  uint32_t kor = 0u, kand = ~0u;
+  // the finite keys
   for (int b0 = sg.lo; b0 < sg.hi; b0 += kWave) {
     const int i = b0 + lane;
     const float zi = i < sg.hi ? src.z(i) : neg_inf();
@@ -513,36 +518,14 @@ __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh,
     uint32_t slot = 0u;
     if (lane == 0 && m != 0ull) slot = atomicAdd(&sh.counter, (uint32_t)__popcll(m));
     slot = (uint32_t)__shfl((int)slot, 0, kWave);
-    if (fin) {
-      const uint32_t k = fkey(zi);
-      buf[slot + __popcll(m & lanemask_lt())] = k;
-      kor |= k;
-      kand &= k;
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    kor |= (uint32_t)__shfl_xor((int)kor, o, kWave);
-    kand &= (uint32_t)__shfl_xor((int)kand, o, kWave);
-  }
-  if (lane == 0) {
-    sh.redu[w] = kor;
-    sh.wcnt[w] = kand;
+    if (fin) buf[slot + __popcll(m & lanemask_lt())] = fkey(zi);
   }
   __syncthreads();
-  const int nf = (int)sh.counter;
-  kor = 0u;
-  kand = ~0u;
-#pragma unroll
-  for (int i = 0; i < NWX; ++i) {
-    kor |= sh.redu[i];
-    kand &= sh.wcnt[i];
-  }
+  const int nf = __builtin_amdgcn_readfirstlane((int)sh.counter);
   C4S_PHASE(11);
   const size_t cap = src.sort_bytes();
-  if (cap >= 8 * (size_t)nf) {
-    // the second half of the work area and the selection histograms (free here)
-    radix_sort_asc_u32<NWX>(buf, buf + nf, nf, kor ^ kand, reinterpret_cast<uint32_t*>(sh.hmass), sh.hcnt);
+  if (cap >= 8 * (size_t)nf && nf <= 31 * NTX) {
+    merge_sort_asc_u32<NWX>(buf, nf, nf);   // the second half of the work area
   } else {
     int P = 1;
     while (P < nf) P <<= 1;
@@ -555,10 +538,10 @@ __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh,
   const int W2 = cap > kb ? (int)min((size_t)2048, (cap - kb) / 16) & ~(kWave - 1) : 0;
   if (W2 >= kWave) {
     // window k of the masses (divided by div unless it is 0) and zeros up to
-    // its last 16-term block, by threads t0, t0 + nt, ...
+    // the next multiple of 32 terms, by threads t0, t0 + nt, ...
     auto fill = [&](double* dst, int k, double div, int t0, int nt) {
-      const int w0 = k * W2, wn = min(W2, nf - w0), wn16 = (wn + 15) & ~15;
-      for (int j = t0; j < wn16; j += nt) {
+      const int w0 = k * W2, wn = min(W2, nf - w0), wn32 = (wn + 31) & ~31;
+      for (int j = t0; j < wn32; j += nt) {
         double e = 0.0;
         if (j < wn) {
           e = exp((double)(kfloat(buf[w0 + j]) - maxv));
@@ -569,20 +552,22 @@ __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh,
     };
     const int nwin = (nf + W2 - 1) / W2;
     double* const ew = reinterpret_cast<double*>(reinterpret_cast<unsigned char*>(buf) + kb);
-    double* const win[2] = {ew, ew + W2};
-    fill(win[0], 0, 0.0, threadIdx.x, NTX);
+    // window k's buffer: offsets from one base (a select between two pointers
+    // would hide from the compiler that they are LDS addresses)
+    auto win = [&](int k) { return ew + (k & 1) * W2; };
+    fill(win(0), 0, 0.0, threadIdx.x, NTX);
     __syncthreads();
     double total = 0.0;
     for (int k = 0; k < nwin; ++k) {
-      if (w == 0) total = seq_sum_blk(total, win[k & 1], min(W2, nf - k * W2));
-      else if (k + 1 < nwin) fill(win[(k + 1) & 1], k + 1, 0.0, threadIdx.x - kWave, NTX - kWave);
+      if (w == 0) total = seq_sum_blk(total, win(k), min(W2, nf - k * W2));
+      else if (k + 1 < nwin) fill(win(k + 1), k + 1, 0.0, threadIdx.x - kWave, NTX - kWave);
       __syncthreads();
     }
     if (threadIdx.x == 0) sh.bd[7] = total;
     __syncthreads();
     total = sh.bd[7];
     C4S_PHASE(13);
-    fill(win[0], 0, total, threadIdx.x, NTX);
+    fill(win(0), 0, total, threadIdx.x, NTX);
     __syncthreads();
     double cum = 0.0;
     for (int k = 0; k < nwin; ++k) {
@@ -590,13 +575,13 @@ __device__ long long exact_top_p_fast(const Src& src, Seg sg, ScratchT<NWX>& sh,
       // one while the other waves may still read this one
       if (w == 0) {
         bool stop = false;
-        const uint32_t removed = k * W2 + seq_cut_blk(cum, win[k & 1], min(W2, nf - k * W2), thr, stop);
+        const uint32_t removed = k * W2 + seq_cut_blk(cum, win(k), min(W2, nf - k * W2), thr, stop);
         if (lane == 0) {
           sh.bu[4] = removed;
           sh.bu[6 + (k & 1)] = stop ? 1u : 0u;
         }
       } else if (k + 1 < nwin) {
-        fill(win[(k + 1) & 1], k + 1, total, threadIdx.x - kWave, NTX - kWave);
+        fill(win(k + 1), k + 1, total, threadIdx.x - kWave, NTX - kWave);
       }
       __syncthreads();
       if (sh.bu[6 + (k & 1)]) break;

@@ -308,43 +308,47 @@ __device__ __forceinline__ int seq_cut_mem(double& cum, const double* p, int n, 
   return n;
 }
 // seq_sum_blk / seq_cut_blk: seq_sum_mem / seq_cut_mem over terms padded with
-// +0.0 to a multiple of 16 (read up to there), so that the blocks need no
-// bounds: the chain is loads and dependent FP64 adds only. An added +0.0
-// leaves a sum >= 0 unchanged and never takes cum above thr. The terms are
-// >= 0, so cum only grows: a block whose last sum is <= thr has every sum
-// <= thr, and only the block that ends above thr is added again, term by
-// term, to find the first.
+// +0.0 to a multiple of 32, for callers whose n is uniform: blocks of 32 terms
+// need no bounds, so the loop is 32 loads (the adds start as the first ones
+// arrive) and 32 dependent FP64 adds. An added +0.0 leaves a sum >= 0
+// unchanged and never takes cum above thr. The terms are >= 0, so cum only
+// grows: a block whose last sum is <= thr has every sum <= thr, and only the
+// block that ends above thr is added again, term by term, to find the first.
 __device__ __forceinline__ double seq_sum_blk(double total, const double* p, int n) {
+  n = __builtin_amdgcn_readfirstlane(n);
 #pragma unroll 1
-  for (int j = 0; j < n; j += 16) {
-    double v[16];
+  for (int j = 0; j < n; j += 32) {
+    double v[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = p[j + i];
+    for (int i = 0; i < 32; ++i) v[i] = p[j + i];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) total += v[i];
+    for (int i = 0; i < 32; ++i) total += v[i];
   }
   return total;
 }
 __device__ __forceinline__ int seq_cut_blk(double& cum, const double* p, int n, double thr, bool& stop) {
+  n = __builtin_amdgcn_readfirstlane(n);
+  double x = cum;
 #pragma unroll 1
-  for (int j = 0; j < n; j += 16) {
-    double v[16];
+  for (int j = 0; j < n; j += 32) {
+    double v[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = p[j + i];
-    double x = cum;
+    for (int i = 0; i < 32; ++i) v[i] = p[j + i];
+    double y = x;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x += v[i];
-    if (!(x <= thr)) {
+    for (int i = 0; i < 32; ++i) y += v[i];
+    if (__builtin_amdgcn_readfirstlane(y <= thr ? 0 : 1)) {   // every lane holds the same sums
       int i = 0;
-      x = cum + p[j];
+      x += p[j];
 #pragma unroll 1
-      while (i < 15 && x <= thr) x += p[j + ++i];
+      while (i < 31 && x <= thr) x += p[j + ++i];
       stop = true;
       cum = x;
       return j + i;
     }
-    cum = x;
+    x = y;
   }
+  cum = x;
   return n;
 }
 // seq_cut_lanes: top_p's removal loop (sampling.cpp:60-65) over n terms from
