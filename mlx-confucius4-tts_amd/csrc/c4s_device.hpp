@@ -14,6 +14,12 @@
 #ifndef C4S_PHASE
 #define C4S_PHASE(n) ((void)0)
 #endif
+#ifndef C4S_PHASE_IF
+#define C4S_PHASE_IF(cond, n) ((void)0)
+#endif
+#ifndef C4S_PHASE_VAL
+#define C4S_PHASE_VAL(n, v) ((void)0)
+#endif
 #ifndef C4S_SCAN_PHASE
 #define C4S_SCAN_PHASE(n) ((void)0)
 #endif
@@ -150,6 +156,37 @@ __device__ __forceinline__ double dpp_f64(double v, double fill) {
   const uint32_t hi = dpp_u32<CTRL, ROW_MASK>((uint32_t)(b >> 32), (uint32_t)(f >> 32));
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
+
+// Lane i's value from lane i ^ J. J = 1, 2: quad permutes; J = 4, 8: row shifts
+// by J inside the lane's 16-lane row (lane i reads i + J where bit J of i is
+// clear, i - J where it is set); wider: a cross-lane permute through LDS.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v) {
+  if constexpr (J == 1) {
+    return dpp_u32<0xB1>(v, v);   // quad_perm [1, 0, 3, 2]
+  } else if constexpr (J == 2) {
+    return dpp_u32<0x4E>(v, v);   // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4 || J == 8) {
+    const uint32_t up = dpp_u32<0x100 + J>(v, v), dn = dpp_u32<0x110 + J>(v, v);
+    return (lane_id() & J) ? dn : up;
+  } else {
+    return (uint32_t)__shfl_xor((int)v, J, kWave);
+  }
+}
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
+  return ((uint64_t)xor_lane_u32<J>((uint32_t)(v >> 32)) << 32) | xor_lane_u32<J>((uint32_t)v);
+}
+
+// fl32(x / d) for floats x and d, given r = fl64(1 / d): fl32(fl64(x * r)).
+// Exact for every x (+-0 and +-inf included): fl64(x * r) lies within
+// 2^-52 (1 + 2^-54) relative of x / d, while a quotient of two floats lies
+// farther than 2^-49 relative from every float and every midpoint between
+// floats that it does not equal (x - d M is a nonzero integer multiple of
+// 2^min(e_x, e_d + e_M), so |x / d - M| >= 2^e_M / 2^24 for a midpoint M of
+// 25-bit odd significand, normal or subnormal), so both round to one float.
+// One multiply and two conversions instead of the IEEE divide's ten steps.
+__device__ __forceinline__ float div_rcp(float x, double r) { return (float)((double)x * r); }
 
 // Inclusive scans in lane order (Hillis-Steele inside 16-lane rows, then the
 // row totals through row_bcast:15 / row_bcast:31).

@@ -122,10 +122,11 @@ struct StepRowSh {
   uint32_t tp_exact_first;   // 1: the one pass's top_p test missed its margin in double
 };
 
-template <int PT>
+template <int PT, bool kCached>
 __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, const KeptRule& kr, const float (&z)[PT],
                                             int lo, int n, float m, const Scan2& ds, uint32_t n_kept,
-                                            uint32_t st_path, uint32_t st_exact, StepSh& ss, const StepRowSh& rs) {
+                                            uint32_t st_path, uint32_t st_exact, StepSh& ss, const StepRowSh& rs,
+                                            const float* em) {
   const int t = threadIdx.x;
   const uint64_t st2 = xorshift64(*io.rng);
   const double u = unit_from_state(st2);
@@ -139,20 +140,44 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
   const bool owner = (ds.ex < r && r <= ds.in) || (t == kStepThreads - 1 && r > ds.in);
   int found = -1;
   bool certain = false;
+  C4S_PHASE_IF(owner, 18);
   if (owner) {
-    double acc = ds.ex, prev = ds.ex;
+    // the thread's kept masses first (independent loads and tests, issued
+    // together), then the prefix in id order without branches: the first
+    // kept id whose running sum reaches r, and the sums on both sides of it
+    float e[PT];
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      bool kp;
-      const float ej = j < n ? kept_mass32(kr, z[j], m, lo + j, kp) : 0.0f;
-      if (found < 0 && ej > 0.0f) {
-        const double na = acc + (double)ej;
-        if (na >= r) { found = lo + j; prev = acc; }
-        acc = na;
+      if constexpr (kCached) {   // z is -inf past the thread's ids: not kept here
+        const float ec = em[min(lo + j, c.V - 1)];
+        e[j] = ((int)(z[j] != neg_inf()) & (int)kept_in(kr, z[j], m, lo + j)) ? ec : 0.0f;
+      } else {
+        bool kp;
+        e[j] = kept_mass32(kr, z[j], m, lo + j, kp);
       }
     }
+    // running sums in id order (adding a zero mass leaves a sum as it is),
+    // then the first kept id whose sum reaches r, all as selects
+    double pre[PT];
+    double a = ds.ex;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      a = a + (double)e[j];
+      pre[j] = a;
+    }
+    int fj = PT;
+#pragma unroll
+    for (int j = PT - 1; j >= 0; --j) fj = ((e[j] > 0.0f) & (pre[j] >= r)) ? j : fj;
+    double acc = a, prev = ds.ex;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      acc = (j == fj) ? pre[j] : acc;
+      prev = (j + 1 == fj) ? pre[j] : prev;
+    }
+    found = fj < PT ? lo + fj : -1;
     certain = found >= 0 && (acc - r > margin) && (r - prev > margin);
   }
+  C4S_PHASE_IF(owner, 19);
   if (!__syncthreads_or(owner && !certain)) {
     if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, 0u, n_kept);
     return;
@@ -536,13 +561,14 @@ constexpr int kKindTopK = 0, kKindTopP = 1, kKindDense = 2;
 template <int PT, int kKind>
 __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, const float (&y)[PT], int lo, int n,
                                              float* val, uint32_t* hc, unsigned long long* hm, uint64_t* sbuf,
-                                             uint64_t* list, StepSh& ss, StepRowSh& rs) {
+                                             uint64_t* list, float* em, StepSh& ss, StepRowSh& rs) {
   const int t = threadIdx.x, lane = lane_id(), w = wave_id();
   const float ninf = neg_inf();
   // ---- sampled rows: temperature (sampling.cpp:14-17) and the maximum ----
   float z[PT];
+  const double rt = 1.0 / (double)c.temp;   // used only when the temperature applies
 #pragma unroll
-  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? y[j] / c.temp : y[j];
+  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? div_rcp(y[j], rt) : y[j];
   {
     float lm = ninf;
 #pragma unroll
@@ -583,6 +609,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         atomicAdd(&hc[w * kNB + b], b < kNB - 1 ? 1u : 0u);
       } else {
         float ej = fin ? mass32(tt) : 0.0f;
+        if (j < n) em[lo + j] = ej;   // read again by the kept sums and the draw
         if (dense) {
           // p == 1 removes the zero-mass positions: exp((double)tt) == 0 below
           // about -745.13; near that, and for subnormal kept masses, the chain decides
@@ -591,9 +618,9 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           ej = kp ? ej : 0.0f;
           kc += kp ? 1u : 0u;
         } else {
-          // 2^-32 fixed point, truncated (ej <= 1; 1 itself saturates 256 units low)
+          // 2^-31 fixed point, truncated (ej <= 1)
           const int b = bucket_of(z[j], m);
-          const uint32_t q = (uint32_t)fminf(ej * 0x1p32f, 4294967040.0f);
+          const uint32_t q = (uint32_t)(ej * 0x1p31f);
           atomicAdd(&hm[w * kNB + b], b < kNB - 1 ? (unsigned long long)q + kHistOne : 0ull);
         }
         s32 += ej;
@@ -617,7 +644,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         for (int j = 0; j < PT; ++j)
           if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
       C4S_PHASE(10);
-      draw_finish<PT>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs);
+      draw_finish<PT, true>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs, em);
       C4S_PHASE(15);
       return true;
     } else {
@@ -636,7 +663,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           ms += h & (kHistOne - 1ull);
         }
         bcnt[t] = cn;
-        bmass[t] = (double)ms * 0x1p-32;
+        bmass[t] = (double)ms * 0x1p-31;
       }
       __syncthreads();
       const double B = S - thr * S;   // the mass the kept entries hold
@@ -649,6 +676,8 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           ss.bsel[2] = (int)bd.above;
           ss.thru = bd.thru;
           ss.mab = bd.mabove;
+          ss.mabx = topk ? 0.0 : bd.mabove;   // top_k: nothing lies above X
+          ss.nabx = topk ? 0u : bd.above;
           ss.nx = 0u;
         }
       }
@@ -678,7 +707,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
               if (b >= lo2 && b <= bhi) {
                 const int sb = sub_bucket_of(z[j], m, lo2, sc2);
                 if (topk) atomicAdd(&hc[w * kNB + sb], 1u);
-                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(mass32(z[j] - m) * 0x1p32f) + kHistOne);
+                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(uint32_t)(mass32(z[j] - m) * 0x1p31f) + kHistOne);
               }
             }
           }
@@ -693,7 +722,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
               ms += h & (kHistOne - 1ull);
             }
             bcnt[t] = cn;
-            bmass[t] = (double)ms * 0x1p-32;
+            bmass[t] = (double)ms * 0x1p-31;
           }
           __syncthreads();
           if (w == 0) {
@@ -702,6 +731,10 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
             if (lane == 0) {
               ss.sub[0] = topk ? 0 : b2.lo;   // top_k: every entry above the k-th stays in the sort
               ss.sub[1] = b2.hi;
+              if (!topk) {
+                ss.mabx = b2.mabove;
+                ss.nabx = b2.above;
+              }
             }
           }
           __syncthreads();
@@ -709,6 +742,8 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           shi = ss.sub[1];
         }
       }
+      C4S_PHASE(16);
+      C4S_PHASE_VAL(21, refine ? 1 : 0);
       if (blo < 0 || bhi < 0 || slo < 0 || shi < 0) {
         one_pass = false;
       } else {
@@ -721,45 +756,44 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         auto side = [&](float zj) { return sr.side(zj); };
         // X's entries go to `list`, each wave taking one block of slots with
         // one atomic (slot order is arbitrary: the sort orders them)
-        float ma32 = 0.0f;
-        uint32_t na = 0, xm = 0, cx = 0;   // entries above X; this thread's X entries
+        static_assert(PT < 32, "a thread's X entries as one bit mask");
+        uint32_t xm = 0;   // this thread's X entries (its ids only: the -inf padding may lie in the last bucket)
+        if (!refine) {   // uniform: X is whole buckets xlo .. xhi
 #pragma unroll
-        for (int j = 0; j < PT; ++j) {
-          const int sd = side(z[j]);
-          const bool inx = j < n && sd == 0, abv = j < n && sd < 0;
-          xm |= inx ? 1u << j : 0u;
-          cx += inx ? 1u : 0u;
-          if (abv) {   // few entries lie above X: a branch skips whole waves
-            ma32 += mass32(z[j] - m);
-            ++na;
+          for (int j = 0; j < PT; ++j) {
+            const int b = bucket_of(z[j], m);
+            xm |= ((int)(b >= xlo) & (int)(b <= xhi)) ? 1u << j : 0u;
           }
+        } else {
+#pragma unroll
+          for (int j = 0; j < PT; ++j) xm |= (side(z[j]) == 0) ? 1u << j : 0u;
         }
+        xm &= (1u << n) - 1u;
         {
+          const uint32_t cx = (uint32_t)__popc(xm);
           const uint32_t inc = wave_scan_u32(cx);
           uint32_t wb = 0;
           if (lane == kWave - 1 && inc > 0u) wb = atomicAdd(&ss.nx, inc);
-          uint32_t slot = readlane_u32(wb, kWave - 1) + inc - cx;
+          const uint32_t base = readlane_u32(wb, kWave - 1) + inc - cx;
 #pragma unroll
-          for (int j = 0; j < PT; ++j) {
-            if ((xm >> j) & 1u) {
-              if (slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
-              ++slot;
-            }
+          for (int j = 0; j < PT; ++j) {   // entry j's slot: the X entries before it
+            const uint32_t slot = base + (uint32_t)__popc(xm & ((1u << j) - 1u));
+            if (((xm >> j) & 1u) && slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
           }
         }
-        double ma = (double)ma32;
-        double ema = ma * (0x1p-20 + PT * 0x1p-24) + (double)na * 0x1p-125;
-        ma = wave_sum_dpp(ma);
-        ema = wave_sum_dpp(ema);
-        na = wave_sum_u32(na);
-        if (lane == 0) { ss.wc[w] = ma; ss.wd[w] = ema; ss.wv[w] = na; }
+        C4S_PHASE(17);
         __syncthreads();
         C4S_PHASE(7);
         const int nX = (int)ss.nx;
-        double Ma = 0.0, eMa = 0.0;
-        uint32_t n_above = 0;
-#pragma unroll
-        for (int i = 0; i < kStepWaves; ++i) { Ma += ss.wc[i]; eMa += ss.wd[i]; n_above += ss.wv[i]; }
+        C4S_PHASE_VAL(20, nX);
+        // The mass above X and its count, from the histogram: the fixed-point
+        // masses of the (sub-)buckets above X. Against the exact masses each
+        // entry is off by its fp32 mass error (2^-20 relative + 2^-125) and
+        // the truncation (below 2^-31); the bucket sums are exact integers and
+        // the scan's double prefix adds a few 2^-53 relative.
+        const double Ma = ss.mabx;
+        const uint32_t n_above = ss.nabx;
+        const double eMa = Ma * (0x1p-20 + 0x1p-40) + (double)n_above * 0x1p-30;
         if (nX > kSortCap) {
           // more boundary entries than one sort takes: one_pass only if they
           // all hold one value (ties), which needs no sort
@@ -774,14 +808,14 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           uint64_t v = 0ull;
           if (block) {
             v = t < nX ? list[t] : 0ull;
-            v = sort_desc(v, P2, sbuf);
+            v = sort_desc_block(v, P2, sbuf);
             if (t < nX) list[t] = v;
             __syncthreads();
             C4S_PHASE(8);
             decide_cut<true>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           } else if (w == 0) {
             v = lane < nX ? list[lane] : 0ull;
-            v = sort_desc(v, P2, sbuf);
+            v = sort_desc_wave(v, P2);
             C4S_PHASE(8);
             decide_cut<false>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           }
@@ -812,6 +846,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
             verdict = ss.verdict;
           }
           C4S_PHASE(9);
+          C4S_PHASE_VAL(22, verdict);
           if (verdict != 1) one_pass = false;
           if (verdict == 4 && t == 0) rs.tp_exact_first = 1u;
         }
@@ -827,7 +862,14 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
 #pragma unroll
     for (int j = 0; j < PT; ++j) {   // z is -inf past the thread's ids: never kept with a mass
       bool kp;
-      const float ej = kept_mass32(kr, z[j], m, lo + j, kp);
+      float ej;
+      if (topk) {
+        ej = kept_mass32(kr, z[j], m, lo + j, kp);
+      } else {   // the mass cached by the histogram pass (0 for -inf), read unconditionally
+        const float ec = em[min(lo + j, c.V - 1)];
+        kp = ((int)(z[j] != ninf) & (int)kept_in(kr, z[j], m, lo + j)) != 0;   // z is -inf past the thread's ids
+        ej = kp ? ec : 0.0f;
+      }
       const bool kf = kp && z[j] != ninf;
       flags |= (kf && z[j] - m < -690.0f) ? 1u : 0u;   // subnormal kept masses: libm implementations may disagree
       kc += kf ? 1u : 0u;
@@ -845,8 +887,8 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
     const Scan2 ds = block_scan2(ks, ek, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
     C4S_PHASE(10);
     if ((ds.utot >> 16) == 0u) {
-      draw_finish<PT>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
-                      tp_exact ? 1u : 0u, ss, rs);
+      draw_finish<PT, !topk>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
+                             tp_exact ? 1u : 0u, ss, rs, em);
       C4S_PHASE(15);
       return true;
     }
@@ -981,6 +1023,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   if (c.pen_on) {
     // sampling.cpp:19-28 on this thread's ids in LDS, one set bit at a time
     // (each distinct id once); the row in LDS is the penalised row from here on
+    const double rp = 1.0 / (double)c.pen;
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int b0 = (lo & ~31) + 32 * q;
@@ -991,7 +1034,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
         const int i = b0 + __ffs(bits) - 1;
         bits &= bits - 1;
         const float x = val[i];
-        val[i] = (x < 0) ? x * c.pen : x / c.pen;   // sampling.cpp:26
+        val[i] = (x < 0) ? x * c.pen : div_rcp(x, rp);   // sampling.cpp:26
       }
     }
   }
@@ -1022,9 +1065,10 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   }
 
   bool done;
-  if (c.topk_on) done = sampled_step<PT, kKindTopK>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
-  else if (c.p >= 1.0f) done = sampled_step<PT, kKindDense>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
-  else done = sampled_step<PT, kKindTopP>(io, c, y, lo, n, val, hc, hm, sbuf, list, ss, rs);
+  float* em = reinterpret_cast<float*>(work + kStepWorkBytes);   // per-id fp32 masses
+  if (c.topk_on) done = sampled_step<PT, kKindTopK>(io, c, y, lo, n, val, hc, hm, sbuf, list, em, ss, rs);
+  else if (c.p >= 1.0f) done = sampled_step<PT, kKindDense>(io, c, y, lo, n, val, hc, hm, sbuf, list, em, ss, rs);
+  else done = sampled_step<PT, kKindTopP>(io, c, y, lo, n, val, hc, hm, sbuf, list, em, ss, rs);
   if (done) return;
   // ---- the multi-pass chain on the row staged in LDS (c4s_chain.hpp) ----
   __syncthreads();   // every thread is done with the work area

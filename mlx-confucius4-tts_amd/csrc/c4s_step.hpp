@@ -49,18 +49,19 @@ constexpr int kStepWaves = kStepThreads / kWave;
 static_assert(kStepThreads >= kNB && kStepThreads <= NT, "one bucket per thread in the merge");
 constexpr int kSortCap = kStepThreads;   // boundary entries one sort handles (one per thread)
 // Work area of the one-pass step (aliases the mass cache of the fallback
-// chain): per-wave bucket counters and masses (64-bit fixed point, 2^-32
-// units: integer LDS atomics), two sort exchange buffers, the boundary entries.
+// chain): per-wave bucket counters and masses (64-bit fixed point, 2^-31
+// units: integer LDS atomics), two sort exchange buffers, the boundary
+// entries, then the fp32 mass of every id (top_p and p = 1 rows).
 constexpr size_t kHistBytes = (size_t)kStepWaves * kNB * 4;
 // top_p rows count entries in the same 64-bit atomic as their masses: a mass
-// is at most 2^32 units and a wave's bucket sum stays below 2^46 (at most
+// is at most 2^31 units and a wave's bucket sum stays below 2^44 (at most
 // 64 x 65 entries), so bits 48.. hold the count.
 constexpr unsigned long long kHistOne = 1ull << 48;
 constexpr size_t kStepWorkBytes = 3 * kHistBytes + 3 * (size_t)kSortCap * 8;
 
 __host__ __device__ __forceinline__ size_t step_work_bytes(int V) {
-  const size_t e = 8 * (size_t)vpad(V);
-  return e > kStepWorkBytes ? e : kStepWorkBytes;
+  const size_t e = 8 * (size_t)vpad(V), o = kStepWorkBytes + 4 * (size_t)vpad(V);
+  return e > o ? e : o;
 }
 
 using StepScratch = ScratchT<kStepWaves>;
@@ -109,6 +110,8 @@ struct StepSh {
   float wmin[NW];    // per-wave minimum (the boundary's tie test)
   uint32_t thru;     // entries up to and including the last boundary bucket
   double mab;        // mass of the entries above the first boundary bucket
+  double mabx;       // mass of the entries above X (the boundary (sub-)buckets), from the histogram
+  uint32_t nabx;     // their count
   uint32_t nx;       // boundary entries (compaction counter)
   uint64_t kthr;     // kept iff key64 >= kthr
   int verdict;       // 1 decided, 2 decide again with every mass in double, 0 multi-pass chain
@@ -150,13 +153,14 @@ struct SideRule {
   float m, sc2;
   int xlo, xhi, lo2, slo, shi;
   bool refine;
+  // Every test evaluated and combined by selects: per-value code without
+  // branches (a branch a value costs the wave an exec-mask round trip).
   __device__ __forceinline__ int side(float z) const {
     const int b = bucket_of(z, m);
-    if (b < xlo) return -1;
-    if (b > xhi) return 1;
-    if (!refine || b < lo2) return 0;
     const int sb = sub_bucket_of(z, m, lo2, sc2);
-    return sb < slo ? -1 : (sb > shi ? 1 : 0);
+    const int in_sub = sb < slo ? -1 : (sb > shi ? 1 : 0);
+    const int in_x = ((int)refine & (int)(b >= lo2)) ? in_sub : 0;
+    return b < xlo ? -1 : (b > xhi ? 1 : in_x);
   }
 };
 
@@ -268,27 +272,57 @@ __device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, do
 // Descending bitonic sort of P2 (a power of two, <= kSortCap) distinct keys,
 // one per thread t < P2 (threads at or above P2 carry padding among
 // themselves). Stages across waves exchange through `buf` (two halves of
-// kSortCap keys, one barrier each), stages inside a wave through lane
-// shuffles. For P2 <= 64 only wave 0 calls it and no barrier runs.
-__device__ __forceinline__ uint64_t sort_desc(uint64_t v, int P2, uint64_t* buf) {
+// kSortCap keys, one barrier each), stages inside a wave through DPP lane
+// moves (partners 1-8 lanes apart) or lane permutes (16, 32). Fully unrolled
+// per P2.
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_step(uint64_t v, int t, uint64_t* buf, int& half) {
+  uint64_t p;
+  if constexpr (J >= kWave) {
+    buf[half * kSortCap + t] = v;
+    __syncthreads();
+    p = buf[half * kSortCap + (t ^ J)];
+    half ^= 1;
+  } else {
+    p = xor_lane_u64<J>(v);
+  }
+  const bool take_max = ((t & J) == 0) == ((t & K) == 0);
+  return take_max ? (v > p ? v : p) : (v < p ? v : p);
+}
+template <int K, int J>
+__device__ __forceinline__ uint64_t bitonic_merge(uint64_t v, int t, uint64_t* buf, int& half) {
+  v = bitonic_step<K, J>(v, t, buf, half);
+  if constexpr (J > 1) v = bitonic_merge<K, J / 2>(v, t, buf, half);
+  return v;
+}
+template <int P2, int K = 2>
+__device__ __forceinline__ uint64_t bitonic_sort(uint64_t v, int t, uint64_t* buf, int& half) {
+  v = bitonic_merge<K, K / 2>(v, t, buf, half);
+  if constexpr (K < P2) v = bitonic_sort<P2, 2 * K>(v, t, buf, half);
+  return v;
+}
+// Wave 0 alone (P2 <= 64): no barrier.
+__device__ __forceinline__ uint64_t sort_desc_wave(uint64_t v, int P2) {
   const int t = threadIdx.x;
   int half = 0;
-  for (int k = 2; k <= P2; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      uint64_t p;
-      if (j >= kWave) {
-        buf[half * kSortCap + t] = v;
-        __syncthreads();
-        p = buf[half * kSortCap + (t ^ j)];
-        half ^= 1;
-      } else {
-        p = __shfl_xor(v, j, kWave);
-      }
-      const bool take_max = ((t & j) == 0) == ((t & k) == 0);
-      v = take_max ? (v > p ? v : p) : (v < p ? v : p);
-    }
+  switch (P2) {
+    case 2: return bitonic_sort<2>(v, t, nullptr, half);
+    case 4: return bitonic_sort<4>(v, t, nullptr, half);
+    case 8: return bitonic_sort<8>(v, t, nullptr, half);
+    case 16: return bitonic_sort<16>(v, t, nullptr, half);
+    case 32: return bitonic_sort<32>(v, t, nullptr, half);
+    case 64: return bitonic_sort<64>(v, t, nullptr, half);
+    default: return v;
   }
-  return v;
+}
+// The whole workgroup (64 < P2 <= kSortCap).
+__device__ __forceinline__ uint64_t sort_desc_block(uint64_t v, int P2, uint64_t* buf) {
+  static_assert(kSortCap == 512, "sort sizes up to 512");
+  const int t = threadIdx.x;
+  int half = 0;
+  if (P2 == 128) return bitonic_sort<128>(v, t, buf, half);
+  if (P2 == 256) return bitonic_sort<256>(v, t, buf, half);
+  return bitonic_sort<512>(v, t, buf, half);
 }
 
 // Where one row's inputs and outputs are (the kernel's view of c4s_rows).
