@@ -188,6 +188,72 @@ __device__ __forceinline__ uint64_t xor_lane_u64(uint64_t v) {
 // One multiply and two conversions instead of the IEEE divide's ten steps.
 __device__ __forceinline__ float div_rcp(float x, double r) { return (float)((double)x * r); }
 
+// x_{i+1} = fl(x_i + q) for i < m (q > 0 and x_0 > 0 finite, below 2^53):
+// the final x_m and the number of i <= m with x_i <= thr (a prefix: x does
+// not decrease). Stepping a binade at a time: with x = C ulp (C in [2^52,
+// 2^53), ulp of x's binade) and q = Q ulp + r (0 <= r < ulp), every add that
+// stays in the binade adds exactly D ulp, D = Q + (r > ulp / 2) (r = ulp / 2,
+// a tie resolved by parity, and the add that leaves the binade are taken one
+// at a time), so C grows by D per step while C + D < 2^53.
+// floor(a / b) for 0 <= a < 2^63 and 0 < b < 2^53: the double quotient, then
+// corrected by integer products (the GPU has no 64-bit integer divide).
+__host__ __device__ __forceinline__ long long quot_floor(long long a, long long b) {
+  long long s = (long long)floor((double)a / (double)b);
+  while (s > 0 && s * b > a) --s;
+  while ((s + 1) * b <= a) ++s;
+  return s;
+}
+struct RepAdd {
+  double x;
+  int le;
+};
+__host__ __device__ __noinline__ inline RepAdd repeat_add(double x, double q, int m, double thr, bool need_x) {
+  int i = 0, le = 0;
+  bool counting = true;
+  while (true) {
+    if (counting) {
+      if (x <= thr) le = i + 1;
+      else counting = false;
+    }
+    if (i == m || (!counting && !need_x)) break;
+    const int ex = ilogb(x) + 1;   // x in [2^(ex-1), 2^ex) (no address-taken local: frexp's would live in scratch)
+    const double ulp = ldexp(1.0, ex - 53);
+    const double Qd = floor(ldexp(q, 53 - ex));   // q / ulp (scalings by powers of 2 are exact)
+    const double r = q - Qd * ulp;   // exact: the bits of q below ulp
+    if (r == 0.5 * ulp || Qd >= 0x1p52) {
+      x = x + q;
+      ++i;
+      continue;
+    }
+    const long long Dn = (long long)Qd + (r > 0.5 * ulp ? 1 : 0);
+    if (Dn == 0) {   // every add rounds back to x
+      if (counting) le = m + 1;
+      break;
+    }
+    const long long C = (long long)ldexp(x, 53 - ex);
+    long long sb = quot_floor((1ll << 53) - 1 - C, Dn);   // adds that keep C below 2^53
+    if (sb > (long long)(m - i)) sb = m - i;
+    if (counting) {
+      const double tq = ldexp(thr, 53 - ex);
+      const long long T = tq >= 0x1p62 ? (1ll << 62) : (long long)floor(tq);   // x_k <= thr iff C_k <= T
+      const long long st = quot_floor(T - C, Dn);   // T >= C here
+      if (st < sb) {
+        le = i + (int)st + 1;
+        counting = false;
+        if (!need_x) break;
+      } else {
+        le = i + (int)sb + 1;
+      }
+    }
+    x = (double)(C + sb * Dn) * ulp;   // exact: below 2^53 units of ulp
+    i += (int)sb;
+    if (i == m) break;
+    x = x + q;   // the add that leaves the binade
+    ++i;
+  }
+  return RepAdd{x, le};
+}
+
 // Inclusive scans in lane order (Hillis-Steele inside 16-lane rows, then the
 // row totals through row_bcast:15 / row_bcast:31).
 __device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {

@@ -219,6 +219,26 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
   }
 }
 
+// sampling.cpp:52-65 replayed for a row whose top group X (nX entries at the
+// maximum, mass 1 each) is preceded in ascending order by entries of total
+// mass B (known within relative `re` of the reference's sequential sum):
+// total = B + 1 + ... + 1 and cum = sum of prob / total, both sequential. The
+// sums over the entries below X reach the sequence only through B and B /
+// total; each enters one add (B + 1, then B / total + 1 / total), which rounds
+// every value of its interval to one double, or the replay gives up (-1).
+// Returns the members of X kept (cum > thr), the rest removed in order.
+__device__ __forceinline__ int tie_top_exact(double B, int nX, double thr, double re) {
+  const double t_lo = B * (1.0 - 2.0 * re) + 1.0, t_hi = B * (1.0 + 2.0 * re) + 1.0;
+  if (t_lo != t_hi) return -1;
+  const double tot = repeat_add(t_lo, 1.0, nX - 1, -1.0, true).x;
+  const double q = 1.0 / tot;
+  const double cb = B / tot, cb_hi = cb * (1.0 + 3.0 * re);
+  if (!(cb_hi <= thr)) return -1;   // some entry below X could be kept
+  const double c_lo = cb * (1.0 - 3.0 * re) + q, c_hi = cb_hi + q;
+  if (c_lo != c_hi) return -1;
+  return nX - repeat_add(c_lo, q, nX - 1, thr, false).le;
+}
+
 // The cut when the boundary entries X (more than one sort takes) all hold one
 // value z*: each has the mass e = exp(z* - m), and in the chain's order (value
 // descending, lower id first) X is ordered by id, which is thread order here,
@@ -226,10 +246,12 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
 // below it, M_i = S - (mass above X) - i e, exceeds thr S (sampling.cpp:60-65;
 // top_k rows: every member survives top_k, S = the survivors' mass); kept
 // members are ranks 0 .. k-1. A decision within the margin is taken again with
-// S and the mass above X summed in double. Sets ss.kthr; returns 1 decided, 3
-// decided with the double sums, 4 the margin is not met even in double (the
-// multi-pass chain decides, by the exact emulation), 0 the multi-pass chain
-// decides (X holds more than one value; top-k rows; min_tokens_to_keep).
+// S and the mass above X summed in double, and, when X holds the maximum, by
+// replaying the reference's sums over X (tie_top_exact). Sets ss.kthr;
+// returns 1 decided, 3 decided with the double sums or the replay, 4 neither
+// settles it (the multi-pass chain decides, by the exact emulation), 0 the
+// multi-pass chain decides (X holds more than one value; top-k rows;
+// min_tokens_to_keep).
 template <int PT>
 __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, int n, const SideRule sr, int nX,
                                     double thr, double S, double errS, double Ma, double eMa, uint32_t n_above,
@@ -256,10 +278,12 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
 #pragma unroll
   for (int i = 0; i < kStepWaves; ++i) { zs = fmaxf(zs, ss.wmax[i]); zl = fminf(zl, ss.wmin[i]); }
   if (!(zs == zl) || zs == ninf) return 0;   // not one value (or nothing finite)
+  C4S_PHASE(24);
   const double e = exp((double)(zs - sr.m));
   const double N = (double)nX;
   const uint32_t mk = (uint32_t)max(0, c.min_keep);
   double Sx = topk ? N * e : S, base = topk ? 0.0 : Ma, err = topk ? 0.0 : 2.0 * errS + eMa;
+  double nB = 0.0;   // the mass below X, in double (pass 1)
   int k = 0, verdict = 1;
   for (int pass = 0; pass < 2; ++pass) {
     if (thr <= 0.0) {   // p >= 1: only zero-mass positions can go
@@ -277,26 +301,44 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
                       (k == nX || fabs(Sx - base - (double)k * e - A) > mg);
     if (sure) break;
     if (topk) return 0;
-    if (pass == 1) return 4;
-    // decide again with S and the mass above X in double
-    double se = 0.0, sa = 0.0;
+    if (pass == 1) {
+      // X holds the maximum and nothing lies above it: the reference's sums
+      // in ascending order are the entries below X, then X's nX masses of 1.
+      // The entries below enter only through their sums, known within
+      // rel_eps, which the first add of a mass of 1 (or of 1 / total) rounds
+      // to one double unless the interval straddles a rounding boundary; from
+      // there the sums over X are replayed exactly.
+      if (n_above != 0u || zs != sr.m) return 4;
+      C4S_PHASE(25);
+      if (threadIdx.x == 0) ss.bsel[0] = tie_top_exact(nB, nX, thr, rel_eps(c.V));   // one thread; the rest wait
+      __syncthreads();
+      k = ss.bsel[0];
+      C4S_PHASE(26);
+      if (k < 0) return 4;
+      break;
+    }
+    // decide again with S and the mass above X in double (and the mass below X)
+    double se = 0.0, sa = 0.0, sb = 0.0;
     for (int j = 0; j < n; ++j) {
       const float y = val[lo + j];
       const float z = c.temp_on ? y / c.temp : y;
       if (z != ninf) {
         const double ed = exp((double)(z - sr.m));
+        const int sd = sr.side(z);
         se += ed;
-        if (sr.side(z) < 0) sa += ed;
+        if (sd < 0) sa += ed;
+        if (sd > 0) sb += ed;
       }
     }
     se = wave_sum_dpp(se);
     sa = wave_sum_dpp(sa);
-    if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; }
+    sb = wave_sum_dpp(sb);
+    if (lane == 0) { ss.wc[w] = se; ss.wd[w] = sa; ss.wa[w] = sb; }
     __syncthreads();
     Sx = 0.0;
     base = 0.0;
 #pragma unroll
-    for (int i = 0; i < kStepWaves; ++i) { Sx += ss.wc[i]; base += ss.wd[i]; }
+    for (int i = 0; i < kStepWaves; ++i) { Sx += ss.wc[i]; base += ss.wd[i]; nB += ss.wa[i]; }
     err = 0.0;
     verdict = 3;
   }
@@ -309,6 +351,7 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
   }
   // the last kept member's key (rank k - 1), or with none kept, one above
   // every member (the lowest id's key + 1)
+  C4S_PHASE(27);
   const int want = k > 0 ? k - 1 : 0;
   const int r0 = (int)rk.ex;
   if (cnt > 0 && want >= r0 && want < r0 + (int)cnt) {
@@ -798,6 +841,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           // more boundary entries than one sort takes: one_pass only if they
           // all hold one value (ties), which needs no sort
           verdict = tie_cut<PT>(rs.cfg, val, lo, n, sr, nX, thr, S, errS, Ma, eMa, n_above, ss);
+          C4S_PHASE(28);
           tp_exact = verdict == 3;
           if (verdict != 1 && verdict != 3) one_pass = false;
           if (verdict == 4 && t == 0) rs.tp_exact_first = 1u;
