@@ -142,7 +142,8 @@ struct LdsRow {
   __device__ double cached(int i) const { return E[i]; }
   __device__ void cache(int i, double e) { E[i] = e; }
   __device__ void apply_temperature(float t, int lo, int hi) {
-    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = val[i] / t;
+    const double r = 1.0 / (double)t;
+    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = div_rcp(val[i], r);
     __syncthreads();
   }
   __device__ uint32_t* sort_buf() const { return reinterpret_cast<uint32_t*>(E); }
@@ -169,7 +170,8 @@ struct LdsRowNC {
   __device__ double cached(int) const { return 0.0; }
   __device__ void cache(int, double) {}
   __device__ void apply_temperature(float t, int lo, int hi) {
-    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = val[i] / t;
+    const double r = 1.0 / (double)t;
+    for (int i = lo + lane_id(); i < hi; i += kWave) val[i] = div_rcp(val[i], r);
     __syncthreads();
   }
   __device__ uint32_t* sort_buf() const { return sortbuf; }
@@ -1441,6 +1443,7 @@ __device__ __forceinline__ float* store_row(const float* p, int V, const RowFetc
 // set in `bitmap` is penalised once. Thread t of NTX handles its own id chunk.
 template <int NTX = NT>
 __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitmap, int V, float pen) {
+  const double rp = 1.0 / (double)pen;
   const int ch = odd_chunk<NTX>(V);
   const int lo = min(V, (int)threadIdx.x * ch);
   const int hi = min(V, lo + ch);
@@ -1455,7 +1458,7 @@ __device__ __forceinline__ void penalise_chunk(float* val, const uint32_t* bitma
       const int i = b0 + __ffsll((unsigned long long)bits) - 1;
       bits &= bits - 1;
       const float s = val[i];
-      val[i] = (s < 0) ? s * pen : s / pen;   // sampling.cpp:26
+      val[i] = (s < 0) ? s * pen : div_rcp(s, rp);   // sampling.cpp:26
     }
   }
 }

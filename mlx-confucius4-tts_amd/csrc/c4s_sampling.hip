@@ -1198,9 +1198,10 @@ struct T2Row {
   const uint32_t* bitmap;
   bool pen_on, temp_on;
   float pen, temp;
+  double rpen, rtemp;   // fl64(1 / pen), fl64(1 / temp)
   __device__ __forceinline__ float z(int i, float x) const {
-    if (pen_on && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = (x < 0) ? x * pen : x / pen;
-    return temp_on ? x / temp : x;
+    if (pen_on && ((bitmap[i >> 5] >> (i & 31)) & 1u)) x = (x < 0) ? x * pen : div_rcp(x, rpen);
+    return temp_on ? div_rcp(x, rtemp) : x;
   }
   // f(i, z) for every id, each by one thread: 16-byte loads over the aligned body
   template <class F>
@@ -1661,6 +1662,8 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
     tr.pen = c.pen;
     tr.temp_on = c.temp_on;
     tr.temp = c.temp;
+    tr.rpen = 1.0 / (double)c.pen;
+    tr.rtemp = 1.0 / (double)c.temp;
     if (topk_two_pass(a, row, c, tr, *reinterpret_cast<T2Sh*>(smem + t2_offset(V)))) return;
     __syncthreads();
   }

@@ -2788,6 +2788,7 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
     uint32_t acc[4] = {ctl.acc[0], ctl.acc[1], ctl.acc[2], ctl.acc[3]};
     bool stopped = false, bad = ctl.err != 0, expired = false;
     const float rpen = 1.0f / c.pen;
+    const double rtemp = 1.0 / (double)c.temp;
     // the last kHist steps: lane (step % kHist) holds the step, its token and
     // whether the token joined the drawn ids
     int htok = -1, hstep = -1;
@@ -2845,7 +2846,7 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
         break;
       }
       C4S_SPEC_T(2);
-      const float z = c.temp_on ? x / c.temp : x;
+      const float z = c.temp_on ? div_rcp(x, rtemp) : x;
       float e0, e1;
       const float m1 = mass_approx(x, mk, e0);
       const float m2 = mass_approx(pen_approx(x, c.pen, rpen), mk, e1);
@@ -2853,14 +2854,10 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
       const double e = isnew ? (double)e0 + (double)e1 : 0.0;
       // the history and the drawn list agree unless the decision is older than the history
       bool accept = rok != 0 && nn == n - nFd && q - Fd <= kHist;
-      double DL = 0.0, EL = 0.0, Da = 0.0;
-      for (uint64_t b = nm; b; b &= b - 1) {
-        const int j = __ffsll((unsigned long long)b) - 1;
-        const double dj = readlane_f64(d, j);
-        DL += dj;
-        EL += readlane_f64(e, j);
-        Da += ((int)readlane_u32((uint32_t)htok, j) < rtok) ? dj : 0.0;
-      }
+      // sums over the new ids (d and e are 0 in the other lanes), by wave
+      // reductions: any order of at most kHist non-negative terms stays within
+      // the |DL| 2^-50 that Y allows for rounding
+      const double DL = wave_sum_dpp(d), EL = wave_sum_dpp(e), Da = wave_sum_dpp(htok < rtok ? d : 0.0);
       if (accept && nn > 0) {
         const double Y = EL + fabs(DL) * 0x1p-50;
         if (kind == 1) {
