@@ -476,15 +476,19 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     t1 = max(t1, ky[j]);
   }
   // L0: two 11-bit passes over the threads' top-2 keys
+  C4S_PHASE(20);
   for (int i = t; i < 2 * 2048; i += kStepThreads) (&fs.hist[0][0])[i] = 0u;
   __syncthreads();
+  C4S_PHASE(21);
   if (t1) atomicAdd(&fs.hist[0][t1 >> 21], 1u);
   if (t2) atomicAdd(&fs.hist[0][t2 >> 21], 1u);
   __syncthreads();
   uint32_t L0 = 0;
   {
     uint32_t b1, ab1;
+    C4S_PHASE(22);
     if (fast_pick(fs.hist[0], fs.red[0], fs.bu, kFastSel, b1, ab1)) {
+      C4S_PHASE(23);
       if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[1][(t1 >> 10) & 2047u], 1u);
       if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[1][(t2 >> 10) & 2047u], 1u);
       __syncthreads();
@@ -503,29 +507,37 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     below = max(below, ky[j] < L0 ? ky[j] : 0u);
   }
   {
-    const uint32_t bm = wave_max_u32(below);
+    const uint32_t bm = wave_max_u32_dpp(below);   // every lane of the workgroup is here
     if (lane == 0) fs.redm[wv] = bm;
   }
   uint32_t C;
-  uint32_t pos = fast_scan(cnt, fs.red[2], C);   // its barrier also publishes redm
+  const uint32_t pos = fast_scan(cnt, fs.red[2], C);   // its barrier also publishes redm
   uint32_t tout = 0;
 #pragma unroll
   for (int w = 0; w < kStepWaves; ++w) tout = max(tout, fs.redm[w]);
-  if (tout != 0u && c.temp_on) tout = fkey(kfloat(tout) / c.temp);   // the quotient is monotone in y
+  const double rt = 1.0 / (double)c.temp;
+  if (tout != 0u && c.temp_on) tout = fkey(div_rcp(kfloat(tout), rt));   // the quotient is monotone in y
   if (C > (uint32_t)kCandCap || C == 0u) return false;   // uniform
+  {
+    uint32_t cm = 0;   // this thread's candidates; each goes to pos + the candidates before it
 #pragma unroll
-  for (int j = 0; j < PT; ++j)
-    if (ky[j] >= L0) fs.cand[pos++] = ((uint64_t)ky[j] << 32) | (uint32_t)(lo + j);
+    for (int j = 0; j < PT; ++j) cm |= (ky[j] >= L0) ? 1u << j : 0u;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      if ((cm >> j) & 1u)
+        fs.cand[pos + (uint32_t)__popc(cm & ((1u << j) - 1u))] = ((uint64_t)ky[j] << 32) | (uint32_t)(lo + j);
+  }
   __syncthreads();
   // entries: z = fl(y / T) (sampling.cpp:16) with the candidate's position
   for (int i = t; i < (int)C; i += kStepThreads) {
     const uint64_t cw = fs.cand[i];
     const float yv = kfloat((uint32_t)(cw >> 32));
-    fs.cand[i] = make_entry(c.temp_on ? yv / c.temp : yv, (int)(uint32_t)cw, i);
+    fs.cand[i] = make_entry(c.temp_on ? div_rcp(yv, rt) : yv, (int)(uint32_t)cw, i);
     fs.candy[i] = yv;
   }
-  const int C8 = ((int)C + 7) & ~7;
-  if (t < C8 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
+  static_assert(kCandCap % 16 == 0, "padding to 16 entries stays in the candidate array");
+  const int C16 = ((int)C + 15) & ~15;
+  if (t < C16 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
   __syncthreads();
   C4S_PHASE(12);
   // sort by rank counting (entries are distinct: their ids are); the first
@@ -537,12 +549,12 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     const uint64_t mine = (i < (int)C) ? fs.cand[i] : ~0ull;
     uint32_t r = 0;
     if (base + wv * kWave < (int)C)   // waves without an entry skip the count
-      for (int j = 0; j < C8; j += 8) {
-        uint64_t o[8];
+      for (int j = 0; j < C16; j += 16) {   // 16 broadcast reads in flight a round
+        uint64_t o[16];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) o[q] = fs.cand[j + q];
+        for (int q = 0; q < 16; ++q) o[q] = fs.cand[j + q];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) r += (o[q] > mine) ? 1u : 0u;
+        for (int q = 0; q < 16; ++q) r += (o[q] > mine) ? 1u : 0u;
       }
     if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;
   }
