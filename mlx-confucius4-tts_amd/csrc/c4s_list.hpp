@@ -80,16 +80,18 @@ struct LSpecCS {   // list_step's survivor arrays
   int lslot[kWave + 1];
 };
 
-// Candidate-list step for greedy and top-k rows (one wave; two entries per
-// lane: keys e0, e1 and their values before the temperature yb0, yb1).
-// Returns false (nothing changed) when a decision needs the exact step.
 // Drawn-id set as a bitmap (hit test of list_step).
 struct BitsHit {
   const uint32_t* bm;
   __device__ __forceinline__ bool hit(int id) const { return bit_of(bm, id); }
 };
 
-template <class Hit, class CS>
+// Candidate-list step for greedy and top-k rows (one wave; two entries per
+// lane: keys e0, e1 and their values before the temperature yb0, yb1).
+// Returns false (nothing changed) when a decision needs the exact step. The
+// entries' rank fields order them by id (kSB bits); kNoHits: the hit test is
+// never true (no id drawn since the list was made).
+template <int kSB = kSlotBits, bool kNoHits = false, class Hit, class CS>
 __device__ __forceinline__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t e1, float yb0, float yb1,
                           const RowCfg& c, int V, const Hit& hs, uint64_t& rng, CS& cs,
                           StepOut& o) {
@@ -148,13 +150,21 @@ __device__ __forceinline__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t
   if (nsurv > kWave) return false;
   o.nsurv = (uint32_t)nsurv;
   // survivors are the unhit ranks [0, nsurv): one per lane in rank order
-  if (s0) { cs.lz[r0] = z0; cs.lid[r0] = id0; cs.lslot[r0] = ent_rank(e0); }
-  if (s1) { cs.lz[r1] = z1; cs.lid[r1] = id1; cs.lslot[r1] = ent_rank(e1); }
-  wave_sync();
   const bool sv = lane < nsurv;
-  const float zs = sv ? cs.lz[lane] : ninf;
-  const int ids = sv ? cs.lid[lane] : 0;
-  const int slot = sv ? cs.lslot[lane] : 0;
+  float zs;
+  int ids, slot;
+  if constexpr (kNoHits) {   // every entry unhit: the survivors are lanes [0, nsurv) of e0 already
+    zs = sv ? z0 : ninf;
+    ids = sv ? id0 : 0;
+    slot = sv ? ent_rank(e0) : 0;
+  } else {
+    if (s0) { cs.lz[r0] = z0; cs.lid[r0] = id0; cs.lslot[r0] = ent_rank(e0); }
+    if (s1) { cs.lz[r1] = z1; cs.lid[r1] = id1; cs.lslot[r1] = ent_rank(e1); }
+    wave_sync();
+    zs = sv ? cs.lz[lane] : ninf;
+    ids = sv ? cs.lid[lane] : 0;
+    slot = sv ? cs.lslot[lane] : 0;
+  }
   C4S_LIST_PHASE(4);
   // masses, top_p (sampling.cpp:52-65), min_keep (:67-68)
   const float zmax = readlane_f32(zs, 0);
@@ -183,7 +193,7 @@ __device__ __forceinline__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t
   const bool kept = sv && (long long)lane < m;
   const uint64_t st = xorshift64(rng);
   C4S_LIST_PHASE(5);
-  o.tok = lane_draw<kSlotBits>(kept, ids, slot, e, unit_from_state(st), V, o.dex);
+  o.tok = lane_draw<kSB>(kept, ids, slot, e, unit_from_state(st), V, o.dex);
   C4S_LIST_PHASE(6);
   o.kept = (uint32_t)__popcll(__ballot(kept));
   rng = st;

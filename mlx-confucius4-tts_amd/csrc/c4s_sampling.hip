@@ -409,15 +409,15 @@ struct NoHit {   // no id drawn since the list was made
 
 struct FastSh {
   uint32_t hist[2][2048];      // the two histogram passes; the first then holds the sorted head (uint64)
-  uint64_t cand[kCandCap];     // candidates: key(y) | id, then their entries
-  float candy[kCandCap];       // y by candidate position
-  uint32_t lmark[kCandCap / 32];
+  uint64_t cand[kCandCap];     // candidates as entries (key of z, id, candidate position)
   uint32_t red[4][kStepWaves];   // one set per workgroup scan (no barrier between reuses)
   uint32_t redm[kStepWaves];
   uint32_t bu[8];
   LSpecCS cs;
 };
 static_assert(sizeof(FastSh) <= kStepWorkBytes, "the list step's area lies in the one pass's work area");
+static_assert(offsetof(FastSh, hist) == 0 && sizeof(FastSh::hist) <= 3 * kHistBytes,
+              "the list step's histograms lie in the area the step clears before staging");
 
 // Exclusive scan of v over the workgroup (thread order); total in `tot`. One
 // barrier: each call uses its own `red`.
@@ -475,25 +475,27 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     t2 = max(t2, min(t1, ky[j]));
     t1 = max(t1, ky[j]);
   }
-  // L0: two 11-bit passes over the threads' top-2 keys
+  // L0: two 11-bit passes over the threads' top-2 keys, on histograms that are
+  // zero on entry (the caller clears the one-pass histogram area, which they lie in)
   C4S_PHASE(20);
-  for (int i = t; i < 2 * 2048; i += kStepThreads) (&fs.hist[0][0])[i] = 0u;
-  __syncthreads();
   C4S_PHASE(21);
   if (t1) atomicAdd(&fs.hist[0][t1 >> 21], 1u);
   if (t2) atomicAdd(&fs.hist[0][t2 >> 21], 1u);
   __syncthreads();
+  // L0 lies at or below the msel-th largest of those keys, so at least msel
+  // values are candidates: for k < kFastSel the k-th largest and the next one
+  const uint32_t msel = min((uint32_t)kFastSel, (uint32_t)c.k + 1u);
   uint32_t L0 = 0;
   {
     uint32_t b1, ab1;
     C4S_PHASE(22);
-    if (fast_pick(fs.hist[0], fs.red[0], fs.bu, kFastSel, b1, ab1)) {
+    if (fast_pick(fs.hist[0], fs.red[0], fs.bu, msel, b1, ab1)) {
       C4S_PHASE(23);
       if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[1][(t1 >> 10) & 2047u], 1u);
       if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[1][(t2 >> 10) & 2047u], 1u);
       __syncthreads();
       uint32_t b2, ab2;
-      fast_pick(fs.hist[1], fs.red[1], fs.bu + 2, kFastSel - ab1, b2, ab2);
+      fast_pick(fs.hist[1], fs.red[1], fs.bu + 2, msel - ab1, b2, ab2);
       L0 = (b1 << 21) | (b2 << 10);
     }
   }
@@ -519,23 +521,21 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   if (tout != 0u && c.temp_on) tout = fkey(div_rcp(kfloat(tout), rt));   // the quotient is monotone in y
   if (C > (uint32_t)kCandCap || C == 0u) return false;   // uniform
   {
-    uint32_t cm = 0;   // this thread's candidates; each goes to pos + the candidates before it
+    // this thread's candidates as entries: z = fl(y / T) (sampling.cpp:16), the
+    // id, and the candidate's position (pos + the candidates before it), which
+    // is the id order: the draw's order key
+    uint32_t cm = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) cm |= (ky[j] >= L0) ? 1u << j : 0u;
 #pragma unroll
     for (int j = 0; j < PT; ++j)
-      if ((cm >> j) & 1u)
-        fs.cand[pos + (uint32_t)__popc(cm & ((1u << j) - 1u))] = ((uint64_t)ky[j] << 32) | (uint32_t)(lo + j);
+      if ((cm >> j) & 1u) {
+        const uint32_t i = pos + (uint32_t)__popc(cm & ((1u << j) - 1u));
+        fs.cand[i] = make_entry(c.temp_on ? div_rcp(y[j], rt) : y[j], lo + j, (int)i);
+      }
   }
-  __syncthreads();
-  // entries: z = fl(y / T) (sampling.cpp:16) with the candidate's position
-  for (int i = t; i < (int)C; i += kStepThreads) {
-    const uint64_t cw = fs.cand[i];
-    const float yv = kfloat((uint32_t)(cw >> 32));
-    fs.cand[i] = make_entry(c.temp_on ? div_rcp(yv, rt) : yv, (int)(uint32_t)cw, i);
-    fs.candy[i] = yv;
-  }
-  static_assert(kCandCap % 16 == 0, "padding to 16 entries stays in the candidate array");
+  static_assert(kCandCap % 16 == 0 && kCandCap <= 1024, "padding to 16 entries stays in the candidate array; "
+                "positions fit the entry's rank field");
   const int C16 = ((int)C + 15) & ~15;
   if (t < C16 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
   __syncthreads();
@@ -573,31 +573,19 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     const float ztop = kfloat(ent_key(srt[0]));   // C >= 1
     // the draw starts its maximum at -1e30 (text2semantic.cpp:150): below it the one pass decides
     bool ok = nlist > 0 && ztop >= -1e30f;
+    C4S_PHASE(24);
     if (ok) {
-      // id-order rank among the list: candidates sit in id order, so it counts
-      // the list's candidate positions below the entry's own
-      const bool v0 = lane < nlist, v1 = lane + kWave < nlist;
-      const int c0 = ent_rank(e0), c1 = ent_rank(e1);
-      if (lane < kCandCap / 32) fs.lmark[lane] = 0u;
-      wave_sync();
-      if (v0) atomicOr(&fs.lmark[c0 >> 5], 1u << (c0 & 31));
-      if (v1) atomicOr(&fs.lmark[c1 >> 5], 1u << (c1 & 31));
-      wave_sync();
-      const uint32_t pc = (lane < kCandCap / 32) ? (uint32_t)__popc(fs.lmark[lane]) : 0u;
-      const uint32_t pre = wave_scan_u32(pc) - pc;   // lane w: marks before word w
-      const uint32_t p0 = (uint32_t)__builtin_amdgcn_ds_bpermute((c0 >> 5) << 2, (int)pre);
-      const uint32_t p1 = (uint32_t)__builtin_amdgcn_ds_bpermute((c1 >> 5) << 2, (int)pre);
-      const uint32_t m0 = fs.lmark[c0 >> 5], m1 = fs.lmark[c1 >> 5];
-      const float y0 = fs.candy[c0], y1 = fs.candy[c1];
-      e0 = v0 ? (e0 & ~1023ull) | (p0 + (uint32_t)__popc(m0 & ((1u << (c0 & 31)) - 1u))) : 0ull;
-      e1 = v1 ? (e1 & ~1023ull) | (p1 + (uint32_t)__popc(m1 & ((1u << (c1 & 31)) - 1u))) : 0ull;
+      // each entry keeps its candidate position as its id-order key (10 bits)
+      e0 = lane < nlist ? e0 : 0ull;
+      e1 = lane + kWave < nlist ? e1 : 0ull;
       SumHdr h{};
       h.n = nlist;
       h.tout = tout;
       h.flags = 0u;
       uint64_t r = io.rng ? *io.rng : 0ull;
       StepOut o{0, 0u, 0u, 0u, 0u};
-      ok = list_step(h, e0, e1, v0 ? y0 : 0.0f, v1 ? y1 : 0.0f, c, V, NoHit{}, r, fs.cs, o);
+      ok = list_step<10, true>(h, e0, e1, 0.0f, 0.0f, c, V, NoHit{}, r, fs.cs, o);
+      C4S_PHASE(25);
       if (ok && lane == 0) step_out(io, V, o.tok, r, true, 1u | 2u | 4u | 16u | 32u, 0u, o.dex, o.kept);
     }
     if (lane == 0) fs.bu[4] = ok ? 1u : 0u;
@@ -863,16 +851,26 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           const bool block = P2 > kWave;
           uint64_t v = 0ull;
           if (block) {
-            v = t < nX ? list[t] : 0ull;
-            v = sort_desc_block(v, P2, sbuf);
-            if (t < nX) list[t] = v;
-            __syncthreads();
+            // up to 256 entries by rank counting (two to four threads a key,
+            // two barriers); more by the bitonic network (six barriers)
+            if (nX <= 128) {
+              v = rank_sort_desc<128>(list, nX, reinterpret_cast<uint32_t*>(sbuf));
+            } else if (nX <= 256) {
+              v = rank_sort_desc<256>(list, nX, reinterpret_cast<uint32_t*>(sbuf));
+            } else {
+              v = t < nX ? list[t] : 0ull;
+              v = sort_desc_block(v, P2, sbuf);
+              if (t < nX) list[t] = v;
+              __syncthreads();
+            }
             C4S_PHASE(8);
+            if (t == 0) ss.zx = key_value(v);   // X's largest value (read after the barriers below)
             decide_cut<true>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           } else if (w == 0) {
             v = lane < nX ? list[lane] : 0ull;
             v = sort_desc_wave(v, P2);
             C4S_PHASE(8);
+            if (t == 0) ss.zx = key_value(v);
             decide_cut<false>(rs.cfg, v, nX, m, thr, S, errS, Ma, eMa, n_above, list, ss);
           }
           __syncthreads();
@@ -880,13 +878,25 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           if (verdict == 2) {
             // decide again with every mass in double (S and the mass above the boundary)
             tp_exact = true;
+            // every value through the same instructions, so that the exps
+            // interleave: z is -inf past the thread's ids and exp(-inf) = 0.
+            // side() is monotone in z and equal values share a side, so the
+            // entries above X are exactly those above X's largest value.
             double se = 0.0, sa = 0.0;
+            if (nX > 0) {
+              const float zx = ss.zx;
 #pragma unroll
-            for (int j = 0; j < PT; ++j) {
-              if (j < n && z[j] != ninf) {
+              for (int j = 0; j < PT; ++j) {
                 const double ed = exp((double)(z[j] - m));
                 se += ed;
-                if (side(z[j]) < 0) sa += ed;
+                sa += z[j] > zx ? ed : 0.0;
+              }
+            } else {
+#pragma unroll
+              for (int j = 0; j < PT; ++j) {
+                const double ed = exp((double)(z[j] - m));
+                se += ed;
+                sa += side(z[j]) < 0 ? ed : 0.0;
               }
             }
             se = wave_sum_dpp(se);

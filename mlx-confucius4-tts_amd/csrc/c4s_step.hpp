@@ -14,8 +14,9 @@
 //    value (top_k) or the nucleus boundary (top_p: a window of +-1e-3 relative
 //    around the kept mass p * S, far wider than the fp32 errors);
 //  * only the entries of the boundary buckets (every bucket up to the k-th
-//    value for top_k) are sorted, by (value desc, id asc), with a bitonic
-//    network (lane shuffles inside a wave, LDS across waves), and their masses
+//    value for top_k) are sorted, by (value desc, id asc): up to 64 by a
+//    bitonic network on lane shuffles, up to 256 by rank counting, more by a
+//    bitonic network across waves, and their masses
 //    are the reference's exp((double)t) (sampling.cpp:55);
 //  * the cut is taken on the sorted entries with sums formed in parallel, each
 //    decision with the margin rel_eps(V) * S plus the fp32 error bounds; a
@@ -113,6 +114,7 @@ struct StepSh {
   double mabx;       // mass of the entries above X (the boundary (sub-)buckets), from the histogram
   uint32_t nabx;     // their count
   uint32_t nx;       // boundary entries (compaction counter)
+  float zx;          // the largest value among them (after their sort)
   uint64_t kthr;     // kept iff key64 >= kthr
   int verdict;       // 1 decided, 2 decide again with every mass in double, 0 multi-pass chain
 };
@@ -323,6 +325,42 @@ __device__ __forceinline__ uint64_t sort_desc_block(uint64_t v, int P2, uint64_t
   if (P2 == 128) return bitonic_sort<128>(v, t, buf, half);
   if (P2 == 256) return bitonic_sort<256>(v, t, buf, half);
   return bitonic_sort<512>(v, t, buf, half);
+}
+
+// Descending order of list[0 .. nX), nX <= E, distinct keys, in place, by rank
+// counting: kStepThreads / E threads per key, each counting the keys above it
+// in its share of the list (16 broadcast reads in flight a round), the shares'
+// counts meeting in `part` (E * kStepThreads / E words). Returns the t-th
+// largest key (0 for t >= nX). The whole workgroup enters with the list
+// complete and visible; two barriers inside.
+template <int E>
+__device__ __forceinline__ uint64_t rank_sort_desc(uint64_t* list, int nX, uint32_t* part) {
+  constexpr int G = kStepThreads / E;
+  static_assert(G * E == kStepThreads && E % kWave == 0 && (E / G) % 16 == 0, "whole waves and rounds per share");
+  const int t = threadIdx.x;
+  const int i = t % E, q = t / E;
+  const int chunk = ((nX + G - 1) / G + 15) & ~15;   // <= E / G: every read below E
+  const int j0 = q * chunk, j1 = min(nX, j0 + chunk);
+  const uint64_t mine = list[i];
+  uint32_t r = 0;
+  if ((i & ~(kWave - 1)) < nX)   // waves whose keys all lie past nX skip the count (uniform)
+    for (int j = j0; j < j1; j += 16) {
+      uint64_t o[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) o[u] = list[j + u];   // in bounds: j + u < G * chunk
+#pragma unroll
+      for (int u = 0; u < 16; ++u) r += ((int)(j + u < j1) & (int)(o[u] > mine)) ? 1u : 0u;
+    }
+  part[q * E + i] = r;
+  __syncthreads();
+  if (t < nX) {
+    uint32_t rank = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) rank += part[g * E + t];
+    list[rank] = mine;
+  }
+  __syncthreads();
+  return t < nX ? list[t] : 0ull;
 }
 
 // Where one row's inputs and outputs are (the kernel's view of c4s_rows).

@@ -57,6 +57,23 @@ def test_batch64_general_rows(orc, gpu_ctx):
 
 
 @pytest.mark.parametrize("masked", [True, False])
+def test_nucleus_rows_many(orc, gpu_ctx, masked):
+    """1024 full-vocabulary nucleus rows (p 0.8-0.99, assorted temperatures and
+    penalties): boundaries from a few entries to several hundred (the one-wave
+    sort, the rank-counted sorts of up to 128 and 256 entries, the network
+    across waves), and cuts close enough to the error bound that the masses are
+    taken again in double."""
+    b = W.batch64(seed=71, rows=1024)
+    b.top_k[:] = 0
+    b.top_p[:] = np.resize(np.array([0.8, 0.9, 0.95, 0.99, 0.85], np.float32), 1024)
+    print(f"nucleus rows x1024 masked={masked}", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=masked)
+    print("exact top_p passes", int(st[:, 1].sum()))
+    assert ((st[:, 0] & 16) != 0).mean() > 0.9
+    assert st[:, 1].sum() > 0
+
+
+@pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("sigma", [0.3, 0.7, 1.5])
 def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma, masked):
     """Narrow logit ranges (an LM head's output): hundreds of entries share the
