@@ -466,6 +466,7 @@ template <int PT>
 __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int V, const float (&y)[PT], int lo,
                                           int n, FastSh& fs) {
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
+  const double rt = 1.0 / (double)c.temp;   // used only when the temperature applies
   uint32_t ky[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) ky[j] = (j < n) ? fkey(y[j]) : 0u;   // 0: below every key of a value
@@ -514,10 +515,10 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   }
   uint32_t C;
   const uint32_t pos = fast_scan(cnt, fs.red[2], C);   // its barrier also publishes redm
+  C4S_PHASE(26);
   uint32_t tout = 0;
 #pragma unroll
   for (int w = 0; w < kStepWaves; ++w) tout = max(tout, fs.redm[w]);
-  const double rt = 1.0 / (double)c.temp;
   if (tout != 0u && c.temp_on) tout = fkey(div_rcp(kfloat(tout), rt));   // the quotient is monotone in y
   if (C > (uint32_t)kCandCap || C == 0u) return false;   // uniform
   {
@@ -538,6 +539,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
                 "positions fit the entry's rank field");
   const int C16 = ((int)C + 15) & ~15;
   if (t < C16 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
+  C4S_PHASE(27);
   __syncthreads();
   C4S_PHASE(12);
   // sort by rank counting (entries are distinct: their ids are); the first
@@ -948,6 +950,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         kept_mass32(kr, z[j], m, lo + j, kp);
         if (j < n) io.masked[lo + j] = kp ? z[j] : ninf;
       }
+    C4S_PHASE(27);
     const double ks = (double)ks32;
     const double ek = ks * (0x1p-20 + PT * 0x1p-24) + (double)kc * 0x1p-125;
     const Scan2 ds = block_scan2(ks, ek, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
@@ -1045,17 +1048,17 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   if (!csr) h0 = h1 = 0;
   const int hid = (csr && h0 + t < h1) ? a.hist_ids[h0 + t] : -1;
   const int hid2 = (csr && h0 + t + kStepThreads < h1) ? a.hist_ids[h0 + t + kStepThreads] : -1;
-  // penalty bits of this thread's ids: words lo/32 .. lo/32 + 2 (up to 65 ids
-  // from bit lo % 32 span at most three words)
-  static_assert(PT <= 65, "a thread's ids span at most three bitmap words");
-  uint32_t pw[3] = {0u, 0u, 0u};
+  // penalty bits of this thread's ids: words lo/32 and lo/32 + 1 (up to 33 ids
+  // from bit lo % 32 span at most two words)
+  static_assert(PT <= 33, "a thread's ids span at most two bitmap words");
+  uint32_t pw[2] = {0u, 0u};
   if (io.hbits) {
     // every load unconditional (index clamped), so nothing waits for them here:
     // the penalty below keeps only the bits of ids lo .. lo + n - 1, and a
     // clamped word past the set would stand for ids at or above V
     const int w0 = lo >> 5, hwn = hist_words(V);
 #pragma unroll
-    for (int q = 0; q < 3; ++q) pw[q] = io.hbits[min(w0 + q, hwn - 1)];
+    for (int q = 0; q < 2; ++q) pw[q] = io.hbits[min(w0 + q, hwn - 1)];
   }
   // the row into LDS (fp32: its loads went out above)
   float* val;
@@ -1079,34 +1082,36 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
       if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
     }
     __syncthreads();
-    if (n > 0) {
-      const int w0 = lo >> 5;
+    // unconditional reads (index clamped, as for the caller's set above)
+    const int w0 = lo >> 5;
 #pragma unroll
-      for (int q = 0; q < 3; ++q) pw[q] = (w0 + q < nw) ? bitmap[w0 + q] : 0u;
-    }
+    for (int q = 0; q < 2; ++q) pw[q] = bitmap[min(w0 + q, nw - 1)];
   }
   C4S_PHASE(1);
   if (c.pen_on) {
     // sampling.cpp:19-28 on this thread's ids in LDS, one set bit at a time
     // (each distinct id once); the row in LDS is the penalised row from here on
+    // (dividing only the set bits: every value of the thread through the
+    // double reciprocal costs more than this loop)
     const double rp = 1.0 / (double)c.pen;
-#pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const int b0 = (lo & ~31) + 32 * q;
-      uint32_t bits = pw[q];
-      if (b0 < lo) bits &= ~0u << (lo - b0);
-      if (b0 + 32 > lo + n) bits &= (lo + n - b0 <= 0) ? 0u : (lo + n - b0 >= 32 ? ~0u : (1u << (lo + n - b0)) - 1u);
-      while (bits) {
-        const int i = b0 + __ffs(bits) - 1;
-        bits &= bits - 1;
-        const float x = val[i];
-        val[i] = (x < 0) ? x * c.pen : div_rcp(x, rp);   // sampling.cpp:26
-      }
+    uint32_t pm = (uint32_t)(((((uint64_t)pw[1] << 32) | pw[0]) >> (lo & 31))) & ((1u << n) - 1u);
+    while (pm) {
+      const int i = lo + __ffs(pm) - 1;
+      pm &= pm - 1;
+      const float x = val[i];
+      val[i] = (x < 0) ? x * c.pen : div_rcp(x, rp);   // sampling.cpp:26
     }
   }
-  float y[PT];   // this thread's ids (odd stride: no LDS bank conflicts)
+  C4S_PHASE(14);
+  // this thread's ids (odd stride: no LDS bank conflicts), every read
+  // unconditional (index clamped) and the padding selected afterwards
+  float y[PT];
 #pragma unroll
-  for (int j = 0; j < PT; ++j) y[j] = (j < n) ? val[lo + j] : ninf;
+  for (int j = 0; j < PT; ++j) {
+    const float v = val[min(lo + j, V - 1)];
+    y[j] = (j < n) ? v : ninf;
+  }
+  C4S_PHASE(29);
 
   if (c.greedy) {   // text2semantic.cpp:144-145: argmax of the penalised row, first maximum
     float bv = ninf;
