@@ -108,10 +108,14 @@ __device__ __forceinline__ void step_out(const StepIO& io, int V, int tok, uint6
 // is known: the kept fp32 masses of each thread and ds, the workgroup scan of
 // their sums with the error bound in tot2. The thread whose interval holds r
 // decides. When it cannot (r within the bound of one end of its entry: on a
-// flat row of thousands of kept entries a few percent of rows a call), every
-// thread recomputes its kept masses in double and the workgroup scans them
-// again (bound rel_eps, about 1e-11 relative); only if that still does not
-// decide does one wave replay the draw sequentially (draw_replay).
+// flat row of thousands of kept entries a few percent of rows a call), the
+// masses are taken again in double: at most 64 kept ids go in id order (kl, by
+// the scan's kept counts) to one wave, which draws on them and replays the
+// sums sequentially if that is too close (lane_draw); otherwise every thread
+// recomputes its kept masses, the workgroup scans them (bound rel_eps, about
+// 1e-11 relative) and the owner's wave walks the owner's ids, one a lane; only
+// if that still does not decide does one wave replay the draw sequentially
+// over the row (draw_replay).
 // The row's configuration and I/O as one LDS copy for the workgroup: the
 // out-of-line helpers take them by reference, and a reference to a copy in
 // registers would make the compiler keep that copy in per-lane scratch memory
@@ -126,7 +130,7 @@ template <int PT, bool kCached>
 __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, const KeptRule& kr, const float (&z)[PT],
                                             int lo, int n, float m, const Scan2& ds, uint32_t n_kept,
                                             uint32_t st_path, uint32_t st_exact, StepSh& ss, const StepRowSh& rs,
-                                            const float* em) {
+                                            const float* em, uint64_t* kl) {
   const int t = threadIdx.x;
   const uint64_t st2 = xorshift64(*io.rng);
   const double u = unit_from_state(st2);
@@ -182,33 +186,68 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
     if (owner) step_out(io, c.V, found, st2, true, st_path, st_exact, 0u, n_kept);
     return;
   }
-  // the kept masses in double, scanned by the workgroup. The kept test is the
-  // one pass's (kept_in): a dense row reaches this draw only without values
-  // whose double mass lies near underflow, so `z - m > -745` there is
-  // exactly `exp((double)(z - m)) > 0`.
+  // the kept masses in double. The kept test is the one pass's (kept_in): a
+  // dense row reaches this draw only without values whose double mass lies
+  // near underflow, so `z - m > -745` there is exactly `exp((double)(z - m)) > 0`.
+  C4S_PHASE(24);
+  if (n_kept <= (uint32_t)kWave) {
+    // at most 64 kept ids: in id order (thread order, then the thread's own)
+    // to one wave, which draws on them in double and replays the sums
+    // sequentially when that is too close (lane_draw)
+    uint32_t km = 0;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      km |= ((int)(j < n) & (int)(z[j] != neg_inf()) & (int)kept_in(kr, z[j], m, lo + j)) ? 1u << j : 0u;
+#pragma unroll
+    for (int j = 0; j < PT; ++j)
+      if ((km >> j) & 1u)
+        kl[ds.uex + (uint32_t)__popc(km & ((1u << j) - 1u))] = ((uint64_t)__float_as_uint(z[j]) << 32) | (uint32_t)(lo + j);
+    __syncthreads();
+    if (wave_id() == 0) {
+      const int l = lane_id();
+      const bool in = l < (int)n_kept;
+      const uint64_t ent = kl[in ? l : 0];
+      const double e = in ? exp((double)(__uint_as_float((uint32_t)(ent >> 32)) - m)) : 0.0;
+      uint32_t ex2 = 0;
+      const int tk = lane_draw<6>(in, (int)(uint32_t)ent, l, e, u, c.V, ex2);
+      if (l == 0) step_out(io, c.V, tk, st2, true, st_path, st_exact, 1u + ex2, n_kept);
+    }
+    return;
+  }
   double dk = 0.0;
 #pragma unroll
   for (int j = 0; j < PT; ++j)
     if (j < n && z[j] != neg_inf() && kept_in(kr, z[j], m, lo + j)) dk += exp((double)(z[j] - m));
   const Scan2 d2 = block_scan2(dk, 0.0, 0u, ss.wa, ss.wb, ss.wu);
+  C4S_PHASE(25);
   const double r2 = u * d2.tot;
   const double m2 = 2.0 * rel_eps(c.V) * d2.tot;
   const bool own2 = (d2.ex < r2 && r2 <= d2.in) || (t == kStepThreads - 1 && r2 > d2.in);
   found = -1;
   certain = false;
-  if (own2 && r2 > 0.0) {
-    double acc = d2.ex, prev = d2.ex;
+  const uint64_t ob = __ballot(own2);
+  if (ob) {   // the owner's wave: lane j takes the owner's id lo + j, the prefix by a wave scan
+    const int ol = __ffsll((unsigned long long)ob) - 1, l = lane_id();
+    float zl = neg_inf();
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      const double ej = (j < n && z[j] != neg_inf() && kept_in(kr, z[j], m, lo + j)) ? exp((double)(z[j] - m)) : 0.0;
-      if (found < 0 && ej > 0.0) {
-        const double na = acc + ej;
-        if (na >= r2) { found = lo + j; prev = acc; }
-        acc = na;
-      }
+      const float zj = readlane_f32(z[j], ol);
+      zl = (l == j) ? zj : zl;
     }
-    certain = found >= 0 && (acc - r2 > m2) && (r2 - prev > m2);
+    const int lo_o = readlane_u32((uint32_t)lo, ol), n_o = readlane_u32((uint32_t)n, ol);
+    const double ex_o = readlane_f64(d2.ex, ol);
+    const bool kp = ((int)(l < n_o) & (int)(zl != neg_inf()) & (int)kept_in(kr, zl, m, lo_o + l)) != 0;
+    const double el = kp ? exp((double)(zl - m)) : 0.0;
+    const double al = ex_o + wave_scan_f64(el);
+    const uint64_t hit = __ballot(el > 0.0 && al >= r2);
+    if (r2 > 0.0 && hit) {
+      const int f = __ffsll((unsigned long long)hit) - 1;
+      const double af = readlane_f64(al, f), pf = af - readlane_f64(el, f);
+      found = lo_o + f;
+      certain = (af - r2 > m2) && (r2 - pf > m2);
+    }
   }
+  C4S_PHASE(26);
   if (!__syncthreads_or(own2 && !certain)) {
     if (own2) step_out(io, c.V, found, st2, true, st_path, st_exact, 1u, n_kept);
     return;
@@ -689,7 +728,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         for (int j = 0; j < PT; ++j)
           if (j < n) io.masked[lo + j] = (thr < 0.0 || (z[j] != ninf && z[j] - m > -745.0f)) ? z[j] : ninf;
       C4S_PHASE(10);
-      draw_finish<PT, true>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs, em);
+      draw_finish<PT, true>(io, c, kr, z, lo, n, m, sc, n_pos, 1u | 4u | 16u, 0u, ss, rs, em, list);
       C4S_PHASE(15);
       return true;
     } else {
@@ -957,7 +996,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
     C4S_PHASE(10);
     if ((ds.utot >> 16) == 0u) {
       draw_finish<PT, !topk>(io, c, kr, z, lo, n, m, ds, ds.utot & 0xFFFFu, 1u | (topk ? 2u : 0u) | 4u | 16u,
-                             tp_exact ? 1u : 0u, ss, rs, em);
+                             tp_exact ? 1u : 0u, ss, rs, em, list);
       C4S_PHASE(15);
       return true;
     }

@@ -234,13 +234,13 @@ __device__ __forceinline__ uint64_t key64(float z, int id) {
 __device__ __forceinline__ float key_value(uint64_t k) { return kfloat((uint32_t)(k >> 32)); }
 
 // Workgroup scan (thread order) of a double v: exclusive and inclusive prefix
-// and total, with a second double summed and a u32 summed over the
-// workgroup, one barrier. The inclusive prefix of thread t is bitwise the
-// exclusive prefix of thread t + 1 and the last thread's is the total, so the
-// intervals (ex, in] tile (0, total].
+// and total, with a second double summed and a u32 scanned (exclusive prefix,
+// total) over the workgroup, one barrier. The inclusive prefix of thread t is
+// bitwise the exclusive prefix of thread t + 1 and the last thread's is the
+// total, so the intervals (ex, in] tile (0, total].
 struct Scan2 {
   double ex, in, tot, tot2;
-  uint32_t utot;
+  uint32_t utot, uex;
 };
 __device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, double* wa, double* wb,
                                              uint32_t* wu) {
@@ -249,16 +249,16 @@ __device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, do
   double exc = __shfl_up(inc, 1, kWave);
   if (lane == 0) exc = 0.0;
   const double s2 = wave_sum_dpp(v2);
-  const uint32_t us = wave_sum_u32(u);
-  if (lane == kWave - 1) wa[w] = inc;
-  if (lane == 0) { wb[w] = s2; wu[w] = us; }
+  const uint32_t uinc = wave_scan_u32(u);
+  if (lane == kWave - 1) { wa[w] = inc; wu[w] = uinc; }
+  if (lane == 0) wb[w] = s2;
   __syncthreads();
   Scan2 r;
   double base = 0.0, run = 0.0, t2 = 0.0;
-  uint32_t ut = 0;
+  uint32_t ut = 0, ubase = 0;
 #pragma unroll
   for (int i = 0; i < kStepWaves; ++i) {
-    if (i == w) base = run;
+    if (i == w) { base = run; ubase = ut; }
     run += wa[i];
     t2 += wb[i];
     ut += wu[i];
@@ -268,6 +268,7 @@ __device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, do
   r.tot = run;
   r.tot2 = t2;
   r.utot = ut;
+  r.uex = ubase + uinc - u;
   return r;
 }
 

@@ -73,6 +73,25 @@ def test_nucleus_rows_many(orc, gpu_ctx, masked):
     assert st[:, 1].sum() > 0
 
 
+def test_draw_in_double(orc, gpu_ctx):
+    """Draws that the fp32 masses cannot settle go to double: a row of 5 kept
+    ids whose r lies 2^-23.7 (relative) from a boundary (one wave, the kept ids
+    in id order), and flat rows of thousands of kept ids (the owner's wave)."""
+    b = W.batch64(seed=2, rows=64)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=False)
+    assert st[0, 3] == 5 and st[0, 2] >= 1, st[0].tolist()
+    f = W.batch64(seed=81, rows=1024)
+    g = np.random.default_rng(82)
+    f.logits[:] = (0.3 * g.standard_normal(f.logits.shape)).astype(np.float32)
+    f.top_k[:] = 0
+    f.top_p[:] = np.resize(np.array([0.95, 0.99, 1.0, 0.9], np.float32), 1024)
+    print("flat rows x1024 for the draw in double", flush=True)
+    tok, st = compare_with_oracle(orc, gpu_ctx, f, masked=False)
+    wide = (st[:, 2] >= 1) & (st[:, 3] > 64)
+    print("draws in double with more than 64 kept ids:", int(wide.sum()))
+    assert wide.any()
+
+
 @pytest.mark.parametrize("masked", [True, False])
 @pytest.mark.parametrize("sigma", [0.3, 0.7, 1.5])
 def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma, masked):
