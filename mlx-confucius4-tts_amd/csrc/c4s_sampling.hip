@@ -576,7 +576,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   }
   static_assert(kCandCap % 16 == 0 && kCandCap <= 1024, "padding to 16 entries stays in the candidate array; "
                 "positions fit the entry's rank field");
-  const int C16 = ((int)C + 15) & ~15;
+  const int C16 = __builtin_amdgcn_readfirstlane(((int)C + 15) & ~15);   // uniform: scalar loop control below
   if (t < C16 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
   C4S_PHASE(27);
   __syncthreads();
@@ -585,11 +585,12 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   // kFastList + 1 places are kept
   uint64_t* srt = reinterpret_cast<uint64_t*>(fs.hist[0]);
   static_assert(sizeof(FastSh::hist[0]) >= (kFastList + 1) * sizeof(uint64_t), "the sorted head fits");
-  for (int base = 0; base < (int)C; base += kStepThreads) {
+  const int Cs = __builtin_amdgcn_readfirstlane((int)C);
+  for (int base = 0; base < Cs; base += kStepThreads) {
     const int i = base + t;
-    const uint64_t mine = (i < (int)C) ? fs.cand[i] : ~0ull;
+    const uint64_t mine = (i < Cs) ? fs.cand[i] : ~0ull;
     uint32_t r = 0;
-    if (base + wv * kWave < (int)C)   // waves without an entry skip the count
+    if (base + __builtin_amdgcn_readfirstlane(wv) * kWave < Cs)   // waves without an entry skip the count
       for (int j = 0; j < C16; j += 16) {   // 16 broadcast reads in flight a round
         uint64_t o[16];
 #pragma unroll
@@ -597,7 +598,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
 #pragma unroll
         for (int q = 0; q < 16; ++q) r += (o[q] > mine) ? 1u : 0u;
       }
-    if (i < (int)C && r < (uint32_t)(kFastList + 1)) srt[r] = mine;
+    if (i < Cs && r < (uint32_t)(kFastList + 1)) srt[r] = mine;
   }
   __syncthreads();
   C4S_PHASE(13);

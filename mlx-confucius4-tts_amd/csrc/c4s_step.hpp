@@ -339,12 +339,15 @@ __device__ __forceinline__ uint64_t rank_sort_desc(uint64_t* list, int nX, uint3
   constexpr int G = kStepThreads / E;
   static_assert(G * E == kStepThreads && E % kWave == 0 && (E / G) % 16 == 0, "whole waves and rounds per share");
   const int t = threadIdx.x;
-  const int i = t % E, q = t / E;
-  const int chunk = ((nX + G - 1) / G + 15) & ~15;   // <= E / G: every read below E
-  const int j0 = q * chunk, j1 = min(nX, j0 + chunk);
+  // the share and the bounds are the same on every lane of a wave: scalar
+  // loop control and bound tests (a vector loop costs several times as much)
+  const int nXs = __builtin_amdgcn_readfirstlane(nX);
+  const int i = t % E, q = __builtin_amdgcn_readfirstlane(t / E);
+  const int chunk = ((nXs + G - 1) / G + 15) & ~15;   // <= E / G: every read below E
+  const int j0 = q * chunk, j1 = min(nXs, j0 + chunk);
   const uint64_t mine = list[i];
   uint32_t r = 0;
-  if ((i & ~(kWave - 1)) < nX)   // waves whose keys all lie past nX skip the count (uniform)
+  if (__builtin_amdgcn_readfirstlane(i & ~(kWave - 1)) < nXs)   // waves whose keys all lie past nX skip the count
     for (int j = j0; j < j1; j += 16) {
       uint64_t o[16];
 #pragma unroll
@@ -352,8 +355,10 @@ __device__ __forceinline__ uint64_t rank_sort_desc(uint64_t* list, int nX, uint3
 #pragma unroll
       for (int u = 0; u < 16; ++u) r += ((int)(j + u < j1) & (int)(o[u] > mine)) ? 1u : 0u;
     }
+  C4S_PHASE(24);
   part[q * E + i] = r;
   __syncthreads();
+  C4S_PHASE(25);
   if (t < nX) {
     uint32_t rank = 0;
 #pragma unroll

@@ -2949,9 +2949,12 @@ __global__ __launch_bounds__(NTS) void k_stream_spec(StreamArgs a, StreamWs w) {
         // A late gather could still overwrite this ring row: the row stops
         // after this step (its decision stands), at the loop's test.
         if (spins > spin_max) bad = expired = true;
-        issue_ring(q, tokq);
-        wait_vm(0);
-        if (lane == 0) vstore(&ctl.ringtag[q & (kRing - 1)], q);
+        // the same token as the decider's: its gather (landed, tagged q) is this row
+        if (exact || !rc.ring || tokq != rtok || spins > spin_max) {
+          issue_ring(q, tokq);
+          wait_vm(0);
+          if (lane == 0) vstore(&ctl.ringtag[q & (kRing - 1)], q);
+        }
       }
       C4S_SPEC_T(5);
       if (lane == 0) {
