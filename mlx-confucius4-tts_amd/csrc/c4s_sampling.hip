@@ -440,6 +440,7 @@ __device__ __noinline__ void chain_fallback(const StepIO& io, const RowCfg& c, u
 // row takes the one-pass step.
 constexpr int kFastList = kListSmall;           // list entries the decision sees
 constexpr int kFastSel = kListSmall - 16;       // thread-top keys at or above L0
+constexpr int kFastCands = 256;                 // candidates the list step sorts
 static_assert(kStepThreads * 4 == 2048, "four histogram bins a thread");
 
 struct NoHit {   // no id drawn since the list was made
@@ -448,7 +449,7 @@ struct NoHit {   // no id drawn since the list was made
 
 struct FastSh {
   uint32_t hist[2][2048];      // the two histogram passes; the first then holds the sorted head (uint64)
-  uint64_t cand[kCandCap];     // candidates as entries (key of z, id, candidate position)
+  uint64_t cand[kFastCands];   // candidates as entries (key of z, id, candidate position)
   uint32_t red[4][kStepWaves];   // one set per workgroup scan (no barrier between reuses)
   uint32_t redm[kStepWaves];
   uint32_t bu[8];
@@ -559,7 +560,9 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
 #pragma unroll
   for (int w = 0; w < kStepWaves; ++w) tout = max(tout, fs.redm[w]);
   if (tout != 0u && c.temp_on) tout = fkey(div_rcp(kfloat(tout), rt));   // the quotient is monotone in y
-  if (C > (uint32_t)kCandCap || C == 0u) return false;   // uniform
+  // uniform; past kFastCands the rank sort costs more than the one pass
+  // (a tie group of hundreds at the k-th value, which the list cannot take anyway)
+  if (C > (uint32_t)kFastCands || C == 0u) return false;
   {
     // this thread's candidates as entries: z = fl(y / T) (sampling.cpp:16), the
     // id, and the candidate's position (pos + the candidates before it), which
@@ -574,7 +577,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
         fs.cand[i] = make_entry(c.temp_on ? div_rcp(y[j], rt) : y[j], lo + j, (int)i);
       }
   }
-  static_assert(kCandCap % 16 == 0 && kCandCap <= 1024, "padding to 16 entries stays in the candidate array; "
+  static_assert(kFastCands % 16 == 0 && kFastCands <= 1024, "padding to 16 entries stays in the candidate array; "
                 "positions fit the entry's rank field");
   const int C16 = __builtin_amdgcn_readfirstlane(((int)C + 15) & ~15);   // uniform: scalar loop control below
   if (t < C16 - (int)C) fs.cand[C + t] = 0ull;   // every entry is positive
@@ -681,7 +684,9 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
     // relative (terms and summation) + 2^-125 a term (underflow).
     // Every value goes through the same instructions (no branch a value): z is
     // -inf past the thread's ids, and an entry of the unbounded last bucket
-    // adds zero to it.
+    // adds to a word of its own thread instead (in the boundary list, unused
+    // until the compaction): on a wide row most values lie there, and lanes
+    // adding to one LDS word take turns.
     float s32 = 0.0f;
     uint32_t flags = 0, kc = 0, nf = 0;
 #pragma unroll
@@ -691,7 +696,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
       nf += fin ? 1u : 0u;
       if (topk) {
         const int b = bucket_of(z[j], m);   // the last bucket for -inf
-        atomicAdd(&hc[w * kNB + b], b < kNB - 1 ? 1u : 0u);
+        atomicAdd(b < kNB - 1 ? &hc[w * kNB + b] : reinterpret_cast<uint32_t*>(list) + t, 1u);
       } else {
         float ej = fin ? mass32(tt) : 0.0f;
         if (j < n) em[lo + j] = ej;   // read again by the kept sums and the draw
@@ -706,7 +711,8 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           // 2^-31 fixed point, truncated (ej <= 1)
           const int b = bucket_of(z[j], m);
           const uint32_t q = (uint32_t)(ej * 0x1p31f);
-          atomicAdd(&hm[w * kNB + b], b < kNB - 1 ? (unsigned long long)q + kHistOne : 0ull);
+          atomicAdd(b < kNB - 1 ? &hm[w * kNB + b] : reinterpret_cast<unsigned long long*>(list) + t,
+                    (unsigned long long)q + kHistOne);
         }
         s32 += ej;
       }
