@@ -194,13 +194,16 @@ __device__ __forceinline__ float div_rcp(float x, double r) { return (float)((do
 // 2^53), ulp of x's binade) and q = Q ulp + r (0 <= r < ulp), every add that
 // stays in the binade adds exactly D ulp, D = Q + (r > ulp / 2) (r = ulp / 2,
 // a tie resolved by parity, and the add that leaves the binade are taken one
-// at a time), so C grows by D per step while C + D < 2^53.
-// floor(a / b) for 0 <= a < 2^63 and 0 < b < 2^53: the double quotient, then
-// corrected by integer products (the GPU has no 64-bit integer divide).
-__host__ __device__ __forceinline__ long long quot_floor(long long a, long long b) {
-  long long s = (long long)floor((double)a / (double)b);
-  while (s > 0 && s * b > a) --s;
-  while ((s + 1) * b <= a) ++s;
+// at a time), so C grows by D per step while C + D < 2^53. Every count is an
+// integer below 2^53, held in a double (exact; the GPU has no 64-bit integer
+// divide, and double arithmetic beats emulated 64-bit integers).
+// floor(a / b) for integers 0 <= a < 2^53 and 0 < b < 2^53 held in doubles:
+// the rounded quotient lies within 1 of a / b and not below floor(a / b) (an
+// integer below 2^53, representable), so it is floor(a / b) or one more, and
+// the remainder a - s b, an integer of magnitude below b, is exact in one fma.
+__host__ __device__ __forceinline__ double floor_div(double a, double b) {
+  double s = floor(a / b);
+  if (fma(-s, b, a) < 0.0) s -= 1.0;
   return s;
 }
 struct RepAdd {
@@ -225,19 +228,20 @@ __host__ __device__ __noinline__ inline RepAdd repeat_add(double x, double q, in
       ++i;
       continue;
     }
-    const long long Dn = (long long)Qd + (r > 0.5 * ulp ? 1 : 0);
-    if (Dn == 0) {   // every add rounds back to x
+    const double D = Qd + (r > 0.5 * ulp ? 1.0 : 0.0);
+    if (D == 0.0) {   // every add rounds back to x
       if (counting) le = m + 1;
       break;
     }
-    const long long C = (long long)ldexp(x, 53 - ex);
-    long long sb = quot_floor((1ll << 53) - 1 - C, Dn);   // adds that keep C below 2^53
-    if (sb > (long long)(m - i)) sb = m - i;
+    const double C = ldexp(x, 53 - ex);   // an integer in [2^52, 2^53)
+    double sb = floor_div(0x1p53 - 1.0 - C, D);   // adds that keep C below 2^53
+    if (sb > (double)(m - i)) sb = (double)(m - i);
     if (counting) {
-      const double tq = ldexp(thr, 53 - ex);
-      const long long T = tq >= 0x1p62 ? (1ll << 62) : (long long)floor(tq);   // x_k <= thr iff C_k <= T
-      const long long st = quot_floor(T - C, Dn);   // T >= C here
-      if (st < sb) {
+      // x_k <= thr iff C_k <= T = floor(thr / ulp) (T >= C here); the binade's
+      // adds all stay at or below thr when T - C >= sb D
+      const double T = floor(ldexp(thr, 53 - ex));
+      if (T - C < sb * D) {   // T - C below 2^53
+        const double st = floor_div(T - C, D);
         le = i + (int)st + 1;
         counting = false;
         if (!need_x) break;
@@ -245,7 +249,7 @@ __host__ __device__ __noinline__ inline RepAdd repeat_add(double x, double q, in
         le = i + (int)sb + 1;
       }
     }
-    x = (double)(C + sb * Dn) * ulp;   // exact: below 2^53 units of ulp
+    x = (C + sb * D) * ulp;   // exact: below 2^53 units of ulp
     i += (int)sb;
     if (i == m) break;
     x = x + q;   // the add that leaves the binade

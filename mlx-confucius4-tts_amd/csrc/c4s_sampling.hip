@@ -298,16 +298,19 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
   const int lane = lane_id(), w = wave_id();
   const float ninf = neg_inf();
   const bool topk = c.topk_on;
+  // z = fl(y / T) by the exact reciprocal division; every read unconditional
+  // (index clamped); the loops rolled (code size: this path is rare)
+  const double rt = 1.0 / (double)c.temp;
   float zmax = ninf, zmin = -ninf;
   uint32_t cnt = 0;
-  for (int j = 0; j < n; ++j) {
-    const float y = val[lo + j];
-    const float z = c.temp_on ? y / c.temp : y;
-    if (sr.side(z) == 0) {
-      zmax = fmaxf(zmax, z);
-      zmin = fminf(zmin, z);
-      ++cnt;
-    }
+#pragma unroll 1
+  for (int j = 0; j < PT; ++j) {
+    const float y = val[min(lo + j, c.V - 1)];
+    const float z = c.temp_on ? div_rcp(y, rt) : y;
+    const bool inx = ((int)(j < n) & (int)(sr.side(z) == 0)) != 0;
+    zmax = inx ? fmaxf(zmax, z) : zmax;
+    zmin = inx ? fminf(zmin, z) : zmin;
+    cnt += inx ? 1u : 0u;
   }
   zmax = wave_max_dpp(zmax);
   zmin = -wave_max_dpp(-zmin);
@@ -356,18 +359,19 @@ __device__ __noinline__ int tie_cut(const RowCfg& c, const float* val, int lo, i
       if (k < 0) return 4;
       break;
     }
-    // decide again with S and the mass above X in double (and the mass below X)
+    // decide again with S and the mass above X in double (and the mass below
+    // X). X holds the one value zs and side() is monotone in z, so the entries
+    // above X are those above zs and the entries below X those below it; z is
+    // -inf past the thread's ids (exp(-inf) = 0)
     double se = 0.0, sa = 0.0, sb = 0.0;
-    for (int j = 0; j < n; ++j) {
-      const float y = val[lo + j];
-      const float z = c.temp_on ? y / c.temp : y;
-      if (z != ninf) {
-        const double ed = exp((double)(z - sr.m));
-        const int sd = sr.side(z);
-        se += ed;
-        if (sd < 0) sa += ed;
-        if (sd > 0) sb += ed;
-      }
+#pragma unroll 1
+    for (int j = 0; j < PT; ++j) {
+      const float y = val[min(lo + j, c.V - 1)];
+      const float z = (j < n) ? (c.temp_on ? div_rcp(y, rt) : y) : ninf;
+      const double ed = exp((double)(z - sr.m));
+      se += ed;
+      sa += z > zs ? ed : 0.0;
+      sb += z < zs ? ed : 0.0;
     }
     se = wave_sum_dpp(se);
     sa = wave_sum_dpp(sa);

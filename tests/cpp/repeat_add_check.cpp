@@ -5,7 +5,8 @@
 // Input families: repeated adds of 1 (the total over a tie group), of
 // 1 / total from just above 1 / total (the cumulative probabilities), of
 // arbitrary q across binades, and of q with few significand bits (adds whose
-// rounding is a tie, resolved by parity).
+// rounding is a tie, resolved by parity); the last two put the threshold on
+// one of the sums and just below it.
 #include <cmath>
 #include <cstdio>
 #include <random>
@@ -32,7 +33,7 @@ int main() {
   std::uniform_real_distribution<double> U(0.0, 1.0);
   long bad = 0, n = 0;
   for (int it = 0; it < 200000; ++it) {
-    const int family = it % 4;
+    const int family = it % 6;
     const int m = 1 + (int)(U(g) * (family == 0 ? 20000 : 3000));
     double x, q, thr;
     if (family == 0) {
@@ -47,10 +48,16 @@ int main() {
       q = std::ldexp(U(g) + 0.5, -(int)(U(g) * 20));
       x = q * (1.0 + U(g));
       thr = 2.0 * U(g);
-    } else {
+    } else if (family == 3) {
       q = std::ldexp(1.0 + std::floor(U(g) * 8) * 0x1p-52, -10);
       x = std::ldexp(1.0 + std::floor(U(g) * 16) * 0x1p-52, -(int)(U(g) * 9));
       thr = U(g);
+    } else {
+      q = 1.0 / (1.0 + U(g) * 1000.0);
+      x = q * (1.0 + U(g));
+      const int k = (int)(U(g) * (m + 1));
+      thr = literal(x, q, k, -1.0).x;   // the k-th sum
+      if (family == 5) thr = std::nextafter(thr, 0.0);
     }
     const c4s::RepAdd want = literal(x, q, m, thr);
     const c4s::RepAdd got = c4s::repeat_add(x, q, m, thr, true);
