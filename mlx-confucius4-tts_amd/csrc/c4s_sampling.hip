@@ -1228,6 +1228,7 @@ struct T2Sh {
   int bstar;
   uint32_t nge, nkeep;
   int tok;
+  uint32_t dex;                     // the draw replayed sequentially (1) or not
   uint32_t pick[2];                 // one read: the picked candidate's bin and the candidates above it
   uint32_t nq;                      // one read: gathered entries whose penalised key reaches the bound
 };
@@ -1389,21 +1390,44 @@ __device__ __forceinline__ bool one_pick(const uint32_t* hist, uint32_t m, T2Sh&
   return true;
 }
 
+// Buffer resource of `bytes` bytes from p (raw: byte offsets; a load past
+// the end returns zeros without an access). Loads through one issue on every
+// path, so that the waits of later loads count them exactly.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 rsrc_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// The first kOneUnroll 16-byte loads of this thread's stream of an f32 row
+// (the layout of topk_one_read), issued before the row's set-up so that they
+// are in flight meanwhile; with `on` false nothing is read (xf need only be
+// a pointer).
+struct OneFirst {
+  float4 v[kOneUnroll];
+};
+__device__ __forceinline__ void one_first(const float* xf, int V, bool on, OneFirst& f) {
+  const RowShape rs = row_shape(xf, V);
+  const __amdgpu_buffer_rsrc_t r = raw_rsrc(xf + rs.head, on ? 16 * rs.nq : 0);
+  const float ninf = neg_inf();
+#pragma unroll
+  for (int u = 0; u < kOneUnroll; ++u) {
+    const int q = threadIdx.x + NT * u;
+    const float4 v = rsrc_load16(r, 16 * q);
+    f.v[u] = (q < rs.nq) ? v : make_float4(ninf, ninf, ninf, ninf);
+  }
+}
+
 __device__ __forceinline__ bool topk_one_read(const RowsArgs& a, const RowCfg& c, const float* xf, const uint32_t* bitmap,
-                              T2Sh& ts, uint32_t& qkey) {
+                              T2Sh& ts, uint32_t& qkey, const OneFirst& first) {
   const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
   const RowShape rs = row_shape(xf, V);
   const float4* p4 = reinterpret_cast<const float4*>(xf + rs.head);
   const float ninf = neg_inf();
   uint32_t t0 = 0u, t1 = 0u, t2 = 0u, t3 = 0u;   // 0: below every packed key
   const int iters = (rs.nq + NT - 1) / NT;
-  for (int j0 = 0; j0 < iters; j0 += kOneUnroll) {
-    float4 v[kOneUnroll];
-#pragma unroll
-    for (int u = 0; u < kOneUnroll; ++u) {
-      const int q = t + NT * (j0 + u);
-      v[u] = (q < rs.nq) ? p4[q] : make_float4(ninf, ninf, ninf, ninf);
-    }
+  auto take = [&](const float4 (&v)[kOneUnroll], int j0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kOneUnroll; ++u) {
       const uint32_t i0 = 4u * (uint32_t)(j0 + u);
@@ -1412,6 +1436,16 @@ __device__ __forceinline__ bool topk_one_read(const RowsArgs& a, const RowCfg& c
       one_insert(t0, t1, t2, t3, one_pack(v[u].z, i0 + 2u));
       one_insert(t0, t1, t2, t3, one_pack(v[u].w, i0 + 3u));
     }
+  };
+  take(first.v, 0);   // loads 0 .. kOneUnroll - 1 (past the row: -inf)
+  for (int j0 = kOneUnroll; j0 < iters; j0 += kOneUnroll) {
+    float4 v[kOneUnroll];
+#pragma unroll
+    for (int u = 0; u < kOneUnroll; ++u) {
+      const int q = t + NT * (j0 + u);
+      v[u] = (q < rs.nq) ? p4[q] : make_float4(ninf, ninf, ninf, ninf);
+    }
+    take(v, j0);
   }
   const int edge = (t < rs.head) ? t : ((t < rs.head + rs.tail) ? rs.head + 4 * rs.nq + (t - rs.head) : -1);
   if (edge >= 0) one_insert(t0, t1, t2, t3, one_pack(xf[edge], kOneEdge));
@@ -1529,8 +1563,51 @@ __device__ __forceinline__ bool topk_finish(const RowsArgs& a, int row, const Ro
     int ns = (int)k;
     while (ns < n && (uint32_t)(ts.list[ns] >> 32) >= kkey) ++ns;
     const float vmax = kfloat((uint32_t)(ts.list[0] >> 32));
-    int nkeep = ns;
-    if (c.topp_on) {
+    int nkeep = ns, tok = -2;   // -2: not decided here
+    uint32_t dex = 0u;
+    if (ns <= kWave) {
+      // At most 64 survivors, one a lane in value order: top_p and the draw
+      // with sums formed in parallel, each decision farther than rel_eps from
+      // its boundary or taken by the sequential sums below (top_p) or the
+      // sequential replay of lane_draw (the draw), as the candidate-list step
+      // does. Survivor j's mass is exp(z_j - vmax), vmax the first survivor's.
+      const bool sv = lane < ns;
+      const uint64_t ent = ts.list[sv ? lane : 0];
+      const float zs = sv ? kfloat((uint32_t)(ent >> 32)) : ninf;
+      const int ids = (int)~(uint32_t)ent;
+      const double e = sv ? exp((double)(zs - vmax)) : 0.0;
+      // the sequential path for subnormal masses and below the draw's -1e30 floor
+      bool ok = !__ballot(sv && e < 0x1p-1000) && !(vmax < -1e30f);
+      const double thr = 1.0 - (double)c.p;
+      if (ok && c.topp_on && thr >= 0.0) {
+        // entry j removed iff the mass at or below it in ascending order,
+        // M = S - (mass above it), is <= thr S (sampling.cpp:60-65)
+        const double S = wave_sum_dpp(e);
+        const double M = S - (wave_scan_f64(e) - e);
+        bool rem, unsure = false;
+        if (thr == 0.0) {
+          rem = sv && M == 0.0;
+        } else {
+          const double A = thr * S;
+          rem = sv && M <= A;
+          unsure = sv && lane >= c.min_keep && !(fabs(M - A) > rel_eps(V) * fmax(M, A));
+        }
+        if (__ballot(unsure)) {
+          ok = false;
+        } else {
+          nkeep = ns - __popcll(__ballot(rem));
+          const int mk = min(max(0, c.min_keep), ns);   // sampling.cpp:67-68
+          if (nkeep < mk) nkeep = mk;
+        }
+      }
+      if (ok) {   // text2semantic.cpp:150-165 over the kept survivors in id order
+        const uint64_t st2 = xorshift64(a.rng[row]);
+        tok = lane_draw<19>(sv && lane < nkeep, ids, ids, e, unit_from_state(st2), V, dex);
+      } else {
+        nkeep = ns;
+      }
+    }
+    if (tok == -2 && c.topp_on) {
       // sampling.cpp:52-65 in ascending order (list position ns - 1 - j)
       double total = 0.0;
       for (int base = 0; base < ns; base += kWave) {
@@ -1551,7 +1628,11 @@ __device__ __forceinline__ bool topk_finish(const RowsArgs& a, int row, const Ro
       const int mk = min(max(0, c.min_keep), ns);   // sampling.cpp:67-68
       if (nkeep < mk) nkeep = mk;
     }
-    if (lane == 0) ts.nkeep = (uint32_t)nkeep;
+    if (lane == 0) {
+      ts.nkeep = (uint32_t)nkeep;
+      ts.tok = tok;
+      ts.dex = dex;
+    }
   }
   __syncthreads();
   const int nkeep = (int)ts.nkeep;
@@ -1565,6 +1646,22 @@ __device__ __forceinline__ bool topk_finish(const RowsArgs& a, int row, const Ro
       const int i = (int)~(uint32_t)ts.list[j];
       mrow[i] = src.z(i, src.xf ? src.xf[i] : __uint_as_float((uint32_t)src.xb[i] << 16));
     }
+  }
+  if (ts.tok != -2) {   // drawn above
+    if (t == 0) {
+      const int tok = ts.tok;
+      a.out_tok[row] = tok;
+      a.rng[row] = xorshift64(a.rng[row]);
+      join_history(a, row, tok);
+      if (a.stats) {
+        uint32_t* st = a.stats + 4 * (int64_t)row;
+        st[0] = 1u | 2u | 4u | 32u | stat_bits;
+        st[1] = 0u;
+        st[2] = ts.dex;
+        st[3] = (uint32_t)nkeep;
+      }
+    }
+    return true;
   }
   // the kept entries in id order: (~id) as the high half sorts descending by it
   int Pk = 1;
@@ -1626,14 +1723,15 @@ __device__ __forceinline__ bool topk_finish(const RowsArgs& a, int row, const Ro
 
 // Returns false (nothing written) when the survivors' bucket holds more than
 // the sort takes; the multi-pass chain decides the row then.
-__device__ __forceinline__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts) {
+__device__ __forceinline__ bool topk_two_pass(const RowsArgs& a, int row, const RowCfg& c, const T2Row& src, T2Sh& ts,
+                                              const OneFirst& first) {
   const int V = c.V, t = threadIdx.x, w = wave_id(), lane = lane_id();
   const float ninf = neg_inf();
   const uint32_t k = (uint32_t)c.k;
   // one read of the row when its checks pass
   uint32_t qkey = 0u;
   bool one = src.xf && V <= kOneMaxV && (!c.pen_on || c.pen >= 1.0f) &&
-             topk_one_read(a, c, src.xf, src.bitmap, ts, qkey);
+             topk_one_read(a, c, src.xf, src.bitmap, ts, qkey, first);
   if (one) {
     const int n = (int)ts.n;
     if (n <= kRankSortMax) {
@@ -1704,12 +1802,40 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
   __shared__ Scratch sh;
   const int row = blockIdx.x;
   const int V = a.vocab;
-  if (a.row_active && !a.row_active[row]) {
+  // the row's flags and parameters by scalar loads, all issued before any
+  // waits for them (a byte flag read as its aligned word: flag_byte)
+  const bool act = a.row_active ? flag_byte(a.row_active, row) : true;
+  const bool sample = a.do_sample ? flag_byte(a.do_sample, row) : true;
+  const float pv = a.pen ? a.pen[row] : 1.0f, tv = a.temp ? a.temp[row] : 1.0f;
+  const int32_t kv = a.top_k ? a.top_k[row] : 0, mv = a.min_keep ? a.min_keep[row] : 1;
+  const float ppv = a.top_p ? a.top_p[row] : 1.0f;
+  if (!act) {
     if (threadIdx.x == 0) a.out_tok[row] = -1;
     return;
   }
-  const RowCfg c = make_cfg(a.mode, V, row, a.temp, a.top_k, a.top_p, a.pen, a.min_keep,
-                            a.do_sample);
+  const RowCfg c = make_cfg_vals(a.mode, V, pv, tv, kv, ppv, mv, (a.mode & kCustom) || sample);
+  const int64_t roff = (int64_t)row * a.ld;
+  // The history's first ids (four a thread), then, for a row that the top-k
+  // read takes, that read's first loads: in flight during the set-up (loads
+  // complete in issue order, so the ids come first)
+  constexpr int kPreIds = 4;
+  const bool csr = c.pen_on && !a.hist_bits;
+  const int64_t h0 = csr ? a.hist_off[row] : 0, h1 = csr ? a.hist_off[row + 1] : 0;
+  int hid[kPreIds];
+  {
+    const int nb = (int)min(h1 - h0, (int64_t)NT * kPreIds) * 4;   // the first ids' bytes
+    const __amdgpu_buffer_rsrc_t r = raw_rsrc(csr ? a.hist_ids + h0 : a.out_tok, nb);
+#pragma unroll
+    for (int i = 0; i < kPreIds; ++i) {
+      const int jo = threadIdx.x + NT * i;
+      const int id = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * jo, 0, 0);
+      hid[i] = 4 * jo < nb ? id : -1;
+    }
+  }
+  const bool one_row = c.draw && c.topk_on && c.k <= kT2MaxK && V <= kT2MaxV && a.rng && a.dtype == 0 &&
+                       V <= kOneMaxV && (!c.pen_on || c.pen >= 1.0f);
+  OneFirst first;
+  one_first(static_cast<const float*>(a.logits) + (one_row ? roff : 0), V, one_row, first);
   uint32_t* bitmap = reinterpret_cast<uint32_t*>(smem);
   const int nw = (V + 31) / 32;
   for (int w = threadIdx.x; w < nw; w += NT) bitmap[w] = 0u;
@@ -1719,8 +1845,10 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
       const uint32_t* hb = a.hist_bits + (int64_t)row * hist_words(V);
       for (int w = threadIdx.x; w < nw; w += NT) bitmap[w] = hb[w];
     } else {
-      const int64_t h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-      for (int64_t j = h0 + threadIdx.x; j < h1; j += NT) {
+#pragma unroll
+      for (int i = 0; i < kPreIds; ++i)
+        if (hid[i] >= 0 && hid[i] < V) atomicOr(&bitmap[hid[i] >> 5], 1u << (hid[i] & 31));
+      for (int64_t j = h0 + threadIdx.x + (int64_t)NT * kPreIds; j < h1; j += NT) {
         const int id = a.hist_ids[j];
         if (id < 0 || id >= V) continue;
         atomicOr(&bitmap[id >> 5], 1u << (id & 31));
@@ -1728,7 +1856,6 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
     }
     __syncthreads();
   }
-  const int64_t roff = (int64_t)row * a.ld;
   C4S_PHASE(0);
   if (c.draw && c.topk_on && c.k <= kT2MaxK && V <= kT2MaxV && a.rng) {
     T2Row tr;
@@ -1741,7 +1868,7 @@ __global__ __launch_bounds__(NT) void k_rows_global(RowsArgs a) {
     tr.temp = c.temp;
     tr.rpen = 1.0 / (double)c.pen;
     tr.rtemp = 1.0 / (double)c.temp;
-    if (topk_two_pass(a, row, c, tr, *reinterpret_cast<T2Sh*>(smem + t2_offset(V)))) return;
+    if (topk_two_pass(a, row, c, tr, *reinterpret_cast<T2Sh*>(smem + t2_offset(V)), first)) return;
     __syncthreads();
   }
   GlobalRow src;
