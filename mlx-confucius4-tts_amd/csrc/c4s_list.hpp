@@ -134,12 +134,14 @@ __device__ __forceinline__ bool list_step(const SumHdr& h, uint64_t e0, uint64_t
   const uint64_t mk0 = __ballot(u0 && r0 == k - 1), mk1 = __ballot(u1 && r1 == k - 1);
   const float zk = mk0 ? readlane_f32(z0, __ffsll((unsigned long long)mk0) - 1)
                        : readlane_f32(z1, __ffsll((unsigned long long)mk1) - 1);
-  float zh = ninf;
-  if (h0) zh = z0;
-  if (h1) zh = fmaxf(zh, z1);
-  zh = wave_max_dpp(zh);
-  o.why = kWhyHit;
-  if (!(zh < zk) && zh != ninf) return false;
+  if constexpr (!kNoHits) {
+    float zh = ninf;
+    if (h0) zh = z0;
+    if (h1) zh = fmaxf(zh, z1);
+    zh = wave_max_dpp(zh);
+    o.why = kWhyHit;
+    if (!(zh < zk) && zh != ninf) return false;
+  }
   o.why = kWhyBound;
   if (!(zk > ninf)) return false;
   if (h.tout != 0u && !(kfloat(h.tout) < zk)) return false;   // everything outside stays below

@@ -445,6 +445,7 @@ __device__ __noinline__ void chain_fallback(const StepIO& io, const RowCfg& c, u
 constexpr int kFastList = kListSmall;           // list entries the decision sees
 constexpr int kFastSel = kListSmall - 16;       // thread-top keys at or above L0
 constexpr int kFastCands = 256;                 // candidates the list step sorts
+constexpr int kFastOneBin = 64;                 // thread-top keys from the first pass's bin up: no second pass
 static_assert(kStepThreads * 4 == 2048, "four histogram bins a thread");
 
 struct NoHit {   // no id drawn since the list was made
@@ -536,12 +537,16 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     C4S_PHASE(22);
     if (fast_pick(fs.hist[0], fs.red[0], fs.bu, msel, b1, ab1)) {
       C4S_PHASE(23);
-      if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[1][(t1 >> 10) & 2047u], 1u);
-      if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[1][(t2 >> 10) & 2047u], 1u);
-      __syncthreads();
-      uint32_t b2, ab2;
-      fast_pick(fs.hist[1], fs.red[1], fs.bu + 2, msel - ab1, b2, ab2);
-      L0 = (b1 << 21) | (b2 << 10);
+      if (ab1 + fs.hist[0][b1] <= (uint32_t)kFastOneBin) {
+        L0 = b1 << 21;   // few keys from b1 up: its floor bounds them closely enough (uniform)
+      } else {
+        if (t1 && (t1 >> 21) == b1) atomicAdd(&fs.hist[1][(t1 >> 10) & 2047u], 1u);
+        if (t2 && (t2 >> 21) == b1) atomicAdd(&fs.hist[1][(t2 >> 10) & 2047u], 1u);
+        __syncthreads();
+        uint32_t b2, ab2;
+        fast_pick(fs.hist[1], fs.red[1], fs.bu + 2, msel - ab1, b2, ab2);
+        L0 = (b1 << 21) | (b2 << 10);
+      }
     }
   }
   L0 = max(L0, 1u);   // the same values; excludes the zero keys past the row
@@ -624,7 +629,7 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     bool ok = nlist > 0 && ztop >= -1e30f;
     C4S_PHASE(24);
     if (ok) {
-      // each entry keeps its candidate position as its id-order key (10 bits)
+      // each entry keeps its candidate position as its id-order key (8 bits)
       e0 = lane < nlist ? e0 : 0ull;
       e1 = lane + kWave < nlist ? e1 : 0ull;
       SumHdr h{};
@@ -633,7 +638,8 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
       h.flags = 0u;
       uint64_t r = io.rng ? *io.rng : 0ull;
       StepOut o{0, 0u, 0u, 0u, 0u};
-      ok = list_step<10, true>(h, e0, e1, 0.0f, 0.0f, c, V, NoHit{}, r, fs.cs, o);
+      static_assert(kFastCands <= 256, "candidate positions in 8 bits");
+      ok = list_step<8, true>(h, e0, e1, 0.0f, 0.0f, c, V, NoHit{}, r, fs.cs, o);
       C4S_PHASE(25);
       if (ok && lane == 0) step_out(io, V, o.tok, r, true, 1u | 2u | 4u | 16u | 32u, 0u, o.dex, o.kept);
     }
