@@ -158,9 +158,15 @@ typedef struct c4s_stream {
  * calls of at most 1024 steps). Both give the same tokens. */
 #define C4S_STREAM_NO_SPECULATION 2u
 
-/* LM head: LayerNorm(hidden) -> bf16 -> hidden @ weight^T + bias -> f32 logits
+/* LM head: LayerNorm(hidden) @ weight^T + bias -> f32 logits
  * (text2semantic.cpp:118-121; nn.cpp:73-83 eps/biased variance, nn.cpp:11-16
- * weight stored (out, in)). hidden_dim must be a multiple of 32. */
+ * weight stored (out, in)). The LayerNorm is folded into the product, never
+ * materialised: logits[m][n] = inv_m (G[m][n] - mu_m c[n]) + d[n] + bias[n],
+ * G = (W gamma) x^T with W gamma split into two bf16 terms, c = W gamma and
+ * d = W beta over the inputs, mu_m and inv_m = 1 / sqrt(var_m + eps) from the
+ * row's sums; accumulation in fp32 (the tests hold it within 2e-4 absolute of
+ * an fp64 evaluation for logits up to 4 in magnitude). hidden_dim must be a positive multiple of 32; hidden, gamma,
+ * beta and weight must be 16-byte aligned (8-bit weights: 8), else C4S_EINVAL. */
 typedef struct c4s_head {
   const uint16_t* hidden;       /* [M][D] bf16 */
   const float* gamma;           /* [D] */
