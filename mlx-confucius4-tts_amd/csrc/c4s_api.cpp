@@ -23,9 +23,9 @@ struct c4s_ctx {
   size_t ws_bytes = 0;
   void* logits_ws = nullptr;          // LM head + sample: logits when the caller gives none
   size_t logits_bytes = 0;
-  // host-helper staging (device)
-  void* stage = nullptr;
-  size_t stage_bytes = 0;
+  // host-helper staging: pinned host memory that the device maps
+  void* hstage = nullptr;
+  size_t hstage_bytes = 0;
   // two-phase stream: summaries of one chunk of steps, per-row carried state
   void* sum_ws = nullptr;
   size_t sum_bytes = 0;
@@ -310,7 +310,7 @@ int c4s_destroy(c4s_ctx* ctx) {
   if (ctx->scan_s) (void)hipStreamSynchronize(ctx->scan_s);
   for (hipStream_t st : {ctx->scan_m, ctx->chain_m, ctx->side_m})
     if (st) (void)hipStreamSynchronize(st);
-  for (void* p : {ctx->ws, ctx->logits_ws, ctx->stage, ctx->sum_ws, ctx->state_ws, ctx->segres})
+  for (void* p : {ctx->ws, ctx->logits_ws, ctx->sum_ws, ctx->state_ws, ctx->segres})
     if (p) (void)hipFree(p);
   for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->host_stream) (void)hipStreamDestroy(ctx->host_stream);
@@ -323,6 +323,7 @@ int c4s_destroy(c4s_ctx* ctx) {
                         ctx->ev_side[1], ctx->ev_side[2]})
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->status_host) (void)hipHostFree(const_cast<uint32_t*>(ctx->status_host));
+  if (ctx->hstage) (void)hipHostFree(ctx->hstage);
   delete ctx;
   return C4S_OK;
 }
@@ -748,13 +749,12 @@ struct Stage {
   int32_t* tok;
 };
 
-int stage_for(c4s_ctx* ctx, int32_t n, int64_t n_ids, Stage* st) {
+// The staging layout of one single-row call from `base` (device or host
+// address); returns its size in bytes (through tok).
+size_t stage_at(char* base, int32_t n, int64_t n_ids, Stage* st) {
   auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t b_logits = al((size_t)n * 4), b_ids = al((size_t)std::max<int64_t>(n_ids, 1) * 4);
-  const size_t need = b_logits + b_ids + al(16) + al(12) + al(8) + al(8) + al(4);
-  int rc = ensure(ctx, &ctx->stage, &ctx->stage_bytes, need, "staging", ctx->host_stream);
-  if (rc) return rc;
-  char* p = static_cast<char*>(ctx->stage);
+  char* p = base;
   st->logits = reinterpret_cast<float*>(p); p += b_logits;
   st->ids = reinterpret_cast<int32_t*>(p); p += b_ids;
   st->off = reinterpret_cast<int64_t*>(p); p += al(16);
@@ -762,9 +762,31 @@ int stage_for(c4s_ctx* ctx, int32_t n, int64_t n_ids, Stage* st) {
   st->iparams = reinterpret_cast<int32_t*>(p); p += al(8);
   st->rng = reinterpret_cast<uint64_t*>(p); p += al(8);
   st->tok = reinterpret_cast<int32_t*>(p);
+  return (size_t)(p - base) + 4;
+}
+
+// The pinned host staging area, at least `need` bytes.
+int ensure_host_stage(c4s_ctx* ctx, size_t need) {
+  if (need <= ctx->hstage_bytes) return C4S_OK;
+  if (ctx->hstage) {
+    hipError_t e = hipHostFree(ctx->hstage);
+    ctx->hstage = nullptr;
+    ctx->hstage_bytes = 0;
+    if (e != hipSuccess) return hip_fail(ctx, e, "host staging");
+  }
+  hipError_t e = hipHostMalloc(&ctx->hstage, need, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    ctx->hstage = nullptr;
+    return e == hipErrorOutOfMemory ? fail(ctx, C4S_ENOMEM, "host staging: out of pinned memory")
+                                    : hip_fail(ctx, e, "host staging");
+  }
+  ctx->hstage_bytes = need;
   return C4S_OK;
 }
 
+// One synchronous single-row call: the row, the history and the parameters
+// gathered into pinned host memory, which the step reads and writes in place
+// (the device maps it), then the results copied out after the step.
 int host_call(c4s_ctx* ctx, float* logits, int32_t n, const int32_t* ids, int64_t n_ids,
               float temp, int32_t k, float p, float pen, int32_t min_keep, uint64_t* rng,
               uint32_t mode, bool write_back, int32_t* tok_out) {
@@ -775,51 +797,50 @@ int host_call(c4s_ctx* ctx, float* logits, int32_t n, const int32_t* ids, int64_
   if (n_ids > 0 && !ids) return fail(ctx, C4S_EINVAL, "ids is NULL");
   DeviceGuard g(ctx->device);
   if (g.err != hipSuccess) return hip_fail(ctx, g.err, "hipSetDevice");
-  Stage st;
-  int rc = stage_for(ctx, n, n_ids, &st);
+  Stage hs, ds;
+  int rc = ensure_host_stage(ctx, stage_at(nullptr, n, n_ids, &hs));
   if (rc) return rc;
+  void* dev = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&dev, ctx->hstage, 0);
+  if (e != hipSuccess) return hip_fail(ctx, e, "host staging: device address");
+  stage_at(static_cast<char*>(ctx->hstage), n, n_ids, &hs);
+  stage_at(static_cast<char*>(dev), n, n_ids, &ds);
   hipStream_t s = ctx->host_stream;
   const int64_t off[2] = {0, n_ids};
   const float fp[3] = {temp, p, pen};
   const int32_t ip[2] = {k, min_keep};
-  hipError_t e = hipMemcpyAsync(st.logits, logits, (size_t)n * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && n_ids > 0)
-    e = hipMemcpyAsync(st.ids, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(st.off, off, sizeof(off), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(st.fparams, fp, sizeof(fp), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess) e = hipMemcpyAsync(st.iparams, ip, sizeof(ip), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && rng) e = hipMemcpyAsync(st.rng, rng, 8, hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) return hip_fail(ctx, e, "staging copy");
+  if (n > 0) std::memcpy(hs.logits, logits, (size_t)n * 4);
+  if (n_ids > 0) std::memcpy(hs.ids, ids, (size_t)n_ids * 4);
+  std::memcpy(hs.off, off, sizeof(off));
+  std::memcpy(hs.fparams, fp, sizeof(fp));
+  std::memcpy(hs.iparams, ip, sizeof(ip));
+  if (rng) std::memcpy(hs.rng, rng, 8);
   c4s_rows r{};
-  r.logits = st.logits;
+  r.logits = ds.logits;
   r.ld = n;
   r.dtype = C4S_DTYPE_F32;
   r.n_rows = 1;
   r.vocab = n;
-  r.hist_ids = st.ids;
-  r.hist_offsets = st.off;
-  r.temperature = st.fparams;
-  r.top_p = st.fparams + 1;
-  r.rep_penalty = st.fparams + 2;
-  r.top_k = st.iparams;
-  r.min_keep = st.iparams + 1;
-  r.rng_state = st.rng;
-  r.out_token = st.tok;
-  r.out_masked = write_back ? st.logits : nullptr;
+  r.hist_ids = ds.ids;
+  r.hist_offsets = ds.off;
+  r.temperature = ds.fparams;
+  r.top_p = ds.fparams + 1;
+  r.rep_penalty = ds.fparams + 2;
+  r.top_k = ds.iparams;
+  r.min_keep = ds.iparams + 1;
+  r.rng_state = ds.rng;
+  r.out_token = ds.tok;
+  r.out_masked = write_back ? ds.logits : nullptr;
   r.mode = mode;
   rc = validate_rows(ctx, &r);
   if (rc) return rc;
   rc = launch_rows_checked(ctx, &r, s);
   if (rc) return rc;
-  if (write_back) e = hipMemcpyAsync(logits, st.logits, (size_t)n * 4, hipMemcpyDeviceToHost, s);
-  int32_t tok = 0;
-  if (e == hipSuccess) e = hipMemcpyAsync(&tok, st.tok, 4, hipMemcpyDeviceToHost, s);
-  uint64_t r_out = 0;
-  if (e == hipSuccess && rng) e = hipMemcpyAsync(&r_out, st.rng, 8, hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(ctx, e, "single-row call");
-  if (rng) *rng = r_out;
-  if (tok_out) *tok_out = tok;
+  if (write_back && n > 0) std::memcpy(logits, hs.logits, (size_t)n * 4);
+  if (rng) std::memcpy(rng, hs.rng, 8);
+  if (tok_out) std::memcpy(tok_out, hs.tok, 4);
   return C4S_OK;
 }
 
