@@ -181,6 +181,30 @@ def test_large_vocab_general_and_bf16(orc, gpu_ctx):
     compare_with_oracle(orc, gpu_ctx, b)
 
 
+def test_large_vocab_one_wave_finish(orc, gpu_ctx):
+    """Large-vocabulary top-k rows with at most 64 survivors decide top_p and
+    the draw on one wave with parallel sums; a cut within the error margin
+    goes to the sequential sums. Rows: two tied maxima at p = 0.5 (the cut
+    lies exactly on the boundary: cum = 0.5 <= 1 - p), four tied maxima at
+    p = 0.75, min_tokens_to_keep above the survivors' count, k = 64 with
+    ties past the k-th value (65 survivors: the sequential path), and plain
+    rows; tokens and masked rows bit for bit. Statistics bit 6 (read once) on
+    every row."""
+    V, n = 20000, 8
+    b = W.large_vocab(seed=51, rows=n, V=V, hist_len=300)
+    b.pen[:] = 1.0
+    b.top_k[:] = np.array([2, 4, 10, 64, 50, 30, 5, 1], np.int32)
+    b.top_p[:] = np.array([0.5, 0.75, 0.9, 0.95, 0.5, 0.3, 0.999, 0.8], np.float32)
+    x = b.logits
+    top = x.max(axis=1) + 3.0
+    x[0, [11, 4000]] = top[0]
+    x[1, [7, 19, 9000, 15000]] = top[1]
+    x[3, 100:165] = top[3]   # 65 equal values at the top: all survive top_k = 64
+    mk = np.array([1, 1, 12, 1, 1, 1, 1, 1], np.int32)
+    tok, st = compare_with_oracle(orc, gpu_ctx, b, min_keep=mk)
+    assert ((st[:, 0] >> 6) & 1).all(), st[:, 0].tolist()
+
+
 def _rows_from(rows, temp, top_k, top_p, pen, hist, do_sample=None, seed=1234):
     n = len(rows)
     V = max(len(r) for r in rows)
