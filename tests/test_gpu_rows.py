@@ -93,23 +93,30 @@ def test_draw_in_double(orc, gpu_ctx):
 
 
 @pytest.mark.parametrize("masked", [True, False])
-@pytest.mark.parametrize("sigma", [0.3, 0.7, 1.5])
-def test_flat_rows_refined_boundary(orc, gpu_ctx, sigma, masked):
+@pytest.mark.parametrize("shape,sigma", [("gauss", 0.3), ("gauss", 0.7), ("gauss", 1.5), ("gauss", 1e-4),
+                                         ("cluster", 0.02), ("cluster", 0.2)])
+def test_flat_rows_refined_boundary(orc, gpu_ctx, shape, sigma, masked):
     """Narrow logit ranges (an LM head's output): hundreds of entries share the
     boundary bucket of the nucleus cut or of the k-th value, so the one-pass
-    step refines the boundary buckets in a second histogram."""
+    step refines the boundary buckets in a second histogram. "cluster": a
+    tight cluster and a few values 40 below it. sigma 1e-4: every entry in one
+    bucket and nearly all in one sub-bucket (more than one sort takes, not one
+    value: the multi-pass chain decides)."""
     b = W.batch64(seed=40, rows=64)
     g = np.random.default_rng(41)
     b.logits[:] = (sigma * g.standard_normal(b.logits.shape)).astype(np.float32)
+    if shape == "cluster":
+        b.logits[:, 1::2000] = -40.0
     b.top_k[:] = np.resize(np.array([0, 0, 0, 50, 200, 0, 400, 0], np.int32), 64)
     b.top_p[:] = np.resize(np.array([0.9, 0.8, 0.95, 1.0, 0.9, 0.5, 1.0, 0.99], np.float32), 64)
-    print(f"flat rows sigma={sigma} masked={masked}", flush=True)
+    print(f"flat rows {shape} sigma={sigma} masked={masked}", flush=True)
     tok, st = compare_with_oracle(orc, gpu_ctx, b, masked=masked)
     one_pass = (st[:, 0] & 16) != 0
     print("rows decided in one pass", int(one_pass.sum()), "of", b.n_rows)
     for i in np.flatnonzero(~one_pass):
         print(f"  row {i}: top_k {b.top_k[i]} top_p {b.top_p[i]} temp {b.temp[i]:.3f} pen {b.pen[i]} stats {st[i]}")
-    assert one_pass.mean() > 0.9
+    if sigma >= 0.01:
+        assert one_pass.mean() > 0.9
 
 
 @pytest.mark.parametrize("masked", [True, False])
