@@ -801,15 +801,22 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           sc2 = (float)kNB / (float)(bhi + 1 - lo2);
           for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
           __syncthreads();
+          // Per value: no branch, and the fp32 mass the first pass cached (the
+          // same mass32), read unconditionally (index clamped). -inf and the
+          // padding past the thread's ids lie in the last bucket, never in the
+          // window (bhi < kNB - 1); entries outside it add to a word of the
+          // thread's own (the boundary list, unused until the compaction).
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
-            if (j < n && z[j] != ninf) {
-              const int b = bucket_of(z[j], m);
-              if (b >= lo2 && b <= bhi) {
-                const int sb = sub_bucket_of(z[j], m, lo2, sc2);
-                if (topk) atomicAdd(&hc[w * kNB + sb], 1u);
-                else atomicAdd(&hm[w * kNB + sb], (unsigned long long)(uint32_t)(mass32(z[j] - m) * 0x1p31f) + kHistOne);
-              }
+            const int b = bucket_of(z[j], m);
+            const bool inw = ((int)(b >= lo2) & (int)(b <= bhi)) != 0;
+            const int sb = sub_bucket_of(z[j], m, lo2, sc2);
+            if (topk) {
+              atomicAdd(inw ? &hc[w * kNB + sb] : reinterpret_cast<uint32_t*>(list) + t, 1u);
+            } else {
+              const float ec = em[min(lo + j, c.V - 1)];
+              atomicAdd(inw ? &hm[w * kNB + sb] : reinterpret_cast<unsigned long long*>(list) + t,
+                        (unsigned long long)(uint32_t)(ec * 0x1p31f) + kHistOne);
             }
           }
           __syncthreads();
