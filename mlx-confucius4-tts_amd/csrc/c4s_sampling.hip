@@ -145,41 +145,39 @@ __device__ __forceinline__ void draw_finish(const StepIO& io, const RowCfg& c, c
   int found = -1;
   bool certain = false;
   C4S_PHASE_IF(owner, 18);
-  if (owner) {
-    // the thread's kept masses first (independent loads and tests, issued
-    // together), then the prefix in id order without branches: the first
-    // kept id whose running sum reaches r, and the sums on both sides of it
-    float e[PT];
+  const uint64_t obw = __ballot(owner);
+  if (obw) {
+    // the owner's wave: lane j takes the owner's id lo + j and its kept fp32
+    // mass (independent loads and tests, one a lane), the running sums in id
+    // order by a wave scan in double from the owner's exclusive prefix (its
+    // rounding, about 2^-53 relative a step, lies far inside the margin), then
+    // the first kept id whose sum reaches r and the sums on both sides of it
+    const int ol = __ffsll((unsigned long long)obw) - 1, l = lane_id();
+    float zl = neg_inf();
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      if constexpr (kCached) {   // z is -inf past the thread's ids: not kept here
-        const float ec = em[min(lo + j, c.V - 1)];
-        e[j] = ((int)(z[j] != neg_inf()) & (int)kept_in(kr, z[j], m, lo + j)) ? ec : 0.0f;
-      } else {
-        bool kp;
-        e[j] = kept_mass32(kr, z[j], m, lo + j, kp);
-      }
+      const float zj = readlane_f32(z[j], ol);
+      zl = (l == j) ? zj : zl;
     }
-    // running sums in id order (adding a zero mass leaves a sum as it is),
-    // then the first kept id whose sum reaches r, all as selects
-    double pre[PT];
-    double a = ds.ex;
-#pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      a = a + (double)e[j];
-      pre[j] = a;
+    const int lo_o = (int)readlane_u32((uint32_t)lo, ol);
+    const double ex_o = readlane_f64(ds.ex, ol);
+    float el;   // lanes past the owner's ids hold -inf: not kept
+    if constexpr (kCached) {
+      const float ec = em[min(lo_o + l, c.V - 1)];
+      el = ((int)(zl != neg_inf()) & (int)kept_in(kr, zl, m, lo_o + l)) ? ec : 0.0f;
+    } else {
+      bool kp;
+      el = kept_mass32(kr, zl, m, lo_o + l, kp);
     }
-    int fj = PT;
-#pragma unroll
-    for (int j = PT - 1; j >= 0; --j) fj = ((e[j] > 0.0f) & (pre[j] >= r)) ? j : fj;
-    double acc = a, prev = ds.ex;
-#pragma unroll
-    for (int j = 0; j < PT; ++j) {
-      acc = (j == fj) ? pre[j] : acc;
-      prev = (j + 1 == fj) ? pre[j] : prev;
+    const double al = ex_o + wave_scan_f64((double)el);
+    const uint64_t hit = __ballot(el > 0.0f && al >= r);
+    if (hit) {
+      const int f = __ffsll((unsigned long long)hit) - 1;
+      const double af = readlane_f64(al, f);
+      const double pf = f > 0 ? readlane_f64(al, max(f - 1, 0)) : ex_o;
+      found = lo_o + f;
+      certain = (af - r > margin) && (r - pf > margin);
     }
-    found = fj < PT ? lo + fj : -1;
-    certain = found >= 0 && (acc - r > margin) && (r - prev > margin);
   }
   C4S_PHASE_IF(owner, 19);
   if (!__syncthreads_or(owner && !certain)) {
