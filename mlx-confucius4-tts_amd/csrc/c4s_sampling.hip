@@ -864,11 +864,17 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         // one atomic (slot order is arbitrary: the sort orders them)
         static_assert(PT < 32, "a thread's X entries as one bit mask");
         uint32_t xm = 0;   // this thread's X entries (its ids only: the -inf padding may lie in the last bucket)
-        if (!refine) {   // uniform: X is whole buckets xlo .. xhi
+        if (!refine) {
+          // uniform: X is whole buckets xlo .. xhi. With q = (m - z) 4 (exact:
+          // a power of two; q >= 0, +inf for -inf) bucket_of is trunc(q) below
+          // 255, else 255: b >= xlo iff !(q < xlo) (NaN in the last bucket), and
+          // b <= xhi iff q < xhi + 1 unless xhi is the last bucket
+          const float qlo = (float)xlo, qhi = xhi >= kNB - 1 ? __builtin_inff() : (float)(xhi + 1);
+          const bool last = xhi >= kNB - 1;
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
-            const int b = bucket_of(z[j], m);
-            xm |= ((int)(b >= xlo) & (int)(b <= xhi)) ? 1u << j : 0u;
+            const float q = (m - z[j]) * kBucketScale;
+            xm |= ((int)!(q < qlo) & (int)(last || q < qhi)) ? 1u << j : 0u;
           }
         } else {
 #pragma unroll
@@ -881,10 +887,14 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
           uint32_t wb = 0;
           if (lane == kWave - 1 && inc > 0u) wb = atomicAdd(&ss.nx, inc);
           const uint32_t base = readlane_u32(wb, kWave - 1) + inc - cx;
-#pragma unroll
-          for (int j = 0; j < PT; ++j) {   // entry j's slot: the X entries before it
-            const uint32_t slot = base + (uint32_t)__popc(xm & ((1u << j) - 1u));
-            if (((xm >> j) & 1u) && slot < (uint32_t)kSortCap) list[slot] = key64(z[j], lo + j);
+          // the set bits only, in id order (a wave takes as many rounds as its
+          // lane with the most X entries: usually one or two), each value read
+          // again from the row in LDS (z = fl(y / T), the same division)
+          uint32_t slot = base;
+          for (uint32_t bits = xm; bits != 0u; bits &= bits - 1u, ++slot) {
+            const int j = __ffs(bits) - 1;
+            const float yv = val[lo + j];
+            if (slot < (uint32_t)kSortCap) list[slot] = key64(c.temp_on ? div_rcp(yv, rt) : yv, lo + j);
           }
         }
         C4S_PHASE(17);
