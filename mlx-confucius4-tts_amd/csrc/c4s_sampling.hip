@@ -695,29 +695,31 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
     // adds to a word of its own thread instead (in the boundary list, unused
     // until the compaction): on a wide row most values lie there, and lanes
     // adding to one LDS word take turns.
+    // The error bound counts every id of the thread (at least its finite ones).
     float s32 = 0.0f;
-    uint32_t flags = 0, kc = 0, nf = 0;
+    uint32_t flags = 0, kc = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
-      const bool fin = z[j] != ninf;
       const float tt = z[j] - m;
-      nf += fin ? 1u : 0u;
       if (topk) {
-        const int b = bucket_of(z[j], m);   // the last bucket for -inf
+        const int b = bucket_of_diff(-tt);   // the last bucket for -inf
         atomicAdd(b < kNB - 1 ? &hc[w * kNB + b] : reinterpret_cast<uint32_t*>(list) + t, 1u);
       } else {
-        float ej = fin ? mass32(tt) : 0.0f;
+        // 0 for -inf without a select: below about -150 the fp32 exp2 is 0
+        // and mass32 returns +0, so clamping at -1000 changes no mass
+        float ej = mass32(fmaxf(tt, -1000.0f));
         if (j < n) em[lo + j] = ej;   // read again by the kept sums and the draw
         if (dense) {
           // p == 1 removes the zero-mass positions: exp((double)tt) == 0 below
           // about -745.13; near that, and for subnormal kept masses, the chain decides
+          const bool fin = z[j] != ninf;
           const bool kp = fin && (thr < 0.0 || tt > -745.0f);
           if (fin && ((thr == 0.0 && tt <= -745.0f && tt >= -745.25f) || (kp && tt < -690.0f))) flags = 1u;
           ej = kp ? ej : 0.0f;
           kc += kp ? 1u : 0u;
         } else {
           // 2^-31 fixed point, truncated (ej <= 1)
-          const int b = bucket_of(z[j], m);
+          const int b = bucket_of_diff(-tt);
           const uint32_t q = (uint32_t)(ej * 0x1p31f);
           atomicAdd(b < kNB - 1 ? &hm[w * kNB + b] : reinterpret_cast<unsigned long long*>(list) + t,
                     (unsigned long long)q + kHistOne);
@@ -726,7 +728,7 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
       }
     }
     const double s = (double)s32;
-    const double er = s * (0x1p-20 + PT * 0x1p-24) + (double)nf * 0x1p-125;
+    const double er = s * (0x1p-20 + PT * 0x1p-24) + (double)max(n, 0) * 0x1p-125;
     C4S_PHASE(4);
     const Scan2 sc = block_scan2(s, er, kc | (flags << 16), ss.wa, ss.wb, ss.wu);
     C4S_PHASE(5);
@@ -1010,10 +1012,12 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
         ej = kp ? ec : 0.0f;
       }
       const bool kf = kp && z[j] != ninf;
-      flags |= (kf && z[j] - m < -690.0f) ? 1u : 0u;   // subnormal kept masses: libm implementations may disagree
       kc += kf ? 1u : 0u;
       ks32 += ej;
     }
+    // subnormal kept masses (libm implementations may disagree): the smallest
+    // kept value is the last kept key's (a -inf there also sends the row on)
+    flags = (t == 0 && key_value(kthr) - m < -690.0f) ? 1u : 0u;
     if (io.masked)
 #pragma unroll
       for (int j = 0; j < PT; ++j) {

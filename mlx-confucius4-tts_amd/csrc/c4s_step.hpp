@@ -139,6 +139,12 @@ __device__ __forceinline__ int bucket_of(float z, float m) {
   const float q = (m - z) * kBucketScale;   // monotone in z; +inf for z = -inf
   return q < (float)(kNB - 1) ? (int)q : kNB - 1;
 }
+// The same bucket from d = fl(m - z) (= -fl(z - m): IEEE subtraction is
+// symmetric in sign).
+__device__ __forceinline__ int bucket_of_diff(float d) {
+  const float q = d * kBucketScale;
+  return q < (float)(kNB - 1) ? (int)q : kNB - 1;
+}
 
 // The refined histogram: kNB sub-buckets over buckets lo2 .. lo2 + kNB / sc2 - 1
 // (an entry of those buckets; monotone in z like bucket_of).
