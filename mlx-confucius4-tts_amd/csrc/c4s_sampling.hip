@@ -512,7 +512,11 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
   const double rt = 1.0 / (double)c.temp;   // used only when the temperature applies
   uint32_t ky[PT];
 #pragma unroll
-  for (int j = 0; j < PT; ++j) ky[j] = (j < n) ? fkey(y[j]) : 0u;   // 0: below every key of a value
+  for (int j = 0; j < PT; ++j) ky[j] = fkey(y[j]);
+  if (n < PT) {   // the last threads: 0 past the row, below every key of a value
+#pragma unroll
+    for (int j = 0; j < PT; ++j) ky[j] = j < n ? ky[j] : 0u;
+  }
   uint32_t t1 = 0, t2 = 0;
 #pragma unroll
   for (int j = 0; j < PT; ++j) {
@@ -664,7 +668,11 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
   float z[PT];
   const double rt = 1.0 / (double)c.temp;   // used only when the temperature applies
 #pragma unroll
-  for (int j = 0; j < PT; ++j) z[j] = (c.temp_on && j < n) ? div_rcp(y[j], rt) : y[j];
+  for (int j = 0; j < PT; ++j) z[j] = c.temp_on ? div_rcp(y[j], rt) : y[j];
+  if (n < PT) {   // the last threads: the padding past the row stays -inf whatever the temperature
+#pragma unroll
+    for (int j = 0; j < PT; ++j) z[j] = j < n ? z[j] : ninf;
+  }
   {
     float lm = ninf;
 #pragma unroll
