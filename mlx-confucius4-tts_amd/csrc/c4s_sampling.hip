@@ -1008,14 +1008,16 @@ __device__ __forceinline__ bool sampled_step(const StepIO& io, const RowCfg& c, 
     const KeptRule kr{false, false, kthr};
     float ks32 = 0.0f;
     uint32_t kc = 0, flags = 0;
+    float ecs[PT];   // top_p: the masses cached by the histogram pass (0 for -inf)
+    if (!topk) read_row(em, lo, n, c.V, ecs);
 #pragma unroll
     for (int j = 0; j < PT; ++j) {   // z is -inf past the thread's ids: never kept with a mass
       bool kp;
       float ej;
       if (topk) {
         ej = kept_mass32(kr, z[j], m, lo + j, kp);
-      } else {   // the mass cached by the histogram pass (0 for -inf), read unconditionally
-        const float ec = em[min(lo + j, c.V - 1)];
+      } else {
+        const float ec = ecs[j];
         kp = ((int)(z[j] != ninf) & (int)kept_in(kr, z[j], m, lo + j)) != 0;   // z is -inf past the thread's ids
         ej = kp ? ec : 0.0f;
       }
@@ -1189,10 +1191,10 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
   // this thread's ids (odd stride: no LDS bank conflicts), every read
   // unconditional (index clamped) and the padding selected afterwards
   float y[PT];
+  read_row(val, lo, n, V, y);
+  if (n < PT) {
 #pragma unroll
-  for (int j = 0; j < PT; ++j) {
-    const float v = val[min(lo + j, V - 1)];
-    y[j] = (j < n) ? v : ninf;
+    for (int j = 0; j < PT; ++j) y[j] = j < n ? y[j] : ninf;
   }
   C4S_PHASE(29);
 

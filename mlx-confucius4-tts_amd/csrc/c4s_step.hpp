@@ -139,6 +139,22 @@ __device__ __forceinline__ int bucket_of(float z, float m) {
   const float q = (m - z) * kBucketScale;   // monotone in z; +inf for z = -inf
   return q < (float)(kNB - 1) ? (int)q : kNB - 1;
 }
+// out[j] = row[lo + j] for j < n and row[V - 1] past it: every read in bounds
+// and issued together. A thread whose ids all lie in the row (all but the last
+// few) reads at immediate offsets from one address instead of clamping each
+// index.
+template <int PT>
+__device__ __forceinline__ void read_row(const float* row, int lo, int n, int V, float (&out)[PT]) {
+  if (n == PT) {
+    const float* p = row + lo;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) out[j] = p[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < PT; ++j) out[j] = row[min(lo + j, V - 1)];
+  }
+}
+
 // The same bucket from d = fl(m - z) (= -fl(z - m): IEEE subtraction is
 // symmetric in sign).
 __device__ __forceinline__ int bucket_of_diff(float d) {
