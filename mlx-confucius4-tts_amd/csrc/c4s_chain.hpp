@@ -315,8 +315,7 @@ __device__ bool cut_by_mass(const Src& src, Seg sg, ScratchT<NWX>& sh, float max
         lm += m[j];
       }
       const double mincl = wave_incl_scan_f64(lm);
-      double mexcl = __shfl_up(mincl, 1, kWave);
-      if (l == 0) mexcl = 0.0;
+      const double mexcl = wave_shr1_f64(mincl, 0.0);
       const uint32_t cincl = wave_incl_scan_u32(lc);
       uint32_t crun = cincl - lc;
       double run = blow + mexcl;
@@ -1296,7 +1295,7 @@ __device__ __forceinline__ int run_chain(Src& src, ScratchT<NWX>& sh, const RowC
           const int L = __ffsll((unsigned long long)hit) - 1;
           found = base + L;
           acc = __shfl(inc, L, kWave);
-          const double before = __shfl_up(inc, 1, kWave);
+          const double before = wave_shr1_f64(inc, 0.0);
           const double pb = __shfl(before, L, kWave);
           prev = (L == 0) ? carry_m : pb;
         }

@@ -157,6 +157,11 @@ __device__ __forceinline__ double dpp_f64(double v, double fill) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
+// Lane i's value from lane i - 1 across the whole wave (wave_shr:1 = 0x138,
+// a gfx9 DPP control), `fill` in lane 0: the exclusive prefix from an
+// inclusive one without the LDS crossbar.
+__device__ __forceinline__ double wave_shr1_f64(double v, double fill) { return dpp_f64<0x138>(v, fill); }
+
 // Lane i's value from lane i ^ J. J = 1, 2: quad permutes; J = 4, 8: row shifts
 // by J inside the lane's 16-lane row (lane i reads i + J where bit J of i is
 // clear, i - J where it is set); wider: a cross-lane permute through LDS.

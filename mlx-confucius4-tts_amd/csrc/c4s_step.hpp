@@ -268,8 +268,7 @@ __device__ __forceinline__ Scan2 block_scan2(double v, double v2, uint32_t u, do
                                              uint32_t* wu) {
   const int lane = lane_id(), w = wave_id();
   const double inc = wave_scan_f64(v);
-  double exc = __shfl_up(inc, 1, kWave);
-  if (lane == 0) exc = 0.0;
+  const double exc = wave_shr1_f64(inc, 0.0);
   const double s2 = wave_sum_dpp(v2);
   const uint32_t uinc = wave_scan_u32(u);
   if (lane == kWave - 1) { wa[w] = inc; wu[w] = uinc; }
@@ -494,7 +493,7 @@ __device__ __noinline__ int draw_replay(const StepIO& io, const RowCfg& c, const
 template <bool kBlock>
 __device__ __noinline__ void decide_cut(const RowCfg& c, uint64_t v, int nX, float m, double thr, double S, double errS,
                            double Ma, double errMa, uint32_t n_above, const uint64_t* list, StepSh& sh) {
-  const int t = threadIdx.x, lane = lane_id();
+  const int t = threadIdx.x;
   const bool topk = c.topk_on;
   const bool valid = t < nX;
   const float ninf = neg_inf();
@@ -511,8 +510,7 @@ __device__ __noinline__ void decide_cut(const RowCfg& c, uint64_t v, int nX, flo
     tot = sc.tot;
   } else {
     const double inc = wave_scan_f64(et);
-    ex = __shfl_up(inc, 1, kWave);
-    if (lane == 0) ex = 0.0;
+    ex = wave_shr1_f64(inc, 0.0);
     tot = readlane_f64(inc, kWave - 1);
   }
   // entry removed iff the mass at or below it in ascending order,
