@@ -507,7 +507,7 @@ __device__ __forceinline__ bool fast_pick(const uint32_t* hist, uint32_t* red, u
 
 template <int PT>
 __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int V, const float (&y)[PT], int lo,
-                                          int n, FastSh& fs) {
+                                          int n, const float* val, FastSh& fs) {
   const int t = threadIdx.x, lane = lane_id(), wv = wave_id();
   const double rt = 1.0 / (double)c.temp;   // used only when the temperature applies
   uint32_t ky[PT];
@@ -578,15 +578,17 @@ __device__ __forceinline__ bool list_fast(const StepIO& io, const RowCfg& c, int
     // this thread's candidates as entries: z = fl(y / T) (sampling.cpp:16), the
     // id, and the candidate's position (pos + the candidates before it), which
     // is the id order: the draw's order key
+    // (the set bits only: a wave takes as many rounds as its lane with the
+    // most candidates, each value read again from the row in LDS)
     uint32_t cm = 0;
 #pragma unroll
     for (int j = 0; j < PT; ++j) cm |= (ky[j] >= L0) ? 1u << j : 0u;
-#pragma unroll
-    for (int j = 0; j < PT; ++j)
-      if ((cm >> j) & 1u) {
-        const uint32_t i = pos + (uint32_t)__popc(cm & ((1u << j) - 1u));
-        fs.cand[i] = make_entry(c.temp_on ? div_rcp(y[j], rt) : y[j], lo + j, (int)i);
-      }
+    uint32_t i = pos;
+    for (uint32_t bits = cm; bits != 0u; bits &= bits - 1u, ++i) {
+      const int j = __ffs(bits) - 1;
+      const float yv = val[lo + j];
+      fs.cand[i] = make_entry(c.temp_on ? div_rcp(yv, rt) : yv, lo + j, (int)i);
+    }
   }
   static_assert(kFastCands % 16 == 0 && kFastCands <= 1024, "padding to 16 entries stays in the candidate array; "
                 "positions fit the entry's rank field");
@@ -1215,7 +1217,7 @@ __global__ __launch_bounds__(kStepThreads) void k_rows_step(RowsArgs a) {
 
   // top-k rows with k <= 64: on a candidate list when it settles the step
   if (c.draw && c.topk_on && c.k <= kWave && c.p > 0.0f && !io.masked) {
-    if (list_fast<PT>(io, c, V, y, lo, n, *reinterpret_cast<FastSh*>(work))) return;
+    if (list_fast<PT>(io, c, V, y, lo, n, val, *reinterpret_cast<FastSh*>(work))) return;
     for (int i = t; i < (int)(3 * kHistBytes / 4); i += kStepThreads) hc[i] = 0u;
     __syncthreads();
   }
